@@ -1,0 +1,116 @@
+// Shared device helpers for the gfx950 KV-repair kernels: element traits, 16-byte vector
+// loads and stores, round-to-nearest-even casts and wavefront reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "chunkkv_amd.h"
+
+namespace ckv {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// 16-byte vector: the unit of every global load and store (global_load_dwordx4).
+typedef unsigned int vec16 __attribute__((ext_vector_type(4)));
+
+// ---- element conversions --------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 round-to-nearest-even; NaN becomes the canonical quiet NaN 0x7fc0, which is
+// what torch's BFloat16 conversion produces.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Element traits: VEC elements per 16-byte vector, unpack to fp32, pack with rounding.
+template <int DTYPE>
+struct Elem;
+
+template <>
+struct Elem<CKV_DTYPE_BF16> {
+  static constexpr int kBytes = 2;
+  static constexpr int kVec = 8;
+  __device__ __forceinline__ static void unpack(const vec16& v, float (&f)[kVec]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+      f[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+    }
+  }
+  __device__ __forceinline__ static vec16 pack(const float (&f)[kVec]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = f32_to_bf16_bits(f[2 * i]) | (f32_to_bf16_bits(f[2 * i + 1]) << 16);
+    return vec16{w[0], w[1], w[2], w[3]};
+  }
+  // value after rounding to the element type, back in fp32
+  __device__ __forceinline__ static float round_trip(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+};
+
+template <>
+struct Elem<CKV_DTYPE_F32> {
+  static constexpr int kBytes = 4;
+  static constexpr int kVec = 4;
+  __device__ __forceinline__ static void unpack(const vec16& v, float (&f)[kVec]) {
+    f[0] = __uint_as_float(v.x);
+    f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z);
+    f[3] = __uint_as_float(v.w);
+  }
+  __device__ __forceinline__ static vec16 pack(const float (&f)[kVec]) {
+    return vec16{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+  }
+  __device__ __forceinline__ static float round_trip(float f) { return f; }
+};
+
+// ---- memory -----------------------------------------------------------------------------
+
+// All kernel operands live in global memory; saying so (address space 1) makes the compiler
+// emit global_load/global_store, which wait on vmcnt alone, instead of flat accesses.
+typedef __attribute__((address_space(1))) vec16 gvec16;
+
+__device__ __forceinline__ vec16 ld16(const void* p) { return *(const gvec16*)p; }
+__device__ __forceinline__ void st16(void* p, const vec16& v) { *(gvec16*)p = v; }
+
+// Streaming variants: data touched once per launch, so keep it out of the caches' way.
+__device__ __forceinline__ vec16 ld16_stream(const void* p) { return __builtin_nontemporal_load((const gvec16*)p); }
+__device__ __forceinline__ void st16_stream(void* p, const vec16& v) { __builtin_nontemporal_store(v, (gvec16*)p); }
+
+// ---- wavefront reductions -----------------------------------------------------------------
+
+// Butterfly sum over the 64 lanes (xor 32, 16, 8, 4, 2, 1). Every lane ends with the same
+// value because fp32 addition is commutative; the tree is part of the bit-exact contract.
+__device__ __forceinline__ float wave_butterfly_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = x + __shfl_xor(x, m, kWave);
+  return x;
+}
+
+__device__ __forceinline__ void flag_error(int32_t* err, uint32_t bits) {
+  if (err != nullptr) atomicOr(reinterpret_cast<unsigned int*>(err), bits);
+}
+
+// ---- rotary frequencies -------------------------------------------------------------------
+
+// inv_freq_i = fp32(theta_f ** e_i), e_i = fp32(-(2i) / D), evaluated in fp64 and rounded
+// once to fp32: the correctly rounded value of the reference's fp32 expression
+// `base ** (-arange(0, D, 2) / D)`.
+__device__ __forceinline__ float rope_inv_freq(int i, int head_dim, double theta) {
+  const float theta_f = (float)theta;
+  const float e = (float)(-2 * i) / (float)head_dim;
+  return (float)pow((double)theta_f, (double)e);
+}
+
+}  // namespace ckv
+
+// Host-side status helper shared by the entry points.
+#define CKV_RETURN_IF_LAUNCH_FAILED()              \
+  do {                                             \
+    if (hipGetLastError() != hipSuccess) return CKV_ERR_HIP; \
+  } while (0)

@@ -1,0 +1,264 @@
+// Re-RoPE + gather: rebuild every layer's base K/V cache from cached chunks moved to new
+// offsets, in one launch for all layers and placements.
+//
+// Reference semantics (src/chunkkv/engine/torch_engine.py):
+//   inv_freq           :33   base ** (-arange(0, D, 2) / D)            (fp32)
+//   _rotate            :46-51  y1 = x1*cos - x2*sin, y2 = x1*sin + x2*cos in fp32, rounded
+//                               once to the element type; halves are [0, D/2) and [D/2, D)
+//   shift_keys         :56-59  angles = delta * inv_freq, same for every token; delta == 0
+//                               returns the keys unchanged
+//   base_kv            :96-103 per layer, per placement: K[:, :, s:e] = shift_keys(chunk K),
+//                               V[:, :, s:e] = chunk V
+// (MLX twin: src/chunkkv/scheduler/rerope.py:31-61.)
+//
+// Design (gfx950): one workgroup = one (segment, 32-token tile, layer). cos/sin depend only on
+// (delta, frequency index), so each workgroup builds a D/2-entry table in LDS once, from theta,
+// while its first 16-byte loads are in flight. The table holds the correctly rounded fp32 cos/sin
+// of the fp32 angle (evaluated in fp64, rounded once). Every thread then rotates VEC frequency
+// pairs (the 16 bytes at column c of the first half and the matching 16 bytes of the second
+// half) of several rows. Memory traffic is exactly one read and one write of every gathered
+// byte. Products and sums are separately rounded fp32 operations (built with -ffp-contract=off),
+// like the reference's separate torch kernels, so every output is reproducible bit-for-bit on
+// any IEEE host from the same table.
+#include "ckv_common.hpp"
+
+namespace ckv {
+
+constexpr int kGatherThreads = 256;
+constexpr int kGatherTile = 32;  // tokens per workgroup and layer
+constexpr int kGatherUnroll = 4;
+
+template <int DTYPE, int D>
+__global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
+    char* __restrict__ dst_k, char* __restrict__ dst_v, int64_t dst_layer_stride_b,
+    int64_t dst_head_stride_b, const uint64_t* __restrict__ src_tab, int n_chunks,
+    const ckv_segment* __restrict__ segs, ckv_segment one_seg, uint64_t one_src_k,
+    uint64_t one_src_v, int64_t one_src_head_stride_b, int n_layers, int n_heads,
+    int n_tokens, double theta, int32_t* __restrict__ err) {
+  using E = Elem<DTYPE>;
+  constexpr int VEC = E::kVec;
+  constexpr int HALF = D / 2;
+  static_assert(HALF % VEC == 0, "head_dim/2 must be a multiple of the vector width");
+  constexpr int TPR = HALF / VEC;                  // threads per row
+  constexpr int RPP = kGatherThreads / TPR;        // rows per pass of the workgroup
+  constexpr int64_t ROW_B = (int64_t)D * E::kBytes;
+  constexpr int HALF_B = HALF * E::kBytes;
+  static_assert(kGatherThreads % TPR == 0, "rows must tile the workgroup");
+
+  __shared__ float2 cs_tab[HALF];
+
+  ckv_segment s = one_seg;
+  if (segs != nullptr) {
+    typedef __attribute__((address_space(1))) const int32_t gi32;
+    gi32* f = (gi32*)(segs + blockIdx.x);
+    s = ckv_segment{f[0], f[1], f[2], f[3], f[4], f[5]};
+  }
+  const int layer = blockIdx.z;
+  const int t0 = blockIdx.y * kGatherTile;
+  if (t0 >= s.n_tokens) return;  // uniform: tile past this segment's end
+  if (s.dst_start < 0 || s.src_start < 0 || s.chunk < 0 || s.chunk >= n_chunks ||
+      (int64_t)s.dst_start + s.n_tokens > n_tokens ||
+      (int64_t)s.src_start + s.n_tokens > s.src_len) {
+    if (threadIdx.x == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+    return;
+  }
+
+  const char* src_k;
+  const char* src_v;
+  int64_t src_head_b;
+  if (segs != nullptr) {
+    const int64_t ti = ((int64_t)s.chunk * n_layers + layer) * 2;
+    src_k = reinterpret_cast<const char*>(src_tab[ti]);
+    src_v = reinterpret_cast<const char*>(src_tab[ti + 1]);
+    src_head_b = (int64_t)s.src_len * ROW_B;
+  } else {
+    src_k = reinterpret_cast<const char*>(one_src_k);
+    src_v = reinterpret_cast<const char*>(one_src_v);
+    src_head_b = one_src_head_stride_b;
+  }
+  const bool with_v = src_v != nullptr && dst_v != nullptr;
+
+  const int ntok = min(kGatherTile, s.n_tokens - t0);
+  const int rows = n_heads * kGatherTile;  // (head, token) grid of the tile; tokens >= ntok idle
+  const int col = threadIdx.x % TPR;
+  const int rl = threadIdx.x / TPR;
+  const int64_t col_b = (int64_t)col * 16;
+
+  const char* sk0 = src_k + (int64_t)(s.src_start + t0) * ROW_B + col_b;
+  const char* sv0 = with_v ? src_v + (int64_t)(s.src_start + t0) * ROW_B + col_b : nullptr;
+  char* dk0 = dst_k + (int64_t)layer * dst_layer_stride_b + (int64_t)(s.dst_start + t0) * ROW_B + col_b;
+  char* dv0 = with_v ? dst_v + (int64_t)layer * dst_layer_stride_b + (int64_t)(s.dst_start + t0) * ROW_B + col_b
+                     : nullptr;
+
+  vec16 kx1[kGatherUnroll], kx2[kGatherUnroll], vx1[kGatherUnroll], vx2[kGatherUnroll];
+
+  auto row_ok = [&](int r) { return r < rows && (r % kGatherTile) < ntok; };
+  auto src_off = [&](int r) { return (int64_t)(r / kGatherTile) * src_head_b + (int64_t)(r % kGatherTile) * ROW_B; };
+  auto dst_off = [&](int r) { return (int64_t)(r / kGatherTile) * dst_head_stride_b + (int64_t)(r % kGatherTile) * ROW_B; };
+
+  auto issue_loads = [&](int r0) {
+#pragma unroll
+    for (int u = 0; u < kGatherUnroll; ++u) {
+      const int r = r0 + u * RPP + rl;
+      if (row_ok(r)) {
+        const int64_t o = src_off(r);
+        kx1[u] = ld16_stream(sk0 + o);
+        kx2[u] = ld16_stream(sk0 + o + HALF_B);
+        if (with_v) {
+          vx1[u] = ld16_stream(sv0 + o);
+          vx2[u] = ld16_stream(sv0 + o + HALF_B);
+        }
+      }
+    }
+  };
+
+  issue_loads(0);
+
+  // cos/sin of this segment's shift for every frequency, computed once per workgroup.
+  const bool rotate = s.delta != 0;
+  float c[VEC], sn[VEC];
+  if (rotate) {
+    if (threadIdx.x < HALF) {
+      const float inv = rope_inv_freq(threadIdx.x, D, theta);
+      const float ang = (float)s.delta * inv;  // fp32 angle, as torch forms delta * inv_freq
+      double sd, cd;                           // cos/sin of that angle, correctly rounded to fp32
+      sincos((double)ang, &sd, &cd);
+      cs_tab[threadIdx.x] = make_float2((float)cd, (float)sd);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float2 t = cs_tab[col * VEC + e];
+      c[e] = t.x;
+      sn[e] = t.y;
+    }
+  }
+
+  for (int r0 = 0;;) {
+#pragma unroll
+    for (int u = 0; u < kGatherUnroll; ++u) {
+      const int r = r0 + u * RPP + rl;
+      if (row_ok(r)) {
+        const int64_t o = dst_off(r);
+        if (rotate) {
+          float a[VEC], b[VEC], y1[VEC], y2[VEC];
+          E::unpack(kx1[u], a);
+          E::unpack(kx2[u], b);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float p1 = a[e] * c[e];
+            const float p2 = b[e] * sn[e];
+            const float p3 = a[e] * sn[e];
+            const float p4 = b[e] * c[e];
+            y1[e] = p1 - p2;
+            y2[e] = p3 + p4;
+          }
+          st16_stream(dk0 + o, E::pack(y1));
+          st16_stream(dk0 + o + HALF_B, E::pack(y2));
+        } else {
+          st16_stream(dk0 + o, kx1[u]);
+          st16_stream(dk0 + o + HALF_B, kx2[u]);
+        }
+        if (with_v) {
+          st16_stream(dv0 + o, vx1[u]);
+          st16_stream(dv0 + o + HALF_B, vx2[u]);
+        }
+      }
+    }
+    r0 += kGatherUnroll * RPP;
+    if (r0 >= rows) break;
+    issue_loads(r0);
+  }
+}
+
+// Writes the D/2 inverse frequencies the kernels above inline.
+__global__ void inv_freq_kernel(float* out, int head_dim, double theta) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < head_dim / 2) out[i] = rope_inv_freq(i, head_dim, theta);
+}
+
+template <int DTYPE, int D>
+static void launch_gather(char* dk, char* dv, int64_t ls_b, int64_t hs_b, const uint64_t* tab,
+                          int n_chunks, const ckv_segment* segs, ckv_segment one, uint64_t one_k, uint64_t one_v,
+                          int64_t one_hs_b, int n_segs, int max_tiles, int n_layers, int n_heads,
+                          int n_tokens, double theta, int32_t* err, hipStream_t st) {
+  dim3 grid((unsigned)n_segs, (unsigned)max_tiles, (unsigned)n_layers);
+  hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D>), grid, dim3(kGatherThreads), 0, st, dk, dv,
+                     ls_b, hs_b, tab, n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, n_heads,
+                     n_tokens, theta, err);
+}
+
+using GatherFn = void (*)(char*, char*, int64_t, int64_t, const uint64_t*, int, const ckv_segment*,
+                          ckv_segment, uint64_t, uint64_t, int64_t, int, int, int, int, int,
+                          double, int32_t*, hipStream_t);
+
+static GatherFn pick_gather(int dtype, int head_dim) {
+#define CKV_CASE(DT, HD) \
+  if (dtype == DT && head_dim == HD) return &launch_gather<DT, HD>;
+  CKV_CASE(CKV_DTYPE_BF16, 64)
+  CKV_CASE(CKV_DTYPE_BF16, 128)
+  CKV_CASE(CKV_DTYPE_BF16, 256)
+  CKV_CASE(CKV_DTYPE_F32, 64)
+  CKV_CASE(CKV_DTYPE_F32, 128)
+  CKV_CASE(CKV_DTYPE_F32, 256)
+#undef CKV_CASE
+  return nullptr;
+}
+
+static int elem_bytes(int dtype) { return dtype == CKV_DTYPE_BF16 ? 2 : 4; }
+
+}  // namespace ckv
+
+extern "C" int32_t ckv_inv_freq(float* out, int32_t head_dim, double theta, void* stream) {
+  if (out == nullptr || head_dim <= 0 || (head_dim & 1) || !(theta > 0.0)) return CKV_ERR_INVALID_ARGUMENT;
+  const int half = head_dim / 2;
+  hipLaunchKernelGGL(ckv::inv_freq_kernel, dim3((half + 63) / 64), dim3(64), 0, (hipStream_t)stream, out,
+                     (int)head_dim, theta);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}
+
+extern "C" int32_t ckv_rerope_gather(void* dst_k, void* dst_v, int64_t dst_layer_stride,
+                                     int64_t dst_head_stride, const uint64_t* src_tab,
+                                     int32_t n_chunks, const ckv_segment* segs, int32_t n_segs,
+                                     int32_t max_seg_tokens, int32_t n_layers, int32_t n_heads,
+                                     int32_t n_tokens, int32_t head_dim, int32_t dtype,
+                                     double theta, int32_t* err, void* stream) {
+  using namespace ckv;
+  GatherFn fn = pick_gather(dtype, head_dim);
+  if (fn == nullptr || dst_k == nullptr || dst_v == nullptr || src_tab == nullptr || segs == nullptr)
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_chunks < 0 || n_segs < 0 || max_seg_tokens < 0 || n_layers <= 0 || n_heads <= 0 || n_tokens < 0 || !(theta > 0.0))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (dst_head_stride < (int64_t)n_tokens * head_dim || dst_layer_stride < dst_head_stride * n_heads)
+    return CKV_ERR_OUT_OF_RANGE;
+  if (n_segs == 0 || max_seg_tokens == 0) return CKV_OK;
+  const int max_tiles = (max_seg_tokens + kGatherTile - 1) / kGatherTile;
+  if (n_segs > 0x7fffffff / 2 || max_tiles > 65535 || n_layers > 65535) return CKV_ERR_TOO_LARGE;
+  const int64_t eb = elem_bytes(dtype);
+  fn((char*)dst_k, (char*)dst_v, dst_layer_stride * eb, dst_head_stride * eb, src_tab, n_chunks, segs, ckv_segment{},
+     0, 0, 0, n_segs, max_tiles, n_layers, n_heads, n_tokens, theta, err, (hipStream_t)stream);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}
+
+extern "C" int32_t ckv_shift_keys(void* dst, int64_t dst_head_stride, const void* src,
+                                  int64_t src_head_stride, int32_t n_heads, int32_t n_rows,
+                                  int32_t head_dim, int32_t dtype, int32_t delta, double theta,
+                                  void* stream) {
+  using namespace ckv;
+  GatherFn fn = pick_gather(dtype, head_dim);
+  if (fn == nullptr || dst == nullptr || src == nullptr || n_heads <= 0 || n_rows < 0 || !(theta > 0.0))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (dst_head_stride < (int64_t)n_rows * head_dim || src_head_stride < (int64_t)n_rows * head_dim)
+    return CKV_ERR_OUT_OF_RANGE;
+  if (n_rows == 0) return CKV_OK;
+  const int max_tiles = (n_rows + kGatherTile - 1) / kGatherTile;
+  if (max_tiles > 65535) return CKV_ERR_TOO_LARGE;
+  const int64_t eb = elem_bytes(dtype);
+  ckv_segment one{0, n_rows, 0, 0, n_rows, delta};
+  fn((char*)dst, nullptr, 0, dst_head_stride * eb, nullptr, 1, nullptr, one, (uint64_t)(uintptr_t)src, 0,
+     src_head_stride * eb, 1, max_tiles, 1, n_heads, n_rows, theta, nullptr, (hipStream_t)stream);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}

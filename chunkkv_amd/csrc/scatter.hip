@@ -1,0 +1,66 @@
+// Scatter freshly computed K/V rows of the active set into one layer's cache.
+//
+// Reference semantics (src/chunkkv/engine/torch_engine.py:155-156):
+//   K[:, :, active] = k;  V[:, :, active] = v      (row overwrite, bit-exact copy)
+//
+// Design (gfx950): each thread moves one 16-byte vector of K and the matching vector of V.
+// Consecutive threads walk one row (D elements), then the next head, then the next active
+// token, so the destination writes of a row are one contiguous 256-byte burst (D = 128, bf16)
+// and the source reads follow the fresh tensor's own strides.
+#include "ckv_common.hpp"
+
+namespace ckv {
+
+constexpr int kScatterThreads = 256;
+
+__global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
+    char* dst_k, char* dst_v, int64_t d_hs_b, const char* __restrict__ sk, int64_t sk_hs_b,
+    int64_t sk_ts_b, const char* __restrict__ sv, int64_t sv_hs_b, int64_t sv_ts_b,
+    const int64_t* __restrict__ rows, int n_rows, int n_tokens, int n_heads, int vecs_per_row,
+    int64_t row_b, int32_t* __restrict__ err) {
+  const int64_t g = (int64_t)blockIdx.x * kScatterThreads + threadIdx.x;
+  const int64_t per_tok = (int64_t)n_heads * vecs_per_row;
+  const int64_t j = g / per_tok;
+  if (j >= n_rows) return;
+  const int rem = (int)(g - j * per_tok);
+  const int h = rem / vecs_per_row;
+  const int64_t cb = (int64_t)(rem % vecs_per_row) * 16;
+  const int64_t t = rows[j];
+  if (t < 0 || t >= n_tokens) {
+    if (rem == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+    return;
+  }
+  const vec16 a = ld16(sk + h * sk_hs_b + j * sk_ts_b + cb);
+  const vec16 b = ld16(sv + h * sv_hs_b + j * sv_ts_b + cb);
+  const int64_t o = h * d_hs_b + t * row_b + cb;
+  st16(dst_k + o, a);
+  st16(dst_v + o, b);
+}
+
+}  // namespace ckv
+
+extern "C" int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
+                                    int64_t sk_head_stride, int64_t sk_token_stride, const void* src_v,
+                                    int64_t sv_head_stride, int64_t sv_token_stride, const int64_t* rows,
+                                    int32_t n_rows, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
+                                    int32_t dtype, int32_t* err, void* stream) {
+  using namespace ckv;
+  if (dtype != CKV_DTYPE_BF16 && dtype != CKV_DTYPE_F32) return CKV_ERR_INVALID_ARGUMENT;
+  const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
+  if (head_dim <= 0 || (head_dim * eb) % 16 != 0 || n_heads <= 0 || n_rows < 0 || n_tokens < 0)
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_rows > 0 && (dst_k == nullptr || dst_v == nullptr || src_k == nullptr || src_v == nullptr || rows == nullptr))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (dst_head_stride < (int64_t)n_tokens * head_dim) return CKV_ERR_OUT_OF_RANGE;
+  if (n_rows == 0) return CKV_OK;
+  const int vecs_per_row = (int)(head_dim * eb / 16);
+  const int64_t total = (int64_t)n_rows * n_heads * vecs_per_row;
+  const int64_t blocks = (total + kScatterThreads - 1) / kScatterThreads;
+  if (blocks > 0x7fffffffLL) return CKV_ERR_TOO_LARGE;
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)blocks), dim3(kScatterThreads), 0, (hipStream_t)stream,
+                     (char*)dst_k, (char*)dst_v, dst_head_stride * eb, (const char*)src_k, sk_head_stride * eb,
+                     sk_token_stride * eb, (const char*)src_v, sv_head_stride * eb, sv_token_stride * eb, rows,
+                     (int)n_rows, (int)n_tokens, (int)n_heads, vecs_per_row, (int64_t)head_dim * eb, err);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}

@@ -1,0 +1,284 @@
+// Layer-1 selection: per-chunk relative deviation and escalation, pooled budget, pooled top-k
+// with forced sinks, and compaction of the new active set — one single-workgroup launch, so
+// the host never synchronises inside the layer loop.
+//
+// Reference semantics (src/chunkkv/engine/torch_engine.py:125-153):
+//   keep = ~cached | sink
+//   for each non-exact placement p:                              (:128-140)
+//     rel = diff[span].sum() / norm[span].sum()                   (fp32, .item())
+//     escalated = thr is not None and rel > thr                   (Python float compare)
+//     if escalated: keep[span] = True
+//     elif ratio > 0: pool[span] = True; budget += int(round(ratio * len))
+//   budget = min(budget, (pool & ~keep).sum())                    (:142)
+//   top = argsort(-where(pool & ~keep, diff, -1))[:budget]; keep[top] = True   (:143-145)
+//   keep_abs = keep.nonzero(); sel = local[keep_abs]              (:146-152)
+// torch's argsort is not stable, so the reference leaves the order of equal deviations open;
+// this kernel fixes it: larger diff first, then lower token index (NaN ranks last).
+//
+// Design (gfx950): 1024 threads (16 wavefronts). keep/pool live as N-bit masks in LDS.
+// Chunk sums: one wavefront per chunk, lane-strided fp32 partials + xor butterfly (the order
+// the oracle restates). Top-k: MSB-first radix select over order-preserving 32-bit keys, four
+// 8-bit passes with an LDS histogram, which yields the exact threshold key T and how many ties
+// at T to take; a final pass in token order takes key > T plus the lowest-index ties and
+// compacts the kept positions with wavefront ballots (popcount prefix sums).
+#include "ckv_common.hpp"
+
+namespace ckv {
+
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / kWave;
+
+// Order-preserving key of a deviation: larger float -> larger key; -0 == +0; NaN -> 0.
+__device__ __forceinline__ uint32_t dev_key(float f) {
+  if (f != f) return 0u;
+  if (f == 0.0f) f = 0.0f;
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ bool bit_of(const uint32_t* w, int p) { return (w[p >> 5] >> (p & 31)) & 1u; }
+
+// Exclusive prefix count of `pred` over the workgroup in thread order, plus the total.
+__device__ __forceinline__ int block_excl_count(bool pred, int* wave_tot, int& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const uint64_t m = __ballot(pred);
+  const int in_wave = __popcll(m & ((1ull << lane) - 1ull));
+  if (lane == 0) wave_tot[wave] = __popcll(m);
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const int t = wave_tot[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  __syncthreads();  // wave_tot is reused by the next call
+  total = all;
+  return before + in_wave;
+}
+
+// Set bits [a, b) of an LDS bitmask, spreading the words over the lanes of one wavefront.
+__device__ __forceinline__ void set_bit_range(uint32_t* w, int a, int b, int lane) {
+  if (a >= b) return;
+  for (int word = (a >> 5) + lane; word <= ((b - 1) >> 5); word += kWave) {
+    const int lo = max(a, word << 5) - (word << 5);
+    const int hi = min(b, (word << 5) + 32) - (word << 5);  // exclusive, 1..32
+    const uint32_t m = (hi - lo == 32) ? 0xffffffffu : (((1u << (hi - lo)) - 1u) << lo);
+    atomicOr(&w[word], m);
+  }
+}
+
+__global__ __launch_bounds__(kSelThreads) void select_kernel(
+    const float* __restrict__ diff, const float* __restrict__ norm, const uint8_t* __restrict__ flags,
+    const int32_t* __restrict__ local, int n_tokens, const ckv_chunk_span* __restrict__ chunks,
+    int n_chunks, int has_thr, double thr, int64_t* __restrict__ keep_abs,
+    int64_t* __restrict__ keep_local, float* __restrict__ rel_out, uint8_t* __restrict__ esc_out,
+    int32_t* __restrict__ counts) {
+  extern __shared__ uint32_t masks[];  // keep[W], pool[W]
+  __shared__ uint32_t hist[256];
+  __shared__ int wave_tot[kSelWaves];
+  __shared__ int s_budget_req, s_bad_span, s_digit, s_above;
+
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int W = (n_tokens + 31) >> 5;
+  uint32_t* keepw = masks;
+  uint32_t* poolw = masks + W;
+
+  if (tid == 0) {
+    s_budget_req = 0;
+    s_bad_span = 0;
+  }
+  // keep = ~cached | sink; pool = 0. Each wavefront covers 64 positions = 2 words per step.
+  for (int base = wave * kWave; base < W * 32; base += kSelThreads) {
+    const int p = base + lane;
+    bool k = false;
+    if (p < n_tokens) {
+      const uint8_t f = flags[p];
+      k = !(f & CKV_POS_CACHED) || (f & CKV_POS_SINK);
+    }
+    const uint64_t m = __ballot(k);
+    if (lane == 0) {
+      keepw[base >> 5] = (uint32_t)m;
+      poolw[base >> 5] = 0u;
+    } else if (lane == 32 && ((base >> 5) + 1) < W) {
+      keepw[(base >> 5) + 1] = (uint32_t)(m >> 32);
+      poolw[(base >> 5) + 1] = 0u;
+    }
+  }
+  __syncthreads();
+
+  // Per-chunk relative deviation, escalation and budget (one wavefront per chunk).
+  for (int c = wave; c < n_chunks; c += kSelWaves) {
+    const ckv_chunk_span sp = chunks[c];
+    const bool ok = sp.start >= 0 && sp.length >= 0 && (int64_t)sp.start + sp.length <= n_tokens;
+    float sd = 0.0f, sn = 0.0f;
+    if (ok) {
+      for (int q = lane; q < sp.length; q += kWave) {
+        sd = sd + diff[sp.start + q];
+        sn = sn + norm[sp.start + q];
+      }
+    }
+    sd = wave_butterfly_sum(sd);
+    sn = wave_butterfly_sum(sn);
+    const float rel = sd / sn;
+    const bool esc = ok && has_thr && ((double)rel > thr);
+    if (lane == 0) {
+      rel_out[c] = rel;
+      esc_out[c] = esc ? 1 : 0;
+      if (!ok) atomicAdd(&s_bad_span, 1);
+    }
+    if (!ok) continue;
+    if (esc) {
+      set_bit_range(keepw, sp.start, sp.start + sp.length, lane);
+    } else if (sp.pooled) {
+      set_bit_range(poolw, sp.start, sp.start + sp.length, lane);
+      if (lane == 0) atomicAdd(&s_budget_req, sp.budget);
+    }
+  }
+  __syncthreads();
+
+  // Candidates = pool & ~keep; budget = min(requested, #candidates).
+  int my_cand = 0;
+  for (int w = tid; w < W; w += kSelThreads) my_cand += __popc(poolw[w] & ~keepw[w]);
+  int n_cand = 0;
+  {
+    // integer block sum via the count helper is not applicable (counts > 1 per thread)
+    int v = my_cand;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+    if (lane == 0) wave_tot[wave] = v;
+    __syncthreads();
+    for (int w = 0; w < kSelWaves; ++w) n_cand += wave_tot[w];
+    __syncthreads();
+  }
+  const int budget_req = s_budget_req;
+  const int budget = max(0, min(budget_req, n_cand));
+
+  // Radix select of the budget-th largest key among candidates.
+  uint32_t prefix = 0u, pmask = 0u;
+  int need = budget;  // after the passes: ties at T still to take
+  if (budget > 0) {
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int b = tid; b < 256; b += kSelThreads) hist[b] = 0u;
+      __syncthreads();
+      for (int p = tid; p < n_tokens; p += kSelThreads) {
+        if (bit_of(poolw, p) && !bit_of(keepw, p)) {
+          const uint32_t key = dev_key(diff[p]);
+          if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // lane l owns digits 255-4l .. 252-4l (descending); inclusive scan from the top.
+        uint32_t h4[4];
+        uint32_t local_sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          h4[i] = hist[255 - (lane * 4 + i)];
+          local_sum += h4[i];
+        }
+        uint32_t incl = local_sum;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+          const uint32_t t = __shfl_up(incl, off, kWave);
+          if (lane >= off) incl += t;
+        }
+        uint32_t above = incl - local_sum;  // keys with a larger digit than this lane's first
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (above < (uint32_t)need && (uint32_t)need <= above + h4[i]) {
+            s_digit = 255 - (lane * 4 + i);
+            s_above = (int)above;
+          }
+          above += h4[i];
+        }
+      }
+      __syncthreads();
+      need -= s_above;
+      prefix |= (uint32_t)s_digit << shift;
+      pmask |= 255u << shift;
+      __syncthreads();
+    }
+  }
+  const uint32_t T = prefix;
+
+  // Final pass in token order: take key > T and the first `need` ties, then compact keep.
+  int tie_carry = 0, keep_carry = 0, my_cached = 0, my_bad = 0;
+  for (int base = 0; base < n_tokens; base += kSelThreads) {
+    const int p = base + tid;
+    const bool valid = p < n_tokens;
+    bool take = false, tie = false;
+    if (valid && budget > 0 && bit_of(poolw, p) && !bit_of(keepw, p)) {
+      const uint32_t key = dev_key(diff[p]);
+      take = key > T;
+      tie = key == T;
+    }
+    int tie_total = 0;
+    const int tie_rank = block_excl_count(tie, wave_tot, tie_total) + tie_carry;
+    tie_carry += tie_total;
+    take = take || (tie && tie_rank < need);
+    const bool kept = valid && (bit_of(keepw, p) || take);
+    int keep_total = 0;
+    const int rank = block_excl_count(kept, wave_tot, keep_total) + keep_carry;
+    keep_carry += keep_total;
+    if (kept) {
+      const int l = local[p];
+      keep_abs[rank] = p;
+      keep_local[rank] = l < 0 ? 0 : l;
+      my_bad += l < 0;
+      my_cached += (flags[p] & CKV_POS_CACHED) ? 1 : 0;
+    }
+  }
+
+  // Reduce the per-thread counters.
+  int v1 = my_cached, v2 = my_bad;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    v1 += __shfl_xor(v1, m, kWave);
+    v2 += __shfl_xor(v2, m, kWave);
+  }
+  __shared__ int red1[kSelWaves], red2[kSelWaves];
+  if (lane == 0) {
+    red1[wave] = v1;
+    red2[wave] = v2;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int c1 = 0, c2 = 0;
+    for (int w = 0; w < kSelWaves; ++w) {
+      c1 += red1[w];
+      c2 += red2[w];
+    }
+    counts[CKV_COUNT_KEEP] = keep_carry;
+    counts[CKV_COUNT_SELECTED_CACHED] = c1;
+    counts[CKV_COUNT_BUDGET] = budget;
+    counts[CKV_COUNT_CANDIDATES] = n_cand;
+    counts[CKV_COUNT_UNCOMPUTED] = c2;
+    counts[CKV_COUNT_BUDGET_REQUESTED] = budget_req;
+    counts[6] = s_bad_span;
+    counts[7] = 0;
+  }
+}
+
+}  // namespace ckv
+
+extern "C" int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flags,
+                              const int32_t* local, int32_t n_tokens, const ckv_chunk_span* chunks,
+                              int32_t n_chunks, int32_t has_threshold, double escalate_threshold,
+                              int64_t* keep_abs, int64_t* keep_local, float* rel_dev, uint8_t* escalated,
+                              int32_t* counts, void* stream) {
+  using namespace ckv;
+  if (diff == nullptr || norm == nullptr || pos_flags == nullptr || local == nullptr || keep_abs == nullptr ||
+      keep_local == nullptr || counts == nullptr || n_tokens < 0 || n_chunks < 0)
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_chunks > 0 && (chunks == nullptr || rel_dev == nullptr || escalated == nullptr))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_tokens > CKV_SELECT_MAX_TOKENS) return CKV_ERR_TOO_LARGE;
+  const int W = (n_tokens + 31) / 32;
+  const size_t lds = (size_t)(W > 0 ? W : 1) * 2 * sizeof(uint32_t);
+  hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, (hipStream_t)stream, diff, norm,
+                     pos_flags, local, (int)n_tokens, chunks, (int)n_chunks, (int)(has_threshold != 0),
+                     escalate_threshold, keep_abs, keep_local, rel_dev, escalated, counts);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}

@@ -1,0 +1,205 @@
+"""HipEngine: drop-in replacement for the reference TorchEngine with the KV-repair path on
+hand-written gfx950 kernels.
+
+Public surface = src/chunkkv/engine/torch_engine.py:18-207: constructor ``(model, tokenizer)``,
+``load(repo, dtype)``, ``prefill(tokens, placements, config, logits_from) -> PrefillResult``,
+``generate``, ``last_logprobs``, ``sync``, ``clear_cache``, ``shift_keys``, ``tokenizer``.
+The model's GEMMs, RMSNorm, MLP and SDPA attention stay on PyTorch-ROCm (chunkkv_amd.model).
+The KV repair runs on the HIP kernels:
+
+  reference (torch_engine.py)                        here
+  base_kv every layer (:96-103; ~13 launches per     one ckv_rerope_gather launch for all layers
+    placement and layer, zero-filled caches)           and placements into one (L,1,H,N,D) slab
+  deviation (:117-124)                               ckv_deviation (one wavefront per token)
+  rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
+    one .item() per chunk)                             nothing back unless a threshold is set
+  K[:, :, active] = k (:155-156)                     ckv_scatter_rows per layer
+
+Contracts where the reference leaves the result open: the selection breaks deviation ties by
+the lower token index (torch's argsort is unstable), deviation sums use a fixed order, and
+inv_freq is the correctly rounded fp32 value of the reference's expression (torch's fp32 pow
+may be one ulp off). Errors keep the reference's types: NotImplementedError for rope scaling,
+ValueError for logits at non-recomputed positions, AssertionError when the selection keeps a
+token that was never computed.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from chunkkv_amd import _native, ops
+from chunkkv_amd.model import DecoderPieces
+from chunkkv_amd.planner import RequestPlan, local_index, plan_request, stats_dict
+from chunkkv_amd.types import BlendConfig, ChunkKV, Placement, PrefillResult, plan_positions  # noqa: F401
+
+_ALIGN = 256
+
+_TORCH_OF = {
+    np.dtype(np.uint8): torch.uint8,
+    np.dtype(np.int32): torch.int32,
+    np.dtype(np.int64): torch.int64,
+    np.dtype(np.uint64): torch.int64,  # device addresses; the kernels read them as uint64
+}
+
+
+class HipEngine(DecoderPieces):
+    def __init__(self, model, tokenizer):
+        self._init_model(model, tokenizer)
+        if self.device.type != "cuda":
+            raise ValueError("HipEngine runs on a HIP device: move the model to 'cuda' first")
+        _native.lib()  # raises now if the kernels were never built: there is no CPU fallback
+        self.kv_dtype = self.layers[0].self_attn.k_proj.weight.dtype
+        ops.dtype_code(self.kv_dtype)
+        self.inv_freq = ops.inv_freq(self.head_dim, self.theta, self.device)
+
+    @classmethod
+    def load(cls, repo: str, dtype=torch.bfloat16) -> "HipEngine":
+        from transformers import AutoModelForCausalLM, AutoTokenizer
+
+        model = AutoModelForCausalLM.from_pretrained(repo, dtype=dtype).to("cuda")
+        return cls(model, AutoTokenizer.from_pretrained(repo))
+
+    def shift_keys(self, keys: torch.Tensor, delta: int) -> torch.Tensor:
+        """Move post-RoPE keys by `delta` positions on the HIP kernel (torch_engine.py:56-59)."""
+        return ops.shift_keys(keys, delta, self.theta)
+
+    # -- device-side request state --------------------------------------------------------
+
+    def _chunk_pointers(self, chunk, keepalive: list) -> np.ndarray:
+        """(n_layers, 2) uint64 device addresses of a chunk's per-layer K and V.
+
+        Conforming chunks (this device, the kv dtype, contiguous (1, H, L, D)) are read in
+        place and their table is memoised on the chunk object (chunk tensors are treated as
+        immutable once stored, as KVStore entries are); others are converted first.
+        """
+        n_layers = len(self.layers)
+        keys, values = chunk.keys, chunk.values
+        if len(keys) != n_layers or len(values) != n_layers:
+            raise ValueError(f"chunk has {len(keys)} key / {len(values)} value layers, model has {n_layers}")
+        sig = (id(keys), id(values), keys[0].data_ptr(), values[-1].data_ptr(), self.kv_dtype, self.device)
+        memo = getattr(chunk, "_ckv_ptrs", None)
+        if memo is not None and memo[0] == sig:
+            return memo[1]
+        want = (1, self.n_kv, keys[0].shape[2], self.head_dim)
+        ptrs = np.empty((n_layers, 2), dtype=np.uint64)
+        converted = False
+        for li in range(n_layers):
+            for j, t in enumerate((keys[li], values[li])):
+                if tuple(t.shape) != want:
+                    raise ValueError(f"chunk layer {li} tensor has shape {tuple(t.shape)}, expected {want}")
+                if t.device != self.device or t.dtype != self.kv_dtype or not t.is_contiguous() or t.data_ptr() % 16:
+                    t = t.to(device=self.device, dtype=self.kv_dtype).contiguous()
+                    keepalive.append(t)
+                    converted = True
+                ptrs[li, j] = t.data_ptr()
+        if not converted:
+            try:
+                chunk._ckv_ptrs = (sig, ptrs)
+            except AttributeError:
+                pass
+        return ptrs
+
+    def _upload(self, parts: list[np.ndarray]) -> list[torch.Tensor]:
+        """Pack host arrays into one pinned buffer, copy it with one async H2D, return views."""
+        offs, total = [], 0
+        for a in parts:
+            offs.append(total)
+            total += (a.nbytes + _ALIGN - 1) // _ALIGN * _ALIGN
+        host = torch.empty(max(total, _ALIGN), dtype=torch.uint8, pin_memory=True)
+        hv = host.numpy()
+        for a, o in zip(parts, offs):
+            if a.nbytes:
+                hv[o : o + a.nbytes] = np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+        dev = host.to(self.device, non_blocking=True)
+        return [
+            dev[o : o + a.nbytes].view(_TORCH_OF[a.dtype])
+            if a.nbytes
+            else torch.empty(0, dtype=_TORCH_OF[a.dtype], device=self.device)
+            for a, o in zip(parts, offs)
+        ]
+
+    # -- main entry -----------------------------------------------------------------------
+
+    @torch.inference_mode()
+    def prefill(self, tokens, placements=None, config=None, logits_from=None) -> PrefillResult:
+        placements = placements or []
+        config = config or BlendConfig()
+        N = len(tokens)
+        n_layers = len(self.layers)
+        logits_from = N - 1 if logits_from is None else logits_from
+        dev, H, D = self.device, self.n_kv, self.head_dim
+
+        plan: RequestPlan = plan_request(N, placements, config.n_sink, config.recompute_ratio)
+        select_layer = bool(placements) and config.full_first_layer and n_layers > 1
+        active_np = plan.layer0_idx if config.full_first_layer else plan.fresh_idx
+        local_np = local_index(N, active_np) if select_layer else np.zeros(0, dtype=np.int32)
+
+        keepalive: list = []
+        tab = np.zeros(0, dtype=np.uint64)
+        if plan.chunks:
+            tab = np.concatenate([self._chunk_pointers(c, keepalive).reshape(-1) for c in plan.chunks])
+        flags_d, local_d, active_d, segs_d, spans_d, tab_d = self._upload(
+            [plan.flags, local_np, active_np.astype(np.int64), plan.segments.reshape(-1), plan.spans.reshape(-1), tab]
+        )
+
+        # Base caches of every layer: uncovered rows stay unwritten here because they are
+        # uncached positions, which are in the active set at every layer and get scattered.
+        k_slab = torch.empty((n_layers, 1, H, N, D), dtype=self.kv_dtype, device=dev)
+        v_slab = torch.empty_like(k_slab)
+        err = torch.zeros(1, dtype=torch.int32, device=dev)
+        if len(plan.segments):
+            ops.rerope_gather(k_slab, v_slab, tab_d, segs_d, len(plan.segments), plan.max_seg_tokens, self.theta, err)
+        keys_out = list(k_slab.unbind(0))
+        values_out = list(v_slab.unbind(0))
+
+        active = active_d
+        h = self.inner.embed_tokens(torch.tensor([tokens], device=dev))[:, active]
+        ar = torch.arange(N, device=dev)
+        sel = None
+        for li, layer in enumerate(self.layers):
+            q, k, v = self._qkv(layer.self_attn, layer.input_layernorm(h), active)
+            K, V = keys_out[li], values_out[li]
+            if li == 1 and select_layer:
+                diff, norm = ops.deviation(k, v, K, V, flags_d, local_d, err)
+                sel = ops.select(diff, norm, flags_d, local_d, spans_d, config.escalate_threshold)
+                if config.escalate_threshold is None and not plan.has_overlap:
+                    n_keep = plan.n_keep  # fixed by the layout: no device round trip
+                else:
+                    counts = sel.counts.cpu()
+                    if int(counts[_native.COUNT_UNCOMPUTED]) > 0:
+                        raise AssertionError("selected a token that was never computed")
+                    n_keep = int(counts[_native.COUNT_KEEP])
+                rows = sel.keep_local[:n_keep]
+                h, q, k, v = h.index_select(1, rows), q.index_select(2, rows), k.index_select(2, rows), v.index_select(2, rows)
+                active = sel.keep_abs[:n_keep]
+            ops.scatter_rows(K, V, k, v, active, err)
+            h = self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :])
+
+        n_want = N - logits_from
+        if 0 <= logits_from <= N and not plan.cached[logits_from:].any():
+            # Uncached positions are in every active set, and active sets are sorted, so the
+            # requested positions are the last n_want rows.
+            logits = self._logits(h[:, h.shape[1] - n_want :])[0]
+        else:
+            want = (active >= logits_from).nonzero().squeeze(1)
+            if len(want) != n_want:
+                raise ValueError("logits requested for positions that were not recomputed")
+            logits = self._logits(h[:, want])[0]
+
+        chunk_stats: list[dict] = []
+        selected_cached = 0
+        if sel is not None:
+            counts = sel.counts.cpu()
+            if int(counts[_native.COUNT_UNCOMPUTED]) > 0:
+                raise AssertionError("selected a token that was never computed")
+            selected_cached = int(counts[_native.COUNT_SELECTED_CACHED])
+            for (s, L, _, _), r, e in zip(plan.spans.tolist(), sel.rel_dev.cpu().tolist(), sel.escalated.cpu().tolist()):
+                chunk_stats.append({"start": s, "length": L, "rel_dev": r, "escalated": bool(e)})
+        if int(err.item()) != 0:
+            raise RuntimeError("a KV-repair kernel reported an out-of-range descriptor")
+        del keepalive
+
+        layer0 = len(plan.layer0_idx) if config.full_first_layer else N - plan.n_cached
+        stats = stats_dict(N, plan.n_cached, n_layers, layer0, selected_cached, chunk_stats)
+        return PrefillResult(logits, torch.arange(logits_from, N), keys_out, values_out, stats, copy=lambda t: t.contiguous())

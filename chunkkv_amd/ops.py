@@ -1,0 +1,234 @@
+"""torch-facing wrappers of the C-ABI entry points (include/chunkkv_amd.h).
+
+Each wrapper checks shapes, dtypes, devices and 16-byte alignment on the host, passes raw
+device pointers and torch's current HIP stream, and maps a non-zero status to an exception.
+Every wrapper launches a HIP kernel; none computes anything on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from chunkkv_amd import _native
+from chunkkv_amd._native import check, lib
+
+_DTYPES = {torch.float32: _native.DTYPE_F32, torch.bfloat16: _native.DTYPE_BF16}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported K/V dtype {dtype}; the HIP kernels take float32 or bfloat16") from None
+
+
+def _dev(*ts: torch.Tensor) -> torch.device:
+    d = ts[0].device
+    for t in ts:
+        if t.device.type != "cuda":
+            raise ValueError("chunkkv_amd ops run on a HIP device; got a tensor on " + str(t.device))
+        if t.device != d:
+            raise ValueError(f"tensors on different devices: {t.device} vs {d}")
+    return d
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _rows_ok(t: torch.Tensor) -> bool:
+    """Last dim contiguous, base and every other stride on a 16-byte boundary."""
+    eb = t.element_size()
+    if t.stride(-1) != 1 or t.data_ptr() % 16:
+        return False
+    return all((s * eb) % 16 == 0 for s in t.stride()[:-1])
+
+
+def _rows_view(t: torch.Tensor) -> torch.Tensor:
+    return t if _rows_ok(t) else t.contiguous()
+
+
+def inv_freq(head_dim: int, theta: float, device) -> torch.Tensor:
+    """(head_dim/2,) fp32 inverse frequencies from the kernels' own device function (a1)."""
+    out = torch.empty(head_dim // 2, dtype=torch.float32, device=device)
+    _dev(out)
+    check(lib().ckv_inv_freq(_ptr(out), head_dim, float(theta), _stream(out.device)), "ckv_inv_freq")
+    return out
+
+
+def shift_keys(keys: torch.Tensor, delta: int, theta: float) -> torch.Tensor:
+    """Re-rotate post-RoPE keys (..., L, D) by `delta` positions (torch_engine.py:56-59).
+
+    delta == 0 returns `keys` itself, like the reference.
+    """
+    delta = int(delta)
+    if delta == 0:
+        return keys
+    if not -(2**31) <= delta < 2**31:
+        raise ValueError("delta does not fit in int32")
+    _dev(keys)
+    x = keys.contiguous()
+    L, D = x.shape[-2], x.shape[-1]
+    heads = x.numel() // max(1, L * D)
+    out = torch.empty_like(x)
+    if x.numel() == 0:
+        return out
+    check(
+        lib().ckv_shift_keys(
+            _ptr(out), L * D, _ptr(x), L * D, heads, L, D, dtype_code(x.dtype), delta, float(theta), _stream(x.device)
+        ),
+        "ckv_shift_keys",
+    )
+    return out
+
+
+def rerope_gather(
+    k_slab: torch.Tensor,
+    v_slab: torch.Tensor,
+    src_tab: torch.Tensor,
+    segments: torch.Tensor,
+    n_segs: int,
+    max_seg_tokens: int,
+    theta: float,
+    err: torch.Tensor | None = None,
+) -> None:
+    """Fill every layer's base K/V from cached chunks (torch_engine.py:96-103), one launch.
+
+    k_slab/v_slab: (n_layers, 1, H, N, D) contiguous. src_tab: uint64/int64 device table
+    [(chunk*n_layers + layer)*2 + {0, 1}]. segments: int32 (n_segs, 6) device descriptors.
+    """
+    _dev(k_slab, v_slab, src_tab, segments)
+    if not (k_slab.is_contiguous() and v_slab.is_contiguous() and k_slab.shape == v_slab.shape):
+        raise ValueError("K/V slabs must be contiguous and of equal shape")
+    if k_slab.dtype != v_slab.dtype:
+        raise ValueError("K/V slabs must share a dtype")
+    n_layers, _, H, N, D = k_slab.shape
+    if src_tab.dtype != torch.int64 or src_tab.numel() % (2 * n_layers):
+        raise ValueError("src_tab must be int64 with 2 addresses per (chunk, layer)")
+    if segments.dtype != torch.int32 or segments.numel() < 6 * int(n_segs):
+        raise ValueError("segments must be int32 with 6 fields per segment")
+    n_chunks = src_tab.numel() // (2 * n_layers)
+    check(
+        lib().ckv_rerope_gather(
+            _ptr(k_slab), _ptr(v_slab), H * N * D, N * D, _ptr(src_tab), n_chunks, _ptr(segments), int(n_segs),
+            int(max_seg_tokens), n_layers, H, N, D, dtype_code(k_slab.dtype), float(theta), _ptr(err),
+            _stream(k_slab.device),
+        ),
+        "ckv_rerope_gather",
+    )
+
+
+def deviation(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    flags: torch.Tensor,
+    local: torch.Tensor,
+    err: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Layer-1 per-position deviation and norm (torch_engine.py:117-124); returns (diff, norm)."""
+    _dev(k, v, K, V, flags, local)
+    k, v = _rows_view(k), _rows_view(v)
+    if K.dtype != k.dtype or V.dtype != k.dtype or v.dtype != k.dtype:
+        raise TypeError("fresh and cached K/V must share a dtype")
+    _, H, N, D = K.shape
+    if not (K.is_contiguous() and V.is_contiguous() and V.shape == K.shape):
+        raise ValueError("cached K/V must be contiguous (1, H, N, D)")
+    if k.shape[1] != H or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"fresh k/v shape {tuple(k.shape)} does not match cache {tuple(K.shape)}")
+    if flags.dtype != torch.uint8 or local.dtype != torch.int32 or flags.numel() != N or local.numel() != N:
+        raise ValueError("flags must be uint8 (N,) and local int32 (N,)")
+    if not (flags.is_contiguous() and local.is_contiguous()):
+        raise ValueError("flags and local must be contiguous")
+    diff = torch.empty(N, dtype=torch.float32, device=K.device)
+    norm = torch.empty(N, dtype=torch.float32, device=K.device)
+    check(
+        lib().ckv_deviation(
+            _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2), _ptr(K), _ptr(V), N * D,
+            _ptr(flags), _ptr(local), N, k.shape[2], H, D, dtype_code(K.dtype), _ptr(diff), _ptr(norm), _ptr(err),
+            _stream(K.device),
+        ),
+        "ckv_deviation",
+    )
+    return diff, norm
+
+
+@dataclass
+class Selection:
+    keep_abs: torch.Tensor  # int64 (N,), first counts[KEEP] valid, ascending
+    keep_local: torch.Tensor  # int64 (N,)
+    rel_dev: torch.Tensor  # float32 (C,)
+    escalated: torch.Tensor  # uint8 (C,)
+    counts: torch.Tensor  # int32 (COUNT_N,)
+
+
+def select(
+    diff: torch.Tensor,
+    norm: torch.Tensor,
+    flags: torch.Tensor,
+    local: torch.Tensor,
+    spans: torch.Tensor,
+    escalate_threshold: float | None,
+    out: Selection | None = None,
+) -> Selection:
+    """Per-chunk rel/escalation/budget + pooled top-k + sinks + compaction (torch_engine.py:125-153)."""
+    _dev(diff, norm, flags, local, spans)
+    N = diff.numel()
+    if N > _native.SELECT_MAX_TOKENS:
+        raise ValueError(f"selection supports at most {_native.SELECT_MAX_TOKENS} tokens, got {N}")
+    if spans.dtype != torch.int32 or (spans.numel() % 4):
+        raise ValueError("spans must be int32 (C, 4)")
+    C = spans.numel() // 4
+    dev = diff.device
+    if out is None:
+        out = Selection(
+            keep_abs=torch.empty(N, dtype=torch.int64, device=dev),
+            keep_local=torch.empty(N, dtype=torch.int64, device=dev),
+            rel_dev=torch.empty(C, dtype=torch.float32, device=dev),
+            escalated=torch.empty(C, dtype=torch.uint8, device=dev),
+            counts=torch.empty(_native.COUNT_N, dtype=torch.int32, device=dev),
+        )
+    has_thr = escalate_threshold is not None
+    check(
+        lib().ckv_select(
+            _ptr(diff), _ptr(norm), _ptr(flags), _ptr(local), N, _ptr(spans), C, int(has_thr),
+            float(escalate_threshold) if has_thr else 0.0, _ptr(out.keep_abs), _ptr(out.keep_local),
+            _ptr(out.rel_dev), _ptr(out.escalated), _ptr(out.counts), _stream(dev),
+        ),
+        "ckv_select",
+    )
+    return out
+
+
+def scatter_rows(
+    K: torch.Tensor, V: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rows: torch.Tensor, err: torch.Tensor | None = None
+) -> None:
+    """K[:, :, rows] = k; V[:, :, rows] = v for one layer (torch_engine.py:155-156)."""
+    _dev(K, V, k, v, rows)
+    k, v = _rows_view(k), _rows_view(v)
+    _, H, N, D = K.shape
+    if not (K.is_contiguous() and V.is_contiguous() and V.shape == K.shape):
+        raise ValueError("cache K/V must be contiguous (1, H, N, D)")
+    if k.dtype != K.dtype or v.dtype != K.dtype:
+        raise TypeError("fresh rows and cache must share a dtype")
+    n = rows.numel()
+    if k.shape != (1, H, n, D) or v.shape != k.shape:
+        raise ValueError(f"fresh rows {tuple(k.shape)} do not match ({1}, {H}, {n}, {D})")
+    if rows.dtype != torch.int64:
+        raise ValueError("rows must be int64")
+    rows = rows.contiguous()
+    check(
+        lib().ckv_scatter_rows(
+            _ptr(K), _ptr(V), N * D, _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2),
+            _ptr(rows), n, N, H, D, dtype_code(K.dtype), _ptr(err), _stream(K.device),
+        ),
+        "ckv_scatter_rows",
+    )

@@ -1,0 +1,86 @@
+"""Boundary types of the blend-prefill API.
+
+Field names, defaults and semantics follow src/chunkkv/engine/base.py:13-73 so that callers of
+the reference engine (runtime, store, bench) can hand these objects, or the reference's own,
+to :class:`chunkkv_amd.engine.HipEngine` unchanged. The engine only reads attributes, so the
+reference's dataclasses work as well as these.
+
+K/V tensors are (1, n_kv_heads, L, head_dim) with RoPE applied.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Callable
+
+
+@dataclass
+class ChunkKV:
+    """Per-layer K/V of one chunk, computed at positions start .. start+length (base.py:13-23)."""
+
+    keys: list[Any]
+    values: list[Any]
+    start: int
+
+    @property
+    def length(self) -> int:
+        return self.keys[0].shape[2]
+
+
+@dataclass
+class Placement:
+    """A cached chunk placed at a new offset of the request (base.py:26-33)."""
+
+    chunk: ChunkKV
+    start: int
+    ratio: float | None = None  # per-chunk recompute budget; None = the config default
+    exact: bool = False  # computed after the same prefix: never recomputed, not even at layer 0
+
+
+@dataclass
+class BlendConfig:
+    """Blend-prefill knobs (base.py:36-43)."""
+
+    recompute_ratio: float = 0.15  # fraction of cached tokens recomputed at layers >= 1
+    n_sink: int = 2  # first tokens of each non-exact chunk, always recomputed
+    full_first_layer: bool = True  # False = naive reuse (no repair)
+    escalate_threshold: float | None = None  # whole-chunk recompute above this layer-1 deviation
+
+
+@dataclass
+class PrefillResult:
+    """Prefill output (base.py:46-60). keys/values hold one (1, H, N, D) tensor per layer."""
+
+    logits: Any  # (n, vocab) for the positions in logit_positions
+    logit_positions: Any
+    keys: list[Any]
+    values: list[Any]
+    stats: dict = field(default_factory=dict)
+    copy: Callable[[Any], Any] = lambda a: a  # backend copy, so stored chunks don't pin request buffers
+
+    def chunk(self, start: int, end: int) -> ChunkKV:
+        return ChunkKV(
+            keys=[self.copy(k[:, :, start:end, :]) for k in self.keys],
+            values=[self.copy(v[:, :, start:end, :]) for v in self.values],
+            start=start,
+        )
+
+
+def plan_positions(n: int, placements: list, n_sink: int):
+    """Per-position flags as Python lists: cached, exact, sink (base.py:63-73).
+
+    Kept for API compatibility; the engine uses the vectorised planner in
+    :mod:`chunkkv_amd.planner`, which produces the same flags.
+    """
+    cached, exact, sink = [False] * n, [False] * n, [False] * n
+    for p in placements:
+        end = p.start + p.chunk.length
+        for i in range(p.start, end):
+            cached[i] = True
+        if p.exact:
+            for i in range(p.start, end):
+                exact[i] = True
+        else:
+            for i in range(p.start, min(end, p.start + n_sink)):
+                sink[i] = True
+    return cached, exact, sink

@@ -1,0 +1,209 @@
+/*
+ * chunkkv_amd — C ABI of the MI355X (gfx950) blend-prefill KV-repair kernels.
+ *
+ * The reference engine has no FFI: its KV repair is a sequence of PyTorch ops inside
+ * TorchEngine.prefill (src/chunkkv/engine/torch_engine.py:80-178). Each entry point below
+ * replaces one group of those ops; the comment on each names the lines it stands in for.
+ *
+ * Conventions shared by every entry point
+ *  - All array arguments are DEVICE addresses (hipMalloc / torch CUDA tensors) unless the
+ *    comment says otherwise. Pointers are borrowed: nothing is freed or retained.
+ *  - Every launch goes to `stream` (a hipStream_t; NULL = the legacy default stream). No entry
+ *    point synchronises, allocates or keeps global mutable state, so calls are re-entrant and
+ *    may run concurrently on different streams.
+ *  - K/V rows are head_dim contiguous elements. A "cache" tensor has layout (H, N, D): head
+ *    stride given in elements, token stride == head_dim.
+ *  - Element type is one of ckv_dtype. Arithmetic is fp32; results are rounded to the element
+ *    type with round-to-nearest-even, matching torch's `.to(dtype)`.
+ *  - Return value is a ckv_status. Argument errors are detected on the host before any
+ *    launch. Descriptor errors that only the device can see (an index or a placement outside
+ *    the cache) make the kernel skip that item and OR CKV_DEVICE_ERR_RANGE into `*err` when
+ *    `err` is non-NULL; the caller reads `err` whenever it next synchronises.
+ */
+#ifndef CHUNKKV_AMD_H
+#define CHUNKKV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CKV_ABI_VERSION 1
+
+typedef enum ckv_status {
+  CKV_OK = 0,
+  CKV_ERR_INVALID_ARGUMENT = 1, /* NULL pointer, unknown dtype, unsupported head_dim, bad count */
+  CKV_ERR_OUT_OF_RANGE = 2,     /* a host-visible size or index outside its range              */
+  CKV_ERR_TOO_LARGE = 3,        /* the request exceeds a kernel's capacity (see limits below)   */
+  CKV_ERR_HIP = 4               /* the HIP runtime rejected a launch                            */
+} ckv_status;
+
+typedef enum ckv_dtype {
+  CKV_DTYPE_F32 = 0,
+  CKV_DTYPE_BF16 = 1
+} ckv_dtype;
+
+/* Bits a kernel ORs into the optional device status word `err`. */
+#define CKV_DEVICE_ERR_RANGE 1u
+
+/* Per-position flags (one byte per token position), built by the host planner.
+ * Mirrors the lists returned by plan_positions (src/chunkkv/engine/base.py:63-73). */
+#define CKV_POS_CACHED 1u /* covered by a placement                                   */
+#define CKV_POS_SINK 2u   /* one of the first n_sink tokens of a non-exact placement    */
+#define CKV_POS_EXACT 4u  /* covered by an exact placement (never recomputed)          */
+
+/* Supported head dimensions (template instantiations). */
+#define CKV_SELECT_MAX_TOKENS 131072 /* ckv_select keeps two N-bit masks in LDS */
+
+/*
+ * One run of destination rows filled from one cached chunk: destination token positions
+ * [dst_start, dst_start + n_tokens) of every layer receive source tokens
+ * [src_start, src_start + n_tokens) of chunk `chunk`, keys re-rotated by `delta` positions.
+ * A placement (src/chunkkv/engine/base.py:26-33) becomes one segment; overlapping
+ * placements are split by the host so that the last placement wins, as in the reference's
+ * sequential slice assignment (torch_engine.py:99-102).
+ */
+typedef struct ckv_segment {
+  int32_t dst_start;
+  int32_t n_tokens;
+  int32_t chunk;     /* index into the source pointer table                       */
+  int32_t src_start; /* first source token inside the chunk                         */
+  int32_t src_len;   /* chunk length = token count between two heads in the source */
+  int32_t delta;     /* placement start - chunk start (torch_engine.py:101)         */
+} ckv_segment;
+
+/*
+ * One non-exact placement as the layer-1 selection sees it (torch_engine.py:128-140):
+ * its span, the token budget it adds to the pool, and whether it joins the pool at all.
+ * `budget` = int(round(ratio * length)) with Python's round-half-even; `pooled` = ratio > 0.
+ */
+typedef struct ckv_chunk_span {
+  int32_t start;
+  int32_t length;
+  int32_t budget;
+  int32_t pooled;
+} ckv_chunk_span;
+
+/* Indices of the `counts` output of ckv_select. */
+#define CKV_COUNT_KEEP 0            /* tokens in the new active set                         */
+#define CKV_COUNT_SELECTED_CACHED 1 /* cached tokens in it (stats recomputed_cached_tokens)  */
+#define CKV_COUNT_BUDGET 2          /* pooled budget after the cap (torch_engine.py:142)     */
+#define CKV_COUNT_CANDIDATES 3      /* pooled tokens not already kept                       */
+#define CKV_COUNT_UNCOMPUTED 4      /* kept tokens absent from the previous active set      */
+#define CKV_COUNT_BUDGET_REQUESTED 5
+#define CKV_COUNT_N 8
+
+/* ABI version compiled into the library (CKV_ABI_VERSION). */
+int32_t ckv_abi_version(void);
+
+/* Static text for a ckv_status value. */
+const char* ckv_status_string(int32_t status);
+
+/*
+ * Rotary inverse frequencies, computed on the device by the same function the re-RoPE
+ * kernels inline: out[i] = fp32(theta_f ** e_i) correctly rounded, with
+ * theta_f = fp32(theta) and e_i = fp32(-(2i) / head_dim), i in [0, head_dim/2).
+ * Replaces: TorchEngine.__init__ inv_freq (torch_engine.py:33); scheduler/rerope.py:31-33.
+ * out: head_dim/2 floats.
+ */
+int32_t ckv_inv_freq(float* out, int32_t head_dim, double theta, void* stream);
+
+/*
+ * Re-RoPE + gather for every layer in one launch: builds each layer's base K/V cache from
+ * cached chunks placed at new offsets.
+ *   dst_k/dst_v  per-layer caches; layer l, head h, token t lives at
+ *                base + l*dst_layer_stride + h*dst_head_stride + t*head_dim (elements).
+ *   src_tab      device table of source addresses, src_tab[(chunk*n_layers + l)*2 + 0] = keys
+ *                and [...+1] = values of chunk `chunk` at layer l; each is a contiguous
+ *                (H, src_len, D) tensor of dtype `dtype`. n_chunks = table rows; a segment
+ *                naming a chunk outside [0, n_chunks) is skipped and flagged.
+ *   segs         n_segs device descriptors; max_seg_tokens >= every segs[i].n_tokens.
+ *   Keys are re-rotated by delta (delta == 0 copies bit-for-bit); values are copied.
+ * Destination rows covered by no segment are left untouched (the engine always overwrites
+ * them with freshly computed rows).
+ * Replaces: base_kv (torch_engine.py:96-103) with shift_keys/_rotate (:46-59);
+ *           scheduler/rerope.py:36-47, :56-61.
+ */
+int32_t ckv_rerope_gather(void* dst_k, void* dst_v, int64_t dst_layer_stride,
+                          int64_t dst_head_stride, const uint64_t* src_tab, int32_t n_chunks,
+                          const ckv_segment* segs, int32_t n_segs, int32_t max_seg_tokens,
+                          int32_t n_layers, int32_t n_heads, int32_t n_tokens,
+                          int32_t head_dim, int32_t dtype, double theta, int32_t* err,
+                          void* stream);
+
+/*
+ * Re-rotate one key tensor by delta positions: dst = shift_keys(src, delta).
+ * src and dst are (n_heads, n_rows, head_dim) with the given head strides (elements) and
+ * token stride head_dim; dst may equal src. delta == 0 copies.
+ * Replaces: TorchEngine.shift_keys (torch_engine.py:56-59); scheduler/rerope.py:56-61.
+ */
+int32_t ckv_shift_keys(void* dst, int64_t dst_head_stride, const void* src,
+                       int64_t src_head_stride, int32_t n_heads, int32_t n_rows,
+                       int32_t head_dim, int32_t dtype, int32_t delta, double theta,
+                       void* stream);
+
+/*
+ * Layer-1 fresh-vs-cached deviation, one value pair per token position p in [0, n_tokens):
+ *   j = local[p] (row of p in the fresh tensors, -1 when p is not in the active set)
+ *   diff[p] = sum_{h,d} fp32(round(k[h,j,d] - K[h,p,d]))^2 + same for v     (0 when j < 0)
+ *   norm[p] = sum_{h,d} fp32(k[h,j,d])^2 + fp32(v[h,j,d])^2                (0 when j < 0)
+ * where round() is rounding to `dtype` (torch subtracts in the element type) and K/V read
+ * as zero at positions without CKV_POS_CACHED (the reference zero-fills them).
+ * Summation order (the bit-exact contract): the H*D products of one tensor are split into
+ * 16-byte vectors; vector q goes to lane q mod 64 of a 64-lane wavefront, each lane adds
+ * its elements in ascending order into an fp32 accumulator starting at +0, then the lanes
+ * are combined by a butterfly (xor 32, 16, 8, 4, 2, 1). diff = Sk + Sv, norm = Nk + Nv.
+ *   k_fresh/v_fresh  strides in elements (head, token); rows contiguous.
+ *   k_cache/v_cache  (H, n_tokens, D) with head stride cache_head_stride.
+ * Replaces: torch_engine.py:117-124.
+ */
+int32_t ckv_deviation(const void* k_fresh, int64_t kf_head_stride, int64_t kf_token_stride,
+                      const void* v_fresh, int64_t vf_head_stride, int64_t vf_token_stride,
+                      const void* k_cache, const void* v_cache, int64_t cache_head_stride,
+                      const uint8_t* pos_flags, const int32_t* local, int32_t n_tokens,
+                      int32_t n_fresh, int32_t n_heads, int32_t head_dim, int32_t dtype,
+                      float* diff, float* norm, int32_t* err, void* stream);
+
+/*
+ * Per-chunk relative deviation, escalation, pooled budget, pooled top-k with forced sinks,
+ * and compaction of the new active set, in one single-workgroup launch.
+ *   rel_dev[c]   = fp32(S_diff / S_norm) over chunk c's span (S = the lane-strided sum:
+ *                  lane l adds positions start+l, start+l+64, ... then a xor butterfly)
+ *   escalated[c] = has_threshold && (double)rel_dev[c] > escalate_threshold
+ *   keep         = !cached | sink | spans of escalated chunks | top-`budget` candidates,
+ *                  candidates = pooled spans minus keep, ranked by diff descending and
+ *                  token index ascending (NaN ranks last),
+ *                  budget = min(sum of budget over pooled non-escalated chunks, #candidates)
+ *   keep_abs[i]  = i-th kept position in ascending order, i < counts[CKV_COUNT_KEEP]
+ *   keep_local[i]= local[keep_abs[i]] (0 where local is -1; counted in CKV_COUNT_UNCOMPUTED)
+ *   counts       CKV_COUNT_N int32 values (indices CKV_COUNT_*).
+ * keep_abs and keep_local must hold n_tokens entries. n_tokens <= CKV_SELECT_MAX_TOKENS.
+ * Replaces: torch_engine.py:125-153 (rel/escalation/budget :128-142, argsort top-k :143-146,
+ *           keep.nonzero and local compaction :146-153).
+ */
+int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flags,
+                   const int32_t* local, int32_t n_tokens, const ckv_chunk_span* chunks,
+                   int32_t n_chunks, int32_t has_threshold, double escalate_threshold,
+                   int64_t* keep_abs, int64_t* keep_local, float* rel_dev, uint8_t* escalated,
+                   int32_t* counts, void* stream);
+
+/*
+ * Scatter freshly computed K/V rows into one layer's cache:
+ *   K[h, rows[j], :] = k[h, j, :],  V[h, rows[j], :] = v[h, j, :]   for j < n_rows.
+ * rows are distinct positions in [0, n_tokens) (any order).
+ * Replaces: torch_engine.py:155-156.
+ */
+int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride,
+                         const void* src_k, int64_t sk_head_stride, int64_t sk_token_stride,
+                         const void* src_v, int64_t sv_head_stride, int64_t sv_token_stride,
+                         const int64_t* rows, int32_t n_rows, int32_t n_tokens,
+                         int32_t n_heads, int32_t head_dim, int32_t dtype, int32_t* err,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHUNKKV_AMD_H */

@@ -1,0 +1,196 @@
+"""ORACLE — test infrastructure only (tests/, __graft_entry__.smoke(), bench.py cpu_baseline).
+
+numpy-facing wrapper of the C restatement in oracle/ckv_oracle.c, plus small helpers to move
+bf16 data between torch and numpy (bf16 travels as uint16 bit patterns). Function-by-function
+citations of the reference lines are in ckv_oracle.c.
+
+Parity status of each function (how it is pinned is in tests/test_oracle.py):
+  inv_freq        pinned: fp64 closed form, exact exponents
+  shift_keys      pinned: fp64 rotation (<= 1 bf16 ulp), composition/round trip at the
+                  reference's own tolerances (tests/test_rerope.py:15-22), delta=0 identity
+  rerope_gather   pinned: per-row equality with shift_keys + bit-exact value copies, brute force
+  deviation       pinned: fp64 brute force; exact 4x scaling; zero for identical rows; torch's
+                  own .sum(dim=(0,1,3)) within fp32 rounding
+  select          pinned: numpy lexsort and torch stable argsort of the reference expression,
+                  closed-form budgets/stats of tests/test_mlx_engine.py
+  scatter_rows    pinned: brute-force Python loop on small shapes
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "_build" / "libckv_oracle.so"
+DT_F32, DT_BF16 = 0, 1
+COUNT_N = 8
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            from oracle.build import build
+
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        P, I, L, D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
+        sig = {
+            "ckvo_inv_freq": [I, D, P],
+            "ckvo_shift_keys": [P, L, P, L, I, I, I, I, ctypes.c_int32, D],
+            "ckvo_rerope_gather": [P, P, L, L, P, P, I, I, I, I, I, I, D],
+            "ckvo_deviation": [P, L, L, P, L, L, P, P, L, P, P, I, I, I, I, I, P, P],
+            "ckvo_select": [P, P, P, P, I, P, I, I, D, P, P, P, P, P],
+            "ckvo_scatter_rows": [P, P, L, P, L, L, P, L, L, P, I, I, I, I, I],
+        }
+        for name, args in sig.items():
+            fn = getattr(_lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int if name != "ckvo_inv_freq" else None
+    return _lib
+
+
+def _p(a: np.ndarray | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if a is None else a.ctypes.data)
+
+
+def dt_of(a: np.ndarray) -> int:
+    if a.dtype == np.uint16:
+        return DT_BF16
+    if a.dtype == np.float32:
+        return DT_F32
+    raise TypeError(f"oracle element arrays are float32 or uint16 (bf16 bits), got {a.dtype}")
+
+
+# ---- bf16 helpers --------------------------------------------------------------------------
+
+
+def bf16_bits_to_f32(a: np.ndarray) -> np.ndarray:
+    return (a.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even, NaN -> 0x7fc0 (torch's rule)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = 0x7FC0
+    return r
+
+
+def to_numpy(t) -> np.ndarray:
+    """torch tensor (cpu or device) -> numpy; bf16 becomes uint16 bits."""
+    import torch
+
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def from_numpy(a: np.ndarray, device=None):
+    import torch
+
+    if a.dtype == np.uint16:
+        t = torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(a))
+    return t if device is None else t.to(device)
+
+
+def as_f32(a: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+
+
+# ---- restated functions --------------------------------------------------------------------
+
+
+def inv_freq(head_dim: int, theta: float) -> np.ndarray:
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    lib().ckvo_inv_freq(head_dim, float(theta), _p(out))
+    return out
+
+
+def shift_keys(x: np.ndarray, delta: int, theta: float) -> np.ndarray:
+    """x (..., L, D) -> re-rotated copy (delta == 0 returns x itself, as the reference)."""
+    if delta == 0:
+        return x
+    x = np.ascontiguousarray(x)
+    L, D = x.shape[-2], x.shape[-1]
+    heads = x.size // max(1, L * D)
+    out = np.empty_like(x)
+    rc = lib().ckvo_shift_keys(_p(out), L * D, _p(x), L * D, heads, L, D, dt_of(x), int(delta), float(theta))
+    assert rc == 0
+    return out
+
+
+def rerope_gather(
+    k_dst: np.ndarray, v_dst: np.ndarray, chunks_k: list, chunks_v: list, segments: np.ndarray, theta: float
+) -> int:
+    """k_dst/v_dst: (n_layers, H, N, D) arrays filled in place. chunks_k[c][l]: (H, L_c, D)."""
+    n_layers, H, N, D = k_dst.shape
+    keep = []
+    tab = np.zeros((len(chunks_k), n_layers, 2), dtype=np.uint64)
+    for c, (ks, vs) in enumerate(zip(chunks_k, chunks_v)):
+        for l in range(n_layers):
+            a, b = np.ascontiguousarray(ks[l]), np.ascontiguousarray(vs[l])
+            keep += [a, b]
+            tab[c, l, 0] = a.ctypes.data
+            tab[c, l, 1] = b.ctypes.data
+    segs = np.ascontiguousarray(segments, dtype=np.int32)
+    return lib().ckvo_rerope_gather(
+        _p(k_dst), _p(v_dst), H * N * D, N * D, _p(tab), _p(segs), len(segs), n_layers, H, N, D, dt_of(k_dst), float(theta)
+    )
+
+
+def deviation(k: np.ndarray, v: np.ndarray, K: np.ndarray, V: np.ndarray, flags: np.ndarray, local: np.ndarray):
+    """k, v: (H, n, D) fresh rows; K, V: (H, N, D) cache. Returns (diff, norm) float32 (N,)."""
+    k, v, K, V = (np.ascontiguousarray(a) for a in (k, v, K, V))
+    H, n, D = k.shape
+    N = K.shape[1]
+    diff = np.empty(N, dtype=np.float32)
+    norm = np.empty(N, dtype=np.float32)
+    flags = np.ascontiguousarray(flags, dtype=np.uint8)
+    local = np.ascontiguousarray(local, dtype=np.int32)
+    rc = lib().ckvo_deviation(
+        _p(k), n * D, D, _p(v), n * D, D, _p(K), _p(V), N * D, _p(flags), _p(local), N, n, H, D, dt_of(K), _p(diff), _p(norm)
+    )
+    assert rc == 0
+    return diff, norm
+
+
+def select(diff, norm, flags, local, spans: np.ndarray, escalate_threshold: float | None):
+    """Returns dict(keep_abs, keep_local, rel_dev, escalated, counts) like ckv_select."""
+    N = len(diff)
+    spans = np.ascontiguousarray(spans, dtype=np.int32).reshape(-1, 4)
+    C = len(spans)
+    diff = np.ascontiguousarray(diff, dtype=np.float32)
+    norm = np.ascontiguousarray(norm, dtype=np.float32)
+    flags = np.ascontiguousarray(flags, dtype=np.uint8)
+    local = np.ascontiguousarray(local, dtype=np.int32)
+    keep_abs = np.zeros(N + 1, dtype=np.int64)
+    keep_local = np.zeros(N + 1, dtype=np.int64)
+    rel = np.zeros(max(C, 1), dtype=np.float32)
+    esc = np.zeros(max(C, 1), dtype=np.uint8)
+    counts = np.zeros(COUNT_N, dtype=np.int32)
+    has = escalate_threshold is not None
+    rc = lib().ckvo_select(
+        _p(diff), _p(norm), _p(flags), _p(local), N, _p(spans), C, int(has), float(escalate_threshold) if has else 0.0,
+        _p(keep_abs), _p(keep_local), _p(rel), _p(esc), _p(counts),
+    )
+    assert rc == 0
+    n = int(counts[0])
+    return dict(keep_abs=keep_abs[:n], keep_local=keep_local[:n], rel_dev=rel[:C], escalated=esc[:C], counts=counts)
+
+
+def scatter_rows(K: np.ndarray, V: np.ndarray, k: np.ndarray, v: np.ndarray, rows: np.ndarray) -> int:
+    """K, V: (H, N, D) in place; k, v: (H, n, D); rows int64 (n,)."""
+    H, N, D = K.shape
+    n = k.shape[1]
+    k, v = np.ascontiguousarray(k), np.ascontiguousarray(v)
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    return lib().ckvo_scatter_rows(_p(K), _p(V), N * D, _p(k), n * D, D, _p(v), n * D, D, _p(rows), n, N, H, D, dt_of(K))

@@ -1,0 +1,320 @@
+"""GPU parity of each HIP kernel against the C oracle on the same seeded inputs.
+
+Bar (from the north star): gather, scatter and the selected index set bit-exact; deviation
+bit-exact under the fixed summation order; re-RoPE keys within one bf16 ulp (fp32 keys within
+a few fp32 ulps: cos/sin come from different libraries on host and device).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from chunkkv_amd import _native, ops
+from chunkkv_amd.planner import plan_request
+from oracle import oracle as O
+from tests.helpers import bf16_ulp_distance
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+THETA = 1e6
+
+
+def dev(a):
+    return O.from_numpy(a, DEV)
+
+
+def host(t):
+    return O.to_numpy(t)
+
+
+def rand_elems(rng, shape, bf16, scale=1.0):
+    a = (rng.standard_normal(shape) * scale).astype(np.float32)
+    return O.f32_to_bf16_bits(a) if bf16 else a
+
+
+def assert_keys_close(got, want, bf16, frac_exact=None):
+    """Re-rotated keys: the kernel and the oracle use the same correctly rounded cos/sin table
+    and IEEE fp32 products/sums, so they agree bit-for-bit (well inside the 1-ulp contract)."""
+    if bf16:
+        d = bf16_ulp_distance(got, want)
+        assert d.max() == 0, f"max ulp distance {d.max()} at {np.argwhere(d == d.max())[:3].tolist()}"
+    else:
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("theta", [1e4, 5e5, 1e6])
+def test_inv_freq_kernel_bit_exact(D, theta):
+    got = host(ops.inv_freq(D, theta, DEV))
+    np.testing.assert_array_equal(got.view(np.uint32), O.inv_freq(D, theta).view(np.uint32))
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("D", [64, 128])
+def test_shift_keys_kernel(bf16, D):
+    rng = np.random.default_rng(D + bf16)
+    x = rand_elems(rng, (1, 4, 300, D), bf16)
+    xt = dev(x)
+    assert ops.shift_keys(xt, 0, THETA) is xt
+    for delta in [1, -1, 37, 4096, -4096, 123457]:
+        got = host(ops.shift_keys(xt, delta, THETA))
+        assert_keys_close(got, O.shift_keys(x, delta, THETA), bf16)
+
+
+def _gather_case(rng, bf16, n_layers, H, D, lens, N, overlap=False):
+    class C:  # minimal ChunkKV stand-in for the planner
+        def __init__(self, L, start):
+            self.keys = [np.zeros((1, H, L, D))]
+            self.start = start
+
+    class P:
+        def __init__(self, chunk, start, exact=False):
+            self.chunk, self.start, self.exact, self.ratio = chunk, start, exact, None
+
+    chunks = [C(L, int(rng.integers(0, 5000))) for L in lens]
+    for i, c in enumerate(chunks):
+        c.idx = i  # position in ks/vs; plan.chunks lists chunks in placement order
+    # place chunks at shuffled non-overlapping slots (or overlapping ones)
+    order = rng.permutation(len(chunks))
+    pos, placements = 0, []
+    for i in order:
+        placements.append(P(chunks[i], pos, exact=bool(rng.random() < 0.2)))
+        pos += lens[i] - (lens[i] // 3 if overlap else 0) + int(rng.integers(0, 5))
+    assert pos <= N
+    plan = plan_request(N, placements, 4, 0.3)
+    ks = [[rand_elems(rng, (H, L, D), bf16) for _ in range(n_layers)] for L in lens]
+    vs = [[rand_elems(rng, (H, L, D), bf16) for _ in range(n_layers)] for L in lens]
+    return plan, ks, vs
+
+
+def _run_gather(plan, ks, vs, n_layers, H, D, N, bf16):
+    dt = torch.bfloat16 if bf16 else torch.float32
+    src = [([dev(k) for k in kl], [dev(v) for v in vl]) for kl, vl in zip(ks, vs)]
+    # chunk order in the plan follows first appearance; map back to the list index
+    tab = np.zeros((len(plan.chunks), n_layers, 2), dtype=np.uint64)
+    for ci, ch in enumerate(plan.chunks):
+        kl, vl = src[ch.idx]
+        for l in range(n_layers):
+            tab[ci, l, 0] = kl[l].data_ptr()
+            tab[ci, l, 1] = vl[l].data_ptr()
+    sentinel = -7.0
+    K = torch.full((n_layers, 1, H, N, D), sentinel, dtype=dt, device=DEV)
+    V = torch.full_like(K, sentinel)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    tab_t = torch.from_numpy(tab.view(np.int64)).to(DEV)
+    segs_t = torch.from_numpy(plan.segments.reshape(-1)).to(DEV)
+    ops.rerope_gather(K, V, tab_t, segs_t, len(plan.segments), plan.max_seg_tokens, THETA, err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    # oracle, same segments (chunk indices refer to plan.chunks order)
+    okl = [ks[ch.idx] for ch in plan.chunks]
+    ovl = [vs[ch.idx] for ch in plan.chunks]
+    npdt = np.uint16 if bf16 else np.float32
+    sent = O.f32_to_bf16_bits(np.float32([sentinel]))[0] if bf16 else np.float32(sentinel)
+    Ko = np.full((n_layers, H, N, D), sent, dtype=npdt)
+    Vo = np.full_like(Ko, sent)
+    assert O.rerope_gather(Ko, Vo, okl, ovl, plan.segments, THETA) == 0
+    return host(K).reshape(n_layers, H, N, D), host(V).reshape(n_layers, H, N, D), Ko, Vo, src
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("overlap", [False, True])
+def test_rerope_gather_matches_oracle(bf16, D, overlap):
+    rng = np.random.default_rng(100 + D + 2 * bf16 + overlap)
+    n_layers, H = 3, 2
+    lens = [40, 70, 33, 64, 1, 97]
+    N = sum(lens) + 40
+    plan, ks, vs = _gather_case(rng, bf16, n_layers, H, D, lens, N, overlap)
+    Kg, Vg, Ko, Vo, _ = _run_gather(plan, ks, vs, n_layers, H, D, N, bf16)
+    np.testing.assert_array_equal(Vg, Vo)  # values: pure copies
+    rot = np.zeros(N, dtype=bool)
+    for s, n, c, s0, L, delta in plan.segments:
+        if delta != 0:
+            rot[s : s + n] = True
+    np.testing.assert_array_equal(Kg[:, :, ~rot], Ko[:, :, ~rot])  # delta 0 and untouched rows
+    assert_keys_close(Kg[:, :, rot], Ko[:, :, rot], bf16)
+
+
+def test_rerope_gather_config2_full_size():
+    """Re-RoPE + gather at the Qwen2.5-7B KV shape: 28 layers, 4 heads, D=128, bf16,
+    16 chunks x 256 tokens moved by delta ~ U[-4096, 4096] into a 4096-token cache."""
+    rng = np.random.default_rng(2)
+    n_layers, H, D, L, C = 28, 4, 128, 256, 16
+    N = L * C
+    dst_slots = rng.permutation(C)
+    deltas = rng.integers(-4096, 4097, C)
+    Kc = torch.randn((C, n_layers, 1, H, L, D), device=DEV).to(torch.bfloat16)
+    Vc = torch.randn((C, n_layers, 1, H, L, D), device=DEV).to(torch.bfloat16)
+    segs = np.array([[dst_slots[c] * L, L, c, 0, L, deltas[c]] for c in range(C)], dtype=np.int32)
+    tab = np.zeros((C, n_layers, 2), dtype=np.uint64)
+    for c in range(C):
+        for l in range(n_layers):
+            tab[c, l, 0] = Kc[c, l].data_ptr()
+            tab[c, l, 1] = Vc[c, l].data_ptr()
+    K = torch.empty((n_layers, 1, H, N, D), dtype=torch.bfloat16, device=DEV)
+    V = torch.empty_like(K)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.rerope_gather(K, V, torch.from_numpy(tab.view(np.int64)).to(DEV), torch.from_numpy(segs.reshape(-1)).to(DEV),
+                      C, L, THETA, err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    Kc_h, Vc_h = host(Kc), host(Vc)
+    Ko = np.empty((n_layers, H, N, D), dtype=np.uint16)
+    Vo = np.empty_like(Ko)
+    okl = [[Kc_h[c, l, 0] for l in range(n_layers)] for c in range(C)]
+    ovl = [[Vc_h[c, l, 0] for l in range(n_layers)] for c in range(C)]
+    assert O.rerope_gather(Ko, Vo, okl, ovl, segs, THETA) == 0
+    np.testing.assert_array_equal(host(V).reshape(Vo.shape), Vo)
+    assert_keys_close(host(K).reshape(Ko.shape), Ko, True)
+
+
+def test_rerope_gather_flags_bad_segment_without_writing():
+    H, D, N = 2, 64, 32
+    src = torch.randn((1, H, 8, D), device=DEV)
+    tab = torch.tensor([src.data_ptr(), src.data_ptr()], dtype=torch.int64, device=DEV)
+    segs = torch.tensor([28, 8, 0, 0, 8, 5], dtype=torch.int32, device=DEV)  # runs past N
+    K = torch.zeros((1, 1, H, N, D), device=DEV)
+    V = torch.zeros_like(K)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.rerope_gather(K, V, tab, segs, 1, 8, THETA, err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == _native.DEVICE_ERR_RANGE
+    assert not K.any() and not V.any()
+
+
+def _deviation_case(rng, N, H, D, bf16, token_major_v=True):
+    """Config-3 style: cached = fresh + per-chunk lognormal(-3, 1) noise."""
+    n_chunks = max(1, N // 256)
+    sigma = np.exp(rng.normal(-3.0, 1.0, n_chunks)).astype(np.float32)
+    fresh_k = rng.standard_normal((H, N, D)).astype(np.float32)
+    fresh_v = rng.standard_normal((H, N, D)).astype(np.float32)
+    sig_tok = np.repeat(sigma, int(np.ceil(N / n_chunks)))[:N][None, :, None]
+    K = fresh_k + sig_tok * rng.standard_normal((H, N, D)).astype(np.float32)
+    V = fresh_v + sig_tok * rng.standard_normal((H, N, D)).astype(np.float32)
+    conv = (lambda a: O.f32_to_bf16_bits(a)) if bf16 else (lambda a: a.astype(np.float32))
+    return conv(fresh_k), conv(fresh_v), conv(K), conv(V)
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("N", [1, 77, 8192])
+def test_deviation_bit_exact(bf16, N):
+    rng = np.random.default_rng(N + bf16)
+    H, D = 4, 128
+    k, v, K, V = _deviation_case(rng, N, H, D, bf16)
+    flags = (rng.random(N) < 0.9).astype(np.uint8)
+    active = np.sort(rng.choice(N, max(1, int(N * 0.85)), replace=False))
+    local = np.full(N, -1, dtype=np.int32)
+    local[active] = np.arange(len(active))
+    kf, vf = k[:, active], v[:, active]
+    kt = dev(kf)[None]
+    # fresh v as the engine produces it: a token-major (1, n, H, D) buffer viewed as (1, H, n, D)
+    vt = dev(np.ascontiguousarray(vf.transpose(1, 0, 2)))[None].transpose(1, 2)
+    assert vt.stride(2) == H * D  # token stride of the token-major buffer
+    diff, norm = ops.deviation(kt, vt, dev(K)[None], dev(V)[None], dev(flags), dev(local))
+    od, on = O.deviation(kf, vf, K, V, flags, local)
+    np.testing.assert_array_equal(host(diff).view(np.uint32), od.view(np.uint32))
+    np.testing.assert_array_equal(host(norm).view(np.uint32), on.view(np.uint32))
+
+
+def _spans(n_chunks, L, ratio, n_sink, N):
+    flags = np.zeros(N, dtype=np.uint8)
+    spans = []
+    for c in range(n_chunks):
+        s = c * L
+        flags[s : s + L] |= 1
+        flags[s : s + min(n_sink, L)] |= 2
+        spans.append((s, L, int(round(ratio * L)), int(ratio > 0)))
+    return flags, np.array(spans, dtype=np.int32).reshape(-1, 4)
+
+
+def _check_select(diff, norm, flags, local, spans, thr):
+    got = ops.select(dev(diff), dev(norm), dev(flags), dev(local), dev(spans.reshape(-1)), thr)
+    want = O.select(diff, norm, flags, local, spans, thr)
+    counts = host(got.counts)
+    np.testing.assert_array_equal(counts[:6], want["counts"][:6])
+    n = int(counts[0])
+    np.testing.assert_array_equal(host(got.keep_abs)[:n], want["keep_abs"])
+    np.testing.assert_array_equal(host(got.keep_local)[:n], want["keep_local"])
+    C = len(spans)
+    np.testing.assert_array_equal(host(got.rel_dev)[:C].view(np.uint32), want["rel_dev"].view(np.uint32))
+    np.testing.assert_array_equal(host(got.escalated)[:C], want["escalated"])
+    return want
+
+
+@pytest.mark.parametrize("ratio", [0.15, 0.3, 0.5])
+def test_select_config3_bit_exact(ratio):
+    """32 chunks x 256 tokens, 4 sinks each, deviations from the config-3 noise model."""
+    rng = np.random.default_rng(int(ratio * 100))
+    N, H, D = 8192, 4, 128
+    k, v, K, V = _deviation_case(rng, N, H, D, True)
+    flags, spans = _spans(32, 256, ratio, 4, N)
+    local = np.arange(N, dtype=np.int32)
+    diff, norm = O.deviation(k, v, K, V, flags, local)
+    want = _check_select(diff, norm, flags, local, spans, None)
+    expect_keep = {0.15: 1344, 0.3: 2592, 0.5: 4224}[ratio]
+    assert want["counts"][0] == expect_keep
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_select_planted_ties_and_escalation(seed):
+    rng = np.random.default_rng(1000 + seed)
+    n_chunks, L, tail = int(rng.integers(1, 40)), int(rng.integers(5, 300)), int(rng.integers(0, 100))
+    N = n_chunks * L + tail
+    flags, spans = _spans(n_chunks, L, float(rng.choice([0.0, 0.1, 0.3, 1.0, 2.0])), int(rng.integers(0, 6)), N)
+    levels = rng.gamma(2.0, 1.0, 7).astype(np.float32)
+    diff = levels[rng.integers(0, 7, N)]  # heavy ties
+    if seed % 2:
+        diff[rng.integers(0, N, 5)] = np.nan
+        diff[rng.integers(0, N, 5)] = 0.0
+    norm = (np.abs(diff) + rng.gamma(3.0, 1.0, N)).astype(np.float32)
+    local = np.full(N, -1, dtype=np.int32)
+    act = np.sort(rng.choice(N, int(N * 0.95), replace=False))
+    local[act] = np.arange(len(act))
+    thr = None if seed < 3 else float(np.nanmedian(diff) / np.mean(norm))
+    _check_select(diff, norm, flags, local, spans, thr)
+
+
+@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 1023, 1024, 1025, 131072])
+def test_select_sizes(N):
+    rng = np.random.default_rng(N)
+    L = max(1, N // 3)
+    n_chunks = N // L
+    flags, spans = _spans(n_chunks, L, 0.3, 2, N)
+    diff = rng.gamma(2.0, 1.0, N).astype(np.float32)
+    norm = (diff + 1).astype(np.float32)
+    _check_select(diff, norm, flags, np.arange(N, dtype=np.int32), spans, None)
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_scatter_bit_exact(bf16):
+    rng = np.random.default_rng(7 + bf16)
+    H, N, D = 4, 3000, 128
+    n = 977
+    K = rand_elems(rng, (H, N, D), bf16)
+    V = rand_elems(rng, (H, N, D), bf16)
+    k = rand_elems(rng, (H, n, D), bf16)
+    v = rand_elems(rng, (H, n, D), bf16)
+    rows = np.sort(rng.choice(N, n, replace=False)).astype(np.int64)
+    Kt, Vt = dev(K)[None].contiguous(), dev(V)[None].contiguous()
+    vt = dev(np.ascontiguousarray(v.transpose(1, 0, 2)))[None].transpose(1, 2)  # token-major like v_proj
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.scatter_rows(Kt, Vt, dev(k)[None], vt, dev(rows), err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert O.scatter_rows(K, V, k, v, rows) == 0
+    np.testing.assert_array_equal(host(Kt)[0], K)
+    np.testing.assert_array_equal(host(Vt)[0], V)
+
+
+def test_scatter_flags_out_of_range_row():
+    H, N, D = 2, 16, 64
+    K = torch.zeros((1, H, N, D), device=DEV)
+    V = torch.zeros_like(K)
+    k = torch.ones((1, H, 2, D), device=DEV)
+    rows = torch.tensor([3, 16], dtype=torch.int64, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.scatter_rows(K, V, k, k.clone(), rows, err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == _native.DEVICE_ERR_RANGE
+    assert K[0, :, 3].eq(1).all() and int(K.count_nonzero()) == H * D
