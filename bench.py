@@ -1,0 +1,408 @@
+"""Blend-prefill KV-repair benchmark on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--ttft-requests R] [--cpu-seconds S]
+
+Workload (the Qwen2.5-7B 8k-context blend prefill): 28 layers, 4 KV heads, head_dim 128,
+bf16, rope theta 1e6; a request of N = 8256 tokens = 24 cached chunks of 320 tokens placed at
+shuffled positions (each chunk computed at its own original offset, so every placement shifts
+its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
+
+A step is one request's whole KV repair with every input already resident in HBM:
+re-RoPE + gather of all 28 layers (one launch), the layer-0 scatter of all 8256 rows, the
+layer-1 deviation and selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows), and
+the scatters of layers 1-27. Algorithmic bytes per step (read + write of every byte moved):
+    gather          28 x 24 x 320 x 4 heads x 128 x 2 B x 2 (K,V) x 2 (r+w) =   880,803,840
+    deviation       8256 x (4 rows x 1 KiB) + 8256 x 8 B                       =    33,882,624
+    scatter L0      8256 x 4096 B                                              =    33,816,576
+    scatter L1-27   27 x 2976 x 4096 B                                         =   329,121,792
+    total                                                                      = 1,277,624,832
+`value` = total bytes / measured time per step (GB/s), the step's 31 launches replayed from a
+HIP graph (the eager time, launch-bound from Python, is reported as ms_per_step_eager).
+`roofline` is the dominant kernel (re-RoPE + gather) timed live with HIP events around a burst
+of back-to-back launches on the launch stream. Inputs rotate between two independent copies so
+consecutive steps do not hit in the 256 MB MALL.
+
+Besides the bandwidth line, the run measures blend-prefill TTFT p50 (prefill + last_logprobs,
+the bracket of the reference's bench/replay.py:32-35) over seeded requests of the same shape on
+a random-init Qwen2.5-7B-architecture bf16 model, for HipEngine and for the reference-op
+sequence on PyTorch-ROCm, and the reference op sequence's KV repair on the host CPU
+(cpu_baseline).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "KV-repair HBM GB/s (% of peak) + blend-prefill TTFT p50, Qwen2.5-7B 8k ctx"
+PEAK_GBS = 8000.0  # MI355X HBM3E
+
+N_LAYERS, N_KV, HEAD_DIM, THETA = 28, 4, 128, 1e6
+CHUNK_LEN, N_CHUNKS, TAIL, QUERY = 320, 24, 512, 64
+N_TOKENS = N_CHUNKS * CHUNK_LEN + TAIL + QUERY  # 8256
+RATIO, N_SINK = 0.30, 4
+ROW_BYTES = N_KV * HEAD_DIM * 2  # one token's K (or V) row set, bf16
+
+GATHER_BYTES = N_LAYERS * N_CHUNKS * CHUNK_LEN * ROW_BYTES * 2 * 2
+DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Chunk:
+    """ChunkKV-compatible holder whose per-layer tensors are views of one slab."""
+
+    def __init__(self, k_slab, v_slab, start):
+        self.keys = list(k_slab.unbind(0))
+        self.values = list(v_slab.unbind(0))
+        self.start = start
+
+    @property
+    def length(self):
+        return self.keys[0].shape[2]
+
+
+class Place:
+    def __init__(self, chunk, start, ratio=None, exact=False):
+        self.chunk, self.start, self.ratio, self.exact = chunk, start, ratio, exact
+
+
+def rope_rows(x: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor) -> torch.Tensor:
+    ang = positions.float()[:, None] * inv_freq[None, :]
+    c, s = ang.cos(), ang.sin()
+    a, b = x.float().chunk(2, dim=-1)
+    return torch.cat((a * c - b * s, a * s + b * c), dim=-1).to(x.dtype)
+
+
+def make_request(gen: torch.Generator, dev, inv_freq):
+    """Chunks computed at their own offsets, placed at a shuffled order; returns placements."""
+    chunks = []
+    for _ in range(N_CHUNKS):
+        orig = int(torch.randint(0, 8192, (1,), generator=gen))
+        x = torch.randn((N_LAYERS, 1, N_KV, CHUNK_LEN, HEAD_DIM), generator=gen).to(dev)
+        k = rope_rows(x, torch.arange(orig, orig + CHUNK_LEN, device=dev), inv_freq).to(torch.bfloat16)
+        v = torch.randn((N_LAYERS, 1, N_KV, CHUNK_LEN, HEAD_DIM), generator=gen).to(dev).to(torch.bfloat16)
+        chunks.append(Chunk(k, v, orig))
+    order = torch.randperm(N_CHUNKS, generator=gen).tolist()
+    return [Place(chunks[c], i * CHUNK_LEN) for i, c in enumerate(order)]
+
+
+class RepairWorkload:
+    """All device buffers of one request's KV repair (see module docstring)."""
+
+    def __init__(self, seed: int, dev):
+        from chunkkv_amd import ops
+        from chunkkv_amd.planner import local_index, plan_request
+
+        gen = torch.Generator().manual_seed(seed)
+        self.inv = ops.inv_freq(HEAD_DIM, THETA, dev)
+        self.placements = make_request(gen, dev, self.inv)
+        plan = plan_request(N_TOKENS, self.placements, N_SINK, RATIO)
+        assert plan.n_keep == 2976 and plan.budget == 2304
+        self.plan = plan
+        tab = np.concatenate(
+            [np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(c.keys, c.values)], dtype=np.uint64).reshape(-1)
+             for c in plan.chunks]
+        )
+        self.tab = torch.from_numpy(tab.view(np.int64)).to(dev)
+        self.segs = torch.from_numpy(plan.segments.reshape(-1)).to(dev)
+        self.flags = torch.from_numpy(plan.flags).to(dev)
+        self.local = torch.from_numpy(local_index(N_TOKENS, plan.layer0_idx)).to(dev)
+        self.spans = torch.from_numpy(plan.spans.reshape(-1)).to(dev)
+        self.layer0 = torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev)
+        self.k_slab = torch.empty((N_LAYERS, 1, N_KV, N_TOKENS, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+        self.v_slab = torch.empty_like(self.k_slab)
+        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        # Fresh rows: layer 1 = cached rows + per-chunk lognormal(-3, 1) noise (the model's
+        # layer-1 K/V differ from the cached ones by a chunk-dependent amount); k is
+        # contiguous, v token-major like the v_proj output.
+        sigma = torch.exp(torch.randn(N_CHUNKS, generator=gen) - 3.0)
+        noise = torch.ones(N_TOKENS)
+        for i, p in enumerate(self.placements):
+            noise[p.start : p.start + CHUNK_LEN] = sigma[i]
+        base_k = torch.zeros((1, N_KV, N_TOKENS, HEAD_DIM))
+        base_v = torch.zeros_like(base_k)
+        for p in self.placements:
+            delta = p.start - p.chunk.start
+            ang = (delta * self.inv.cpu())[None, :]
+            kc = p.chunk.keys[1].float().cpu()
+            a, b = kc.chunk(2, dim=-1)
+            base_k[:, :, p.start : p.start + CHUNK_LEN] = torch.cat((a * ang.cos() - b * ang.sin(), a * ang.sin() + b * ang.cos()), -1)
+            base_v[:, :, p.start : p.start + CHUNK_LEN] = p.chunk.values[1].float().cpu()
+        nk = base_k + noise[None, None, :, None] * torch.randn(base_k.shape, generator=gen)
+        nv = base_v + noise[None, None, :, None] * torch.randn(base_v.shape, generator=gen)
+        self.fresh = []
+        for li in range(N_LAYERS):
+            n = N_TOKENS if li < 2 else plan.n_keep
+            if li == 1:
+                k, v = nk, nv
+            else:
+                k = torch.randn((1, N_KV, n, HEAD_DIM), generator=gen)
+                v = torch.randn((1, N_KV, n, HEAD_DIM), generator=gen)
+            k = k.to(torch.bfloat16).to(dev)
+            v = v.to(torch.bfloat16).transpose(1, 2).contiguous().to(dev).transpose(1, 2)
+            self.fresh.append((k, v))
+        self.sel = None
+
+    def gather(self):
+        from chunkkv_amd import ops
+
+        ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(self.plan.segments),
+                          self.plan.max_seg_tokens, THETA, self.err)
+
+    def rest(self):
+        """Everything after the gather: scatter L0, deviation + selection at L1, scatters L1-27."""
+        from chunkkv_amd import ops
+
+        K, V = self.k_slab.unbind(0), self.v_slab.unbind(0)
+        ops.scatter_rows(K[0], V[0], *self.fresh[0], self.layer0, self.err)
+        k1, v1 = self.fresh[1]
+        diff, norm = ops.deviation(k1, v1, K[1], V[1], self.flags, self.local, self.err)
+        self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
+        rows = self.sel.keep_abs[: self.plan.n_keep]
+        for li in range(1, N_LAYERS):
+            k, v = self.fresh[li] if li > 1 else (k1[:, :, : self.plan.n_keep], v1[:, :, : self.plan.n_keep])
+            ops.scatter_rows(K[li], V[li], k, v, rows, self.err)
+
+
+def repair_bytes(n_keep: int) -> int:
+    """Algorithmic bytes of one request's KV repair (module docstring)."""
+    scatter_row = ROW_BYTES * 2 * 2  # K and V rows of one token, read + write
+    return GATHER_BYTES + DEVIATION_BYTES + N_TOKENS * scatter_row + (N_LAYERS - 1) * n_keep * scatter_row
+
+
+def _timed(fn, n: int, stream) -> float:
+    """Average ms of n calls of fn(i), HIP events on `stream` around the whole burst."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(n):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / n
+
+
+def bench_repair(steps: int, warmup: int, dev) -> dict:
+    """Time the KV-repair step. The 31 launches of a step are captured once per input set in a
+    HIP graph and replayed (the step is launch-bound from Python otherwise); the eager time is
+    reported too. The dominant kernel's average duration comes from a burst of back-to-back
+    gather launches on the same stream."""
+    wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
+
+    def step(w):
+        w.gather()
+        w.rest()
+
+    for i in range(max(warmup, 2)):
+        step(wls[i % 2])
+    torch.cuda.synchronize()
+    graphs = []
+    for w in wls:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step(w)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(w)
+        graphs.append(g)
+    stream = torch.cuda.current_stream(dev)
+    for i in range(2):
+        graphs[i].replay()
+    ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
+    ms_eager = _timed(lambda i: step(wls[i % 2]), steps, stream)
+    g_ms = _timed(lambda i: wls[i % 2].gather(), steps, stream)
+    assert all(int(w.err.item()) == 0 for w in wls)
+    n_keep = wls[0].plan.n_keep
+    assert int(wls[0].sel.counts[0].item()) == n_keep
+    nbytes = repair_bytes(n_keep)
+    return dict(ms_per_step=ms, ms_eager=ms_eager, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, gather_ms=g_ms,
+                gather_gbs=GATHER_BYTES / (g_ms * 1e-3) / 1e9, n_keep=n_keep)
+
+
+def random_qwen25_7b(dev):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(vocab_size=152064, hidden_size=3584, intermediate_size=18944, num_hidden_layers=N_LAYERS,
+                      num_attention_heads=28, num_key_value_heads=N_KV, max_position_embeddings=32768,
+                      rope_theta=THETA, tie_word_embeddings=False, rms_norm_eps=1e-6)
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen2ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    return model.eval()
+
+
+class _Tok:
+    eos_token_id = 151645
+
+
+def bench_ttft(n_requests: int, dev) -> dict:
+    """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests."""
+    from chunkkv_amd.baseline import TorchOpsEngine
+    from chunkkv_amd.engine import HipEngine
+    from chunkkv_amd.types import BlendConfig
+
+    t = time.perf_counter()
+    model = random_qwen25_7b(dev)
+    log(f"[bench] random-init Qwen2.5-7B architecture ready in {time.perf_counter() - t:.1f}s")
+    hip, ref = HipEngine(model, _Tok()), TorchOpsEngine(model, _Tok())
+    gen = torch.Generator().manual_seed(7)
+    vocab = model.config.vocab_size
+    # Chunk pool: each chunk prefilled alone at position 0 (its own context), stored like KVStore does.
+    pool = []
+    for _ in range(2 * N_CHUNKS):
+        toks = torch.randint(0, vocab, (CHUNK_LEN,), generator=gen).tolist()
+        res = hip.prefill(toks)
+        pool.append((toks, res.chunk(0, CHUNK_LEN)))
+        del res
+    reqs = []
+    for _ in range(n_requests + 2):
+        pick = torch.randperm(len(pool), generator=gen)[:N_CHUNKS].tolist()
+        tokens, placements = [], []
+        for c in pick:
+            placements.append(Place(pool[c][1], len(tokens)))
+            tokens += pool[c][0]
+        tokens += torch.randint(0, vocab, (TAIL + QUERY,), generator=gen).tolist()
+        reqs.append((tokens, placements))
+    cfg = BlendConfig(recompute_ratio=RATIO, n_sink=N_SINK)
+    out = {}
+    for name, eng in (("hip", hip), ("torch_ops", ref)):
+        times, stats = [], None
+        for i, (tokens, placements) in enumerate(reqs):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            res = eng.prefill(tokens, placements, cfg)
+            eng.last_logprobs(res)
+            dt = time.perf_counter() - t0
+            if i >= 2:
+                times.append(dt * 1e3)
+            stats = res.stats
+            del res
+        out[name] = dict(p50=float(np.percentile(times, 50)), p99=float(np.percentile(times, 99)), stats=stats)
+        log(f"[bench] TTFT {name}: p50 {out[name]['p50']:.2f} ms  p99 {out[name]['p99']:.2f} ms")
+    del hip, ref, model
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_cpu(seconds: float) -> dict:
+    """The reference's KV-repair op sequence on the host's cores, bounded to ~`seconds`."""
+    from types import SimpleNamespace as NS
+
+    from oracle import engine_ref as R
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(99)
+    inv = R.reference_inv_freq(THETA, HEAD_DIM)
+    chunks = [NS(keys=[torch.randn((1, N_KV, CHUNK_LEN, HEAD_DIM), generator=gen).bfloat16() for _ in range(N_LAYERS)],
+                 values=[torch.randn((1, N_KV, CHUNK_LEN, HEAD_DIM), generator=gen).bfloat16() for _ in range(N_LAYERS)],
+                 start=int(torch.randint(0, 8192, (1,), generator=gen))) for _ in range(N_CHUNKS)]
+    order = torch.randperm(N_CHUNKS, generator=gen).tolist()
+    pl = [NS(chunk=chunks[c], start=i * CHUNK_LEN, ratio=None, exact=False) for i, c in enumerate(order)]
+    cfg = NS(recompute_ratio=RATIO, n_sink=N_SINK, full_first_layer=True, escalate_threshold=None)
+    cached_l, _, sink_l = R.plan_positions(N_TOKENS, pl, N_SINK)
+    cached, sink = torch.tensor(cached_l), torch.tensor(sink_l)
+    layer0 = torch.arange(N_TOKENS)
+    fk = [torch.randn((1, N_KV, N_TOKENS if l < 2 else 2976, HEAD_DIM), generator=gen).bfloat16() for l in range(N_LAYERS)]
+    fv = [torch.randn((1, N_KV, N_TOKENS if l < 2 else 2976, HEAD_DIM), generator=gen).bfloat16() for l in range(N_LAYERS)]
+    R.repair_step(pl, fk, fv, N_TOKENS, N_KV, HEAD_DIM, torch.bfloat16, inv, cfg, layer0, cached, sink)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        keep = R.repair_step(pl, fk, fv, N_TOKENS, N_KV, HEAD_DIM, torch.bfloat16, inv, cfg, layer0, cached, sink)
+        times.append(time.perf_counter() - t0)
+    assert len(keep) == 2976
+    med = float(np.median(times))
+    return dict(value=repair_bytes(2976) / med / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"{len(times)} requests of the same workload (one request = 28-layer base_kv + layer-1 "
+                       f"deviation/selection + 28 scatters), torch {torch.__version__} CPU eager, median "
+                       f"{med * 1e3:.0f} ms/request")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ttft-requests", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    r = bench_repair(args.steps, args.warmup, dev)
+    log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_eager']:.3f} ms eager); "
+        f"gather {r['gather_gbs']:.1f} GB/s ({r['gather_ms'] * 1e3:.1f} us)")
+    ttft = bench_ttft(args.ttft_requests, dev) if args.ttft_requests > 0 else None
+    cpu = bench_cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None
+
+    line = {
+        "metric": METRIC,
+        "value": round(r["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "ms_per_step_eager": round(r["ms_eager"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "blend-prefill KV repair, Qwen2.5-7B KV shape (28 layers, 4 KV heads, head_dim 128, bf16), "
+                        "8256-token request: 24 cached chunks x 320 at shuffled positions + 512 uncached + 64 query, "
+                        "30% recompute, 4 sinks",
+            "tokens": N_TOKENS,
+            "kept_rows": r["n_keep"],
+            "bytes_per_step": r["bytes"],
+        },
+        "pct_of_peak": round(100.0 * r["gbs"] / PEAK_GBS, 2),
+        "roofline": {
+            "kernel": "rerope_gather_kernel<bf16,128>",
+            "bound": "hbm",
+            "achieved": round(r["gather_gbs"], 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(r["gather_gbs"] / PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": GATHER_BYTES,
+            "avg_launch_us": round(r["gather_ms"] * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+    if ttft is not None:
+        line["ttft_p50_ms"] = round(ttft["hip"]["p50"], 2)
+        line["ttft_p99_ms"] = round(ttft["hip"]["p99"], 2)
+        line["ttft_p50_ms_torch_ops"] = round(ttft["torch_ops"]["p50"], 2)
+        line["ttft_p99_ms_torch_ops"] = round(ttft["torch_ops"]["p99"], 2)
+        line["ttft_requests"] = args.ttft_requests
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -8,9 +8,10 @@
 // The subtraction happens in the element type (one rounding); squares and sums are fp32.
 // K/V rows outside every placement are zero in the reference (base_kv zero-fills them).
 //
-// Design (gfx950): one 64-lane wavefront per token position; each lane loads 16 bytes of each
-// of the four rows (fresh k, cached K, fresh v, cached V) per step, so a token's H*D elements
-// (1 KiB per tensor at H=4, D=128, bf16) arrive in one coalesced pass. Four fp32 partial sums
+// Design (gfx950): one 64-lane wavefront per kDevTokens token positions; each lane loads 16 bytes
+// of each of the four rows (fresh k, cached K, fresh v, cached V) of every one of its tokens
+// before any arithmetic, so a token's H*D elements (1 KiB per tensor at H=4, D=128, bf16)
+// arrive in one coalesced pass. Four fp32 partial sums
 // per lane are combined by a xor butterfly; the lane/butterfly order is the summation contract
 // that the oracle restates bit-for-bit.
 #include "ckv_common.hpp"
@@ -19,6 +20,10 @@ namespace ckv {
 
 constexpr int kDevThreads = 256;
 constexpr int kDevWaves = kDevThreads / kWave;
+#ifndef CKV_DEV_TOKENS
+#define CKV_DEV_TOKENS 1
+#endif
+constexpr int kDevTokens = CKV_DEV_TOKENS;  // token positions per wavefront
 
 template <int DTYPE>
 __global__ __launch_bounds__(kDevThreads) void deviation_kernel(
@@ -30,56 +35,77 @@ __global__ __launch_bounds__(kDevThreads) void deviation_kernel(
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
   const int lane = threadIdx.x % kWave;
-  const int p = blockIdx.x * kDevWaves + threadIdx.x / kWave;
-  if (p >= n_tokens) return;
-  const int j = local[p];
-  if (j < 0 || j >= n_fresh) {
-    if (j >= n_fresh && lane == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
-    if (lane == 0) {
-      diff[p] = 0.0f;
-      norm[p] = 0.0f;
-    }
-    return;
-  }
-  const bool cached = (flags[p] & CKV_POS_CACHED) != 0;
+  const int p_base = (blockIdx.x * kDevWaves + threadIdx.x / kWave) * kDevTokens;
   const int64_t row_b = (int64_t)head_dim * E::kBytes;
   const int vecs_per_row = head_dim / VEC;
   const int n_vecs = n_heads * vecs_per_row;
 
-  float sk = 0.0f, sv = 0.0f, nk = 0.0f, nv = 0.0f;
+  int jj[kDevTokens];
+  bool cached[kDevTokens];
+  float sk[kDevTokens], sv[kDevTokens], nk[kDevTokens], nv[kDevTokens];
+#pragma unroll
+  for (int t = 0; t < kDevTokens; ++t) {
+    const int p = p_base + t;
+    jj[t] = p < n_tokens ? local[p] : -1;
+    cached[t] = p < n_tokens && (flags[p] & CKV_POS_CACHED) != 0;
+    if (jj[t] >= n_fresh) {
+      if (lane == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+      jj[t] = -1;
+    }
+    sk[t] = sv[t] = nk[t] = nv[t] = 0.0f;
+  }
   for (int q = lane; q < n_vecs; q += kWave) {
     const int h = q / vecs_per_row;
     const int64_t cb = (int64_t)(q % vecs_per_row) * 16;
-    const vec16 k16 = ld16(kf + h * kf_hs_b + j * kf_ts_b + cb);
-    const vec16 v16 = ld16(vf + h * vf_hs_b + j * vf_ts_b + cb);
-    float kx[VEC], vx[VEC], kcx[VEC], vcx[VEC];
-    E::unpack(k16, kx);
-    E::unpack(v16, vx);
-    if (cached) {
-      const int64_t co = h * c_hs_b + (int64_t)p * row_b + cb;
-      E::unpack(ld16(kc + co), kcx);
-      E::unpack(ld16(vc + co), vcx);
-    } else {
+    vec16 k16[kDevTokens], v16[kDevTokens], kc16[kDevTokens], vc16[kDevTokens];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) kcx[e] = vcx[e] = 0.0f;
+    for (int t = 0; t < kDevTokens; ++t) {
+      if (jj[t] >= 0) {
+        k16[t] = ld16(kf + h * kf_hs_b + jj[t] * kf_ts_b + cb);
+        v16[t] = ld16(vf + h * vf_hs_b + jj[t] * vf_ts_b + cb);
+        if (cached[t]) {
+          const int64_t co = h * c_hs_b + (int64_t)(p_base + t) * row_b + cb;
+          kc16[t] = ld16(kc + co);
+          vc16[t] = ld16(vc + co);
+        }
+      }
     }
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float dk = E::round_trip(kx[e] - kcx[e]);
-      const float dv = E::round_trip(vx[e] - vcx[e]);
-      sk = sk + dk * dk;
-      sv = sv + dv * dv;
-      nk = nk + kx[e] * kx[e];
-      nv = nv + vx[e] * vx[e];
+    for (int t = 0; t < kDevTokens; ++t) {
+      if (jj[t] < 0) continue;
+      float kx[VEC], vx[VEC], kcx[VEC], vcx[VEC];
+      E::unpack(k16[t], kx);
+      E::unpack(v16[t], vx);
+      if (cached[t]) {
+        E::unpack(kc16[t], kcx);
+        E::unpack(vc16[t], vcx);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) kcx[e] = vcx[e] = 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float dk = E::round_trip(kx[e] - kcx[e]);
+        const float dv = E::round_trip(vx[e] - vcx[e]);
+        sk[t] = sk[t] + dk * dk;
+        sv[t] = sv[t] + dv * dv;
+        nk[t] = nk[t] + kx[e] * kx[e];
+        nv[t] = nv[t] + vx[e] * vx[e];
+      }
     }
   }
-  sk = wave_butterfly_sum(sk);
-  sv = wave_butterfly_sum(sv);
-  nk = wave_butterfly_sum(nk);
-  nv = wave_butterfly_sum(nv);
-  if (lane == 0) {
-    diff[p] = sk + sv;
-    norm[p] = nk + nv;
+#pragma unroll
+  for (int t = 0; t < kDevTokens; ++t) {
+    const int p = p_base + t;
+    if (p >= n_tokens) continue;  // uniform across the wavefront
+    const float a = wave_butterfly_sum(sk[t]);
+    const float b = wave_butterfly_sum(sv[t]);
+    const float c = wave_butterfly_sum(nk[t]);
+    const float d = wave_butterfly_sum(nv[t]);
+    if (lane == 0) {
+      diff[p] = jj[t] < 0 ? 0.0f : a + b;
+      norm[p] = jj[t] < 0 ? 0.0f : c + d;
+    }
   }
 }
 
@@ -102,7 +128,8 @@ extern "C" int32_t ckv_deviation(const void* k_fresh, int64_t kf_head_stride, in
   if (cache_head_stride < (int64_t)n_tokens * head_dim) return CKV_ERR_OUT_OF_RANGE;
   if (n_tokens == 0) return CKV_OK;
   const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
-  const unsigned blocks = (unsigned)((n_tokens + kDevWaves - 1) / kDevWaves);
+  const int per_block = kDevWaves * kDevTokens;
+  const unsigned blocks = (unsigned)((n_tokens + per_block - 1) / per_block);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == CKV_DTYPE_BF16)
     hipLaunchKernelGGL(deviation_kernel<CKV_DTYPE_BF16>, dim3(blocks), dim3(kDevThreads), 0, st,

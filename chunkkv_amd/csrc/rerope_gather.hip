@@ -11,7 +11,7 @@
 //                               V[:, :, s:e] = chunk V
 // (MLX twin: src/chunkkv/scheduler/rerope.py:31-61.)
 //
-// Design (gfx950): one workgroup = one (segment, 32-token tile, layer). cos/sin depend only on
+// Design (gfx950): one workgroup = one (segment, 16-token tile, layer). cos/sin depend only on
 // (delta, frequency index), so each workgroup builds a D/2-entry table in LDS once, from theta,
 // while its first 16-byte loads are in flight. The table holds the correctly rounded fp32 cos/sin
 // of the fp32 angle (evaluated in fp64, rounded once). Every thread then rotates VEC frequency
@@ -24,9 +24,34 @@
 
 namespace ckv {
 
-constexpr int kGatherThreads = 256;
-constexpr int kGatherTile = 32;  // tokens per workgroup and layer
-constexpr int kGatherUnroll = 4;
+#ifndef CKV_GATHER_THREADS
+#define CKV_GATHER_THREADS 256
+#endif
+#ifndef CKV_GATHER_TILE
+#define CKV_GATHER_TILE 16
+#endif
+#ifndef CKV_GATHER_UNROLL
+#define CKV_GATHER_UNROLL 4
+#endif
+#ifndef CKV_GATHER_NT_LOAD
+#define CKV_GATHER_NT_LOAD 1
+#endif
+#ifndef CKV_GATHER_NT_STORE
+#define CKV_GATHER_NT_STORE 1
+#endif
+
+constexpr int kGatherThreads = CKV_GATHER_THREADS;
+constexpr int kGatherTile = CKV_GATHER_TILE;  // tokens per workgroup and layer (16 measured best)
+constexpr int kGatherUnroll = CKV_GATHER_UNROLL;
+
+__device__ __forceinline__ vec16 gather_ld(const void* p) {
+  if constexpr (CKV_GATHER_NT_LOAD) return ld16_stream(p);
+  else return ld16(p);
+}
+__device__ __forceinline__ void gather_st(void* p, const vec16& v) {
+  if constexpr (CKV_GATHER_NT_STORE) st16_stream(p, v);
+  else st16(p, v);
+}
 
 template <int DTYPE, int D>
 __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
@@ -102,11 +127,11 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
       const int r = r0 + u * RPP + rl;
       if (row_ok(r)) {
         const int64_t o = src_off(r);
-        kx1[u] = ld16_stream(sk0 + o);
-        kx2[u] = ld16_stream(sk0 + o + HALF_B);
+        kx1[u] = gather_ld(sk0 + o);
+        kx2[u] = gather_ld(sk0 + o + HALF_B);
         if (with_v) {
-          vx1[u] = ld16_stream(sv0 + o);
-          vx2[u] = ld16_stream(sv0 + o + HALF_B);
+          vx1[u] = gather_ld(sv0 + o);
+          vx2[u] = gather_ld(sv0 + o + HALF_B);
         }
       }
     }
@@ -153,15 +178,15 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
             y1[e] = p1 - p2;
             y2[e] = p3 + p4;
           }
-          st16_stream(dk0 + o, E::pack(y1));
-          st16_stream(dk0 + o + HALF_B, E::pack(y2));
+          gather_st(dk0 + o, E::pack(y1));
+          gather_st(dk0 + o + HALF_B, E::pack(y2));
         } else {
-          st16_stream(dk0 + o, kx1[u]);
-          st16_stream(dk0 + o + HALF_B, kx2[u]);
+          gather_st(dk0 + o, kx1[u]);
+          gather_st(dk0 + o + HALF_B, kx2[u]);
         }
         if (with_v) {
-          st16_stream(dv0 + o, vx1[u]);
-          st16_stream(dv0 + o + HALF_B, vx2[u]);
+          gather_st(dv0 + o, vx1[u]);
+          gather_st(dv0 + o + HALF_B, vx2[u]);
         }
       }
     }

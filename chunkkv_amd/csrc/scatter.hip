@@ -3,7 +3,9 @@
 // Reference semantics (src/chunkkv/engine/torch_engine.py:155-156):
 //   K[:, :, active] = k;  V[:, :, active] = v      (row overwrite, bit-exact copy)
 //
-// Design (gfx950): each thread moves one 16-byte vector of K and the matching vector of V.
+// Design (gfx950): each thread moves kScatterUnroll 16-byte vectors of K and the matching
+// vectors of V (all loads issued before any store; grid-stride so each load instruction of a
+// wavefront is contiguous).
 // Consecutive threads walk one row (D elements), then the next head, then the next active
 // token, so the destination writes of a row are one contiguous 256-byte burst (D = 128, bf16)
 // and the source reads follow the fresh tensor's own strides.
@@ -12,29 +14,48 @@
 namespace ckv {
 
 constexpr int kScatterThreads = 256;
+#ifndef CKV_SCATTER_UNROLL
+#define CKV_SCATTER_UNROLL 1
+#endif
+constexpr int kScatterUnroll = CKV_SCATTER_UNROLL;  // 16-byte K/V vector pairs per thread
 
 __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
     char* dst_k, char* dst_v, int64_t d_hs_b, const char* __restrict__ sk, int64_t sk_hs_b,
     int64_t sk_ts_b, const char* __restrict__ sv, int64_t sv_hs_b, int64_t sv_ts_b,
     const int64_t* __restrict__ rows, int n_rows, int n_tokens, int n_heads, int vecs_per_row,
     int64_t row_b, int32_t* __restrict__ err) {
-  const int64_t g = (int64_t)blockIdx.x * kScatterThreads + threadIdx.x;
   const int64_t per_tok = (int64_t)n_heads * vecs_per_row;
-  const int64_t j = g / per_tok;
-  if (j >= n_rows) return;
-  const int rem = (int)(g - j * per_tok);
-  const int h = rem / vecs_per_row;
-  const int64_t cb = (int64_t)(rem % vecs_per_row) * 16;
-  const int64_t t = rows[j];
-  if (t < 0 || t >= n_tokens) {
-    if (rem == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
-    return;
+  const int64_t total = (int64_t)n_rows * per_tok;
+  const int64_t stride = (int64_t)gridDim.x * kScatterThreads;
+  const int64_t g0 = (int64_t)blockIdx.x * kScatterThreads + threadIdx.x;
+  vec16 a[kScatterUnroll], b[kScatterUnroll];
+  int64_t dst_o[kScatterUnroll];
+#pragma unroll
+  for (int u = 0; u < kScatterUnroll; ++u) {
+    const int64_t g = g0 + u * stride;
+    dst_o[u] = -1;
+    if (g < total) {
+      const int64_t j = g / per_tok;
+      const int rem = (int)(g - j * per_tok);
+      const int h = rem / vecs_per_row;
+      const int64_t cb = (int64_t)(rem % vecs_per_row) * 16;
+      const int64_t t = rows[j];
+      a[u] = ld16(sk + h * sk_hs_b + j * sk_ts_b + cb);
+      b[u] = ld16(sv + h * sv_hs_b + j * sv_ts_b + cb);
+      if (t >= 0 && t < n_tokens) {
+        dst_o[u] = h * d_hs_b + t * row_b + cb;
+      } else if (rem == 0) {
+        flag_error(err, CKV_DEVICE_ERR_RANGE);
+      }
+    }
   }
-  const vec16 a = ld16(sk + h * sk_hs_b + j * sk_ts_b + cb);
-  const vec16 b = ld16(sv + h * sv_hs_b + j * sv_ts_b + cb);
-  const int64_t o = h * d_hs_b + t * row_b + cb;
-  st16(dst_k + o, a);
-  st16(dst_v + o, b);
+#pragma unroll
+  for (int u = 0; u < kScatterUnroll; ++u) {
+    if (dst_o[u] >= 0) {
+      st16(dst_k + dst_o[u], a[u]);
+      st16(dst_v + dst_o[u], b[u]);
+    }
+  }
 }
 
 }  // namespace ckv
@@ -55,7 +76,8 @@ extern "C" int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_s
   if (n_rows == 0) return CKV_OK;
   const int vecs_per_row = (int)(head_dim * eb / 16);
   const int64_t total = (int64_t)n_rows * n_heads * vecs_per_row;
-  const int64_t blocks = (total + kScatterThreads - 1) / kScatterThreads;
+  const int64_t per_block = (int64_t)kScatterThreads * kScatterUnroll;
+  const int64_t blocks = (total + per_block - 1) / per_block;
   if (blocks > 0x7fffffffLL) return CKV_ERR_TOO_LARGE;
   hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)blocks), dim3(kScatterThreads), 0, (hipStream_t)stream,
                      (char*)dst_k, (char*)dst_v, dst_head_stride * eb, (const char*)src_k, sk_head_stride * eb,

@@ -18,9 +18,12 @@
 // Design (gfx950): 1024 threads (16 wavefronts). keep/pool live as N-bit masks in LDS.
 // Chunk sums: one wavefront per chunk, lane-strided fp32 partials + xor butterfly (the order
 // the oracle restates). Top-k: MSB-first radix select over order-preserving 32-bit keys, four
-// 8-bit passes with an LDS histogram, which yields the exact threshold key T and how many ties
-// at T to take; a final pass in token order takes key > T plus the lowest-index ties and
-// compacts the kept positions with wavefront ballots (popcount prefix sums).
+// 8-bit passes, which yields the exact threshold key T and how many ties at T to take; then
+// key > T plus the lowest-index ties are taken and the kept positions compacted in token order.
+// Up to 33792 tokens (select_reg_kernel) each thread owns a contiguous run of <= 33 positions
+// whose keys stay in registers for all passes, histograms are per wavefront (no atomic pile-up
+// on the few hot bins), and ties and compaction need one workgroup scan each. Larger requests
+// use select_kernel, which re-reads keys from L2 in every pass.
 #include "ckv_common.hpp"
 
 namespace ckv {
@@ -68,6 +71,305 @@ __device__ __forceinline__ void set_bit_range(uint32_t* w, int a, int b, int lan
   }
 }
 
+// Phases shared by both selection kernels: keep = ~cached | sink and pool = 0 as LDS
+// bitmasks, then per-chunk relative deviation, escalation and requested budget.
+__device__ __forceinline__ void select_prologue(const float* __restrict__ diff, const float* __restrict__ norm,
+                                                const uint8_t* __restrict__ flags, int n_tokens,
+                                                const ckv_chunk_span* __restrict__ chunks, int n_chunks, int has_thr,
+                                                double thr, float* __restrict__ rel_out, uint8_t* __restrict__ esc_out,
+                                                uint32_t* keepw, uint32_t* poolw, int W, int* s_budget_req,
+                                                int* s_bad_span) {
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  if (tid == 0) {
+    *s_budget_req = 0;
+    *s_bad_span = 0;
+  }
+  // Each wavefront covers 64 positions = 2 mask words per step.
+  for (int base = wave * kWave; base < W * 32; base += kSelThreads) {
+    const int p = base + lane;
+    bool k = false;
+    if (p < n_tokens) {
+      const uint8_t f = flags[p];
+      k = !(f & CKV_POS_CACHED) || (f & CKV_POS_SINK);
+    }
+    const uint64_t m = __ballot(k);
+    if (lane == 0) {
+      keepw[base >> 5] = (uint32_t)m;
+      poolw[base >> 5] = 0u;
+    } else if (lane == 32 && ((base >> 5) + 1) < W) {
+      keepw[(base >> 5) + 1] = (uint32_t)(m >> 32);
+      poolw[(base >> 5) + 1] = 0u;
+    }
+  }
+  __syncthreads();
+  for (int c = wave; c < n_chunks; c += kSelWaves) {
+    const ckv_chunk_span sp = chunks[c];
+    const bool ok = sp.start >= 0 && sp.length >= 0 && (int64_t)sp.start + sp.length <= n_tokens;
+    float sd = 0.0f, sn = 0.0f;
+    if (ok) {
+      for (int q = lane; q < sp.length; q += kWave) {
+        sd = sd + diff[sp.start + q];
+        sn = sn + norm[sp.start + q];
+      }
+    }
+    sd = wave_butterfly_sum(sd);
+    sn = wave_butterfly_sum(sn);
+    const float rel = sd / sn;
+    const bool esc = ok && has_thr && ((double)rel > thr);
+    if (lane == 0) {
+      rel_out[c] = rel;
+      esc_out[c] = esc ? 1 : 0;
+      if (!ok) atomicAdd(s_bad_span, 1);
+    }
+    if (!ok) continue;
+    if (esc) {
+      set_bit_range(keepw, sp.start, sp.start + sp.length, lane);
+    } else if (sp.pooled) {
+      set_bit_range(poolw, sp.start, sp.start + sp.length, lane);
+      if (lane == 0) atomicAdd(s_budget_req, sp.budget);
+    }
+  }
+  __syncthreads();
+}
+
+// Inclusive wavefront scan + exclusive workgroup scan of one int per thread.
+__device__ __forceinline__ int block_excl_scan(int v, int* wave_tot, int& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) wave_tot[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const int t = wave_tot[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  __syncthreads();
+  total = all;
+  return before + x - v;
+}
+
+// Register-resident selection for n_tokens <= KPT * 1024: thread t owns positions
+// [t*KPT, (t+1)*KPT); their keys stay in registers through the four radix passes.
+template <int KPT>
+__global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
+    const float* __restrict__ diff, const float* __restrict__ norm, const uint8_t* __restrict__ flags,
+    const int32_t* __restrict__ local, int n_tokens, const ckv_chunk_span* __restrict__ chunks, int n_chunks,
+    int has_thr, double thr, int64_t* __restrict__ keep_abs, int64_t* __restrict__ keep_local,
+    float* __restrict__ rel_out, uint8_t* __restrict__ esc_out, int32_t* __restrict__ counts) {
+  static_assert(KPT <= 64, "per-thread position bits live in one 64-bit word");
+  constexpr int kBatch = 8;            // chunk-sum loads in flight per lane
+  extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
+  __shared__ uint32_t hist[kSelWaves][256];
+  __shared__ int wave_tot[kSelWaves];
+  __shared__ int s_budget_req, s_bad_span, s_digit, s_above;
+
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int W = (n_tokens + 31) >> 5;
+  uint32_t* escw = masks;
+  uint32_t* poolw = masks + W;
+
+  // Loads of the owned positions go out first; their latency hides behind the chunk sums.
+  const int p0 = tid * KPT;
+  constexpr int kFlagWords = (KPT + 3) / 4;
+  uint32_t key[KPT];        // order-preserving deviation keys of the owned positions
+  uint32_t fl[kFlagWords];  // their flag bytes, four per register
+#pragma unroll
+  for (int w = 0; w < kFlagWords; ++w) fl[w] = 0u;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int p = p0 + i;
+    key[i] = p < n_tokens ? dev_key(diff[p]) : 0u;
+    if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
+  }
+  if (tid == 0) {
+    s_budget_req = 0;
+    s_bad_span = 0;
+  }
+  for (int w = tid; w < 2 * W; w += kSelThreads) masks[w] = 0u;
+  __syncthreads();
+
+  // Per-chunk rel / escalation / budget: one wavefront per chunk, loads batched per lane, summed
+  // in the contract's order (lane-strided, ascending, then the xor butterfly).
+  for (int c = wave; c < n_chunks; c += kSelWaves) {
+    const ckv_chunk_span sp = chunks[c];
+    const bool ok = sp.start >= 0 && sp.length >= 0 && (int64_t)sp.start + sp.length <= n_tokens;
+    float sd = 0.0f, sn = 0.0f;
+    if (ok) {
+      for (int q0 = 0; q0 < sp.length; q0 += kBatch * kWave) {
+        float bd[kBatch], bn[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int q = q0 + j * kWave + lane;
+          bd[j] = q < sp.length ? diff[sp.start + q] : 0.0f;
+          bn[j] = q < sp.length ? norm[sp.start + q] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          if (q0 + j * kWave + lane < sp.length) {
+            sd = sd + bd[j];
+            sn = sn + bn[j];
+          }
+        }
+      }
+    }
+    sd = wave_butterfly_sum(sd);
+    sn = wave_butterfly_sum(sn);
+    const float rel = sd / sn;
+    const bool esc = ok && has_thr && ((double)rel > thr);
+    if (lane == 0) {
+      rel_out[c] = rel;
+      esc_out[c] = esc ? 1 : 0;
+      if (!ok) atomicAdd(&s_bad_span, 1);
+    }
+    if (!ok) continue;
+    if (esc) {
+      set_bit_range(escw, sp.start, sp.start + sp.length, lane);
+    } else if (sp.pooled) {
+      set_bit_range(poolw, sp.start, sp.start + sp.length, lane);
+      if (lane == 0) atomicAdd(&s_budget_req, sp.budget);
+    }
+  }
+  __syncthreads();
+
+  // keep = ~cached | sink | escalated span; candidates = pooled span minus keep.
+  uint64_t cand = 0u, kept_static = 0u;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int p = p0 + i;
+    if (p < n_tokens) {
+      const uint32_t f = (fl[i / 4] >> (8 * (i % 4))) & 0xffu;
+      const bool k = !(f & CKV_POS_CACHED) || (f & CKV_POS_SINK) || bit_of(escw, p);
+      kept_static |= (uint64_t)k << i;
+      if (!k && bit_of(poolw, p)) cand |= 1ull << i;
+    }
+  }
+  int n_cand = 0;
+  block_excl_scan(__popcll(cand), wave_tot, n_cand);
+  const int budget_req = s_budget_req;
+  const int budget = max(0, min(budget_req, n_cand));
+
+  uint32_t prefix = 0u, pmask = 0u;
+  int need = budget;
+  if (budget > 0) {
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int b = tid; b < kSelWaves * 256; b += kSelThreads) (&hist[0][0])[b] = 0u;
+      __syncthreads();
+      // Run-length aggregate equal digits within the thread first: in the high passes almost
+      // every key shares one or two digits, and unaggregated LDS atomics would serialize.
+      uint32_t run_digit = 0u, run_count = 0u;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        if (((cand >> i) & 1ull) && (key[i] & pmask) == prefix) {
+          const uint32_t d = (key[i] >> shift) & 255u;
+          if (run_count != 0u && d != run_digit) {
+            atomicAdd(&hist[wave][run_digit], run_count);
+            run_count = 0u;
+          }
+          run_digit = d;
+          ++run_count;
+        }
+      }
+      if (run_count != 0u) atomicAdd(&hist[wave][run_digit], run_count);
+      __syncthreads();
+      if (tid < 256) {  // fold the per-wavefront histograms into hist[0]
+        uint32_t t = 0;
+#pragma unroll
+        for (int w = 0; w < kSelWaves; ++w) t += hist[w][tid];
+        hist[0][tid] = t;
+      }
+      __syncthreads();
+      if (wave == 0) {
+        uint32_t h4[4];
+        uint32_t local_sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          h4[i] = hist[0][255 - (lane * 4 + i)];
+          local_sum += h4[i];
+        }
+        uint32_t incl = local_sum;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+          const uint32_t t = __shfl_up(incl, off, kWave);
+          if (lane >= off) incl += t;
+        }
+        uint32_t above = incl - local_sum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (above < (uint32_t)need && (uint32_t)need <= above + h4[i]) {
+            s_digit = 255 - (lane * 4 + i);
+            s_above = (int)above;
+          }
+          above += h4[i];
+        }
+      }
+      __syncthreads();
+      need -= s_above;
+      prefix |= (uint32_t)s_digit << shift;
+      pmask |= 255u << shift;
+    }
+  }
+  const uint32_t T = prefix;
+
+  // Take key > T, then the first `need` ties at T in token order.
+  uint64_t take = 0u, tie = 0u;
+  if (budget > 0) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      if ((cand >> i) & 1ull) {
+        take |= (uint64_t)(key[i] > T) << i;
+        tie |= (uint64_t)(key[i] == T) << i;
+      }
+    }
+  }
+  int tie_total = 0;
+  int tie_rank = block_excl_scan(__popcll(tie), wave_tot, tie_total);
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    if ((tie >> i) & 1ull) {
+      take |= (uint64_t)(tie_rank < need) << i;
+      ++tie_rank;
+    }
+  }
+  const uint64_t kept = kept_static | take;
+  int n_keep = 0;
+  int rank = block_excl_scan(__popcll(kept), wave_tot, n_keep);
+  int my_cached = 0, my_bad = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    if ((kept >> i) & 1ull) {
+      const int p = p0 + i;
+      const int l = local[p];
+      keep_abs[rank] = p;
+      keep_local[rank] = l < 0 ? 0 : l;
+      my_bad += l < 0;
+      my_cached += ((fl[i / 4] >> (8 * (i % 4))) & CKV_POS_CACHED) ? 1 : 0;
+      ++rank;
+    }
+  }
+  int c1 = 0, c2 = 0;
+  block_excl_scan(my_cached, wave_tot, c1);
+  block_excl_scan(my_bad, wave_tot, c2);
+  if (tid == 0) {
+    counts[CKV_COUNT_KEEP] = n_keep;
+    counts[CKV_COUNT_SELECTED_CACHED] = c1;
+    counts[CKV_COUNT_BUDGET] = budget;
+    counts[CKV_COUNT_CANDIDATES] = n_cand;
+    counts[CKV_COUNT_UNCOMPUTED] = c2;
+    counts[CKV_COUNT_BUDGET_REQUESTED] = budget_req;
+    counts[6] = s_bad_span;
+    counts[7] = 0;
+  }
+}
+
+// Selection for any n_tokens <= CKV_SELECT_MAX_TOKENS: keys are re-read from global memory
+// (L2) in every pass and positions are walked in 1024-wide tiles.
 __global__ __launch_bounds__(kSelThreads) void select_kernel(
     const float* __restrict__ diff, const float* __restrict__ norm, const uint8_t* __restrict__ flags,
     const int32_t* __restrict__ local, int n_tokens, const ckv_chunk_span* __restrict__ chunks,
@@ -276,9 +578,26 @@ extern "C" int32_t ckv_select(const float* diff, const float* norm, const uint8_
   if (n_tokens > CKV_SELECT_MAX_TOKENS) return CKV_ERR_TOO_LARGE;
   const int W = (n_tokens + 31) / 32;
   const size_t lds = (size_t)(W > 0 ? W : 1) * 2 * sizeof(uint32_t);
-  hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, (hipStream_t)stream, diff, norm,
-                     pos_flags, local, (int)n_tokens, chunks, (int)n_chunks, (int)(has_threshold != 0),
-                     escalate_threshold, keep_abs, keep_local, rel_dev, escalated, counts);
+  hipStream_t st = (hipStream_t)stream;
+  const int kpt = (n_tokens + kSelThreads - 1) / kSelThreads;
+#define CKV_SEL_REG(K)                                                                                        \
+  if (kpt <= K) {                                                                                             \
+    hipLaunchKernelGGL(select_reg_kernel<K>, dim3(1), dim3(kSelThreads), lds, st, diff, norm, pos_flags, local, \
+                       (int)n_tokens, chunks, (int)n_chunks, (int)(has_threshold != 0), escalate_threshold,      \
+                       keep_abs, keep_local, rel_dev, escalated, counts);                                       \
+    CKV_RETURN_IF_LAUNCH_FAILED();                                                                            \
+    return CKV_OK;                                                                                            \
+  }
+  CKV_SEL_REG(4)
+  CKV_SEL_REG(8)
+  CKV_SEL_REG(12)
+  CKV_SEL_REG(16)
+  CKV_SEL_REG(24)
+  CKV_SEL_REG(33)
+#undef CKV_SEL_REG
+  hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, st, diff, norm, pos_flags, local, (int)n_tokens,
+                     chunks, (int)n_chunks, (int)(has_threshold != 0), escalate_threshold, keep_abs, keep_local,
+                     rel_dev, escalated, counts);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

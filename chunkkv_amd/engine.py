@@ -15,6 +15,14 @@ The KV repair runs on the HIP kernels:
     one .item() per chunk)                             nothing back unless a threshold is set
   K[:, :, active] = k (:155-156)                     ckv_scatter_rows per layer
 
+Attention stays on PyTorch-ROCm SDPA. The reference calls it with enable_gqa and an explicit
+boolean (n_active x N) mask, a combination with no fused kernel on ROCm (it runs the fp32 math
+path). ``attention="fused"`` (default) keeps the same semantics but picks formulations that hit
+the fused kernels: when every position is active (layer 0 without exact placements) the mask is
+the plain causal mask, so ``is_causal=True``; otherwise the KV heads are expanded to the query
+heads and the boolean mask (built once per active set, not once per layer) is passed without
+enable_gqa. ``attention="reference"`` reproduces the reference's SDPA call exactly.
+
 Contracts where the reference leaves the result open: the selection breaks deviation ties by
 the lower token index (torch's argsort is unstable), deviation sums use a fixed order, and
 inv_freq is the correctly rounded fp32 value of the reference's expression (torch's fp32 pow
@@ -27,6 +35,7 @@ from __future__ import annotations
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 from chunkkv_amd import _native, ops
 from chunkkv_amd.model import DecoderPieces
@@ -44,7 +53,13 @@ _TORCH_OF = {
 
 
 class HipEngine(DecoderPieces):
-    def __init__(self, model, tokenizer):
+    def __init__(self, model, tokenizer, attention: str = "fused"):
+        if attention not in ("fused", "reference"):
+            raise ValueError("attention must be 'fused' or 'reference'")
+        self.attention = attention
+        # Set to a dict to record the layer-1 selection inputs/outputs (device tensors) of the
+        # next prefill, for parity checks; None (default) records nothing.
+        self.trace: dict | None = None
         self._init_model(model, tokenizer)
         if self.device.type != "cuda":
             raise ValueError("HipEngine runs on a HIP device: move the model to 'cuda' first")
@@ -59,6 +74,26 @@ class HipEngine(DecoderPieces):
 
         model = AutoModelForCausalLM.from_pretrained(repo, dtype=dtype).to("cuda")
         return cls(model, AutoTokenizer.from_pretrained(repo))
+
+    def _attend_active(self, layer, h, q, K, V, active, ar, masks: dict):
+        """Attention of the active rows over the whole cache: row i sees positions <= active[i]."""
+        n_act, N = active.shape[0], ar.shape[0]
+        key = (active.data_ptr(), n_act)
+        if self.attention == "reference":
+            return self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :])
+        attn = layer.self_attn
+        if n_act == N:  # active == arange(N): the mask is exactly the causal mask
+            o = F.scaled_dot_product_attention(q, K, V, is_causal=True, enable_gqa=True)
+        else:
+            if key not in masks:
+                masks.clear()
+                masks[key] = active[:, None] >= ar[None, :]
+            group = self.n_heads // self.n_kv
+            if group > 1:
+                K, V = K.repeat_interleave(group, dim=1), V.repeat_interleave(group, dim=1)
+            o = F.scaled_dot_product_attention(q, K, V, attn_mask=masks[key])
+        h = h + attn.o_proj(o.transpose(1, 2).reshape(h.shape[0], h.shape[1], -1))
+        return h + layer.mlp(layer.post_attention_layernorm(h))
 
     def shift_keys(self, keys: torch.Tensor, delta: int) -> torch.Tensor:
         """Move post-RoPE keys by `delta` positions on the HIP kernel (torch_engine.py:56-59)."""
@@ -156,6 +191,7 @@ class HipEngine(DecoderPieces):
         active = active_d
         h = self.inner.embed_tokens(torch.tensor([tokens], device=dev))[:, active]
         ar = torch.arange(N, device=dev)
+        masks: dict = {}
         sel = None
         for li, layer in enumerate(self.layers):
             q, k, v = self._qkv(layer.self_attn, layer.input_layernorm(h), active)
@@ -170,11 +206,14 @@ class HipEngine(DecoderPieces):
                     if int(counts[_native.COUNT_UNCOMPUTED]) > 0:
                         raise AssertionError("selected a token that was never computed")
                     n_keep = int(counts[_native.COUNT_KEEP])
+                if self.trace is not None:
+                    self.trace.update(k=k, v=v, K=K.clone(), V=V.clone(), flags=flags_d, local=local_d, spans=spans_d,
+                                      diff=diff, norm=norm, sel=sel, n_keep=n_keep)
                 rows = sel.keep_local[:n_keep]
                 h, q, k, v = h.index_select(1, rows), q.index_select(2, rows), k.index_select(2, rows), v.index_select(2, rows)
                 active = sel.keep_abs[:n_keep]
             ops.scatter_rows(K, V, k, v, active, err)
-            h = self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :])
+            h = self._attend_active(layer, h, q, K, V, active, ar, masks)
 
         n_want = N - logits_from
         if 0 <= logits_from <= N and not plan.cached[logits_from:].any():

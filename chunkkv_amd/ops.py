@@ -7,7 +7,6 @@ Every wrapper launches a HIP kernel; none computes anything on the CPU.
 
 from __future__ import annotations
 
-import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -28,19 +27,23 @@ def dtype_code(dtype: torch.dtype) -> int:
 def _dev(*ts: torch.Tensor) -> torch.device:
     d = ts[0].device
     for t in ts:
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise ValueError("chunkkv_amd ops run on a HIP device; got a tensor on " + str(t.device))
         if t.device != d:
             raise ValueError(f"tensors on different devices: {t.device} vs {d}")
     return d
 
 
-def _stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+_raw_stream = torch._C._cuda_getCurrentRawStream
 
 
-def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
-    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+def _stream(device: torch.device) -> int:
+    """torch's current HIP stream on `device` as a raw handle (what hipLaunchKernel takes)."""
+    return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+
+
+def _ptr(t: torch.Tensor | None) -> int:
+    return 0 if t is None else t.data_ptr()
 
 
 def _rows_ok(t: torch.Tensor) -> bool:

@@ -23,6 +23,15 @@ import torch
 import torch.nn.functional as F
 
 
+class BlendDefaults:
+    """BlendConfig defaults (base.py:36-43)."""
+
+    recompute_ratio = 0.15
+    n_sink = 2
+    full_first_layer = True
+    escalate_threshold = None
+
+
 def reference_inv_freq(theta: float, head_dim: int, device="cpu") -> torch.Tensor:
     """torch_engine.py:33 as torch evaluates it (fp32 pow)."""
     return theta ** (-torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim)
@@ -105,10 +114,8 @@ def layer1_selection(k, v, K, V, active, cached, sink, placements, config, tie_s
 def prefill(model, tokens, placements=None, config=None, logits_from=None, inv_freq=None, tie_stable=True) -> dict:
     """TorchEngine.prefill on a CPU model. Returns logits, keys, values, stats, plus the
     layer-1 keep_abs / diff / norm for parity checks."""
-    from chunkkv_amd.types import BlendConfig  # dataclass defaults only (base.py:36-43)
-
     placements = placements or []
-    config = config or BlendConfig()
+    config = config or BlendDefaults()
     cfg = model.config
     inner, layers = model.model, model.model.layers
     n_heads, n_kv = cfg.num_attention_heads, cfg.num_key_value_heads
@@ -178,16 +185,20 @@ def prefill(model, tokens, placements=None, config=None, logits_from=None, inv_f
 
 def repair_step(placements, fresh_k, fresh_v, N, n_kv, head_dim, dtype, inv_freq, config, layer0_idx, cached, sink):
     """The KV-repair ops of one request (torch_engine.py:96-103, :117-156), without the model:
-    per layer base_kv, at layer 1 the deviation/selection, then the scatter of the active rows.
-    fresh_k[li]/fresh_v[li]: (1, H, n_active(li), D). Returns the final keep_abs."""
+    per layer base_kv, at layer 1 the deviation, selection and compaction of the fresh rows,
+    then the scatter of the active rows. fresh_k[li]/fresh_v[li]: (1, H, n_active(li), D) with
+    n_active = len(layer0_idx) for layers 0-1. Returns the final active set."""
     active = layer0_idx
     for li in range(len(fresh_k)):
         K, V = base_kv(placements, li, N, n_kv, head_dim, dtype, inv_freq)
         k, v = fresh_k[li], fresh_v[li]
         if li == 1:
             keep_abs, _, _, _ = layer1_selection(k, v, K, V, active, cached, sink, placements, config)
+            local = torch.full((N,), -1, dtype=torch.long)
+            local[active] = torch.arange(len(active))
+            sel = local[keep_abs]
+            k, v = k[:, :, sel], v[:, :, sel]
             active = keep_abs
-        k, v = fresh_k[li][:, :, : len(active)], fresh_v[li][:, :, : len(active)]
         K[:, :, active] = k
         V[:, :, active] = v
     return active

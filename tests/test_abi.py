@@ -1,0 +1,112 @@
+"""The C-ABI library on a host without a GPU: it loads, exports every entry point declared in
+include/chunkkv_amd.h with the ABI version, rejects bad arguments on the host before any launch,
+and its structs have the layout the Python side packs. No kernel is launched here."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from chunkkv_amd import _native, ops
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "chunkkv_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int32_t|const char\*)\s+(ckv_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.lib()
+    names = declared_functions()
+    assert len(names) >= 8
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _native.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_native.SIGNATURES) == set(names)
+    assert lib.ckv_abi_version() == _native.ABI_VERSION
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (ckv_\w+)", out))
+    assert set(names) <= exported
+
+
+def test_status_strings():
+    lib = _native.lib()
+    assert lib.ckv_status_string(0) == b"ok"
+    assert b"invalid" in lib.ckv_status_string(1)
+    assert lib.ckv_status_string(99) == b"unknown status"
+
+
+def test_host_side_argument_validation_never_launches():
+    lib = _native.lib()
+    # unknown dtype / unsupported head_dim / NULL pointers / bad strides -> errors before any launch
+    assert lib.ckv_rerope_gather(1, 1, 10, 10, 1, 1, 1, 1, 1, 1, 1, 1, 128, 7, 1e6, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_rerope_gather(1, 1, 10, 10, 1, 1, 1, 1, 1, 1, 1, 1, 96, 1, 1e6, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_rerope_gather(None, 1, 10, 10, 1, 1, 1, 1, 1, 1, 1, 1, 128, 1, 1e6, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_rerope_gather(1, 1, 100, 10, 1, 1, 1, 1, 1, 1, 1, 1, 128, 1, 1e6, None, None) == _native.CKV_ERR_OUT_OF_RANGE
+    assert lib.ckv_rerope_gather(1, 1, 100, 10, 1, 1, 1, 1, 1, 1, 1, 1, 128, 1, -1.0, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_inv_freq(None, 128, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_inv_freq(1, 127, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_shift_keys(1, 10, 1, 10, 1, 1, 100, 1, 3, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_deviation(1, 1, 1, 1, 1, 1, 1, 1, 512, 1, 1, 4, 4, 4, 128, 5, 1, 1, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_deviation(1, 1, 1, 1, 1, 1, 1, 1, 10, 1, 1, 4, 4, 4, 128, 1, 1, 1, None, None) == _native.CKV_ERR_OUT_OF_RANGE
+    assert lib.ckv_select(1, 1, 1, 1, _native.SELECT_MAX_TOKENS + 1, 1, 1, 0, 0.0, 1, 1, 1, 1, 1, None) == _native.CKV_ERR_TOO_LARGE
+    assert lib.ckv_select(None, 1, 1, 1, 10, 1, 1, 0, 0.0, 1, 1, 1, 1, 1, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_scatter_rows(1, 1, 10, 1, 1, 1, 1, 1, 1, 1, 4, 10, 4, 128, 1, None, None) == _native.CKV_ERR_OUT_OF_RANGE
+    assert lib.ckv_scatter_rows(1, 1, 10, 1, 1, 1, 1, 1, 1, 1, 4, 10, 4, 100, 1, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    # zero-sized work is a no-op success
+    assert lib.ckv_scatter_rows(None, None, 0, None, 0, 0, None, 0, 0, None, 0, 0, 4, 128, 1, None, None) == _native.CKV_OK
+
+
+def test_status_maps_to_reference_exception_types():
+    with pytest.raises(ValueError):
+        _native.check(_native.CKV_ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(ValueError):
+        _native.check(_native.CKV_ERR_TOO_LARGE, "x")
+    with pytest.raises(RuntimeError):
+        _native.check(_native.CKV_ERR_HIP, "x")
+    _native.check(_native.CKV_OK, "x")
+
+
+def test_ops_refuse_host_tensors():
+    k = torch.zeros(1, 2, 4, 64)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.shift_keys(k, 3, 1e6)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.scatter_rows(k, k, k, k, torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(TypeError):
+        ops.dtype_code(torch.float16)
+    assert ops.shift_keys(k, 0, 1e6) is k  # delta 0 returns the input before any device check
+
+
+def test_engine_refuses_cpu_model():
+    from chunkkv_amd.engine import HipEngine
+    from tests.helpers import StubTokenizer, tiny_qwen2
+
+    with pytest.raises(ValueError, match="HIP device"):
+        HipEngine(tiny_qwen2(layers=1, hidden=64, heads=1, kv=1, inter=64, vocab=32), StubTokenizer())
+
+
+def test_struct_layouts_match_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "chunkkv_amd.h"\n'
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %d %d %d\\n\", sizeof(ckv_segment), offsetof(ckv_segment, delta),"
+        " sizeof(ckv_chunk_span), offsetof(ckv_chunk_span, pooled), offsetof(ckv_segment, src_len),"
+        " CKV_COUNT_N, CKV_SELECT_MAX_TOKENS, CKV_ABI_VERSION); return 0;}\n"
+    )
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    vals = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()))
+    assert vals == [24, 20, 16, 12, 16, _native.COUNT_N, _native.SELECT_MAX_TOKENS, _native.ABI_VERSION]
+    from chunkkv_amd.planner import SEG_FIELDS, SPAN_FIELDS
+
+    assert SEG_FIELDS * 4 == 24 and SPAN_FIELDS * 4 == 16
+    assert np.dtype(np.int32).itemsize == 4
+    assert ctypes.sizeof(ctypes.c_void_p) == 8

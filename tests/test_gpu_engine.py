@@ -1,0 +1,296 @@
+"""End-to-end parity of HipEngine (HIP KV repair on the GPU) with the oracle's CPU restatement of
+TorchEngine.prefill and with the reference op sequence on PyTorch-ROCm, on tiny random-init
+Qwen2 models (fp32 and bf16), mirroring the reference's engine tests
+(tests/test_torch_engine.py:36-74, tests/test_mlx_engine.py:24-99)."""
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from chunkkv_amd.baseline import TorchOpsEngine
+from chunkkv_amd.engine import HipEngine
+from chunkkv_amd.types import BlendConfig, ChunkKV, Placement
+from oracle import engine_ref as R
+from oracle import oracle as O
+from tests.helpers import StubTokenizer, tiny_qwen2
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def models():
+    cpu = tiny_qwen2(layers=4, hidden=256, heads=4, kv=2, inter=512, vocab=512, seed=0)
+    gpu = copy.deepcopy(cpu).to(DEV)
+    return cpu, gpu
+
+
+@pytest.fixture(scope="module")
+def parts():
+    rng = np.random.default_rng(0)
+    t = lambda n: rng.integers(1, 511, n).tolist()  # noqa: E731
+    return dict(sys=t(11), a=t(37), b=t(29), q=t(9))
+
+
+def _kl(p, q):
+    p, q = torch.log_softmax(p.float(), -1), torch.log_softmax(q.float(), -1)
+    return (p.exp() * (p - q)).sum(-1).mean().item()
+
+
+def _cpu_chunk(ch):
+    return ChunkKV([k.detach().cpu() for k in ch.keys], [v.detach().cpu() for v in ch.values], ch.start)
+
+
+def assert_same_selection(got, ref, tokens, placements, cfg):
+    """Kept sets agree except for candidates whose deviation is within 1e-4 of the top-k
+    threshold (the GPU and CPU models round layer-0/1 activations differently)."""
+    from chunkkv_amd.planner import plan_request
+
+    ref_set = set(ref["sel"]["keep_abs"].tolist())
+    diffset = set(got.tolist()) ^ ref_set
+    if not diffset:
+        return
+    plan = plan_request(len(tokens), placements, cfg.n_sink, cfg.recompute_ratio)
+    cand = np.zeros(len(tokens), dtype=bool)
+    for s0, L, _, pooled in plan.spans:
+        if pooled:
+            cand[s0 : s0 + L] = True
+    cand &= ~(~plan.cached | plan.sink)
+    d = ref["sel"]["diff"].double().numpy()
+    thr = np.sort(d[cand])[::-1][plan.budget - 1]
+    assert all(cand[p] and abs(d[p] - thr) <= 1e-4 * thr for p in diffset), (diffset, thr)
+
+
+def _swap_setup(eng, parts):
+    s = len(parts["sys"])
+    first = eng.prefill(parts["sys"] + parts["a"] + parts["b"] + parts["q"])
+    ca = first.chunk(s, s + len(parts["a"]))
+    cb = first.chunk(s + len(parts["a"]), s + len(parts["a"]) + len(parts["b"]))
+    toks2 = parts["sys"] + parts["b"] + parts["a"] + parts["q"]
+    return toks2, [Placement(cb, s), Placement(ca, s + len(parts["b"]))]
+
+
+def _to_cpu_placements(pl):
+    return [Placement(_cpu_chunk(p.chunk), p.start, p.ratio, p.exact) for p in pl]
+
+
+def test_no_cache_prefill_matches_hf_forward(models, parts):
+    cpu, gpu = models
+    eng = HipEngine(gpu, StubTokenizer())
+    toks = parts["sys"] + parts["a"] + parts["b"] + parts["q"]
+    with torch.inference_mode():
+        ref = gpu(torch.tensor([toks], device=DEV)).logits[0]
+    out = eng.prefill(toks, logits_from=0)
+    torch.testing.assert_close(out.logits, ref, atol=2e-3, rtol=0)
+    assert out.stats["prefill_token_equiv"] == len(toks)
+
+
+@pytest.mark.parametrize("attention", ["reference", "fused"])
+@pytest.mark.parametrize("ratio", [0.3, 1.0])
+def test_blend_matches_oracle_engine(models, parts, attention, ratio):
+    cpu, gpu = models
+    eng = HipEngine(gpu, StubTokenizer(), attention=attention)
+    toks2, pl = _swap_setup(eng, parts)
+    cfg = BlendConfig(recompute_ratio=ratio, n_sink=4)
+    eng.trace = {}
+    out = eng.prefill(toks2, pl, cfg)
+    tr, eng.trace = eng.trace, None
+    ref = R.prefill(cpu, toks2, _to_cpu_placements(pl), cfg, inv_freq=eng.inv_freq.cpu())
+    for key in ("tokens", "cached_tokens", "recomputed_cached_tokens", "prefill_token_equiv"):
+        assert out.stats[key] == ref["stats"][key], key
+    for a, b in zip(out.stats["chunks"], ref["stats"]["chunks"]):
+        assert (a["start"], a["length"], a["escalated"]) == (b["start"], b["length"], b["escalated"])
+        assert a["rel_dev"] == pytest.approx(b["rel_dev"], rel=1e-3)
+    tol = 2e-3 if attention == "reference" else 5e-3
+    torch.testing.assert_close(out.logits.cpu(), ref["logits"], atol=tol, rtol=0)
+    # the engine's own layer-1 selection equals the C oracle's on the same device inputs
+    n = tr["n_keep"]
+    got = O.to_numpy(tr["sel"].keep_abs)[:n]
+    want = O.select(O.to_numpy(tr["diff"]), O.to_numpy(tr["norm"]), O.to_numpy(tr["flags"]), O.to_numpy(tr["local"]),
+                    O.to_numpy(tr["spans"]).reshape(-1, 4), cfg.escalate_threshold)
+    np.testing.assert_array_equal(got, want["keep_abs"])
+    # and the CPU reference's set, up to deviations tied within fp32 rounding
+    assert_same_selection(got, ref, toks2, pl, cfg)
+
+
+def test_blend_matches_rocm_reference_ops(models, parts):
+    """Same device, same model, reference SDPA call: only the KV repair differs."""
+    from chunkkv_amd.baseline import torch_base_kv
+
+    _, gpu = models
+    hip = HipEngine(gpu, StubTokenizer(), attention="reference")
+    ref = TorchOpsEngine(gpu, StubTokenizer())
+    toks2, pl = _swap_setup(hip, parts)
+    cfg = BlendConfig(recompute_ratio=0.3, n_sink=2)
+    hip.trace = {}
+    a = hip.prefill(toks2, pl, cfg)
+    tr, hip.trace = hip.trace, None
+    b = ref.prefill(toks2, pl, cfg)
+    for key in ("tokens", "cached_tokens", "recomputed_cached_tokens", "prefill_token_equiv"):
+        assert a.stats[key] == b.stats[key], key
+    assert _kl(b.logits, a.logits) < 1e-5
+    # the layer-1 base cache built by the HIP gather vs the reference's torch ops
+    K1, V1 = torch_base_kv(pl, 1, len(toks2), hip.n_kv, hip.head_dim, torch.float32, ref.inv_freq, DEV)
+    cached = torch.zeros(len(toks2), dtype=torch.bool)
+    for p in pl:
+        cached[p.start : p.start + p.chunk.length] = True
+    # within one bf16 ulp (2**-8 relative), the re-RoPE contract; torch's fp32 pow/cos are not
+    # correctly rounded, so the two differ by a few fp32 ulps
+    got, want = tr["K"][:, :, cached], K1[:, :, cached]
+    assert ((got - want).abs() <= 2.0**-8 * want.abs() + 1e-6 * want.abs().max()).all()
+    assert torch.equal(tr["V"][:, :, cached], V1[:, :, cached])
+
+
+def test_full_recompute_matches_forward_and_blend_beats_naive(models, parts):
+    """reference tests/test_torch_engine.py:52-65."""
+    _, gpu = models
+    eng = HipEngine(gpu, StubTokenizer())
+    toks2, pl = _swap_setup(eng, parts)
+    with torch.inference_mode():
+        fwd = gpu(torch.tensor([toks2], device=DEV)).logits[0, -1:]
+    full = eng.prefill(toks2, pl, BlendConfig(recompute_ratio=1.0))
+    naive = eng.prefill(toks2, pl, BlendConfig(full_first_layer=False))
+    blend = eng.prefill(toks2, pl, BlendConfig(recompute_ratio=0.3))
+    assert _kl(fwd, full.logits) < 1e-4
+    assert _kl(fwd, blend.logits) < _kl(fwd, naive.logits)
+    assert naive.stats["prefill_token_equiv"] < blend.stats["prefill_token_equiv"] < len(toks2)
+
+
+def test_exact_reuse_and_stats_closed_forms(models, parts):
+    """reference tests/test_torch_engine.py:44-49 and tests/test_mlx_engine.py:32-39, 70-99."""
+    _, gpu = models
+    eng = HipEngine(gpu, StubTokenizer())
+    s = len(parts["sys"])
+    toks = parts["sys"] + parts["a"] + parts["b"] + parts["q"]
+    first = eng.prefill(toks)
+    ca = first.chunk(s, s + len(parts["a"]))
+    same = eng.prefill(toks, [Placement(ca, s, exact=True)], BlendConfig())
+    torch.testing.assert_close(same.logits, first.logits, atol=2e-3, rtol=0)
+    assert same.stats["prefill_token_equiv"] == len(toks) - len(parts["a"])
+    naive = eng.prefill(toks, [Placement(ca, s)], BlendConfig(full_first_layer=False))
+    assert naive.stats["prefill_token_equiv"] == len(toks) - len(parts["a"])
+    # exact chunk at 0 + moved chunk at ratio 1.0: equals the full forward, exact never recomputed
+    other = eng.prefill(parts["sys"] + parts["b"] + parts["q"])
+    cb = other.chunk(s, s + len(parts["b"]))
+    toks3 = parts["a"] + parts["b"] + parts["q"]
+    a0 = eng.prefill(toks3).chunk(0, len(parts["a"]))
+    with torch.inference_mode():
+        fwd = gpu(torch.tensor([toks3], device=DEV)).logits[0, -1:]
+    out = eng.prefill(toks3, [Placement(a0, 0, exact=True), Placement(cb, len(parts["a"]), ratio=1.0)], BlendConfig())
+    assert _kl(fwd, out.logits) < 1e-4
+    assert out.stats["prefill_token_equiv"] == len(toks3) - len(parts["a"])
+
+
+def test_escalation_and_errors(models, parts):
+    _, gpu = models
+    eng = HipEngine(gpu, StubTokenizer())
+    toks2, pl = _swap_setup(eng, parts)
+    out = eng.prefill(toks2, pl, BlendConfig(escalate_threshold=0.0))  # every chunk escalates
+    assert all(c["escalated"] for c in out.stats["chunks"])
+    assert out.stats["recomputed_cached_tokens"] == out.stats["cached_tokens"]
+    with pytest.raises(ValueError):
+        eng.prefill(toks2, pl, BlendConfig(), logits_from=len(parts["sys"]))  # cached positions not recomputed
+    with pytest.raises(ValueError):
+        eng.prefill(toks2, [Placement(pl[0].chunk, len(toks2) - 3)], BlendConfig())  # runs past the request
+
+
+def test_generate_matches_hf_greedy(models, parts):
+    """reference tests/test_torch_engine.py:68-74 (logits sharpened so greedy picks are not
+    near-ties on a random model)."""
+    _, base = models
+    gpu = copy.deepcopy(base)
+    with torch.no_grad():
+        gpu.model.norm.weight.mul_(20.0)
+    eng = HipEngine(gpu, StubTokenizer())
+    toks = parts["sys"] + parts["a"] + parts["q"]
+    ours = eng.generate(eng.prefill(toks), max_tokens=8)
+    with torch.inference_mode():
+        ref = gpu.generate(torch.tensor([toks], device=DEV), max_new_tokens=8, do_sample=False,
+                           attention_mask=torch.ones(1, len(toks), dtype=torch.long, device=DEV))[0, len(toks):]
+    ref = [t for t in ref.tolist() if t not in eng.eos]
+    assert ours == ref[: len(ours)] and len(ours) > 0
+
+
+def test_bf16_blend_matches_rocm_reference_ops():
+    gpu = tiny_qwen2(layers=3, hidden=512, heads=4, kv=4, inter=1024, vocab=512, seed=3, dtype=torch.bfloat16).to(DEV)
+    hip = HipEngine(gpu, StubTokenizer(), attention="reference")
+    ref = TorchOpsEngine(gpu, StubTokenizer())
+    rng = np.random.default_rng(3)
+    t = lambda n: rng.integers(1, 511, n).tolist()  # noqa: E731
+    parts = dict(sys=t(20), a=t(64), b=t(48), q=t(8))
+    toks2, pl = _swap_setup(hip, parts)
+    cfg = BlendConfig(recompute_ratio=0.3, n_sink=4)
+    a, b = hip.prefill(toks2, pl, cfg), ref.prefill(toks2, pl, cfg)
+    assert a.stats["recomputed_cached_tokens"] == b.stats["recomputed_cached_tokens"]
+    assert _kl(b.logits, a.logits) < 1e-3
+
+
+def test_shift_keys_api(models):
+    _, gpu = models
+    eng = HipEngine(gpu, StubTokenizer())
+    k = torch.randn(1, 2, 10, 64, device=DEV)
+    assert eng.shift_keys(k, 0) is k
+    back = eng.shift_keys(eng.shift_keys(k, 37), -37)
+    torch.testing.assert_close(back, k, atol=1e-5, rtol=0)
+
+
+def test_repair_step_graph_replay_matches_eager():
+    """A captured KV-repair step replayed several times, with eager work in between, gives the
+    eager result each time (no memset nodes are recorded)."""
+    from chunkkv_amd import ops
+
+    rng = np.random.default_rng(5)
+    H, D, L, C, n_layers = 4, 128, 64, 6, 3
+    N = C * L + 16
+    chunks = [ChunkKV([torch.randn(1, H, L, D, device=DEV).bfloat16() for _ in range(n_layers)],
+                      [torch.randn(1, H, L, D, device=DEV).bfloat16() for _ in range(n_layers)], int(rng.integers(0, 900)))
+              for _ in range(C)]
+    pl = [Placement(chunks[c], i * L) for i, c in enumerate(rng.permutation(C))]
+    from chunkkv_amd.planner import local_index, plan_request
+
+    plan = plan_request(N, pl, 4, 0.3)
+    tab = np.concatenate([np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(c.keys, c.values)], dtype=np.uint64).reshape(-1)
+                          for c in plan.chunks])
+    tab_d = torch.from_numpy(tab.view(np.int64)).to(DEV)
+    segs = torch.from_numpy(plan.segments.reshape(-1)).to(DEV)
+    flags = torch.from_numpy(plan.flags).to(DEV)
+    local = torch.from_numpy(local_index(N, plan.layer0_idx)).to(DEV)
+    spans = torch.from_numpy(plan.spans.reshape(-1)).to(DEV)
+    Ks = torch.empty((n_layers, 1, H, N, D), dtype=torch.bfloat16, device=DEV)
+    Vs = torch.empty_like(Ks)
+    fk = torch.randn(1, H, N, D, device=DEV).bfloat16()
+    fv = torch.randn(1, H, N, D, device=DEV).bfloat16()
+    state = {}
+
+    def step():
+        ops.rerope_gather(Ks, Vs, tab_d, segs, len(plan.segments), plan.max_seg_tokens, 1e6)
+        diff, norm = ops.deviation(fk, fv, Ks[1], Vs[1], flags, local)
+        state["sel"] = ops.select(diff, norm, flags, local, spans, None, state.get("sel"))
+        rows = state["sel"].keep_abs[: plan.n_keep]
+        for li in range(1, n_layers):
+            ops.scatter_rows(Ks[li], Vs[li], fk[:, :, : plan.n_keep], fv[:, :, : plan.n_keep], rows)
+
+    Ks.fill_(7.0)  # rows the step never writes keep this value in every run below
+    Vs.fill_(7.0)
+    step()
+    torch.cuda.synchronize()
+    eager = (Ks.clone(), Vs.clone(), state["sel"].keep_abs[: plan.n_keep].clone())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(3):
+        Ks.fill_(7.0)
+        Vs.fill_(7.0)
+        state["sel"].keep_abs.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(Ks, eager[0]) and torch.equal(Vs, eager[1])
+        assert torch.equal(state["sel"].keep_abs[: plan.n_keep], eager[2])

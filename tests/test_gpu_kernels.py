@@ -275,7 +275,7 @@ def test_select_planted_ties_and_escalation(seed):
     _check_select(diff, norm, flags, local, spans, thr)
 
 
-@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 1023, 1024, 1025, 131072])
+@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 1023, 1024, 1025, 8256, 33792, 33793, 131072])
 def test_select_sizes(N):
     rng = np.random.default_rng(N)
     L = max(1, N // 3)
