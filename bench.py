@@ -53,6 +53,10 @@ RATIO, N_SINK = 0.30, 4
 ROW_BYTES = N_KV * HEAD_DIM * 2  # one token's K (or V) row set, bf16
 
 GATHER_BYTES = N_LAYERS * N_CHUNKS * CHUNK_LEN * ROW_BYTES * 2 * 2
+# HBM bytes per gather launch of this workload from the FETCH_SIZE / WRITE_SIZE counter passes
+# (profiles/traffic_rerope_gather_qwen25_7b_8k.md; FETCH_SIZE calibrated against a kernel of
+# known traffic). Counters cannot be read inside a timed run, so the measured value is recorded.
+GATHER_TRAFFIC_BYTES = 881_167_672
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 
@@ -194,6 +198,19 @@ def _timed(fn, n: int, stream) -> float:
     return start.elapsed_time(end) / n
 
 
+def _graph_of(fn):
+    """Capture fn() (already run once eagerly) into a HIP graph, warming it on a side stream."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
 def bench_repair(steps: int, warmup: int, dev) -> dict:
     """Time the KV-repair step. The 31 launches of a step are captured once per input set in a
     HIP graph and replayed (the step is launch-bound from Python otherwise); the eager time is
@@ -208,17 +225,7 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     for i in range(max(warmup, 2)):
         step(wls[i % 2])
     torch.cuda.synchronize()
-    graphs = []
-    for w in wls:
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            step(w)
-        torch.cuda.current_stream().wait_stream(side)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step(w)
-        graphs.append(g)
+    graphs = [_graph_of(lambda w=w: step(w)) for w in wls]
     stream = torch.cuda.current_stream(dev)
     for i in range(2):
         graphs[i].replay()
@@ -339,6 +346,229 @@ def bench_cpu(seconds: float) -> dict:
                        f"{med * 1e3:.0f} ms/request")
 
 
+def _workload_line(metric: str, value: float, ms: float, steps: int, warmup: int, config: dict, roofline: dict) -> dict:
+    return {
+        "metric": metric, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic", "config": config, "pct_of_peak": round(100.0 * value / PEAK_GBS, 2), "roofline": roofline,
+    }
+
+
+def _rooffor(kernel: str, nbytes: int, ms: float) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": kernel, "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_GBS, 4), "traffic": None, "bytes_per_launch": nbytes, "avg_launch_us": round(ms * 1e3, 2)}
+
+
+def bench_gather_only(steps: int, warmup: int, dev) -> dict:
+    """Re-RoPE + gather microbenchmark at the Qwen2.5-7B KV shape: 28 layers, 4 heads, D=128,
+    bf16, 16 chunks x 256 tokens (keys rotated at their original offsets), delta ~ U[-4096, 4096],
+    gathered into a 4096-token cache. Bytes per launch = 28 x 4096 x 4 x 1024 = 469,762,048."""
+    from chunkkv_amd import ops
+    from chunkkv_amd.planner import plan_request
+
+    L, C, N = 256, 16, 4096
+    sets = []
+    for seed in range(3):  # 3 x (235 MB chunks + 235 MB cache) rotates past the 256 MB MALL
+        gen = torch.Generator().manual_seed(seed)
+        inv = ops.inv_freq(HEAD_DIM, THETA, dev)
+        slots = torch.randperm(C, generator=gen).tolist()
+        deltas = torch.randint(-4096, 4097, (C,), generator=gen).tolist()
+        pl = []
+        for c in range(C):
+            orig = slots[c] * L - deltas[c]
+            x = torch.randn((N_LAYERS, 1, N_KV, L, HEAD_DIM), generator=gen).to(dev)
+            k = rope_rows(x, torch.arange(orig, orig + L, device=dev), inv).to(torch.bfloat16)
+            v = torch.randn((N_LAYERS, 1, N_KV, L, HEAD_DIM), generator=gen).to(dev).to(torch.bfloat16)
+            pl.append(Place(Chunk(k, v, orig), slots[c] * L))
+        plan = plan_request(N, pl, N_SINK, RATIO)
+        tab = np.concatenate([np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(ch.keys, ch.values)],
+                                       dtype=np.uint64).reshape(-1) for ch in plan.chunks])
+        K = torch.empty((N_LAYERS, 1, N_KV, N, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+        sets.append((pl, plan, torch.from_numpy(tab.view(np.int64)).to(dev), torch.from_numpy(plan.segments.reshape(-1)).to(dev),
+                     K, torch.empty_like(K)))
+
+    def launch(i):
+        _, plan, tab, segs, K, V = sets[i % 3]
+        ops.rerope_gather(K, V, tab, segs, len(plan.segments), plan.max_seg_tokens, THETA)
+
+    for i in range(warmup):
+        launch(i)
+    ms = _timed(launch, steps, torch.cuda.current_stream(dev))
+    nbytes = N_LAYERS * C * L * ROW_BYTES * 4
+    return _workload_line(
+        "re-RoPE + gather HBM GB/s, Qwen2.5-7B KV shape", nbytes / (ms * 1e-3) / 1e9, ms, steps, warmup,
+        {"workload": "re-RoPE + gather: 28 layers, 4 KV heads, head_dim 128, bf16, 16 chunks x 256 tokens, "
+                     "delta ~ U[-4096, 4096], 4096-token cache", "bytes_per_step": nbytes},
+        _rooffor("rerope_gather_kernel<bf16,128>", nbytes, ms))
+
+
+def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
+    """Deviation + pooled top-k + scatter microbenchmark: layer-1 fresh vs cached K/V for 32 chunks
+    x 256 tokens (8192), 4 heads x 128, bf16; cached = fresh + sigma_c N(0,1), sigma_c ~
+    lognormal(-3, 1); pooled top-k at 15/30/50% plus 4 sinks per chunk, then the scatter of the
+    kept rows into one layer's cache."""
+    from chunkkv_amd import ops
+    from chunkkv_amd.planner import local_index, plan_request
+
+    N, C, L = 8192, 32, 256
+    gen = torch.Generator().manual_seed(3)
+    fk = torch.randn((1, N_KV, N, HEAD_DIM), generator=gen)
+    fv = torch.randn((1, N_KV, N, HEAD_DIM), generator=gen)
+    sigma = torch.exp(torch.randn(C, generator=gen) - 3.0).repeat_interleave(L)[None, None, :, None]
+    K = (fk + sigma * torch.randn(fk.shape, generator=gen)).bfloat16().to(dev)
+    V = (fv + sigma * torch.randn(fv.shape, generator=gen)).bfloat16().to(dev)
+    k = fk.bfloat16().to(dev)
+    v = fv.bfloat16().transpose(1, 2).contiguous().to(dev).transpose(1, 2)
+    pl = [Place(Chunk(torch.empty((1, 1, N_KV, L, HEAD_DIM)), torch.empty((1, 1, N_KV, L, HEAD_DIM)), 0), c * L)
+          for c in range(C)]
+    out = {}
+    stream = torch.cuda.current_stream(dev)
+    for ratio in (0.15, 0.30, 0.50):
+        plan = plan_request(N, pl, N_SINK, ratio)
+        flags = torch.from_numpy(plan.flags).to(dev)
+        local = torch.from_numpy(local_index(N, plan.layer0_idx)).to(dev)
+        spans = torch.from_numpy(plan.spans.reshape(-1)).to(dev)
+        Kd, Vd = K.clone(), V.clone()
+        st = {}
+
+        def dev_sel(i):
+            d, n = ops.deviation(k, v, K, V, flags, local)
+            st["sel"] = ops.select(d, n, flags, local, spans, None, st.get("sel"))
+
+        def scat(i):
+            rows = st["sel"].keep_abs[: plan.n_keep]
+            ops.scatter_rows(Kd, Vd, k[:, :, : plan.n_keep], v[:, :, : plan.n_keep], rows)
+
+        for i in range(max(warmup, 1)):
+            dev_sel(i)
+            scat(i)
+        g_dev, g_sc = _graph_of(lambda: dev_sel(0)), _graph_of(lambda: scat(0))  # small kernels: no launch overhead
+        t_dev = _timed(lambda i: g_dev.replay(), steps, stream)
+        t_sc = _timed(lambda i: g_sc.replay(), steps, stream)
+        assert int(st["sel"].counts[0].item()) == plan.n_keep
+        out[ratio] = dict(n_keep=plan.n_keep, dev_sel_ms=t_dev, scatter_ms=t_sc, scatter_bytes=plan.n_keep * ROW_BYTES * 4)
+    dev_bytes = N * 4 * ROW_BYTES
+    r30 = out[0.30]
+    ms = r30["dev_sel_ms"] + r30["scatter_ms"]
+    line = _workload_line(
+        "deviation + pooled top-k + scatter HBM GB/s, Qwen2.5-7B KV shape", (dev_bytes + r30["scatter_bytes"]) / (ms * 1e-3) / 1e9,
+        ms, steps, warmup,
+        {"workload": "layer-1 deviation + pooled top-k (30%) + 4 sinks x 32 chunks x 256 + scatter, 4 KV heads, head_dim 128, bf16",
+         "bytes_per_step": dev_bytes + r30["scatter_bytes"]},
+        _rooffor("deviation_kernel<bf16> + select_reg_kernel", dev_bytes, r30["dev_sel_ms"]))
+    line["ratios"] = {str(r): {k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in o.items()} for r, o in out.items()}
+    return line
+
+
+def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4) -> dict:
+    """Long-context multi-request replay at the Qwen2.5-7B shape: an HBM-resident store of 256
+    chunks x 256 tokens x 2 context variants (7.0 GiB); 4 concurrent requests of 128 chunks
+    sampled with replacement (Zipf s=1.1) at random order + a 64-token query (32832 tokens), 15%
+    recompute + 4 sinks; each request's whole KV repair runs on its own HIP stream."""
+    from chunkkv_amd import ops
+    from chunkkv_amd.planner import local_index, plan_request
+
+    L, POOL, VARIANTS, PER_REQ, Q = 256, 256, 2, 128, 64
+    N = PER_REQ * L + Q
+    gen = torch.Generator(device=dev).manual_seed(11)
+    store = []
+    for _ in range(POOL * VARIANTS):
+        k = torch.randn((N_LAYERS, 1, N_KV, L, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn((N_LAYERS, 1, N_KV, L, HEAD_DIM), generator=gen, device=dev).to(torch.bfloat16)
+        store.append(Chunk(k, v, int(torch.randint(0, 32768, (1,), generator=gen, device=dev).item())))
+    zipf = 1.0 / np.arange(1, POOL + 1) ** 1.1
+    zipf /= zipf.sum()
+    rng = np.random.default_rng(11)
+    reqs = []
+    for r in range(2 * n_streams):
+        ids = rng.choice(POOL, PER_REQ, p=zipf) * VARIANTS + rng.integers(0, VARIANTS, PER_REQ)
+        pl = [Place(store[i], j * L) for j, i in enumerate(ids)]
+        plan = plan_request(N, pl, N_SINK, 0.15)
+        tab = np.concatenate([np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(ch.keys, ch.values)],
+                                       dtype=np.uint64).reshape(-1) for ch in plan.chunks])
+        K = torch.empty((N_LAYERS, 1, N_KV, N, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+        fresh = [(torch.randn((1, N_KV, N if li < 2 else plan.n_keep, HEAD_DIM), device=dev).bfloat16(),
+                  torch.randn((1, N_KV, N if li < 2 else plan.n_keep, HEAD_DIM), device=dev).bfloat16())
+                 for li in range(N_LAYERS)]
+        reqs.append(dict(plan=plan, tab=torch.from_numpy(tab.view(np.int64)).to(dev),
+                         segs=torch.from_numpy(plan.segments.reshape(-1)).to(dev), K=K, V=torch.empty_like(K),
+                         flags=torch.from_numpy(plan.flags).to(dev),
+                         local=torch.from_numpy(local_index(N, plan.layer0_idx)).to(dev),
+                         spans=torch.from_numpy(plan.spans.reshape(-1)).to(dev),
+                         layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), fresh=fresh, sel=None))
+    assert reqs[0]["plan"].budget == 4864
+    streams = [torch.cuda.Stream() for _ in range(n_streams)]
+
+    def repair(rq):
+        plan = rq["plan"]
+        ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], len(plan.segments), plan.max_seg_tokens, THETA)
+        K, V = rq["K"].unbind(0), rq["V"].unbind(0)
+        ops.scatter_rows(K[0], V[0], *rq["fresh"][0], rq["layer0"])
+        k1, v1 = rq["fresh"][1]
+        d, n = ops.deviation(k1, v1, K[1], V[1], rq["flags"], rq["local"])
+        rq["sel"] = ops.select(d, n, rq["flags"], rq["local"], rq["spans"], None, rq["sel"])
+        rows = rq["sel"].keep_abs[: plan.n_keep]
+        for li in range(1, N_LAYERS):
+            k, v = rq["fresh"][li] if li > 1 else (k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep])
+            ops.scatter_rows(K[li], V[li], k, v, rows)
+
+    def round_(i):
+        base = (i % 2) * n_streams
+        for s_i, s in enumerate(streams):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                repair(reqs[base + s_i])
+        for s in streams:
+            torch.cuda.current_stream().wait_stream(s)
+
+    for i in range(max(warmup, 2)):
+        round_(i)
+    torch.cuda.synchronize()
+    ms = _timed(round_, steps, torch.cuda.current_stream(dev))
+    per_req = sum(repair_bytes_for(rq["plan"]) for rq in reqs[:n_streams]) / n_streams
+    nbytes = per_req * n_streams
+    assert all(int(rq["sel"].counts[0].item()) == rq["plan"].n_keep for rq in reqs)
+    line = _workload_line(
+        "aggregate KV-repair HBM GB/s, 4 concurrent 32k-token requests, Qwen2.5-7B KV shape", nbytes / (ms * 1e-3) / 1e9,
+        ms, steps, warmup,
+        {"workload": "replay: store 256 chunks x 256 tokens x 2 variants (7.0 GiB HBM); 4 requests x (128 Zipf(1.1) "
+                     "chunks + 64-token query) = 32832 tokens each, 15% + 4 sinks, one HIP stream per request",
+         "bytes_per_step": int(nbytes), "requests_per_step": n_streams},
+        None)
+    line["store_gib"] = round(len(store) * N_LAYERS * 2 * N_KV * L * HEAD_DIM * 2 / 2**30, 2)
+    return line
+
+
+def traffic_probe(steps: int, warmup: int, dev) -> dict:
+    """Dispatches for the HBM traffic counters (run under rocprofv3 --pmc): `steps` re-RoPE +
+    gather launches of the 8k request alternating two input sets, then `steps` elementwise kernels
+    that read and write exactly COPY_BYTES each, whose FETCH_SIZE / WRITE_SIZE calibrate the
+    counters (a plain D2D copy goes to the DMA engine and is not counted)."""
+    wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
+    for i in range(steps):
+        wls[i % 2].gather()
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = [torch.empty_like(src) for _ in range(2)]
+    for i in range(steps):  # one elementwise kernel: reads and writes exactly COPY_BYTES
+        torch.mul(src, 1.0, out=dst[i % 2])
+    torch.cuda.synchronize()
+    return {"workload": "traffic probe", "gather_launches": steps, "copy_bytes": COPY_BYTES, "copies": steps}
+
+
+COPY_BYTES = 512 << 20
+
+
+def repair_bytes_for(plan) -> int:
+    """Algorithmic repair bytes of a request plan (gather of every cached row, deviation over the
+    layer-0 active set, scatters of layer 0 and layers 1..L-1)."""
+    row = ROW_BYTES
+    n_cached_rows = int(plan.cached.sum())
+    n0 = len(plan.layer0_idx)
+    return (N_LAYERS * n_cached_rows * row * 4 + n0 * 4 * row + plan.n_tokens * 8 + n0 * row * 4
+            + (N_LAYERS - 1) * plan.n_keep * row * 4)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -346,12 +576,20 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ttft-requests", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--workload", default="request", choices=["request", "gather", "deviation", "replay", "traffic"],
+                    help="request: the 8k Qwen2.5-7B blend-prefill KV repair (default); gather / deviation / replay: "
+                         "the re-RoPE+gather, deviation+top-k+scatter and 4x32k replay microbenchmarks")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload != "request":
+        fn = {"gather": bench_gather_only, "deviation": bench_deviation_topk, "replay": bench_replay,
+              "traffic": traffic_probe}[args.workload]
+        print(json.dumps(fn(args.steps, args.warmup, dev)), flush=True)
+        return
 
     r = bench_repair(args.steps, args.warmup, dev)
     log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_eager']:.3f} ms eager); "
@@ -389,7 +627,8 @@ def main() -> None:
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(r["gather_gbs"] / PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GATHER_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_rerope_gather_qwen25_7b_8k.md",
             "bytes_per_launch": GATHER_BYTES,
             "avg_launch_us": round(r["gather_ms"] * 1e3, 2),
         },

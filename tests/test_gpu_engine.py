@@ -294,3 +294,46 @@ def test_repair_step_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert torch.equal(Ks, eager[0]) and torch.equal(Vs, eager[1])
         assert torch.equal(state["sel"].keep_abs[: plan.n_keep], eager[2])
+
+
+@pytest.mark.parametrize("attention", ["reference", "fused"])
+def test_config1_qwen25_05b_shape_matches_oracle(attention):
+    """Config 1: Qwen2.5-0.5B architecture (24 layers, hidden 896, 14 Q / 2 KV heads, head_dim 64,
+    theta 1e6, vocab 151936, intermediate 4864, tied embeddings), random init, fp32. Four chunks of
+    256 random ids prefilled at 0..1023, placed in a shuffled order, plus a 32-token query;
+    15% recompute with 4 sinks. HipEngine on the GPU vs the oracle on the CPU, same chunk bytes."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=896, intermediate_size=4864, num_hidden_layers=24,
+                      num_attention_heads=14, num_key_value_heads=2, max_position_embeddings=32768, rope_theta=1e6,
+                      tie_word_embeddings=True, rms_norm_eps=1e-6)
+    torch.manual_seed(0)
+    cpu = Qwen2ForCausalLM(cfg).eval()
+    gpu = copy.deepcopy(cpu).to(DEV)
+    eng = HipEngine(gpu, StubTokenizer(), attention=attention)
+    rng = np.random.default_rng(1)
+    docs = [rng.integers(0, 151936, 256).tolist() for _ in range(4)]
+    first = eng.prefill(sum(docs, []))
+    chunks = [first.chunk(i * 256, (i + 1) * 256) for i in range(4)]
+    order = rng.permutation(4).tolist()
+    query = rng.integers(0, 151936, 32).tolist()
+    tokens = sum((docs[i] for i in order), []) + query
+    pl = [Placement(chunks[i], k * 256) for k, i in enumerate(order)]
+    bc = BlendConfig(recompute_ratio=0.15, n_sink=4)
+    eng.trace = {}
+    out = eng.prefill(tokens, pl, bc)
+    tr, eng.trace = eng.trace, None
+    ref = R.prefill(cpu, tokens, _to_cpu_placements(pl), bc, inv_freq=eng.inv_freq.cpu())
+    assert out.stats["cached_tokens"] == 1024 and out.stats["recomputed_cached_tokens"] == 16 + 4 * 38
+    for key in ("tokens", "cached_tokens", "recomputed_cached_tokens", "prefill_token_equiv"):
+        assert out.stats[key] == ref["stats"][key], key
+    for a, b in zip(out.stats["chunks"], ref["stats"]["chunks"]):
+        assert (a["start"], a["length"], a["escalated"]) == (b["start"], b["length"], b["escalated"])
+        assert a["rel_dev"] == pytest.approx(b["rel_dev"], rel=1e-3)
+    n = tr["n_keep"]
+    got = O.to_numpy(tr["sel"].keep_abs)[:n]
+    want = O.select(O.to_numpy(tr["diff"]), O.to_numpy(tr["norm"]), O.to_numpy(tr["flags"]), O.to_numpy(tr["local"]),
+                    O.to_numpy(tr["spans"]).reshape(-1, 4), None)
+    np.testing.assert_array_equal(got, want["keep_abs"])
+    assert_same_selection(got, ref, tokens, pl, bc)
+    assert _kl(ref["logits"], out.logits.cpu()) < 1e-4
