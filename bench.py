@@ -7,20 +7,24 @@ bf16, rope theta 1e6; a request of N = 8256 tokens = 24 cached chunks of 320 tok
 shuffled positions (each chunk computed at its own original offset, so every placement shifts
 its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
 
-A step is one request's whole KV repair with every input already resident in HBM:
-re-RoPE + gather of all 28 layers (one launch), the layer-0 scatter of all 8256 rows, the
-layer-1 deviation and selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows), and
-the scatters of layers 1-27. Algorithmic bytes per step (read + write of every byte moved):
+A step is one request's whole KV repair with every input already resident in HBM, issued as
+HipEngine issues it: one assemble launch per layer writes every cache row once (fresh if the
+position is active, else the re-rotated cached row); layer 1 instead builds its base cache,
+runs the deviation and selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows) and
+scatters the kept rows. The unit of work is one request's KV repair as the reference's op
+sequence moves it (re-RoPE + gather of every cached row of all 28 layers, the layer-0 scatter of
+all 8256 rows, the deviation, the scatters of layers 1-27):
     gather          28 x 24 x 320 x 4 heads x 128 x 2 B x 2 (K,V) x 2 (r+w) =   880,803,840
     deviation       8256 x (4 rows x 1 KiB) + 8256 x 8 B                       =    33,882,624
     scatter L0      8256 x 4096 B                                              =    33,816,576
     scatter L1-27   27 x 2976 x 4096 B                                         =   329,121,792
     total                                                                      = 1,277,624,832
-`value` = total bytes / measured time per step (GB/s), the step's 31 launches replayed from a
-HIP graph (the eager time, launch-bound from Python, is reported as ms_per_step_eager).
-`roofline` is the dominant kernel (re-RoPE + gather) timed live with HIP events around a burst
-of back-to-back launches on the launch stream. Inputs rotate between two independent copies so
-consecutive steps do not hit in the 256 MB MALL.
+`value` = that total / measured time per step (GB/s), the step's 31 launches replayed from a
+HIP graph (the eager time, launch-bound from Python, is reported as ms_per_step_eager); the
+fused flow itself moves 990,577,152 B per step (moved_bytes_per_step, moved_gbs). `roofline` is
+the dominant kernel (assemble, 27 of the 31 launches, 33,816,576 B each) timed live with HIP
+events around a burst of back-to-back launches on the launch stream. Inputs rotate between two
+independent copies so consecutive steps do not hit in the 256 MB MALL.
 
 Besides the bandwidth line, the run measures blend-prefill TTFT p50 (prefill + last_logprobs,
 the bracket of the reference's bench/replay.py:32-35) over seeded requests of the same shape on
@@ -57,6 +61,8 @@ GATHER_BYTES = N_LAYERS * N_CHUNKS * CHUNK_LEN * ROW_BYTES * 2 * 2
 # (profiles/traffic_rerope_gather_qwen25_7b_8k.md; FETCH_SIZE calibrated against a kernel of
 # known traffic). Counters cannot be read inside a timed run, so the measured value is recorded.
 GATHER_TRAFFIC_BYTES = 881_167_672
+# Same for one assemble launch (layer >= 2 of the 8k request); None until measured.
+ASSEMBLE_TRAFFIC_BYTES = None
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 
@@ -121,6 +127,7 @@ class RepairWorkload:
         )
         self.tab = torch.from_numpy(tab.view(np.int64)).to(dev)
         self.segs = torch.from_numpy(plan.segments.reshape(-1)).to(dev)
+        self.segs_all = torch.from_numpy(plan.all_segments.reshape(-1)).to(dev)  # cached runs first
         self.flags = torch.from_numpy(plan.flags).to(dev)
         self.local = torch.from_numpy(local_index(N_TOKENS, plan.layer0_idx)).to(dev)
         self.spans = torch.from_numpy(plan.spans.reshape(-1)).to(dev)
@@ -166,7 +173,8 @@ class RepairWorkload:
                           self.plan.max_seg_tokens, THETA, self.err)
 
     def rest(self):
-        """Everything after the gather: scatter L0, deviation + selection at L1, scatters L1-27."""
+        """Everything after the gather: scatter L0, deviation + selection at L1, scatters L1-27
+        (the reference's op order, kept for comparison; HipEngine runs step())."""
         from chunkkv_amd import ops
 
         K, V = self.k_slab.unbind(0), self.v_slab.unbind(0)
@@ -178,6 +186,33 @@ class RepairWorkload:
         for li in range(1, N_LAYERS):
             k, v = self.fresh[li] if li > 1 else (k1[:, :, : self.plan.n_keep], v1[:, :, : self.plan.n_keep])
             ops.scatter_rows(K[li], V[li], k, v, rows, self.err)
+
+    def assemble(self, li: int):
+        """One layer li >= 2 (or 0) as HipEngine builds it: every row written once."""
+        from chunkkv_amd import ops
+
+        plan = self.plan
+        local = self.local if li == 0 else self.sel.keep_rank
+        ops.assemble_layer(self.k_slab[li], self.v_slab[li], self.tab, N_LAYERS, li, self.segs_all,
+                           len(plan.all_segments), plan.max_all_seg_tokens, *self.fresh[li], local, THETA, self.err)
+
+    def step(self):
+        """One request's KV repair exactly as HipEngine issues it: assemble L0; base cache of L1,
+        deviation, selection, scatter of the kept rows of L1; assemble L2..L27 (31 launches)."""
+        from chunkkv_amd import ops
+
+        plan = self.plan
+        K, V = self.k_slab.unbind(0), self.v_slab.unbind(0)
+        self.assemble(0)
+        ops.assemble_layer(K[1], V[1], self.tab, N_LAYERS, 1, self.segs_all, len(plan.segments), plan.max_seg_tokens,
+                           None, None, None, THETA, self.err)
+        k1, v1 = self.fresh[1]
+        diff, norm = ops.deviation(k1, v1, K[1], V[1], self.flags, self.local, self.err)
+        self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
+        ops.scatter_rows(K[1], V[1], k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep], self.sel.keep_abs[: plan.n_keep],
+                         self.err)
+        for li in range(2, N_LAYERS):
+            self.assemble(li)
 
 
 def repair_bytes(n_keep: int) -> int:
@@ -212,32 +247,40 @@ def _graph_of(fn):
 
 
 def bench_repair(steps: int, warmup: int, dev) -> dict:
-    """Time the KV-repair step. The 31 launches of a step are captured once per input set in a
-    HIP graph and replayed (the step is launch-bound from Python otherwise); the eager time is
-    reported too. The dominant kernel's average duration comes from a burst of back-to-back
-    gather launches on the same stream."""
+    """Time the KV-repair step as HipEngine issues it (31 launches, captured once per input set in
+    a HIP graph and replayed; the eager time, launch-bound from Python, is reported too), and the
+    dominant kernel's average duration from a burst of back-to-back assemble launches."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
-
-    def step(w):
-        w.gather()
-        w.rest()
-
     for i in range(max(warmup, 2)):
-        step(wls[i % 2])
+        wls[i % 2].step()
     torch.cuda.synchronize()
-    graphs = [_graph_of(lambda w=w: step(w)) for w in wls]
+    graphs = [_graph_of(w.step) for w in wls]
     stream = torch.cuda.current_stream(dev)
-    for i in range(2):
-        graphs[i].replay()
+    for g in graphs:
+        g.replay()
     ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
-    ms_eager = _timed(lambda i: step(wls[i % 2]), steps, stream)
-    g_ms = _timed(lambda i: wls[i % 2].gather(), steps, stream)
+    ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
+    n_asm = N_LAYERS - 2
+    asm_ms = _timed(lambda i: wls[(i // n_asm) % 2].assemble(2 + i % n_asm), steps * n_asm, stream)
     assert all(int(w.err.item()) == 0 for w in wls)
     n_keep = wls[0].plan.n_keep
     assert int(wls[0].sel.counts[0].item()) == n_keep
     nbytes = repair_bytes(n_keep)
-    return dict(ms_per_step=ms, ms_eager=ms_eager, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, gather_ms=g_ms,
-                gather_gbs=GATHER_BYTES / (g_ms * 1e-3) / 1e9, n_keep=n_keep)
+    return dict(ms_per_step=ms, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(wls[0].plan),
+                gbs=nbytes / (ms * 1e-3) / 1e9, asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9,
+                n_keep=n_keep)
+
+
+def moved_bytes(plan) -> int:
+    """Algorithmic bytes of the step as HipEngine runs it: each assembled layer reads and writes
+    every row once; layer 1 reads and writes its cached rows (base cache), then the deviation
+    and the scatter of the kept rows."""
+    row = ROW_BYTES * 4  # K and V, read + write
+    n_cached = int(plan.cached.sum())
+    return ((N_LAYERS - 1) * plan.n_tokens * row + n_cached * row + DEVIATION_BYTES + plan.n_keep * row)
+
+
+ASSEMBLE_BYTES = N_TOKENS * ROW_BYTES * 4  # one assembled layer: 8256 rows of K and V, read + write
 
 
 def random_qwen25_7b(dev):
@@ -548,6 +591,10 @@ def traffic_probe(steps: int, warmup: int, dev) -> dict:
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
     for i in range(steps):
         wls[i % 2].gather()
+    for w in wls:
+        w.step()  # selection output for the assemble launches below
+    for i in range(steps):
+        wls[i % 2].assemble(2 + i % (N_LAYERS - 2))
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = [torch.empty_like(src) for _ in range(2)]
     for i in range(steps):  # one elementwise kernel: reads and writes exactly COPY_BYTES
@@ -593,7 +640,7 @@ def main() -> None:
 
     r = bench_repair(args.steps, args.warmup, dev)
     log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_eager']:.3f} ms eager); "
-        f"gather {r['gather_gbs']:.1f} GB/s ({r['gather_ms'] * 1e3:.1f} us)")
+        f"assemble {r['asm_gbs']:.1f} GB/s ({r['asm_ms'] * 1e3:.2f} us)")
     ttft = bench_ttft(args.ttft_requests, dev) if args.ttft_requests > 0 else None
     cpu = bench_cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None
 
@@ -618,19 +665,23 @@ def main() -> None:
             "tokens": N_TOKENS,
             "kept_rows": r["n_keep"],
             "bytes_per_step": r["bytes"],
+            "bytes_per_step_note": "KV-repair bytes of one request as the reference's op sequence moves them "
+                                   "(value = these bytes / step time); the fused path moves moved_bytes_per_step",
+            "moved_bytes_per_step": r["moved"],
         },
         "pct_of_peak": round(100.0 * r["gbs"] / PEAK_GBS, 2),
+        "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
         "roofline": {
-            "kernel": "rerope_gather_kernel<bf16,128>",
+            "kernel": "assemble_kernel<bf16,128>",
             "bound": "hbm",
-            "achieved": round(r["gather_gbs"], 1),
+            "achieved": round(r["asm_gbs"], 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(r["gather_gbs"] / PEAK_GBS, 4),
-            "traffic": GATHER_TRAFFIC_BYTES,
-            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_rerope_gather_qwen25_7b_8k.md",
-            "bytes_per_launch": GATHER_BYTES,
-            "avg_launch_us": round(r["gather_ms"] * 1e3, 2),
+            "frac": round(r["asm_gbs"] / PEAK_GBS, 4),
+            "traffic": ASSEMBLE_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_assemble_qwen25_7b_8k.md",
+            "bytes_per_launch": ASSEMBLE_BYTES,
+            "avg_launch_us": round(r["asm_ms"] * 1e3, 2),
         },
         "cpu_baseline": cpu,
     }

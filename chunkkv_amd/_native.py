@@ -55,7 +55,12 @@ SIGNATURES = {
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p],
     ),
-    "ckv_select": (_i32, [_p, _p, _p, _p, _i32, _p, _i32, _i32, _f64, _p, _p, _p, _p, _p, _p]),
+    "ckv_select": (_i32, [_p, _p, _p, _p, _i32, _p, _i32, _i32, _f64, _p, _p, _p, _p, _p, _p, _p]),
+    "ckv_assemble_layer": (
+        _i32,
+        [_p, _p, _i64, _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i32, _i32,
+         _i32, _i32, _f64, _p, _p],
+    ),
     "ckv_scatter_rows": (
         _i32,
         [_p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p, _p],

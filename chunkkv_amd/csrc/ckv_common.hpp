@@ -107,6 +107,40 @@ __device__ __forceinline__ float rope_inv_freq(int i, int head_dim, double theta
   return (float)pow((double)theta_f, (double)e);
 }
 
+// cos/sin of the shift `delta` for frequency i: the fp32 angle fl32(fl32(delta) * inv_freq_i), as
+// torch forms `delta * inv_freq`, then cos/sin of that angle evaluated in fp64 and rounded once,
+// i.e. the correctly rounded fp32 values. (x = cos, y = sin.)
+__device__ __forceinline__ float2 rope_shift_cos_sin(int i, int head_dim, double theta, int delta) {
+  const float ang = (float)delta * rope_inv_freq(i, head_dim, theta);
+  double sd, cd;
+  sincos((double)ang, &sd, &cd);
+  return make_float2((float)cd, (float)sd);
+}
+
+// Rotate VEC frequency pairs held as two 16-byte vectors: a = first-half elements, b = the
+// matching second-half elements. y1 = a*cos - b*sin, y2 = a*sin + b*cos with every product and
+// sum rounded separately in fp32 (callers build with -ffp-contract=off), then one rounding to
+// the element type.
+template <int DTYPE>
+__device__ __forceinline__ void rotate_pairs(const vec16& a16, const vec16& b16, const float* c, const float* s,
+                                             vec16& y1_16, vec16& y2_16) {
+  using E = Elem<DTYPE>;
+  float a[E::kVec], b[E::kVec], y1[E::kVec], y2[E::kVec];
+  E::unpack(a16, a);
+  E::unpack(b16, b);
+#pragma unroll
+  for (int e = 0; e < E::kVec; ++e) {
+    const float p1 = a[e] * c[e];
+    const float p2 = b[e] * s[e];
+    const float p3 = a[e] * s[e];
+    const float p4 = b[e] * c[e];
+    y1[e] = p1 - p2;
+    y2[e] = p3 + p4;
+  }
+  y1_16 = E::pack(y1);
+  y2_16 = E::pack(y2);
+}
+
 }  // namespace ckv
 
 // Host-side status helper shared by the entry points.

@@ -143,13 +143,7 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
   const bool rotate = s.delta != 0;
   float c[VEC], sn[VEC];
   if (rotate) {
-    if (threadIdx.x < HALF) {
-      const float inv = rope_inv_freq(threadIdx.x, D, theta);
-      const float ang = (float)s.delta * inv;  // fp32 angle, as torch forms delta * inv_freq
-      double sd, cd;                           // cos/sin of that angle, correctly rounded to fp32
-      sincos((double)ang, &sd, &cd);
-      cs_tab[threadIdx.x] = make_float2((float)cd, (float)sd);
-    }
+    if (threadIdx.x < HALF) cs_tab[threadIdx.x] = rope_shift_cos_sin(threadIdx.x, D, theta, s.delta);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -166,20 +160,10 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
       if (row_ok(r)) {
         const int64_t o = dst_off(r);
         if (rotate) {
-          float a[VEC], b[VEC], y1[VEC], y2[VEC];
-          E::unpack(kx1[u], a);
-          E::unpack(kx2[u], b);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            const float p1 = a[e] * c[e];
-            const float p2 = b[e] * sn[e];
-            const float p3 = a[e] * sn[e];
-            const float p4 = b[e] * c[e];
-            y1[e] = p1 - p2;
-            y2[e] = p3 + p4;
-          }
-          gather_st(dk0 + o, E::pack(y1));
-          gather_st(dk0 + o + HALF_B, E::pack(y2));
+          vec16 y1, y2;
+          rotate_pairs<DTYPE>(kx1[u], kx2[u], c, sn, y1, y2);
+          gather_st(dk0 + o, y1);
+          gather_st(dk0 + o + HALF_B, y2);
         } else {
           gather_st(dk0 + o, kx1[u]);
           gather_st(dk0 + o + HALF_B, kx2[u]);

@@ -155,27 +155,53 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wave_tot, int& total)
   return before + x - v;
 }
 
+// Exclusive workgroup scan of one int per thread with ONE barrier: each call must get its own
+// `slots` array (kSelWaves ints) that no call in flight since the previous barrier reads.
+__device__ __forceinline__ int block_scan_1b(int v, int* slots, int& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) slots[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const int t = slots[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  total = all;
+  return before + x - v;
+}
+
 // Register-resident selection for n_tokens <= KPT * 1024: thread t owns positions
 // [t*KPT, (t+1)*KPT); their keys stay in registers through the four radix passes.
+// Barrier budget: chunk phase 2, candidate count 1, 2 per radix pass (double-buffered
+// histograms, every wavefront derives the digit itself), tie scan 1, compaction scan 1, counts 2.
 template <int KPT>
 __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
     const float* __restrict__ diff, const float* __restrict__ norm, const uint8_t* __restrict__ flags,
     const int32_t* __restrict__ local, int n_tokens, const ckv_chunk_span* __restrict__ chunks, int n_chunks,
     int has_thr, double thr, int64_t* __restrict__ keep_abs, int64_t* __restrict__ keep_local,
-    float* __restrict__ rel_out, uint8_t* __restrict__ esc_out, int32_t* __restrict__ counts) {
+    int32_t* __restrict__ keep_rank, float* __restrict__ rel_out, uint8_t* __restrict__ esc_out,
+    int32_t* __restrict__ counts) {
   static_assert(KPT <= 64, "per-thread position bits live in one 64-bit word");
   constexpr int kBatch = 8;            // chunk-sum loads in flight per lane
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
-  __shared__ uint32_t hist[kSelWaves][256];
-  __shared__ int wave_tot[kSelWaves];
-  __shared__ int s_budget_req, s_bad_span, s_digit, s_above;
+  __shared__ uint32_t hist[2][kSelWaves][256];
+  __shared__ int slots[5][kSelWaves];
+  __shared__ int s_budget_req, s_bad_span;
 
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int W = (n_tokens + 31) >> 5;
   uint32_t* escw = masks;
   uint32_t* poolw = masks + W;
 
-  // Loads of the owned positions go out first; their latency hides behind the chunk sums.
+  // Phase 0, no barrier before it: every global load this workgroup can issue up front.
   const int p0 = tid * KPT;
   constexpr int kFlagWords = (KPT + 3) / 4;
   uint32_t key[KPT];        // order-preserving deviation keys of the owned positions
@@ -188,17 +214,31 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
     key[i] = p < n_tokens ? dev_key(diff[p]) : 0u;
     if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
   }
+  // this wavefront's first chunk: span and the first batch of its deviations
+  ckv_chunk_span sp0{0, 0, 0, 0};
+  float bd0[kBatch], bn0[kBatch];
+  if (wave < n_chunks) {
+    sp0 = chunks[wave];
+    const bool ok0 = sp0.start >= 0 && sp0.length >= 0 && (int64_t)sp0.start + sp0.length <= n_tokens;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int q = j * kWave + lane;
+      bd0[j] = (ok0 && q < sp0.length) ? diff[sp0.start + q] : 0.0f;
+      bn0[j] = (ok0 && q < sp0.length) ? norm[sp0.start + q] : 0.0f;
+    }
+  }
   if (tid == 0) {
     s_budget_req = 0;
     s_bad_span = 0;
   }
   for (int w = tid; w < 2 * W; w += kSelThreads) masks[w] = 0u;
+  for (int b = tid; b < 2 * kSelWaves * 256; b += kSelThreads) (&hist[0][0][0])[b] = 0u;
   __syncthreads();
 
-  // Per-chunk rel / escalation / budget: one wavefront per chunk, loads batched per lane, summed
-  // in the contract's order (lane-strided, ascending, then the xor butterfly).
+  // Phase 1: per-chunk rel / escalation / budget, one wavefront per chunk, summed in the
+  // contract's order (lane-strided, ascending, then the xor butterfly).
   for (int c = wave; c < n_chunks; c += kSelWaves) {
-    const ckv_chunk_span sp = chunks[c];
+    const ckv_chunk_span sp = c == wave ? sp0 : chunks[c];
     const bool ok = sp.start >= 0 && sp.length >= 0 && (int64_t)sp.start + sp.length <= n_tokens;
     float sd = 0.0f, sn = 0.0f;
     if (ok) {
@@ -207,8 +247,13 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
           const int q = q0 + j * kWave + lane;
-          bd[j] = q < sp.length ? diff[sp.start + q] : 0.0f;
-          bn[j] = q < sp.length ? norm[sp.start + q] : 0.0f;
+          if (c == wave && q0 == 0) {
+            bd[j] = bd0[j];
+            bn[j] = bn0[j];
+          } else {
+            bd[j] = q < sp.length ? diff[sp.start + q] : 0.0f;
+            bn[j] = q < sp.length ? norm[sp.start + q] : 0.0f;
+          }
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
@@ -238,7 +283,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
   }
   __syncthreads();
 
-  // keep = ~cached | sink | escalated span; candidates = pooled span minus keep.
+  // Phase 2: keep = ~cached | sink | escalated span; candidates = pooled span minus keep.
   uint64_t cand = 0u, kept_static = 0u;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
@@ -251,73 +296,81 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
     }
   }
   int n_cand = 0;
-  block_excl_scan(__popcll(cand), wave_tot, n_cand);
+  block_scan_1b(__popcll(cand), slots[0], n_cand);
   const int budget_req = s_budget_req;
   const int budget = max(0, min(budget_req, n_cand));
 
+  // Phase 3: radix select of the budget-th largest candidate key.
   uint32_t prefix = 0u, pmask = 0u;
   int need = budget;
   if (budget > 0) {
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int b = tid; b < kSelWaves * 256; b += kSelThreads) (&hist[0][0])[b] = 0u;
-      __syncthreads();
-      // Run-length aggregate equal digits within the thread first: in the high passes almost
-      // every key shares one or two digits, and unaggregated LDS atomics would serialize.
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      uint32_t(*h)[256] = hist[pass & 1];
+      // Run-length aggregate equal digits within the thread: in the high passes almost every key
+      // shares one or two digits, and unaggregated LDS atomics would serialize.
       uint32_t run_digit = 0u, run_count = 0u;
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         if (((cand >> i) & 1ull) && (key[i] & pmask) == prefix) {
           const uint32_t d = (key[i] >> shift) & 255u;
           if (run_count != 0u && d != run_digit) {
-            atomicAdd(&hist[wave][run_digit], run_count);
+            atomicAdd(&h[wave][run_digit], run_count);
             run_count = 0u;
           }
           run_digit = d;
           ++run_count;
         }
       }
-      if (run_count != 0u) atomicAdd(&hist[wave][run_digit], run_count);
+      if (run_count != 0u) atomicAdd(&h[wave][run_digit], run_count);
       __syncthreads();
-      if (tid < 256) {  // fold the per-wavefront histograms into hist[0]
+      if (tid < 256) {  // fold the per-wavefront histograms into h[0]
         uint32_t t = 0;
 #pragma unroll
-        for (int w = 0; w < kSelWaves; ++w) t += hist[w][tid];
-        hist[0][tid] = t;
+        for (int w = 0; w < kSelWaves; ++w) t += h[w][tid];
+        h[0][tid] = t;
+      } else {  // the other buffer was last read before this pass's barrier: clear it for pass+1
+        uint32_t* o = &hist[(pass + 1) & 1][0][0];
+        for (int b = tid - 256; b < kSelWaves * 256; b += kSelThreads - 256) o[b] = 0u;
       }
       __syncthreads();
-      if (wave == 0) {
-        uint32_t h4[4];
-        uint32_t local_sum = 0;
+      // every wavefront finds the digit: lane l owns digits 255-4l .. 252-4l (descending)
+      uint32_t h4[4];
+      uint32_t local_sum = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          h4[i] = hist[0][255 - (lane * 4 + i)];
-          local_sum += h4[i];
-        }
-        uint32_t incl = local_sum;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-          const uint32_t t = __shfl_up(incl, off, kWave);
-          if (lane >= off) incl += t;
-        }
-        uint32_t above = incl - local_sum;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (above < (uint32_t)need && (uint32_t)need <= above + h4[i]) {
-            s_digit = 255 - (lane * 4 + i);
-            s_above = (int)above;
-          }
-          above += h4[i];
-        }
+      for (int i = 0; i < 4; ++i) {
+        h4[i] = h[0][255 - (lane * 4 + i)];
+        local_sum += h4[i];
       }
-      __syncthreads();
-      need -= s_above;
-      prefix |= (uint32_t)s_digit << shift;
+      uint32_t incl = local_sum;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t t = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += t;
+      }
+      uint32_t above = incl - local_sum;
+      int my_digit = -1;
+      uint32_t my_above = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (above < (uint32_t)need && (uint32_t)need <= above + h4[i]) {
+          my_digit = 255 - (lane * 4 + i);
+          my_above = above;
+        }
+        above += h4[i];
+      }
+      const uint64_t found = __ballot(my_digit >= 0);
+      const int src = found ? (int)__ffsll((unsigned long long)found) - 1 : 0;
+      const int digit = __shfl(my_digit, src, kWave);
+      need -= (int)__shfl(my_above, src, kWave);
+      prefix |= (uint32_t)digit << shift;
       pmask |= 255u << shift;
     }
   }
   const uint32_t T = prefix;
 
-  // Take key > T, then the first `need` ties at T in token order.
+  // Phase 4: take key > T and the first `need` ties at T in token order, then compact.
   uint64_t take = 0u, tie = 0u;
   if (budget > 0) {
 #pragma unroll
@@ -328,8 +381,11 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
       }
     }
   }
+  int lv[KPT];  // the keys are dead now; their registers carry local[] through the scans
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) lv[i] = (p0 + i < n_tokens) ? local[p0 + i] : 0;
   int tie_total = 0;
-  int tie_rank = block_excl_scan(__popcll(tie), wave_tot, tie_total);
+  int tie_rank = block_scan_1b(__popcll(tie), slots[1], tie_total);
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     if ((tie >> i) & 1ull) {
@@ -339,29 +395,29 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
   }
   const uint64_t kept = kept_static | take;
   int n_keep = 0;
-  int rank = block_excl_scan(__popcll(kept), wave_tot, n_keep);
+  int rank = block_scan_1b(__popcll(kept), slots[2], n_keep);
   int my_cached = 0, my_bad = 0;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
+    if (keep_rank != nullptr && p0 + i < n_tokens) keep_rank[p0 + i] = ((kept >> i) & 1ull) ? rank : -1;
     if ((kept >> i) & 1ull) {
       const int p = p0 + i;
-      const int l = local[p];
       keep_abs[rank] = p;
-      keep_local[rank] = l < 0 ? 0 : l;
-      my_bad += l < 0;
+      keep_local[rank] = lv[i] < 0 ? 0 : lv[i];
+      my_bad += lv[i] < 0;
       my_cached += ((fl[i / 4] >> (8 * (i % 4))) & CKV_POS_CACHED) ? 1 : 0;
       ++rank;
     }
   }
-  int c1 = 0, c2 = 0;
-  block_excl_scan(my_cached, wave_tot, c1);
-  block_excl_scan(my_bad, wave_tot, c2);
+  int sel_cached = 0, uncomputed = 0;
+  block_scan_1b(my_cached, slots[3], sel_cached);
+  block_scan_1b(my_bad, slots[4], uncomputed);
   if (tid == 0) {
     counts[CKV_COUNT_KEEP] = n_keep;
-    counts[CKV_COUNT_SELECTED_CACHED] = c1;
+    counts[CKV_COUNT_SELECTED_CACHED] = sel_cached;
     counts[CKV_COUNT_BUDGET] = budget;
     counts[CKV_COUNT_CANDIDATES] = n_cand;
-    counts[CKV_COUNT_UNCOMPUTED] = c2;
+    counts[CKV_COUNT_UNCOMPUTED] = uncomputed;
     counts[CKV_COUNT_BUDGET_REQUESTED] = budget_req;
     counts[6] = s_bad_span;
     counts[7] = 0;
@@ -374,8 +430,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(
     const float* __restrict__ diff, const float* __restrict__ norm, const uint8_t* __restrict__ flags,
     const int32_t* __restrict__ local, int n_tokens, const ckv_chunk_span* __restrict__ chunks,
     int n_chunks, int has_thr, double thr, int64_t* __restrict__ keep_abs,
-    int64_t* __restrict__ keep_local, float* __restrict__ rel_out, uint8_t* __restrict__ esc_out,
-    int32_t* __restrict__ counts) {
+    int64_t* __restrict__ keep_local, int32_t* __restrict__ keep_rank, float* __restrict__ rel_out,
+    uint8_t* __restrict__ esc_out, int32_t* __restrict__ counts) {
   extern __shared__ uint32_t masks[];  // keep[W], pool[W]
   __shared__ uint32_t hist[256];
   __shared__ int wave_tot[kSelWaves];
@@ -523,6 +579,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(
     int keep_total = 0;
     const int rank = block_excl_count(kept, wave_tot, keep_total) + keep_carry;
     keep_carry += keep_total;
+    if (valid && keep_rank != nullptr) keep_rank[p] = kept ? rank : -1;
     if (kept) {
       const int l = local[p];
       keep_abs[rank] = p;
@@ -567,8 +624,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(
 extern "C" int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flags,
                               const int32_t* local, int32_t n_tokens, const ckv_chunk_span* chunks,
                               int32_t n_chunks, int32_t has_threshold, double escalate_threshold,
-                              int64_t* keep_abs, int64_t* keep_local, float* rel_dev, uint8_t* escalated,
-                              int32_t* counts, void* stream) {
+                              int64_t* keep_abs, int64_t* keep_local, int32_t* keep_rank, float* rel_dev,
+                              uint8_t* escalated, int32_t* counts, void* stream) {
   using namespace ckv;
   if (diff == nullptr || norm == nullptr || pos_flags == nullptr || local == nullptr || keep_abs == nullptr ||
       keep_local == nullptr || counts == nullptr || n_tokens < 0 || n_chunks < 0)
@@ -584,7 +641,7 @@ extern "C" int32_t ckv_select(const float* diff, const float* norm, const uint8_
   if (kpt <= K) {                                                                                             \
     hipLaunchKernelGGL(select_reg_kernel<K>, dim3(1), dim3(kSelThreads), lds, st, diff, norm, pos_flags, local, \
                        (int)n_tokens, chunks, (int)n_chunks, (int)(has_threshold != 0), escalate_threshold,      \
-                       keep_abs, keep_local, rel_dev, escalated, counts);                                       \
+                       keep_abs, keep_local, keep_rank, rel_dev, escalated, counts);                            \
     CKV_RETURN_IF_LAUNCH_FAILED();                                                                            \
     return CKV_OK;                                                                                            \
   }
@@ -597,7 +654,7 @@ extern "C" int32_t ckv_select(const float* diff, const float* norm, const uint8_
 #undef CKV_SEL_REG
   hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, st, diff, norm, pos_flags, local, (int)n_tokens,
                      chunks, (int)n_chunks, (int)(has_threshold != 0), escalate_threshold, keep_abs, keep_local,
-                     rel_dev, escalated, counts);
+                     keep_rank, rel_dev, escalated, counts);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

@@ -8,12 +8,16 @@ The model's GEMMs, RMSNorm, MLP and SDPA attention stay on PyTorch-ROCm (chunkkv
 The KV repair runs on the HIP kernels:
 
   reference (torch_engine.py)                        here
-  base_kv every layer (:96-103; ~13 launches per     one ckv_rerope_gather launch for all layers
-    placement and layer, zero-filled caches)           and placements into one (L,1,H,N,D) slab
+  base_kv (:96-103; ~13 launches per placement and   layer != 1: one ckv_assemble_layer launch that
+    layer, zero-filled cache) + K[:, :, active] = k    writes every row once (fresh if active, else
+    (:155-156), every layer                            the re-rotated cached row)
+                                                     layer 1: ckv_assemble_layer with no active set
+                                                       (the base cache), then the selection below,
+                                                       then ckv_scatter_rows of the kept rows
   deviation (:117-124)                               ckv_deviation (one wavefront per token)
   rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
     one .item() per chunk)                             nothing back unless a threshold is set
-  K[:, :, active] = k (:155-156)                     ckv_scatter_rows per layer
+All layers' caches live in one (L, 1, H, N, D) slab; PrefillResult.keys/values are its views.
 
 Attention stays on PyTorch-ROCm SDPA. The reference calls it with enable_gqa and an explicit
 boolean (n_active x N) mask, a combination with no fused kernel on ROCm (it runs the fp32 math
@@ -168,27 +172,26 @@ class HipEngine(DecoderPieces):
         plan: RequestPlan = plan_request(N, placements, config.n_sink, config.recompute_ratio)
         select_layer = bool(placements) and config.full_first_layer and n_layers > 1
         active_np = plan.layer0_idx if config.full_first_layer else plan.fresh_idx
-        local_np = local_index(N, active_np) if select_layer else np.zeros(0, dtype=np.int32)
+        local_np = local_index(N, active_np)
 
         keepalive: list = []
         tab = np.zeros(0, dtype=np.uint64)
         if plan.chunks:
             tab = np.concatenate([self._chunk_pointers(c, keepalive).reshape(-1) for c in plan.chunks])
         flags_d, local_d, active_d, segs_d, spans_d, tab_d = self._upload(
-            [plan.flags, local_np, active_np.astype(np.int64), plan.segments.reshape(-1), plan.spans.reshape(-1), tab]
+            [plan.flags, local_np, active_np.astype(np.int64), plan.all_segments.reshape(-1), plan.spans.reshape(-1), tab]
         )
+        n_cached_segs, n_all_segs = len(plan.segments), len(plan.all_segments)
 
-        # Base caches of every layer: uncovered rows stay unwritten here because they are
-        # uncached positions, which are in the active set at every layer and get scattered.
+        # Every row of every layer is written by the assemble / gather + scatter below.
         k_slab = torch.empty((n_layers, 1, H, N, D), dtype=self.kv_dtype, device=dev)
         v_slab = torch.empty_like(k_slab)
         err = torch.zeros(1, dtype=torch.int32, device=dev)
-        if len(plan.segments):
-            ops.rerope_gather(k_slab, v_slab, tab_d, segs_d, len(plan.segments), plan.max_seg_tokens, self.theta, err)
         keys_out = list(k_slab.unbind(0))
         values_out = list(v_slab.unbind(0))
 
         active = active_d
+        local_cur = local_d  # local index map of the current active set
         h = self.inner.embed_tokens(torch.tensor([tokens], device=dev))[:, active]
         ar = torch.arange(N, device=dev)
         masks: dict = {}
@@ -196,7 +199,13 @@ class HipEngine(DecoderPieces):
         for li, layer in enumerate(self.layers):
             q, k, v = self._qkv(layer.self_attn, layer.input_layernorm(h), active)
             K, V = keys_out[li], values_out[li]
-            if li == 1 and select_layer:
+            if li != 1 or not select_layer:
+                ops.assemble_layer(K, V, tab_d, n_layers, li, segs_d, n_all_segs, plan.max_all_seg_tokens, k, v,
+                                   local_cur, self.theta, err)
+            else:
+                # base cache of layer 1 (cached rows re-rotated), compared with the fresh rows
+                ops.assemble_layer(K, V, tab_d, n_layers, li, segs_d, n_cached_segs, plan.max_seg_tokens, None, None,
+                                   None, self.theta, err)
                 diff, norm = ops.deviation(k, v, K, V, flags_d, local_d, err)
                 sel = ops.select(diff, norm, flags_d, local_d, spans_d, config.escalate_threshold)
                 if config.escalate_threshold is None and not plan.has_overlap:
@@ -212,7 +221,8 @@ class HipEngine(DecoderPieces):
                 rows = sel.keep_local[:n_keep]
                 h, q, k, v = h.index_select(1, rows), q.index_select(2, rows), k.index_select(2, rows), v.index_select(2, rows)
                 active = sel.keep_abs[:n_keep]
-            ops.scatter_rows(K, V, k, v, active, err)
+                local_cur = sel.keep_rank
+                ops.scatter_rows(K, V, k, v, active, err)
             h = self._attend_active(layer, h, q, K, V, active, ar, masks)
 
         n_want = N - logits_from

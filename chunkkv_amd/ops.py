@@ -168,6 +168,7 @@ def deviation(
 class Selection:
     keep_abs: torch.Tensor  # int64 (N,), first counts[KEEP] valid, ascending
     keep_local: torch.Tensor  # int64 (N,)
+    keep_rank: torch.Tensor  # int32 (N,): rank in keep_abs, -1 if not kept (local map of the new active set)
     rel_dev: torch.Tensor  # float32 (C,)
     escalated: torch.Tensor  # uint8 (C,)
     counts: torch.Tensor  # int32 (COUNT_N,)
@@ -195,6 +196,7 @@ def select(
         out = Selection(
             keep_abs=torch.empty(N, dtype=torch.int64, device=dev),
             keep_local=torch.empty(N, dtype=torch.int64, device=dev),
+            keep_rank=torch.empty(N, dtype=torch.int32, device=dev),
             rel_dev=torch.empty(C, dtype=torch.float32, device=dev),
             escalated=torch.empty(C, dtype=torch.uint8, device=dev),
             counts=torch.empty(_native.COUNT_N, dtype=torch.int32, device=dev),
@@ -204,11 +206,67 @@ def select(
         lib().ckv_select(
             _ptr(diff), _ptr(norm), _ptr(flags), _ptr(local), N, _ptr(spans), C, int(has_thr),
             float(escalate_threshold) if has_thr else 0.0, _ptr(out.keep_abs), _ptr(out.keep_local),
-            _ptr(out.rel_dev), _ptr(out.escalated), _ptr(out.counts), _stream(dev),
+            _ptr(out.keep_rank), _ptr(out.rel_dev), _ptr(out.escalated), _ptr(out.counts), _stream(dev),
         ),
         "ckv_select",
     )
     return out
+
+
+def assemble_layer(
+    K: torch.Tensor,
+    V: torch.Tensor,
+    src_tab: torch.Tensor,
+    n_layers: int,
+    layer: int,
+    segments: torch.Tensor,
+    n_segs: int,
+    max_seg_tokens: int,
+    k: torch.Tensor | None,
+    v: torch.Tensor | None,
+    local: torch.Tensor | None,
+    theta: float,
+    err: torch.Tensor | None = None,
+) -> None:
+    """One layer's cache with every row written once: fresh row where local[p] >= 0, else the
+    re-rotated cached row (the reference's base cache + scatter pair, torch_engine.py:96-103 and
+    :155-156). local=None gathers the cached segments only.
+
+    K/V: (1, H, N, D) contiguous. src_tab: the gather's int64 address table (chunk, layer, K/V).
+    segments: int32 descriptors, cached runs and (optionally) uncached runs with chunk = -1.
+    """
+    _dev(K, V, segments)
+    _, H, N, D = K.shape
+    if not (K.is_contiguous() and V.is_contiguous() and V.shape == K.shape):
+        raise ValueError("cache K/V must be contiguous (1, H, N, D)")
+    if src_tab.numel() % (2 * n_layers) or src_tab.dtype != torch.int64:
+        raise ValueError("src_tab must be int64 with 2 addresses per (chunk, layer)")
+    if segments.dtype != torch.int32 or segments.numel() < 6 * int(n_segs):
+        raise ValueError("segments must be int32 with 6 fields per segment")
+    n_chunks = src_tab.numel() // (2 * n_layers)
+    n_fresh = 0
+    kst = vst = (0, 0)
+    if local is not None:
+        _dev(K, local, k, v)
+        if local.dtype != torch.int32 or local.numel() != N or not local.is_contiguous():
+            raise ValueError("local must be int32 (N,) contiguous")
+        k, v = _rows_view(k), _rows_view(v)
+        if k.dtype != K.dtype or v.dtype != K.dtype:
+            raise TypeError("fresh rows and cache must share a dtype")
+        if k.dim() != 4 or k.shape[0] != 1 or k.shape[1] != H or k.shape[3] != D or v.shape != k.shape:
+            raise ValueError(f"fresh rows {tuple(k.shape)} do not match the cache {tuple(K.shape)}")
+        n_fresh = k.shape[2]
+        kst, vst = (k.stride(1), k.stride(2)), (v.stride(1), v.stride(2))
+    else:
+        k = v = None
+    check(
+        lib().ckv_assemble_layer(
+            _ptr(K), _ptr(V), N * D, _ptr(src_tab), n_chunks, n_layers, int(layer), _ptr(segments), int(n_segs),
+            int(max_seg_tokens), _ptr(k), kst[0], kst[1], _ptr(v), vst[0], vst[1], n_fresh, _ptr(local), N, H, D,
+            dtype_code(K.dtype), float(theta), _ptr(err), _stream(K.device),
+        ),
+        "ckv_assemble_layer",
+    )
 
 
 def scatter_rows(

@@ -36,8 +36,10 @@ class RequestPlan:
     flags: np.ndarray  # uint8 (N,) POS_* bits
     fresh_idx: np.ndarray  # int64, positions not covered by any placement
     layer0_idx: np.ndarray  # int64, positions not covered by an exact placement
-    segments: np.ndarray  # int32 (S, 6)
+    segments: np.ndarray  # int32 (S, 6): cached runs (what the gather reads)
     max_seg_tokens: int
+    all_segments: np.ndarray  # int32 (S + F, 6): the cached runs, then uncached runs (chunk = -1)
+    max_all_seg_tokens: int
     chunks: list  # unique ChunkKV objects, indexed by segments[:, 2]
     spans: np.ndarray  # int32 (C, 4) for the non-exact placements, in placement order
     n_cached: int
@@ -119,6 +121,20 @@ def plan_request(n_tokens: int, placements: list, n_sink: int, recompute_ratio: 
         ).astype(np.int32)
         max_seg = int((ends - starts).max())
 
+    # Uncached runs (chunk = -1): their rows always come from the fresh K/V.
+    fresh_segs = np.zeros((0, SEG_FIELDS), dtype=np.int32)
+    if (~covered).any():
+        un = ~covered
+        edge = np.diff(np.concatenate(([0], un.astype(np.int8), [0])))
+        f_starts = np.flatnonzero(edge == 1)
+        f_ends = np.flatnonzero(edge == -1)
+        fresh_segs = np.zeros((len(f_starts), SEG_FIELDS), dtype=np.int32)
+        fresh_segs[:, 0] = f_starts
+        fresh_segs[:, 1] = f_ends - f_starts
+        fresh_segs[:, 2] = -1
+    all_segments = np.concatenate([segments, fresh_segs]) if len(fresh_segs) else segments
+    max_all = int(all_segments[:, 1].max()) if len(all_segments) else 0
+
     total_len = int(lengths.sum()) if len(placements) else 0
     n_cached = int(cached.sum())
     plan = RequestPlan(
@@ -131,6 +147,8 @@ def plan_request(n_tokens: int, placements: list, n_sink: int, recompute_ratio: 
         layer0_idx=np.flatnonzero(~exact),
         segments=segments,
         max_seg_tokens=max_seg,
+        all_segments=all_segments,
+        max_all_seg_tokens=max_all,
         chunks=chunks,
         spans=np.asarray(spans, dtype=np.int32).reshape(-1, SPAN_FIELDS),
         n_cached=n_cached,

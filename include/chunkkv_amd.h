@@ -178,6 +178,8 @@ int32_t ckv_deviation(const void* k_fresh, int64_t kf_head_stride, int64_t kf_to
  *                  budget = min(sum of budget over pooled non-escalated chunks, #candidates)
  *   keep_abs[i]  = i-th kept position in ascending order, i < counts[CKV_COUNT_KEEP]
  *   keep_local[i]= local[keep_abs[i]] (0 where local is -1; counted in CKV_COUNT_UNCOMPUTED)
+ *   keep_rank[p] = i where keep_abs[i] == p, else -1, for every p < n_tokens (optional, may be
+ *                  NULL): the local index map of the new active set, as ckv_assemble_layer takes it
  *   counts       CKV_COUNT_N int32 values (indices CKV_COUNT_*).
  * keep_abs and keep_local must hold n_tokens entries. n_tokens <= CKV_SELECT_MAX_TOKENS.
  * Replaces: torch_engine.py:125-153 (rel/escalation/budget :128-142, argsort top-k :143-146,
@@ -186,8 +188,28 @@ int32_t ckv_deviation(const void* k_fresh, int64_t kf_head_stride, int64_t kf_to
 int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flags,
                    const int32_t* local, int32_t n_tokens, const ckv_chunk_span* chunks,
                    int32_t n_chunks, int32_t has_threshold, double escalate_threshold,
-                   int64_t* keep_abs, int64_t* keep_local, float* rel_dev, uint8_t* escalated,
-                   int32_t* counts, void* stream);
+                   int64_t* keep_abs, int64_t* keep_local, int32_t* keep_rank, float* rel_dev,
+                   uint8_t* escalated, int32_t* counts, void* stream);
+
+/*
+ * Assemble one layer's cache with every row written once: for each segment row at position p,
+ *   local[p] >= 0  -> K/V[h, p, :] = fresh k/v[h, local[p], :]            (an active position)
+ *   otherwise      -> K/V[h, p, :] = the chunk's row, keys re-rotated by delta (as the gather)
+ * This is the reference's per-layer pair "base cache, then scatter the active rows" in one pass
+ * (torch_engine.py:96-103 + :155-156). segs may include uncached runs with chunk == -1 (their
+ * positions must be active). local == NULL gathers only (fresh tensors unused; uncached runs
+ * skipped). src_tab is the gather's table (n_chunks x n_layers x 2); `layer` selects its column.
+ * k/v_fresh: (H, n_fresh, D) with the given strides; local: n_tokens entries.
+ * A row with an active index >= n_fresh, or an inactive position in an uncached run, is left
+ * unwritten and flagged. No counterpart in the reference as one call; see above.
+ */
+int32_t ckv_assemble_layer(void* dst_k, void* dst_v, int64_t dst_head_stride, const uint64_t* src_tab,
+                           int32_t n_chunks, int32_t n_layers, int32_t layer, const ckv_segment* segs,
+                           int32_t n_segs, int32_t max_seg_tokens, const void* k_fresh,
+                           int64_t kf_head_stride, int64_t kf_token_stride, const void* v_fresh,
+                           int64_t vf_head_stride, int64_t vf_token_stride, int32_t n_fresh,
+                           const int32_t* local, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
+                           int32_t dtype, double theta, int32_t* err, void* stream);
 
 /*
  * Scatter freshly computed K/V rows into one layer's cache:

@@ -184,7 +184,10 @@ def select(diff, norm, flags, local, spans: np.ndarray, escalate_threshold: floa
     )
     assert rc == 0
     n = int(counts[0])
-    return dict(keep_abs=keep_abs[:n], keep_local=keep_local[:n], rel_dev=rel[:C], escalated=esc[:C], counts=counts)
+    keep_rank = np.full(N, -1, dtype=np.int32)
+    keep_rank[keep_abs[:n]] = np.arange(n, dtype=np.int32)
+    return dict(keep_abs=keep_abs[:n], keep_local=keep_local[:n], keep_rank=keep_rank, rel_dev=rel[:C],
+                escalated=esc[:C], counts=counts)
 
 
 def scatter_rows(K: np.ndarray, V: np.ndarray, k: np.ndarray, v: np.ndarray, rows: np.ndarray) -> int:

@@ -56,8 +56,16 @@ def test_host_side_argument_validation_never_launches():
     assert lib.ckv_shift_keys(1, 10, 1, 10, 1, 1, 100, 1, 3, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_deviation(1, 1, 1, 1, 1, 1, 1, 1, 512, 1, 1, 4, 4, 4, 128, 5, 1, 1, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_deviation(1, 1, 1, 1, 1, 1, 1, 1, 10, 1, 1, 4, 4, 4, 128, 1, 1, 1, None, None) == _native.CKV_ERR_OUT_OF_RANGE
-    assert lib.ckv_select(1, 1, 1, 1, _native.SELECT_MAX_TOKENS + 1, 1, 1, 0, 0.0, 1, 1, 1, 1, 1, None) == _native.CKV_ERR_TOO_LARGE
-    assert lib.ckv_select(None, 1, 1, 1, 10, 1, 1, 0, 0.0, 1, 1, 1, 1, 1, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_select(1, 1, 1, 1, _native.SELECT_MAX_TOKENS + 1, 1, 1, 0, 0.0, 1, 1, None, 1, 1, 1, None) == _native.CKV_ERR_TOO_LARGE
+    assert lib.ckv_select(None, 1, 1, 1, 10, 1, 1, 0, 0.0, 1, 1, None, 1, 1, 1, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    # assemble: bad dtype, layer outside [0, n_layers), short head stride, fresh rows missing
+    asm = lambda *a: lib.ckv_assemble_layer(*a)  # noqa: E731
+    base = [1, 1, 1024, 1, 1, 2, 0, 1, 1, 8, 1, 128, 128, 1, 128, 128, 8, 1, 8, 1, 128, 1, 1e6, None, None]
+    assert asm(*base[:21], 9, *base[22:]) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert asm(*base[:6], 2, *base[7:]) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert asm(*base[:2], 10, *base[3:]) == _native.CKV_ERR_OUT_OF_RANGE
+    assert asm(*base[:10], None, *base[11:]) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert asm(*base[:7], 1, 0, *base[9:]) == _native.CKV_OK  # no segments: nothing to do
     assert lib.ckv_scatter_rows(1, 1, 10, 1, 1, 1, 1, 1, 1, 1, 4, 10, 4, 128, 1, None, None) == _native.CKV_ERR_OUT_OF_RANGE
     assert lib.ckv_scatter_rows(1, 1, 10, 1, 1, 1, 1, 1, 1, 1, 4, 10, 4, 100, 1, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
     # zero-sized work is a no-op success

@@ -239,6 +239,7 @@ def _check_select(diff, norm, flags, local, spans, thr):
     C = len(spans)
     np.testing.assert_array_equal(host(got.rel_dev)[:C].view(np.uint32), want["rel_dev"].view(np.uint32))
     np.testing.assert_array_equal(host(got.escalated)[:C], want["escalated"])
+    np.testing.assert_array_equal(host(got.keep_rank), want["keep_rank"])
     return want
 
 
@@ -318,3 +319,100 @@ def test_scatter_flags_out_of_range_row():
     torch.cuda.synchronize()
     assert int(err.item()) == _native.DEVICE_ERR_RANGE
     assert K[0, :, 3].eq(1).all() and int(K.count_nonzero()) == H * D
+
+
+def _assemble_case(seed, bf16, D, overlap, active_frac, layer=1):
+    """Oracle gather of every layer + oracle scatter of the active rows of `layer` (the
+    reference's base cache + overwrite pair) against one assemble launch."""
+    rng = np.random.default_rng(seed)
+    n_layers, H = 3, 2
+    lens = [40, 70, 33, 64, 1, 97]
+    N = sum(lens) + 40
+    plan, ks, vs = _gather_case(rng, bf16, n_layers, H, D, lens, N, overlap)
+    Kg, Vg, Ko, Vo, src = _run_gather(plan, ks, vs, n_layers, H, D, N, bf16)
+    # active: every uncached position plus a random share of the cached ones
+    act = ~plan.cached | (rng.random(N) < active_frac)
+    active = np.flatnonzero(act).astype(np.int64)
+    n = len(active)
+    k = rand_elems(rng, (H, n, D), bf16)
+    v = rand_elems(rng, (H, n, D), bf16)
+    Kw, Vw = Ko[layer].copy(), Vo[layer].copy()
+    assert O.scatter_rows(Kw, Vw, k, v, active) == 0
+    local = np.full(N, -1, dtype=np.int32)
+    local[active] = np.arange(n, dtype=np.int32)
+    return plan, src, k, v, local, Kw, Vw, n_layers, H, N
+
+
+def _assemble_run(plan, src, k, v, local, n_layers, H, N, D, bf16, layer, segs=None, fill=-7.0):
+    dt = torch.bfloat16 if bf16 else torch.float32
+    tab = np.zeros((len(plan.chunks), n_layers, 2), dtype=np.uint64)
+    for ci, ch in enumerate(plan.chunks):
+        kl, vl = src[ch.idx]
+        for l in range(n_layers):
+            tab[ci, l, 0] = kl[l].data_ptr()
+            tab[ci, l, 1] = vl[l].data_ptr()
+    segs = plan.all_segments if segs is None else segs
+    K = torch.full((1, H, N, D), fill, dtype=dt, device=DEV)
+    V = torch.full_like(K, fill)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    vt = None if v is None else dev(np.ascontiguousarray(v.transpose(1, 0, 2)))[None].transpose(1, 2)
+    ops.assemble_layer(K, V, torch.from_numpy(tab.view(np.int64)).to(DEV), n_layers, layer,
+                       dev(segs.reshape(-1)), len(segs), int(segs[:, 1].max()) if len(segs) else 0,
+                       None if k is None else dev(k)[None], vt, None if local is None else dev(local), THETA, err)
+    torch.cuda.synchronize()
+    return host(K)[0], host(V)[0], int(err.item())
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("overlap", [False, True])
+@pytest.mark.parametrize("active_frac", [0.0, 0.3, 1.0])
+def test_assemble_matches_gather_then_scatter(bf16, D, overlap, active_frac):
+    layer = 1
+    plan, src, k, v, local, Kw, Vw, n_layers, H, N = _assemble_case(
+        500 + D + 2 * bf16 + overlap + int(active_frac * 10), bf16, D, overlap, active_frac, layer)
+    Kg, Vg, e = _assemble_run(plan, src, k, v, local, n_layers, H, N, D, bf16, layer)
+    assert e == 0
+    np.testing.assert_array_equal(Vg, Vw)
+    assert_keys_close(Kg, Kw, bf16)  # bit-exact: same arithmetic as the gather
+
+
+@pytest.mark.parametrize("layer", [0, 2])
+def test_assemble_gather_only_matches_gather(layer):
+    """local = NULL: the cached segments only, as the gather of that layer; other rows untouched."""
+    bf16, D = True, 128
+    rng = np.random.default_rng(77 + layer)
+    n_layers, H = 3, 2
+    lens = [40, 70, 33, 64, 1, 97]
+    N = sum(lens) + 40
+    plan, ks, vs = _gather_case(rng, bf16, n_layers, H, D, lens, N, False)
+    _, _, Ko, Vo, src = _run_gather(plan, ks, vs, n_layers, H, D, N, bf16)
+    Kg, Vg, e = _assemble_run(plan, src, None, None, None, n_layers, H, N, D, bf16, layer, segs=plan.segments)
+    assert e == 0
+    np.testing.assert_array_equal(Vg, Vo[layer])
+    np.testing.assert_array_equal(Kg, Ko[layer])  # sentinel rows outside cached runs too
+
+
+def test_assemble_flags_uncached_inactive_row():
+    """An uncached position with no active row has no source: flagged, its row left as it was."""
+    bf16, D = True, 64
+    plan, src, k, v, local, Kw, Vw, n_layers, H, N = _assemble_case(9, bf16, D, False, 0.2)
+    p = int(np.flatnonzero(~plan.cached)[0])
+    local = local.copy()
+    local[p] = -1
+    Kg, Vg, e = _assemble_run(plan, src, k, v, local, n_layers, H, N, D, bf16, 1)
+    assert e == _native.DEVICE_ERR_RANGE
+    sent = O.f32_to_bf16_bits(np.float32([-7.0]))[0]
+    assert (Kg[:, p] == sent).all() and (Vg[:, p] == sent).all()
+    others = np.ones(N, dtype=bool)
+    others[p] = False
+    np.testing.assert_array_equal(Vg[:, others], Vw[:, others])
+
+
+def test_assemble_flags_bad_segment():
+    bf16, D = True, 64
+    plan, src, k, v, local, Kw, Vw, n_layers, H, N = _assemble_case(11, bf16, D, False, 0.2)
+    segs = plan.all_segments.copy()
+    segs[0, 2] = len(plan.chunks)  # chunk index past the table
+    _, _, e = _assemble_run(plan, src, k, v, local, n_layers, H, N, D, bf16, 1, segs=segs)
+    assert e == _native.DEVICE_ERR_RANGE
