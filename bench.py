@@ -8,23 +8,27 @@ shuffled positions (each chunk computed at its own original offset, so every pla
 its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
 
 A step is one request's whole KV repair with every input already resident in HBM, issued as
-HipEngine issues it: one assemble launch per layer writes every cache row once (fresh if the
-position is active, else the re-rotated cached row); layer 1 instead builds its base cache,
-runs the deviation and selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows) and
-scatters the kept rows. The unit of work is one request's KV repair as the reference's op
-sequence moves it (re-RoPE + gather of every cached row of all 28 layers, the layer-0 scatter of
-all 8256 rows, the deviation, the scatters of layers 1-27):
+HipEngine issues it (31 launches): layer 0 in one assemble launch (every cache row written once,
+fresh if the position is active, else the re-rotated cached row); layer 1 as the base cache, the
+deviation and the selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows) and the
+scatter of the kept rows; then, forked onto a second stream, one gather launch for the cached
+rows of the 5280 dropped positions of layers 2-27, while the first stream scatters the kept rows
+of layers 2-27 (disjoint rows; the streams join at the end of the step). The unit of work is one
+request's KV repair as the reference's op sequence moves it (re-RoPE + gather of every cached
+row of all 28 layers, the layer-0 scatter of all 8256 rows, the deviation, the scatters of layers
+1-27):
     gather          28 x 24 x 320 x 4 heads x 128 x 2 B x 2 (K,V) x 2 (r+w) =   880,803,840
     deviation       8256 x (4 rows x 1 KiB) + 8256 x 8 B                       =    33,882,624
     scatter L0      8256 x 4096 B                                              =    33,816,576
     scatter L1-27   27 x 2976 x 4096 B                                         =   329,121,792
     total                                                                      = 1,277,624,832
-`value` = that total / measured time per step (GB/s), the step's 31 launches replayed from a
-HIP graph (the eager time, launch-bound from Python, is reported as ms_per_step_eager); the
-fused flow itself moves 990,577,152 B per step (moved_bytes_per_step, moved_gbs). `roofline` is
-the dominant kernel (assemble, 27 of the 31 launches, 33,816,576 B each) timed live with HIP
-events around a burst of back-to-back launches on the launch stream. Inputs rotate between two
-independent copies so consecutive steps do not hit in the 256 MB MALL.
+`value` = that total / measured time per step (GB/s), the step replayed from a HIP graph (the
+eager time, launch-bound from Python, is reported as ms_per_step_eager, and the same rows built
+on one stream with an assemble launch per layer as ms_per_step_one_stream); the fused flow
+itself moves 990,577,152 B per step (moved_bytes_per_step, moved_gbs). `roofline` is the
+dominant kernel (the gather of the dropped rows of layers 2-27, 562,298,880 B per launch) timed
+live with HIP events around a burst of back-to-back launches on the launch stream. Inputs rotate
+between two independent copies so consecutive steps do not hit in the 256 MB MALL.
 
 Besides the bandwidth line, the run measures blend-prefill TTFT p50 (prefill + last_logprobs,
 the bracket of the reference's bench/replay.py:32-35) over seeded requests of the same shape on
@@ -61,8 +65,8 @@ GATHER_BYTES = N_LAYERS * N_CHUNKS * CHUNK_LEN * ROW_BYTES * 2 * 2
 # (profiles/traffic_rerope_gather_qwen25_7b_8k.md; FETCH_SIZE calibrated against a kernel of
 # known traffic). Counters cannot be read inside a timed run, so the measured value is recorded.
 GATHER_TRAFFIC_BYTES = 881_167_672
-# Same for one assemble launch (layer >= 2 of the 8k request); None until measured.
-ASSEMBLE_TRAFFIC_BYTES = None
+# Same for one gather of the dropped rows of layers 2-27 of the 8k request; None until measured.
+DROPPED_TRAFFIC_BYTES = None
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 
@@ -165,6 +169,7 @@ class RepairWorkload:
             v = v.to(torch.bfloat16).transpose(1, 2).contiguous().to(dev).transpose(1, 2)
             self.fresh.append((k, v))
         self.sel = None
+        self.side = torch.cuda.Stream(device=dev)  # default priority
 
     def gather(self):
         from chunkkv_amd import ops
@@ -196,9 +201,38 @@ class RepairWorkload:
         ops.assemble_layer(self.k_slab[li], self.v_slab[li], self.tab, N_LAYERS, li, self.segs_all,
                            len(plan.all_segments), plan.max_all_seg_tokens, *self.fresh[li], local, THETA, self.err)
 
+    def gather_dropped(self):
+        """Layers 2..27 in one launch: the cached rows of every position the selection dropped."""
+        from chunkkv_amd import ops
+
+        ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(self.plan.segments),
+                          self.plan.max_seg_tokens, THETA, self.err, layers=(2, N_LAYERS), skip=self.sel.keep_rank)
+
     def step(self):
-        """One request's KV repair exactly as HipEngine issues it: assemble L0; base cache of L1,
-        deviation, selection, scatter of the kept rows of L1; assemble L2..L27 (31 launches)."""
+        """One request's KV repair exactly as HipEngine issues it (31 launches): assemble L0; base
+        cache of L1, deviation, selection, scatter of the kept rows of L1; then, forked onto a side
+        stream, one gather of the dropped cached rows of L2..L27, while the main stream scatters
+        the kept (fresh) rows of L2..L27; the two write disjoint rows and join at the end."""
+        from chunkkv_amd import ops
+
+        self._head()
+        main = torch.cuda.current_stream()
+        self.side.wait_stream(main)
+        with torch.cuda.stream(self.side):
+            self.gather_dropped()
+        K, V = self.k_slab.unbind(0), self.v_slab.unbind(0)
+        rows = self.sel.keep_abs[: self.plan.n_keep]
+        for li in range(2, N_LAYERS):
+            ops.scatter_rows(K[li], V[li], *self.fresh[li], rows, self.err)
+        main.wait_stream(self.side)
+
+    def step_serial(self):
+        """The same rows on one stream: assemble L0; layer 1 as in step(); assemble L2..L27."""
+        self._head()
+        for li in range(2, N_LAYERS):
+            self.assemble(li)
+
+    def _head(self):
         from chunkkv_amd import ops
 
         plan = self.plan
@@ -211,8 +245,6 @@ class RepairWorkload:
         self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
         ops.scatter_rows(K[1], V[1], k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep], self.sel.keep_abs[: plan.n_keep],
                          self.err)
-        for li in range(2, N_LAYERS):
-            self.assemble(li)
 
 
 def repair_bytes(n_keep: int) -> int:
@@ -247,28 +279,43 @@ def _graph_of(fn):
 
 
 def bench_repair(steps: int, warmup: int, dev) -> dict:
-    """Time the KV-repair step as HipEngine issues it (31 launches, captured once per input set in
-    a HIP graph and replayed; the eager time, launch-bound from Python, is reported too), and the
-    dominant kernel's average duration from a burst of back-to-back assemble launches."""
+    """Time the KV-repair step as HipEngine issues it (31 launches on two streams, captured once
+    per input set in a HIP graph and replayed; the eager time, launch-bound from Python, and the
+    one-stream variant are reported too), and the dominant kernel (the gather of the dropped rows
+    of layers 2..27) from a burst of back-to-back launches."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
     for i in range(max(warmup, 2)):
         wls[i % 2].step()
+        wls[i % 2].step_serial()
     torch.cuda.synchronize()
     graphs = [_graph_of(w.step) for w in wls]
+    serial = [_graph_of(w.step_serial) for w in wls]
     stream = torch.cuda.current_stream(dev)
-    for g in graphs:
+    for g in graphs + serial:
         g.replay()
     ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
+    ms_serial = _timed(lambda i: serial[i % 2].replay(), steps, stream)
     ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
+    gd_ms = _timed(lambda i: wls[i % 2].gather_dropped(), steps, stream)
     n_asm = N_LAYERS - 2
     asm_ms = _timed(lambda i: wls[(i // n_asm) % 2].assemble(2 + i % n_asm), steps * n_asm, stream)
     assert all(int(w.err.item()) == 0 for w in wls)
-    n_keep = wls[0].plan.n_keep
+    plan = wls[0].plan
+    n_keep = plan.n_keep
     assert int(wls[0].sel.counts[0].item()) == n_keep
     nbytes = repair_bytes(n_keep)
-    return dict(ms_per_step=ms, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(wls[0].plan),
-                gbs=nbytes / (ms * 1e-3) / 1e9, asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9,
-                n_keep=n_keep)
+    gd_bytes = dropped_bytes(plan)
+    return dict(ms_per_step=ms, ms_serial=ms_serial, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(plan),
+                gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
+                asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep)
+
+
+def dropped_bytes(plan) -> int:
+    """Algorithmic bytes of the gather of the dropped rows of layers 2..27: every cached row whose
+    position the selection did not keep, K and V, read + write."""
+    n_uncached = plan.n_tokens - int(plan.cached.sum())
+    n_dropped = int(plan.cached.sum()) - (plan.n_keep - n_uncached)
+    return (N_LAYERS - 2) * n_dropped * ROW_BYTES * 4
 
 
 def moved_bytes(plan) -> int:
@@ -592,9 +639,10 @@ def traffic_probe(steps: int, warmup: int, dev) -> dict:
     for i in range(steps):
         wls[i % 2].gather()
     for w in wls:
-        w.step()  # selection output for the assemble launches below
+        w.step()  # selection output for the launches below
+    torch.cuda.synchronize()
     for i in range(steps):
-        wls[i % 2].assemble(2 + i % (N_LAYERS - 2))
+        wls[i % 2].gather_dropped()
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = [torch.empty_like(src) for _ in range(2)]
     for i in range(steps):  # one elementwise kernel: reads and writes exactly COPY_BYTES
@@ -639,7 +687,8 @@ def main() -> None:
         return
 
     r = bench_repair(args.steps, args.warmup, dev)
-    log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_eager']:.3f} ms eager); "
+    log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_serial']:.3f} ms one "
+        f"stream, {r['ms_eager']:.3f} ms eager); dropped-row gather {r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
         f"assemble {r['asm_gbs']:.1f} GB/s ({r['asm_ms'] * 1e3:.2f} us)")
     ttft = bench_ttft(args.ttft_requests, dev) if args.ttft_requests > 0 else None
     cpu = bench_cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None
@@ -671,18 +720,21 @@ def main() -> None:
         },
         "pct_of_peak": round(100.0 * r["gbs"] / PEAK_GBS, 2),
         "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
+        "ms_per_step_one_stream": round(r["ms_serial"], 4),
         "roofline": {
-            "kernel": "assemble_kernel<bf16,128>",
+            "kernel": "rerope_gather_kernel<bf16,128> (layers 2-27, dropped rows)",
             "bound": "hbm",
-            "achieved": round(r["asm_gbs"], 1),
+            "achieved": round(r["gd_gbs"], 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(r["asm_gbs"] / PEAK_GBS, 4),
-            "traffic": ASSEMBLE_TRAFFIC_BYTES,
-            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_assemble_qwen25_7b_8k.md",
-            "bytes_per_launch": ASSEMBLE_BYTES,
-            "avg_launch_us": round(r["asm_ms"] * 1e3, 2),
+            "frac": round(r["gd_gbs"] / PEAK_GBS, 4),
+            "traffic": DROPPED_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_rerope_gather_qwen25_7b_8k.md",
+            "bytes_per_launch": r["gd_bytes"],
+            "avg_launch_us": round(r["gd_ms"] * 1e3, 2),
         },
+        "assemble_kernel": {"bytes_per_launch": ASSEMBLE_BYTES, "avg_launch_us": round(r["asm_ms"] * 1e3, 2),
+                            "achieved_gbs": round(r["asm_gbs"], 1)},
         "cpu_baseline": cpu,
     }
     if ttft is not None:

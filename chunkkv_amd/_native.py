@@ -50,6 +50,10 @@ SIGNATURES = {
         _i32,
         [_p, _p, _i64, _i64, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p],
     ),
+    "ckv_rerope_gather_layers": (
+        _i32,
+        [_p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p, _i32, _i32, _p, _i32, _i32, _i32, _i32, _f64, _p, _p],
+    ),
     "ckv_shift_keys": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f64, _p]),
     "ckv_deviation": (
         _i32,

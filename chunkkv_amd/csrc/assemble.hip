@@ -18,9 +18,18 @@
 
 namespace ckv {
 
-constexpr int kAsmThreads = 256;
-constexpr int kAsmTile = 16;
-constexpr int kAsmUnroll = 4;
+#ifndef CKV_ASM_THREADS
+#define CKV_ASM_THREADS 256
+#endif
+#ifndef CKV_ASM_TILE
+#define CKV_ASM_TILE 16
+#endif
+#ifndef CKV_ASM_UNROLL
+#define CKV_ASM_UNROLL 2
+#endif
+constexpr int kAsmThreads = CKV_ASM_THREADS;
+constexpr int kAsmTile = CKV_ASM_TILE;  // tokens per workgroup
+constexpr int kAsmUnroll = CKV_ASM_UNROLL;  // rows in flight per thread
 
 enum : int { kRowSkip = 0, kRowFresh = 1, kRowCached = 2 };
 

@@ -1,5 +1,8 @@
 // Re-RoPE + gather: rebuild every layer's base K/V cache from cached chunks moved to new
-// offsets, in one launch for all layers and placements.
+// offsets, in one launch for all layers (or a range of layers) and placements. An optional skip
+// map leaves the rows of active positions alone, for callers that write those rows from the
+// fresh K/V themselves (the overwrite of torch_engine.py:155-156 makes the gathered copy of such
+// a row dead).
 //
 // Reference semantics (src/chunkkv/engine/torch_engine.py):
 //   inv_freq           :33   base ** (-arange(0, D, 2) / D)            (fp32)
@@ -58,8 +61,8 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
     char* __restrict__ dst_k, char* __restrict__ dst_v, int64_t dst_layer_stride_b,
     int64_t dst_head_stride_b, const uint64_t* __restrict__ src_tab, int n_chunks,
     const ckv_segment* __restrict__ segs, ckv_segment one_seg, uint64_t one_src_k,
-    uint64_t one_src_v, int64_t one_src_head_stride_b, int n_layers, int n_heads,
-    int n_tokens, double theta, int32_t* __restrict__ err) {
+    uint64_t one_src_v, int64_t one_src_head_stride_b, int n_layers, int layer_begin, int n_heads,
+    int n_tokens, const int32_t* __restrict__ skip, double theta, int32_t* __restrict__ err) {
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
   constexpr int HALF = D / 2;
@@ -78,7 +81,7 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
     gi32* f = (gi32*)(segs + blockIdx.x);
     s = ckv_segment{f[0], f[1], f[2], f[3], f[4], f[5]};
   }
-  const int layer = blockIdx.z;
+  const int layer = layer_begin + (int)blockIdx.z;
   const int t0 = blockIdx.y * kGatherTile;
   if (t0 >= s.n_tokens) return;  // uniform: tile past this segment's end
   if (s.dst_start < 0 || s.src_start < 0 || s.chunk < 0 || s.chunk >= n_chunks ||
@@ -116,8 +119,14 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
                      : nullptr;
 
   vec16 kx1[kGatherUnroll], kx2[kGatherUnroll], vx1[kGatherUnroll], vx2[kGatherUnroll];
+  bool live[kGatherUnroll];
 
-  auto row_ok = [&](int r) { return r < rows && (r % kGatherTile) < ntok; };
+  // A row is gathered unless its token lies past the segment or skip marks it (skip[p] >= 0:
+  // an active position whose row the fresh K/V provides).
+  auto row_ok = [&](int r) {
+    if (r >= rows || (r % kGatherTile) >= ntok) return false;
+    return skip == nullptr || skip[s.dst_start + t0 + (r % kGatherTile)] < 0;
+  };
   auto src_off = [&](int r) { return (int64_t)(r / kGatherTile) * src_head_b + (int64_t)(r % kGatherTile) * ROW_B; };
   auto dst_off = [&](int r) { return (int64_t)(r / kGatherTile) * dst_head_stride_b + (int64_t)(r % kGatherTile) * ROW_B; };
 
@@ -125,7 +134,8 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
 #pragma unroll
     for (int u = 0; u < kGatherUnroll; ++u) {
       const int r = r0 + u * RPP + rl;
-      if (row_ok(r)) {
+      live[u] = row_ok(r);
+      if (live[u]) {
         const int64_t o = src_off(r);
         kx1[u] = gather_ld(sk0 + o);
         kx2[u] = gather_ld(sk0 + o + HALF_B);
@@ -157,7 +167,7 @@ __global__ __launch_bounds__(kGatherThreads) void rerope_gather_kernel(
 #pragma unroll
     for (int u = 0; u < kGatherUnroll; ++u) {
       const int r = r0 + u * RPP + rl;
-      if (row_ok(r)) {
+      if (live[u]) {
         const int64_t o = dst_off(r);
         if (rotate) {
           vec16 y1, y2;
@@ -189,17 +199,18 @@ __global__ void inv_freq_kernel(float* out, int head_dim, double theta) {
 template <int DTYPE, int D>
 static void launch_gather(char* dk, char* dv, int64_t ls_b, int64_t hs_b, const uint64_t* tab,
                           int n_chunks, const ckv_segment* segs, ckv_segment one, uint64_t one_k, uint64_t one_v,
-                          int64_t one_hs_b, int n_segs, int max_tiles, int n_layers, int n_heads,
-                          int n_tokens, double theta, int32_t* err, hipStream_t st) {
-  dim3 grid((unsigned)n_segs, (unsigned)max_tiles, (unsigned)n_layers);
+                          int64_t one_hs_b, int n_segs, int max_tiles, int n_layers, int layer_begin,
+                          int layer_count, int n_heads, int n_tokens, const int32_t* skip, double theta,
+                          int32_t* err, hipStream_t st) {
+  dim3 grid((unsigned)n_segs, (unsigned)max_tiles, (unsigned)layer_count);
   hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D>), grid, dim3(kGatherThreads), 0, st, dk, dv,
-                     ls_b, hs_b, tab, n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, n_heads,
-                     n_tokens, theta, err);
+                     ls_b, hs_b, tab, n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, layer_begin,
+                     n_heads, n_tokens, skip, theta, err);
 }
 
 using GatherFn = void (*)(char*, char*, int64_t, int64_t, const uint64_t*, int, const ckv_segment*,
-                          ckv_segment, uint64_t, uint64_t, int64_t, int, int, int, int, int,
-                          double, int32_t*, hipStream_t);
+                          ckv_segment, uint64_t, uint64_t, int64_t, int, int, int, int, int, int, int,
+                          const int32_t*, double, int32_t*, hipStream_t);
 
 static GatherFn pick_gather(int dtype, int head_dim) {
 #define CKV_CASE(DT, HD) \
@@ -227,28 +238,42 @@ extern "C" int32_t ckv_inv_freq(float* out, int32_t head_dim, double theta, void
   return CKV_OK;
 }
 
+extern "C" int32_t ckv_rerope_gather_layers(void* dst_k, void* dst_v, int64_t dst_layer_stride,
+                                            int64_t dst_head_stride, const uint64_t* src_tab,
+                                            int32_t n_chunks, int32_t n_layers, int32_t layer_begin,
+                                            int32_t layer_end, const ckv_segment* segs, int32_t n_segs,
+                                            int32_t max_seg_tokens, const int32_t* skip, int32_t n_heads,
+                                            int32_t n_tokens, int32_t head_dim, int32_t dtype, double theta,
+                                            int32_t* err, void* stream) {
+  using namespace ckv;
+  GatherFn fn = pick_gather(dtype, head_dim);
+  if (fn == nullptr || dst_k == nullptr || dst_v == nullptr || src_tab == nullptr || segs == nullptr)
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_chunks < 0 || n_segs < 0 || max_seg_tokens < 0 || n_layers <= 0 || n_heads <= 0 || n_tokens < 0 ||
+      !(theta > 0.0) || layer_begin < 0 || layer_end < layer_begin || layer_end > n_layers)
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (dst_head_stride < (int64_t)n_tokens * head_dim || dst_layer_stride < dst_head_stride * n_heads)
+    return CKV_ERR_OUT_OF_RANGE;
+  if (n_segs == 0 || max_seg_tokens == 0 || layer_end == layer_begin) return CKV_OK;
+  const int max_tiles = (max_seg_tokens + kGatherTile - 1) / kGatherTile;
+  if (n_segs > 0x7fffffff / 2 || max_tiles > 65535 || layer_end - layer_begin > 65535) return CKV_ERR_TOO_LARGE;
+  const int64_t eb = elem_bytes(dtype);
+  fn((char*)dst_k, (char*)dst_v, dst_layer_stride * eb, dst_head_stride * eb, src_tab, n_chunks, segs, ckv_segment{},
+     0, 0, 0, n_segs, max_tiles, n_layers, layer_begin, layer_end - layer_begin, n_heads, n_tokens, skip, theta, err,
+     (hipStream_t)stream);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}
+
 extern "C" int32_t ckv_rerope_gather(void* dst_k, void* dst_v, int64_t dst_layer_stride,
                                      int64_t dst_head_stride, const uint64_t* src_tab,
                                      int32_t n_chunks, const ckv_segment* segs, int32_t n_segs,
                                      int32_t max_seg_tokens, int32_t n_layers, int32_t n_heads,
                                      int32_t n_tokens, int32_t head_dim, int32_t dtype,
                                      double theta, int32_t* err, void* stream) {
-  using namespace ckv;
-  GatherFn fn = pick_gather(dtype, head_dim);
-  if (fn == nullptr || dst_k == nullptr || dst_v == nullptr || src_tab == nullptr || segs == nullptr)
-    return CKV_ERR_INVALID_ARGUMENT;
-  if (n_chunks < 0 || n_segs < 0 || max_seg_tokens < 0 || n_layers <= 0 || n_heads <= 0 || n_tokens < 0 || !(theta > 0.0))
-    return CKV_ERR_INVALID_ARGUMENT;
-  if (dst_head_stride < (int64_t)n_tokens * head_dim || dst_layer_stride < dst_head_stride * n_heads)
-    return CKV_ERR_OUT_OF_RANGE;
-  if (n_segs == 0 || max_seg_tokens == 0) return CKV_OK;
-  const int max_tiles = (max_seg_tokens + kGatherTile - 1) / kGatherTile;
-  if (n_segs > 0x7fffffff / 2 || max_tiles > 65535 || n_layers > 65535) return CKV_ERR_TOO_LARGE;
-  const int64_t eb = elem_bytes(dtype);
-  fn((char*)dst_k, (char*)dst_v, dst_layer_stride * eb, dst_head_stride * eb, src_tab, n_chunks, segs, ckv_segment{},
-     0, 0, 0, n_segs, max_tiles, n_layers, n_heads, n_tokens, theta, err, (hipStream_t)stream);
-  CKV_RETURN_IF_LAUNCH_FAILED();
-  return CKV_OK;
+  return ckv_rerope_gather_layers(dst_k, dst_v, dst_layer_stride, dst_head_stride, src_tab, n_chunks, n_layers, 0,
+                                  n_layers, segs, n_segs, max_seg_tokens, nullptr, n_heads, n_tokens, head_dim, dtype,
+                                  theta, err, stream);
 }
 
 extern "C" int32_t ckv_shift_keys(void* dst, int64_t dst_head_stride, const void* src,
@@ -267,7 +292,7 @@ extern "C" int32_t ckv_shift_keys(void* dst, int64_t dst_head_stride, const void
   const int64_t eb = elem_bytes(dtype);
   ckv_segment one{0, n_rows, 0, 0, n_rows, delta};
   fn((char*)dst, nullptr, 0, dst_head_stride * eb, nullptr, 1, nullptr, one, (uint64_t)(uintptr_t)src, 0,
-     src_head_stride * eb, 1, max_tiles, 1, n_heads, n_rows, theta, nullptr, (hipStream_t)stream);
+     src_head_stride * eb, 1, max_tiles, 1, 0, 1, n_heads, n_rows, nullptr, theta, nullptr, (hipStream_t)stream);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

@@ -8,12 +8,20 @@ The model's GEMMs, RMSNorm, MLP and SDPA attention stay on PyTorch-ROCm (chunkkv
 The KV repair runs on the HIP kernels:
 
   reference (torch_engine.py)                        here
-  base_kv (:96-103; ~13 launches per placement and   layer != 1: one ckv_assemble_layer launch that
+  base_kv (:96-103; ~13 launches per placement and   layer 0: one ckv_assemble_layer launch that
     layer, zero-filled cache) + K[:, :, active] = k    writes every row once (fresh if active, else
     (:155-156), every layer                            the re-rotated cached row)
                                                      layer 1: ckv_assemble_layer with no active set
                                                        (the base cache), then the selection below,
                                                        then ckv_scatter_rows of the kept rows
+                                                     layers 2..L-1: right after the selection, one
+                                                       ckv_rerope_gather_layers launch on a side
+                                                       stream writes the cached rows of every
+                                                       position the selection dropped, for all of
+                                                       them at once, while the main stream computes
+                                                       and scatters each layer's fresh rows (the
+                                                       two write disjoint rows); layer 2's attention
+                                                       waits for the side stream
   deviation (:117-124)                               ckv_deviation (one wavefront per token)
   rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
     one .item() per chunk)                             nothing back unless a threshold is set
@@ -57,10 +65,14 @@ _TORCH_OF = {
 
 
 class HipEngine(DecoderPieces):
-    def __init__(self, model, tokenizer, attention: str = "fused"):
+    def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = True):
         if attention not in ("fused", "reference"):
             raise ValueError("attention must be 'fused' or 'reference'")
         self.attention = attention
+        # overlap=False builds layers 2..L-1 with one ckv_assemble_layer launch each on the main
+        # stream instead of the side-stream gather + per-layer scatters (same bytes, same rows).
+        self.overlap = overlap
+        self._side: torch.cuda.Stream | None = None
         # Set to a dict to record the layer-1 selection inputs/outputs (device tensors) of the
         # next prefill, for parity checks; None (default) records nothing.
         self.trace: dict | None = None
@@ -158,6 +170,23 @@ class HipEngine(DecoderPieces):
             for a, o in zip(parts, offs)
         ]
 
+    def _gather_dropped(self, k_slab, v_slab, tab_d, segs_d, n_segs, max_seg, keep_rank, err) -> torch.cuda.Event:
+        """Layers 2..L-1: cached rows of the positions the selection dropped, one launch on the
+        side stream, ordered after the selection. Returns the event that marks its end."""
+        main = torch.cuda.current_stream(self.device)
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=self.device)  # default priority
+        side = self._side
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            ops.rerope_gather(k_slab, v_slab, tab_d, segs_d, n_segs, max_seg, self.theta, err,
+                              layers=(2, k_slab.shape[0]), skip=keep_rank)
+            done = torch.cuda.Event()
+            done.record(side)
+        for t in (k_slab, v_slab, tab_d, segs_d, keep_rank, err):
+            t.record_stream(side)  # allocated on the main stream, read or written on the side stream
+        return done
+
     # -- main entry -----------------------------------------------------------------------
 
     @torch.inference_mode()
@@ -196,10 +225,15 @@ class HipEngine(DecoderPieces):
         ar = torch.arange(N, device=dev)
         masks: dict = {}
         sel = None
+        gathered = None  # event: the side-stream gather of layers 2..L-1 has finished
         for li, layer in enumerate(self.layers):
             q, k, v = self._qkv(layer.self_attn, layer.input_layernorm(h), active)
             K, V = keys_out[li], values_out[li]
-            if li != 1 or not select_layer:
+            if gathered is not None:
+                ops.scatter_rows(K, V, k, v, active, err)
+                if li == 2:
+                    torch.cuda.current_stream(dev).wait_event(gathered)
+            elif li != 1 or not select_layer:
                 ops.assemble_layer(K, V, tab_d, n_layers, li, segs_d, n_all_segs, plan.max_all_seg_tokens, k, v,
                                    local_cur, self.theta, err)
             else:
@@ -223,6 +257,9 @@ class HipEngine(DecoderPieces):
                 active = sel.keep_abs[:n_keep]
                 local_cur = sel.keep_rank
                 ops.scatter_rows(K, V, k, v, active, err)
+                if self.overlap and n_layers > 2 and n_cached_segs > 0:
+                    gathered = self._gather_dropped(k_slab, v_slab, tab_d, segs_d, n_cached_segs, plan.max_seg_tokens,
+                                                    sel.keep_rank, err)
             h = self._attend_active(layer, h, q, K, V, active, ar, masks)
 
         n_want = N - logits_from

@@ -101,11 +101,15 @@ def rerope_gather(
     max_seg_tokens: int,
     theta: float,
     err: torch.Tensor | None = None,
+    layers: tuple[int, int] | None = None,
+    skip: torch.Tensor | None = None,
 ) -> None:
     """Fill every layer's base K/V from cached chunks (torch_engine.py:96-103), one launch.
 
     k_slab/v_slab: (n_layers, 1, H, N, D) contiguous. src_tab: uint64/int64 device table
     [(chunk*n_layers + layer)*2 + {0, 1}]. segments: int32 (n_segs, 6) device descriptors.
+    layers=(begin, end) limits the launch to those layers; skip (int32 (N,), e.g. a selection's
+    keep_rank) leaves the rows of positions with skip[p] >= 0 untouched.
     """
     _dev(k_slab, v_slab, src_tab, segments)
     if not (k_slab.is_contiguous() and v_slab.is_contiguous() and k_slab.shape == v_slab.shape):
@@ -118,13 +122,28 @@ def rerope_gather(
     if segments.dtype != torch.int32 or segments.numel() < 6 * int(n_segs):
         raise ValueError("segments must be int32 with 6 fields per segment")
     n_chunks = src_tab.numel() // (2 * n_layers)
+    if layers is None and skip is None:
+        check(
+            lib().ckv_rerope_gather(
+                _ptr(k_slab), _ptr(v_slab), H * N * D, N * D, _ptr(src_tab), n_chunks, _ptr(segments), int(n_segs),
+                int(max_seg_tokens), n_layers, H, N, D, dtype_code(k_slab.dtype), float(theta), _ptr(err),
+                _stream(k_slab.device),
+            ),
+            "ckv_rerope_gather",
+        )
+        return
+    begin, end = (0, n_layers) if layers is None else (int(layers[0]), int(layers[1]))
+    if skip is not None:
+        _dev(k_slab, skip)
+        if skip.dtype != torch.int32 or skip.numel() != N or not skip.is_contiguous():
+            raise ValueError("skip must be int32 (N,) contiguous")
     check(
-        lib().ckv_rerope_gather(
-            _ptr(k_slab), _ptr(v_slab), H * N * D, N * D, _ptr(src_tab), n_chunks, _ptr(segments), int(n_segs),
-            int(max_seg_tokens), n_layers, H, N, D, dtype_code(k_slab.dtype), float(theta), _ptr(err),
-            _stream(k_slab.device),
+        lib().ckv_rerope_gather_layers(
+            _ptr(k_slab), _ptr(v_slab), H * N * D, N * D, _ptr(src_tab), n_chunks, n_layers, begin, end,
+            _ptr(segments), int(n_segs), int(max_seg_tokens), _ptr(skip), H, N, D, dtype_code(k_slab.dtype),
+            float(theta), _ptr(err), _stream(k_slab.device),
         ),
-        "ckv_rerope_gather",
+        "ckv_rerope_gather_layers",
     )
 
 

@@ -134,6 +134,23 @@ int32_t ckv_rerope_gather(void* dst_k, void* dst_v, int64_t dst_layer_stride,
                           void* stream);
 
 /*
+ * ckv_rerope_gather restricted to layers [layer_begin, layer_end) of the n_layers in src_tab
+ * and, when skip is not NULL, to the rows of positions p with skip[p] < 0 (skip: int32
+ * (n_tokens,), e.g. the rank map ckv_select writes). Rows of positions with skip[p] >= 0 are
+ * left untouched: in the reference those rows of layers >= 2 are gathered and then overwritten
+ * by the fresh K/V (torch_engine.py:96-103 then :155-156), so only the survivors are moved.
+ * dst_k/dst_v address layer 0 of the slab, as for ckv_rerope_gather.
+ * Replaces: the same reference lines as ckv_rerope_gather.
+ */
+int32_t ckv_rerope_gather_layers(void* dst_k, void* dst_v, int64_t dst_layer_stride,
+                                 int64_t dst_head_stride, const uint64_t* src_tab,
+                                 int32_t n_chunks, int32_t n_layers, int32_t layer_begin,
+                                 int32_t layer_end, const ckv_segment* segs, int32_t n_segs,
+                                 int32_t max_seg_tokens, const int32_t* skip, int32_t n_heads,
+                                 int32_t n_tokens, int32_t head_dim, int32_t dtype, double theta,
+                                 int32_t* err, void* stream);
+
+/*
  * Re-rotate one key tensor by delta positions: dst = shift_keys(src, delta).
  * src and dst are (n_heads, n_rows, head_dim) with the given head strides (elements) and
  * token stride head_dim; dst may equal src. delta == 0 copies.

@@ -51,6 +51,13 @@ def test_host_side_argument_validation_never_launches():
     assert lib.ckv_rerope_gather(None, 1, 10, 10, 1, 1, 1, 1, 1, 1, 1, 1, 128, 1, 1e6, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_rerope_gather(1, 1, 100, 10, 1, 1, 1, 1, 1, 1, 1, 1, 128, 1, 1e6, None, None) == _native.CKV_ERR_OUT_OF_RANGE
     assert lib.ckv_rerope_gather(1, 1, 100, 10, 1, 1, 1, 1, 1, 1, 1, 1, 128, 1, -1.0, None, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    # layer range: end past n_layers, begin past end -> invalid; empty range -> nothing to do
+    assert lib.ckv_rerope_gather_layers(1, 1, 1000, 100, 1, 1, 3, 0, 4, 1, 1, 1, None, 1, 10, 64, 1, 1e6, None, None) \
+        == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_rerope_gather_layers(1, 1, 1000, 100, 1, 1, 3, 2, 1, 1, 1, 1, None, 1, 10, 64, 1, 1e6, None, None) \
+        == _native.CKV_ERR_INVALID_ARGUMENT
+    assert lib.ckv_rerope_gather_layers(1, 1, 1000, 640, 1, 1, 3, 2, 2, 1, 1, 1, None, 1, 10, 64, 1, 1e6, None, None) \
+        == _native.CKV_OK
     assert lib.ckv_inv_freq(None, 128, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_inv_freq(1, 127, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_shift_keys(1, 10, 1, 10, 1, 1, 100, 1, 3, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT

@@ -115,6 +115,24 @@ def test_blend_matches_oracle_engine(models, parts, attention, ratio):
     assert_same_selection(got, ref, toks2, pl, cfg)
 
 
+@pytest.mark.parametrize("ratio", [0.3, 0.0])
+def test_side_stream_and_one_stream_builds_identical(models, parts, ratio):
+    """Layers 2..L-1 built by the side-stream gather of dropped rows + per-layer scatters, or by
+    one assemble launch per layer on the main stream: the same caches, bit for bit."""
+    _, gpu = models
+    a = HipEngine(gpu, StubTokenizer())
+    b = HipEngine(gpu, StubTokenizer(), overlap=False)
+    assert a.overlap and not b.overlap
+    toks2, pl = _swap_setup(a, parts)
+    cfg = BlendConfig(recompute_ratio=ratio, n_sink=4)
+    ra, rb = a.prefill(toks2, pl, cfg), b.prefill(toks2, pl, cfg)
+    torch.cuda.synchronize()
+    assert len(ra.keys) > 2
+    for x, y in zip(ra.keys + ra.values, rb.keys + rb.values):
+        assert torch.equal(x, y)
+    assert torch.equal(ra.logits, rb.logits)
+
+
 def test_blend_matches_rocm_reference_ops(models, parts):
     """Same device, same model, reference SDPA call: only the KV repair differs."""
     from chunkkv_amd.baseline import torch_base_kv
@@ -237,51 +255,80 @@ def test_shift_keys_api(models):
 
 
 def test_repair_step_graph_replay_matches_eager():
-    """A captured KV-repair step replayed several times, with eager work in between, gives the
-    eager result each time (no memset nodes are recorded)."""
+    """The KV-repair step as the engine issues it (assemble L0; base cache, deviation, selection
+    and scatter at L1; side-stream gather of the dropped rows of L2.. joined with the per-layer
+    scatters), captured into one HIP graph across both streams and replayed several times with
+    eager work in between: every replay gives the eager result (no memset nodes are recorded),
+    and that result equals the one-stream build with one assemble launch per layer."""
     from chunkkv_amd import ops
+    from chunkkv_amd.planner import local_index, plan_request
 
     rng = np.random.default_rng(5)
-    H, D, L, C, n_layers = 4, 128, 64, 6, 3
+    H, D, L, C, n_layers = 4, 128, 64, 6, 4
     N = C * L + 16
     chunks = [ChunkKV([torch.randn(1, H, L, D, device=DEV).bfloat16() for _ in range(n_layers)],
                       [torch.randn(1, H, L, D, device=DEV).bfloat16() for _ in range(n_layers)], int(rng.integers(0, 900)))
               for _ in range(C)]
     pl = [Placement(chunks[c], i * L) for i, c in enumerate(rng.permutation(C))]
-    from chunkkv_amd.planner import local_index, plan_request
-
     plan = plan_request(N, pl, 4, 0.3)
     tab = np.concatenate([np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(c.keys, c.values)], dtype=np.uint64).reshape(-1)
                           for c in plan.chunks])
     tab_d = torch.from_numpy(tab.view(np.int64)).to(DEV)
-    segs = torch.from_numpy(plan.segments.reshape(-1)).to(DEV)
+    segs = torch.from_numpy(plan.all_segments.reshape(-1)).to(DEV)  # cached runs first
+    n_c, n_all = len(plan.segments), len(plan.all_segments)
     flags = torch.from_numpy(plan.flags).to(DEV)
     local = torch.from_numpy(local_index(N, plan.layer0_idx)).to(DEV)
     spans = torch.from_numpy(plan.spans.reshape(-1)).to(DEV)
-    Ks = torch.empty((n_layers, 1, H, N, D), dtype=torch.bfloat16, device=DEV)
-    Vs = torch.empty_like(Ks)
+    n_keep = plan.n_keep
     fk = torch.randn(1, H, N, D, device=DEV).bfloat16()
     fv = torch.randn(1, H, N, D, device=DEV).bfloat16()
-    state = {}
+    side = torch.cuda.Stream()
 
-    def step():
-        ops.rerope_gather(Ks, Vs, tab_d, segs, len(plan.segments), plan.max_seg_tokens, 1e6)
-        diff, norm = ops.deviation(fk, fv, Ks[1], Vs[1], flags, local)
-        state["sel"] = ops.select(diff, norm, flags, local, spans, None, state.get("sel"))
-        rows = state["sel"].keep_abs[: plan.n_keep]
-        for li in range(1, n_layers):
-            ops.scatter_rows(Ks[li], Vs[li], fk[:, :, : plan.n_keep], fv[:, :, : plan.n_keep], rows)
+    def make(two_streams):
+        Ks = torch.empty((n_layers, 1, H, N, D), dtype=torch.bfloat16, device=DEV)
+        Vs = torch.empty_like(Ks)
+        state = {}
 
-    Ks.fill_(7.0)  # rows the step never writes keep this value in every run below
+        def step():
+            ops.assemble_layer(Ks[0], Vs[0], tab_d, n_layers, 0, segs, n_all, plan.max_all_seg_tokens, fk, fv, local, 1e6)
+            ops.assemble_layer(Ks[1], Vs[1], tab_d, n_layers, 1, segs, n_c, plan.max_seg_tokens, None, None, None, 1e6)
+            diff, norm = ops.deviation(fk, fv, Ks[1], Vs[1], flags, local)
+            sel = state["sel"] = ops.select(diff, norm, flags, local, spans, None, state.get("sel"))
+            rows = sel.keep_abs[:n_keep]
+            ops.scatter_rows(Ks[1], Vs[1], fk[:, :, :n_keep], fv[:, :, :n_keep], rows)
+            if two_streams:
+                main = torch.cuda.current_stream()
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    ops.rerope_gather(Ks, Vs, tab_d, segs, n_c, plan.max_seg_tokens, 1e6, layers=(2, n_layers),
+                                      skip=sel.keep_rank)
+                for li in range(2, n_layers):
+                    ops.scatter_rows(Ks[li], Vs[li], fk[:, :, :n_keep], fv[:, :, :n_keep], rows)
+                main.wait_stream(side)
+            else:
+                for li in range(2, n_layers):
+                    ops.assemble_layer(Ks[li], Vs[li], tab_d, n_layers, li, segs, n_all, plan.max_all_seg_tokens,
+                                       fk[:, :, :n_keep], fv[:, :, :n_keep], sel.keep_rank, 1e6)
+
+        return Ks, Vs, state, step
+
+    Ks, Vs, state, step = make(True)
+    Ks.fill_(7.0)  # every row is written: no 7.0 may survive
     Vs.fill_(7.0)
     step()
     torch.cuda.synchronize()
-    eager = (Ks.clone(), Vs.clone(), state["sel"].keep_abs[: plan.n_keep].clone())
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
+    eager = (Ks.clone(), Vs.clone(), state["sel"].keep_abs[:n_keep].clone())
+    assert not (Ks == 7.0).all(dim=-1).any()
+    Ks1, Vs1, _, step1 = make(False)
+    step1()
+    torch.cuda.synchronize()
+    assert torch.equal(Ks1, eager[0]) and torch.equal(Vs1, eager[1])
+
+    warm = torch.cuda.Stream()
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):
         step()
-    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.current_stream().wait_stream(warm)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         step()
@@ -289,11 +336,12 @@ def test_repair_step_graph_replay_matches_eager():
         Ks.fill_(7.0)
         Vs.fill_(7.0)
         state["sel"].keep_abs.fill_(-1)
+        state["sel"].keep_rank.fill_(-1)
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(Ks, eager[0]) and torch.equal(Vs, eager[1])
-        assert torch.equal(state["sel"].keep_abs[: plan.n_keep], eager[2])
+        assert torch.equal(state["sel"].keep_abs[:n_keep], eager[2])
 
 
 @pytest.mark.parametrize("attention", ["reference", "fused"])

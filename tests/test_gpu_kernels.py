@@ -136,6 +136,41 @@ def test_rerope_gather_matches_oracle(bf16, D, overlap):
     assert_keys_close(Kg[:, :, rot], Ko[:, :, rot], bf16)
 
 
+@pytest.mark.parametrize("layers", [(0, 3), (1, 3), (2, 2)])
+def test_rerope_gather_layer_range_with_skip_map(layers):
+    """Layers [begin, end) only, rows of positions with skip >= 0 untouched: equals the oracle's
+    full gather on exactly the remaining rows."""
+    bf16, D = True, 128
+    rng = np.random.default_rng(300 + layers[0])
+    n_layers, H = 3, 2
+    lens = [40, 70, 33, 64, 1, 97]
+    N = sum(lens) + 40
+    plan, ks, vs = _gather_case(rng, bf16, n_layers, H, D, lens, N, True)
+    _, _, Ko, Vo, src = _run_gather(plan, ks, vs, n_layers, H, D, N, bf16)
+    skip = np.full(N, -1, dtype=np.int32)
+    kept = np.flatnonzero(rng.random(N) < 0.4)
+    skip[kept] = np.arange(len(kept), dtype=np.int32)
+    tab = np.zeros((len(plan.chunks), n_layers, 2), dtype=np.uint64)
+    for ci, ch in enumerate(plan.chunks):
+        for l in range(n_layers):
+            tab[ci, l] = src[ch.idx][0][l].data_ptr(), src[ch.idx][1][l].data_ptr()
+    K = torch.full((n_layers, 1, H, N, D), -7.0, dtype=torch.bfloat16, device=DEV)
+    V = torch.full_like(K, -7.0)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.rerope_gather(K, V, torch.from_numpy(tab.view(np.int64)).to(DEV), dev(plan.segments.reshape(-1)),
+                      len(plan.segments), plan.max_seg_tokens, THETA, err, layers=layers, skip=dev(skip))
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    Kg, Vg = host(K).reshape(n_layers, H, N, D), host(V).reshape(n_layers, H, N, D)
+    sent = O.f32_to_bf16_bits(np.float32([-7.0]))[0]
+    want_k, want_v = np.full_like(Ko, sent), np.full_like(Vo, sent)
+    rows = np.flatnonzero(skip < 0)
+    for l in range(*layers):
+        want_k[l][:, rows], want_v[l][:, rows] = Ko[l][:, rows], Vo[l][:, rows]
+    np.testing.assert_array_equal(Kg, want_k)
+    np.testing.assert_array_equal(Vg, want_v)
+
+
 def test_rerope_gather_config2_full_size():
     """Re-RoPE + gather at the Qwen2.5-7B KV shape: 28 layers, 4 heads, D=128, bf16,
     16 chunks x 256 tokens moved by delta ~ U[-4096, 4096] into a 4096-token cache."""
