@@ -65,8 +65,9 @@ GATHER_BYTES = N_LAYERS * N_CHUNKS * CHUNK_LEN * ROW_BYTES * 2 * 2
 # (profiles/traffic_rerope_gather_qwen25_7b_8k.md; FETCH_SIZE calibrated against a kernel of
 # known traffic). Counters cannot be read inside a timed run, so the measured value is recorded.
 GATHER_TRAFFIC_BYTES = 881_167_672
-# Same for one gather of the dropped rows of layers 2-27 of the 8k request; None until measured.
-DROPPED_TRAFFIC_BYTES = None
+# Same for one gather of the dropped rows of layers 2-27 of the 8k request (FETCH_SIZE median
+# 137,405 KiB / 0.500046 + WRITE_SIZE median 274,573 KiB; 562,298,880 algorithmic bytes).
+DROPPED_TRAFFIC_BYTES = 562_552_203
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 
@@ -654,6 +655,28 @@ def traffic_probe(steps: int, warmup: int, dev) -> dict:
 COPY_BYTES = 512 << 20
 
 
+def bench_dropped(steps: int, warmup: int, dev) -> dict:
+    """The dominant kernel alone: `steps` back-to-back gathers of the dropped rows of layers 2-27
+    (alternating two input sets), timed with HIP events on the launch stream. Its rocprofv3
+    kernel average is the same quantity (no other gather launch runs in this workload)."""
+    wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
+    for w in wls:
+        w.step_serial()  # selection output, without a gather of the dropped rows
+    for i in range(warmup):
+        wls[i % 2].gather_dropped()
+    stream = torch.cuda.current_stream(dev)
+    ms = _timed(lambda i: wls[i % 2].gather_dropped(), steps, stream)
+    assert all(int(w.err.item()) == 0 for w in wls)
+    nb = dropped_bytes(wls[0].plan)
+    gbs = nb / (ms * 1e-3) / 1e9
+    return _workload_line("gather of the dropped rows, HBM GB/s", gbs, ms, steps, warmup,
+                          {"workload": "layers 2-27 of the 8256-token Qwen2.5-7B-shape request: 24 cached chunks x 320, "
+                                       "5280 dropped positions"},
+                          {"kernel": "rerope_gather_kernel<bf16,128>", "bound": "hbm", "achieved": round(gbs, 1),
+                           "peak": PEAK_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4),
+                           "traffic": DROPPED_TRAFFIC_BYTES, "bytes_per_launch": nb, "avg_launch_us": round(ms * 1e3, 2)})
+
+
 def repair_bytes_for(plan) -> int:
     """Algorithmic repair bytes of a request plan (gather of every cached row, deviation over the
     layer-0 active set, scatters of layer 0 and layers 1..L-1)."""
@@ -671,7 +694,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ttft-requests", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--workload", default="request", choices=["request", "gather", "deviation", "replay", "traffic"],
+    ap.add_argument("--workload", default="request",
+                    choices=["request", "gather", "deviation", "replay", "traffic", "dropped"],
                     help="request: the 8k Qwen2.5-7B blend-prefill KV repair (default); gather / deviation / replay: "
                          "the re-RoPE+gather, deviation+top-k+scatter and 4x32k replay microbenchmarks")
     args = ap.parse_args()
@@ -682,7 +706,7 @@ def main() -> None:
     torch.cuda.set_device(dev)
     if args.workload != "request":
         fn = {"gather": bench_gather_only, "deviation": bench_deviation_topk, "replay": bench_replay,
-              "traffic": traffic_probe}[args.workload]
+              "traffic": traffic_probe, "dropped": bench_dropped}[args.workload]
         print(json.dumps(fn(args.steps, args.warmup, dev)), flush=True)
         return
 

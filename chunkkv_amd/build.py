@@ -19,7 +19,7 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 LIB_DIR = PKG / "_lib"
 LIB_NAME = "libchunkkv_amd.so"
-SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "scatter.hip"]
+SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "scatter.hip", "attention.hip"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: products and sums stay separately rounded, like the reference's torch ops.
@@ -31,6 +31,7 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",  # MFMA accumulators in VGPRs (no accumulator-register copies)
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]

@@ -1,0 +1,320 @@
+// Attention of the active rows over the whole cache, with the causal mask given by positions:
+// query row i (absolute position pos[i]) attends to cache rows j <= pos[i] of its KV head.
+//
+// Reference semantics (src/chunkkv/engine/torch_engine.py): the mask is materialised as a
+// boolean (n_active x N) tensor, mask = active[:, None] >= arange(N)[None, :] (:157), and
+// F.scaled_dot_product_attention(q, K, V, attn_mask=mask, enable_gqa=True) (:68-72) runs with
+// the default scale 1/sqrt(head_dim); query head h reads KV head h / (Hq / Hkv). This kernel
+// computes the same function from the positions alone: no mask tensor, no KV-head expansion.
+//
+// Design (gfx950, flash-attention forward): one workgroup = 4 wavefronts = 128 queries of one
+// query head; it walks the cache in 64-row tiles up to the largest position among its queries
+// (tiles past a wavefront's own queries are skipped by that wavefront). Both products run on
+// the bf16 matrix cores (v_mfma_f32_16x16x32_bf16) in transposed form:
+//   S^T = K Q^T   (A = K rows from LDS, B = the wavefront's Q rows held in registers)
+//   O^T = V^T P^T (A = V^T rows from LDS, B = P straight from the S^T accumulators)
+// so that every lane owns one query (lane % 16) for the whole computation: the online-softmax
+// max/sum and the output rows live in that lane and only two xor-shuffles per tile combine the
+// four lane groups. K rows are stored in LDS in the order the fragment reads want (conflict-free
+// 16-byte reads) and V is transposed on its way into LDS. Scores and the output accumulate in
+// fp32; P is rounded to bf16 for the second product (as fused SDPA kernels do). Built with the
+// MFMA VGPR form (no accumulator-register copies around the online-softmax rescale).
+#include "ckv_common.hpp"
+
+namespace ckv {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#ifndef CKV_ATTN_QG
+#define CKV_ATTN_QG 2
+#endif
+#ifndef CKV_ATTN_PREFETCH
+#define CKV_ATTN_PREFETCH 1
+#endif
+constexpr int kAttnWaves = 4;
+constexpr int kAttnQG = CKV_ATTN_QG;                // 16-query groups per wavefront
+constexpr int kAttnBM = kAttnWaves * kAttnQG * 16;  // queries per workgroup
+constexpr int kAttnBN = 64;                         // cache rows per tile
+constexpr bool kAttnPrefetch = CKV_ATTN_PREFETCH;   // next tile's loads in flight during the MFMAs
+
+__device__ __forceinline__ float wave_xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
+
+// Cache row r of a 32-row block goes to LDS slot kslot(r): the 16 rows that lanes 0-15 read for
+// one S^T tile are then 16 consecutive slots (distinct banks with the padded row stride).
+__device__ __forceinline__ int kslot(int r) {
+  const int blk = r & ~31, k = r & 31;  // k = 8a + 4t + b  ->  slot 16t + 4a + b
+  return blk + ((k >> 2) & 1) * 16 + (k >> 3) * 4 + (k & 3);
+}
+
+#ifndef CKV_ATTN_OCC
+#define CKV_ATTN_OCC 0
+#endif
+
+template <int D>
+__global__ __launch_bounds__(kAttnWaves * 64)
+#if CKV_ATTN_OCC > 0
+__attribute__((amdgpu_waves_per_eu(CKV_ATTN_OCC)))
+#endif
+void attn_active_kernel(
+    char* __restrict__ out, const char* __restrict__ q, int64_t q_hs_b, int64_t q_ts_b,
+    const char* __restrict__ kc, const char* __restrict__ vc, int64_t kv_hs_b,
+    const int64_t* __restrict__ pos, int n, int N, int Hq, int group, float scale_log2,
+    int32_t* __restrict__ err) {
+  constexpr int DS = D / 32;          // k-steps of S^T = K Q^T
+  constexpr int DT = D / 16;          // 16-row tiles of O^T
+  constexpr int CPR = D / 8;          // 16-byte chunks per cache row
+  constexpr int KROW = D * 2 + 16;    // padded LDS row of the K tile (bytes)
+  constexpr int VROW = kAttnBN * 2 + 16;  // padded LDS row of V^T: one row per head-dim index
+  constexpr int NT = kAttnWaves * 64;
+  static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
+  static_assert((kAttnBN * CPR) % NT == 0 && ((kAttnBN / 2) * CPR) % NT == 0, "tile loads must tile the workgroup");
+
+  __shared__ __attribute__((aligned(16))) char k_lds[kAttnBN * KROW];
+  __shared__ __attribute__((aligned(16))) char v_lds[D * VROW];
+  __shared__ int blk_max_s[kAttnWaves];
+
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int g = lane / 16, lm = lane % 16;
+  const int hq = blockIdx.y;
+  const int hk = hq / group;
+  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // latest positions (most keys) first
+  const int q0 = qb * kAttnBM + wave * kAttnQG * 16;
+
+  // Positions of this lane's queries (-1 = no query); out-of-range positions are flagged and
+  // clamped so that every read stays inside the cache.
+  int my_pos[kAttnQG];
+  int wmax = -1, wmin = N;
+#pragma unroll
+  for (int qg = 0; qg < kAttnQG; ++qg) {
+    const int m = q0 + qg * 16 + lm;
+    int p = -1;
+    if (m < n) {
+      const int64_t p64 = pos[m];
+      if (p64 < 0 || p64 >= N) {
+        flag_error(err, CKV_DEVICE_ERR_RANGE);
+        p = p64 < 0 ? 0 : N - 1;
+      } else {
+        p = (int)p64;
+      }
+      wmin = min(wmin, p);
+    }
+    my_pos[qg] = p;
+    wmax = max(wmax, p);
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    wmax = max(wmax, __shfl_xor(wmax, s, 64));
+    wmin = min(wmin, __shfl_xor(wmin, s, 64));
+  }
+  if (lane == 0) blk_max_s[wave] = wmax;
+  __syncthreads();
+  int bmax = blk_max_s[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) bmax = max(bmax, blk_max_s[w]);
+  const int n_tiles = bmax < 0 ? 0 : bmax / kAttnBN + 1;
+
+  // Q fragments (B operand of S^T): query q0 + 16 qg + lm, head-dim 32 s + 8 g .. + 8.
+  bf16x8 qf[kAttnQG][DS];
+#pragma unroll
+  for (int qg = 0; qg < kAttnQG; ++qg) {
+    const int m = q0 + qg * 16 + lm;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      vec16 v = {0, 0, 0, 0};
+      if (m < n) v = ld16(q + (int64_t)hq * q_hs_b + (int64_t)m * q_ts_b + (32 * s + 8 * g) * 2);
+      qf[qg][s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  f32x4 o[kAttnQG][DT];
+  float m_run[kAttnQG], l_run[kAttnQG];
+#pragma unroll
+  for (int qg = 0; qg < kAttnQG; ++qg) {
+    m_run[qg] = -INFINITY;
+    l_run[qg] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[qg][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const char* kh = kc + (int64_t)hk * kv_hs_b;
+  const char* vh = vc + (int64_t)hk * kv_hs_b;
+
+  constexpr int KL = (kAttnBN * CPR) / NT;        // 16-byte K loads per thread and tile
+  constexpr int VL = ((kAttnBN / 2) * CPR) / NT;  // V row-pair loads per thread and tile
+  vec16 kr[KL], va[VL], vb[VL];
+  auto load_tile = [&](int n0) {  // global -> registers; rows past the cache read as zero
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int c = threadIdx.x + i * NT, r = c / CPR, col = c % CPR;
+      kr[i] = vec16{0, 0, 0, 0};
+      if (n0 + r < N) kr[i] = ld16(kh + (int64_t)(n0 + r) * (D * 2) + col * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int c = threadIdx.x + i * NT, pr = c % (kAttnBN / 2), col = c / (kAttnBN / 2);
+      const int r = n0 + 2 * pr;
+      va[i] = vb[i] = vec16{0, 0, 0, 0};
+      if (r < N) va[i] = ld16(vh + (int64_t)r * (D * 2) + col * 16);
+      if (r + 1 < N) vb[i] = ld16(vh + (int64_t)(r + 1) * (D * 2) + col * 16);
+    }
+  };
+  if (kAttnPrefetch && n_tiles > 0) load_tile(0);
+
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const int n0 = tile * kAttnBN;
+    if (!kAttnPrefetch) load_tile(n0);
+    __syncthreads();  // previous tile's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int c = threadIdx.x + i * NT, r = c / CPR, col = c % CPR;
+      *(vec16*)(k_lds + kslot(r) * KROW + col * 16) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int c = threadIdx.x + i * NT, pr = c % (kAttnBN / 2), col = c / (kAttnBN / 2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {  // (V[2pr][d], V[2pr+1][d]) for d = 8 col + e, packed
+        const unsigned lo = (e & 1) ? (va[i][e >> 1] >> 16) : (va[i][e >> 1] & 0xffffu);
+        const unsigned hi = (e & 1) ? (vb[i][e >> 1] >> 16) : (vb[i][e >> 1] & 0xffffu);
+        *(unsigned*)(v_lds + (8 * col + e) * VROW + pr * 4) = lo | (hi << 16);
+      }
+    }
+    __syncthreads();
+    if (kAttnPrefetch && tile + 1 < n_tiles) load_tile(n0 + kAttnBN);  // lands during the MFMAs below
+
+    if (n0 > wmax) continue;  // uniform per wavefront: no query of this wavefront reaches the tile
+    const bool need_mask = n0 + kAttnBN - 1 > wmin;
+
+    // S^T for the tile: lane (g, lm) gets query lm, rows n0 + 32 kb + 8 g + 4 t + e.
+    constexpr int KB = kAttnBN / 32;
+    f32x4 s[kAttnQG][KB][2];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int qg = 0; qg < kAttnQG; ++qg) s[qg][kb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const bf16x8 a = *(const bf16x8*)(k_lds + (kb * 32 + 16 * t + lm) * KROW + (32 * ds + 8 * g) * 2);
+#pragma unroll
+          for (int qg = 0; qg < kAttnQG; ++qg)
+            s[qg][kb][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[qg][ds], s[qg][kb][t], 0, 0, 0);
+        }
+      }
+
+    // Online softmax over the tile. The running max is only raised when a query's tile max
+    // exceeds it by more than 2^8 (log2 domain): weights stay <= 256, the output rescale is
+    // skipped for the whole wavefront otherwise, and the result is unchanged (the final division
+    // uses the same max).
+    bf16x8 pb[kAttnQG][KB];
+#pragma unroll
+    for (int qg = 0; qg < kAttnQG; ++qg) {
+      float x[KB][8];
+      float bm = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = s[qg][kb][t][e] * scale_log2;
+            if (need_mask && n0 + 32 * kb + 8 * g + 4 * t + e > my_pos[qg]) v = -INFINITY;
+            x[kb][4 * t + e] = v;
+            bm = fmaxf(bm, v);
+          }
+      bm = wave_xor_max(wave_xor_max(bm, 16), 32);
+      const bool raise = bm > m_run[qg] + 8.f;  // also true on the first visible tile (m_run = -inf)
+      if (__builtin_amdgcn_ballot_w64(raise)) {  // uniform branch
+        const float m_new = raise ? bm : m_run[qg];
+        const float alpha = m_run[qg] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[qg] - m_new);
+        l_run[qg] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[qg][dt] *= alpha;
+        m_run[qg] = m_new;
+      }
+      const bool none = m_run[qg] == -INFINITY;  // no visible row yet (absent queries only)
+      float psum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p = none ? 0.f : __builtin_amdgcn_exp2f(x[kb][e] - m_run[qg]);
+          psum += p;
+          pb[qg][kb][e] = (__bf16)p;
+        }
+      l_run[qg] += psum;
+    }
+
+    // O^T += V^T P^T: A = V^T rows dt*16 + lm, columns 32 kb + 8 g .. + 8.
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 a = *(const bf16x8*)(v_lds + (dt * 16 + lm) * VROW + (kb * 32 + 8 * g) * 2);
+#pragma unroll
+        for (int qg = 0; qg < kAttnQG; ++qg)
+          o[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qg][kb], o[qg][dt], 0, 0, 0);
+      }
+  }
+
+  // Normalise and write: lane (g, lm) holds O[query][dt*16 + 4g + e], 4 bf16 = 8 bytes per tile.
+#pragma unroll
+  for (int qg = 0; qg < kAttnQG; ++qg) {
+    float l = l_run[qg];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int m = q0 + qg * 16 + lm;
+    if (m >= n) continue;
+    const float inv = 1.f / l;
+    char* orow = out + ((int64_t)m * Hq + hq) * (D * 2);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      unsigned w[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const unsigned lo = f32_to_bf16_bits(o[qg][dt][2 * h] * inv), hi = f32_to_bf16_bits(o[qg][dt][2 * h + 1] * inv);
+        w[h] = lo | (hi << 16);
+      }
+      *(uint2*)(orow + (dt * 16 + 4 * g) * 2) = uint2{w[0], w[1]};
+    }
+  }
+}
+
+}  // namespace ckv
+
+extern "C" int32_t ckv_attention_active(void* out, const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                                        const void* k_cache, const void* v_cache, int64_t kv_head_stride,
+                                        const int64_t* positions, int32_t n_queries, int32_t n_tokens,
+                                        int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
+                                        double scale, int32_t* err, void* stream) {
+  using namespace ckv;
+  if (out == nullptr || q == nullptr || k_cache == nullptr || v_cache == nullptr || positions == nullptr)
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (dtype != CKV_DTYPE_BF16 || (head_dim != 64 && head_dim != 128)) return CKV_ERR_INVALID_ARGUMENT;
+  if (n_queries < 0 || n_tokens <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads != 0 ||
+      !(scale > 0.0))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (q_token_stride % 8 || q_head_stride % 8 || kv_head_stride % 8) return CKV_ERR_INVALID_ARGUMENT;  // 16-byte rows
+  if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16) return CKV_ERR_INVALID_ARGUMENT;
+  if (q_token_stride < head_dim || kv_head_stride < (int64_t)n_tokens * head_dim) return CKV_ERR_OUT_OF_RANGE;
+  if (n_queries == 0) return CKV_OK;
+  const int blocks = (n_queries + kAttnBM - 1) / kAttnBM;
+  if (n_q_heads > 65535) return CKV_ERR_TOO_LARGE;
+  const float scale_log2 = (float)(scale * 1.4426950408889634);  // exp(x) = exp2(x log2 e)
+  dim3 grid((unsigned)blocks, (unsigned)n_q_heads);
+  const int group = n_q_heads / n_kv_heads;
+  if (head_dim == 128)
+    hipLaunchKernelGGL((attn_active_kernel<128>), grid, dim3(kAttnWaves * 64), 0, (hipStream_t)stream, (char*)out,
+                       (const char*)q, q_head_stride * 2, q_token_stride * 2, (const char*)k_cache,
+                       (const char*)v_cache, kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group,
+                       scale_log2, err);
+  else
+    hipLaunchKernelGGL((attn_active_kernel<64>), grid, dim3(kAttnWaves * 64), 0, (hipStream_t)stream, (char*)out,
+                       (const char*)q, q_head_stride * 2, q_token_stride * 2, (const char*)k_cache,
+                       (const char*)v_cache, kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group,
+                       scale_log2, err);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}

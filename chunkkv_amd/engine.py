@@ -25,15 +25,19 @@ The KV repair runs on the HIP kernels:
   deviation (:117-124)                               ckv_deviation (one wavefront per token)
   rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
     one .item() per chunk)                             nothing back unless a threshold is set
+  mask + SDPA (:157, :68-72)                          ckv_attention_active: matrix-core
+                                                       attention masked by the active positions
+                                                       (bf16, head_dim 64/128)
 All layers' caches live in one (L, 1, H, N, D) slab; PrefillResult.keys/values are its views.
 
-Attention stays on PyTorch-ROCm SDPA. The reference calls it with enable_gqa and an explicit
-boolean (n_active x N) mask, a combination with no fused kernel on ROCm (it runs the fp32 math
-path). ``attention="fused"`` (default) keeps the same semantics but picks formulations that hit
-the fused kernels: when every position is active (layer 0 without exact placements) the mask is
-the plain causal mask, so ``is_causal=True``; otherwise the KV heads are expanded to the query
-heads and the boolean mask (built once per active set, not once per layer) is passed without
-enable_gqa. ``attention="reference"`` reproduces the reference's SDPA call exactly.
+Attention: the reference calls SDPA with enable_gqa and an explicit boolean (n_active x N) mask,
+a combination with no fused kernel on ROCm (it runs the fp32 math path). ``attention="fused"``
+(default) keeps the same semantics with fast formulations: bf16 models with head_dim 64 or 128
+run every layer on the HIP kernel ckv_attention_active, which reads the positions directly (no
+mask tensor, no KV-head expansion). Other models use SDPA with ``is_causal=True`` when every
+position is active (the mask is then the plain causal mask) and otherwise expand the KV heads and
+pass the boolean mask (built once per active set) without enable_gqa.
+``attention="reference"`` reproduces the reference's SDPA call exactly.
 
 Contracts where the reference leaves the result open: the selection breaks deviation ties by
 the lower token index (torch's argsort is unstable), deviation sums use a fixed order, and
@@ -83,6 +87,8 @@ class HipEngine(DecoderPieces):
         self.kv_dtype = self.layers[0].self_attn.k_proj.weight.dtype
         ops.dtype_code(self.kv_dtype)
         self.inv_freq = ops.inv_freq(self.head_dim, self.theta, self.device)
+        # ckv_attention_active covers bf16 caches with head_dim 64 or 128; other models keep SDPA
+        self._native_attention = self.kv_dtype == torch.bfloat16 and self.head_dim in (64, 128)
 
     @classmethod
     def load(cls, repo: str, dtype=torch.bfloat16) -> "HipEngine":
@@ -91,13 +97,18 @@ class HipEngine(DecoderPieces):
         model = AutoModelForCausalLM.from_pretrained(repo, dtype=dtype).to("cuda")
         return cls(model, AutoTokenizer.from_pretrained(repo))
 
-    def _attend_active(self, layer, h, q, K, V, active, ar, masks: dict):
+    def _attend_active(self, layer, h, q, K, V, active, ar, masks: dict, err=None):
         """Attention of the active rows over the whole cache: row i sees positions <= active[i]."""
         n_act, N = active.shape[0], ar.shape[0]
         key = (active.data_ptr(), n_act)
         if self.attention == "reference":
             return self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :])
         attn = layer.self_attn
+        if self._native_attention:
+            # positions-only mask on the matrix-core kernel; output already token-major
+            o = ops.attention_active(q, K, V, active, err=err)
+            h = h + attn.o_proj(o.view(h.shape[0], h.shape[1], -1))
+            return h + layer.mlp(layer.post_attention_layernorm(h))
         if n_act == N:  # active == arange(N): the mask is exactly the causal mask
             o = F.scaled_dot_product_attention(q, K, V, is_causal=True, enable_gqa=True)
         else:
@@ -260,7 +271,7 @@ class HipEngine(DecoderPieces):
                 if self.overlap and n_layers > 2 and n_cached_segs > 0:
                     gathered = self._gather_dropped(k_slab, v_slab, tab_d, segs_d, n_cached_segs, plan.max_seg_tokens,
                                                     sel.keep_rank, err)
-            h = self._attend_active(layer, h, q, K, V, active, ar, masks)
+            h = self._attend_active(layer, h, q, K, V, active, ar, masks, err)
 
         n_want = N - logits_from
         if 0 <= logits_from <= N and not plan.cached[logits_from:].any():

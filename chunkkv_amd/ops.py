@@ -7,6 +7,8 @@ Every wrapper launches a HIP kernel; none computes anything on the CPU.
 
 from __future__ import annotations
 
+import math
+
 from dataclasses import dataclass
 
 import torch
@@ -312,3 +314,45 @@ def scatter_rows(
         ),
         "ckv_scatter_rows",
     )
+
+
+def attention_active(
+    q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    positions: torch.Tensor,
+    scale: float | None = None,
+    err: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Attention of the active query rows over the cache, query i seeing positions <= positions[i]
+    (the reference's boolean-mask SDPA with enable_gqa, torch_engine.py:157 and :68-72).
+
+    q: (1, Hq, n, D) bf16 with contiguous rows; K/V: (1, Hkv, N, D) contiguous; positions: int64
+    (n,). Returns (1, n, Hq, D) bf16, token-major (``.view(1, n, Hq * D)`` feeds o_proj).
+    """
+    _dev(q, K, V, positions)
+    _, Hq, n, D = q.shape
+    _, Hkv, N, _ = K.shape
+    if q.dtype != torch.bfloat16 or K.dtype != torch.bfloat16 or V.dtype != torch.bfloat16:
+        raise TypeError("attention_active runs on bf16 q/K/V")
+    if not (K.is_contiguous() and V.is_contiguous() and V.shape == K.shape) or K.shape[3] != D:
+        raise ValueError("K/V must be contiguous (1, Hkv, N, D) and match q's head_dim")
+    if q.stride(3) != 1:
+        q = q.contiguous()
+    if positions.dtype != torch.int64 or positions.numel() != n:
+        raise ValueError("positions must be int64 (n,)")
+    positions = positions.contiguous()
+    if out is None:
+        out = torch.empty((1, n, Hq, D), dtype=q.dtype, device=q.device)
+    elif out.shape != (1, n, Hq, D) or not out.is_contiguous() or out.dtype != q.dtype:
+        raise ValueError("out must be contiguous (1, n, Hq, D) bf16")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    check(
+        lib().ckv_attention_active(
+            _ptr(out), _ptr(q), q.stride(1), q.stride(2), _ptr(K), _ptr(V), N * D, _ptr(positions), n, N, Hq, Hkv,
+            D, dtype_code(q.dtype), scale, _ptr(err), _stream(q.device),
+        ),
+        "ckv_attention_active",
+    )
+    return out

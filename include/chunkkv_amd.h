@@ -241,6 +241,31 @@ int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride,
                          int32_t n_heads, int32_t head_dim, int32_t dtype, int32_t* err,
                          void* stream);
 
+/*
+ * Attention of the active rows over the whole cache with the causal mask given by positions:
+ *   out[i, h, :] = softmax_j( scale * q[h, i, :] . K[h / G, j, :] ) V[h / G, j, :],
+ *   j ranging over [0, positions[i]], G = n_q_heads / n_kv_heads.
+ * This is F.scaled_dot_product_attention(q, K, V, attn_mask=active[:, None] >= arange(N),
+ * enable_gqa=True) with positions = active (torch_engine.py:157, :68-72), computed without the
+ * (n_queries x n_tokens) mask and without expanding the KV heads.
+ *   q          bf16 (n_q_heads, n_queries, head_dim) with the given head/token strides (elements,
+ *              multiples of 8; rows contiguous)
+ *   k_cache,   bf16 (n_kv_heads, n_tokens, head_dim), rows contiguous, head stride kv_head_stride
+ *   v_cache
+ *   positions  int64 (n_queries,), each in [0, n_tokens) (out-of-range entries are clamped and
+ *              flagged in *err); any order, ascending is fastest
+ *   out        bf16 (n_queries, n_q_heads, head_dim) contiguous: token-major, the layout the
+ *              output projection reads
+ * dtype must be CKV_DTYPE_BF16 and head_dim 64 or 128. Scores and the output accumulate in
+ * fp32; the softmax weights are rounded to bf16 before they multiply V.
+ * Replaces: the mask construction and SDPA call of torch_engine.py:157, :68-72.
+ */
+int32_t ckv_attention_active(void* out, const void* q, int64_t q_head_stride, int64_t q_token_stride,
+                             const void* k_cache, const void* v_cache, int64_t kv_head_stride,
+                             const int64_t* positions, int32_t n_queries, int32_t n_tokens,
+                             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
+                             double scale, int32_t* err, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,8 @@ Parity status of each function (how it is pinned is in tests/test_oracle.py):
   select          pinned: numpy lexsort and torch stable argsort of the reference expression,
                   closed-form budgets/stats of tests/test_mlx_engine.py
   scatter_rows    pinned: brute-force Python loop on small shapes
+  attention_active pinned: torch's CPU scaled_dot_product_attention with the reference's boolean
+                  mask and enable_gqa (the reference call itself), fp32, on small shapes
 """
 
 from __future__ import annotations
@@ -197,3 +199,26 @@ def scatter_rows(K: np.ndarray, V: np.ndarray, k: np.ndarray, v: np.ndarray, row
     k, v = np.ascontiguousarray(k), np.ascontiguousarray(v)
     rows = np.ascontiguousarray(rows, dtype=np.int64)
     return lib().ckvo_scatter_rows(_p(K), _p(V), N * D, _p(k), n * D, D, _p(v), n * D, D, _p(rows), n, N, H, D, dt_of(K))
+
+
+def attention_active(q: np.ndarray, K: np.ndarray, V: np.ndarray, positions: np.ndarray, scale: float | None = None):
+    """Masked GQA attention in fp64 (torch_engine.py:157 mask, :68-72 SDPA with enable_gqa).
+
+    q: (Hq, n, D); K, V: (Hkv, N, D) (float32, or uint16 bf16 bits); positions: (n,) ints.
+    Query i of head h attends to rows j <= positions[i] of KV head h // (Hq // Hkv).
+    Returns (n, Hq, D) float64, token-major like ckv_attention_active."""
+    q, K, V = (as_f32(np.asarray(a)).astype(np.float64) for a in (q, K, V))
+    Hq, n, D = q.shape
+    Hkv, N, _ = K.shape
+    G = Hq // Hkv
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    pos = np.asarray(positions, dtype=np.int64)
+    visible = pos[:, None] >= np.arange(N)[None, :]
+    out = np.empty((n, Hq, D))
+    for h in range(Hq):
+        s = (q[h] @ K[h // G].T) * scale
+        s = np.where(visible, s, -np.inf)
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        out[:, h] = (p @ V[h // G]) / p.sum(axis=1, keepdims=True)
+    return out

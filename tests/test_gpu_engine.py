@@ -231,9 +231,13 @@ def test_generate_matches_hf_greedy(models, parts):
     assert ours == ref[: len(ours)] and len(ours) > 0
 
 
-def test_bf16_blend_matches_rocm_reference_ops():
-    gpu = tiny_qwen2(layers=3, hidden=512, heads=4, kv=4, inter=1024, vocab=512, seed=3, dtype=torch.bfloat16).to(DEV)
-    hip = HipEngine(gpu, StubTokenizer(), attention="reference")
+@pytest.mark.parametrize("attention,heads,kv", [("reference", 4, 4), ("fused", 4, 4), ("fused", 8, 2)])
+def test_bf16_blend_matches_rocm_reference_ops(attention, heads, kv):
+    """bf16 model: HipEngine (reference SDPA call, or the fused path with the positions-masked
+    matrix-core attention at head_dim 128 and 64 with GQA) vs the reference op sequence."""
+    gpu = tiny_qwen2(layers=3, hidden=512, heads=heads, kv=kv, inter=1024, vocab=512, seed=3, dtype=torch.bfloat16).to(DEV)
+    hip = HipEngine(gpu, StubTokenizer(), attention=attention)
+    assert hip._native_attention
     ref = TorchOpsEngine(gpu, StubTokenizer())
     rng = np.random.default_rng(3)
     t = lambda n: rng.integers(1, 511, n).tolist()  # noqa: E731

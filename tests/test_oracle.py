@@ -347,3 +347,39 @@ def test_scatter_rows_brute_force():
     assert O.scatter_rows(K, V, k, v, rows) == 0
     np.testing.assert_array_equal(K, Kw)
     np.testing.assert_array_equal(V, Vw)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,N,n", [(4, 4, 64, 40, 40), (14, 2, 64, 97, 31), (28, 4, 128, 150, 57)])
+def test_attention_active_matches_reference_sdpa_call(Hq, Hkv, D, N, n):
+    """The oracle against the reference's own call (torch_engine.py:157, :68-72): a boolean mask
+    active[:, None] >= arange(N) and SDPA with enable_gqa, fp32 on the CPU."""
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(Hq + N)
+    q = rng.standard_normal((Hq, n, D)).astype(np.float32)
+    K = rng.standard_normal((Hkv, N, D)).astype(np.float32)
+    V = rng.standard_normal((Hkv, N, D)).astype(np.float32)
+    active = np.sort(rng.choice(N, n, replace=False))
+    got = O.attention_active(q, K, V, active)
+    act = torch.from_numpy(active)
+    mask = act[:, None] >= torch.arange(N)[None, :]
+    want = F.scaled_dot_product_attention(torch.from_numpy(q)[None], torch.from_numpy(K)[None],
+                                          torch.from_numpy(V)[None], attn_mask=mask, enable_gqa=True)
+    np.testing.assert_allclose(got, want[0].transpose(0, 1).numpy(), atol=2e-5, rtol=0)
+
+
+def test_attention_active_closed_forms():
+    """Position 0 sees only row 0 (output = V[0]); equal scores average the visible rows; a row
+    far above the others takes all the weight."""
+    D, N = 64, 10
+    q = np.zeros((1, 3, D), np.float32)
+    K = np.zeros((1, N, D), np.float32)
+    V = np.arange(N * D, dtype=np.float32).reshape(1, N, D)
+    out = O.attention_active(q, K, V, np.array([0, 4, 9]))
+    np.testing.assert_array_equal(out[0, 0], V[0, 0])
+    np.testing.assert_allclose(out[1, 0], V[0, :5].mean(axis=0))
+    np.testing.assert_allclose(out[2, 0], V[0].mean(axis=0))
+    K[0, 7, 0] = 1000.0
+    q[0, 2, 0] = 1.0
+    out = O.attention_active(q, K, V, np.array([0, 4, 9]))
+    np.testing.assert_allclose(out[2, 0], V[0, 7])
