@@ -1,0 +1,164 @@
+// Fresh-token RoPE of the projected q and k rows, written where their consumers read them: q in
+// the layout of the attention kernel, k (and v, copied) either straight into the cache rows of
+// their positions or into a separate tensor.
+//
+// Reference semantics (src/chunkkv/engine/torch_engine.py): _qkv (:61-66) views the q/k/v
+// projections as heads and applies _rope (:53-54) to q and k: angles = positions.float()[:, None]
+// * inv_freq[None, :], then _rotate (:46-51) in fp32 with one rounding to the element type; the
+// cache rows of the active positions are then overwritten with k and v (:155-156). Here the
+// rotation of token t uses the fp32 angle fl32(fl32(pos[t]) * inv_freq_i) with the correctly
+// rounded fp32 cos/sin of that angle (evaluated in fp64), the same rotation ckv_shift_keys
+// applies for a shift by pos[t]; products and sums are separately rounded fp32 operations.
+//
+// Design (gfx950): one workgroup per token. Its D/2 cos/sin pairs are built in LDS while the
+// token's first 16-byte loads are in flight; then every (head, 16-byte column) pair of q and k
+// is rotated and stored, and the v row copied, with 16-byte accesses. The ~20 elementwise torch
+// launches of the reference's RoPE (fp32 temporaries, cat, cast) and the separate scatter of k/v
+// into the cache become one pass over the projection output.
+#include "ckv_common.hpp"
+
+namespace ckv {
+
+constexpr int kRopeThreads = 256;
+
+template <int DTYPE, int D>
+__global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
+    char* __restrict__ q_out, int64_t qo_hs_b, int64_t qo_ts_b, char* __restrict__ k_out, int64_t ko_hs_b,
+    int64_t ko_ts_b, char* __restrict__ v_out, int64_t vo_hs_b, int64_t vo_ts_b, const int64_t* __restrict__ rows,
+    int n_out, const char* __restrict__ q_in, int64_t qi_hs_b, int64_t qi_ts_b, const char* __restrict__ k_in,
+    int64_t ki_hs_b, int64_t ki_ts_b, const char* __restrict__ v_in, int64_t vi_hs_b, int64_t vi_ts_b,
+    const int64_t* __restrict__ pos, int Hq, int Hkv, double theta, int32_t* __restrict__ err) {
+  using E = Elem<DTYPE>;
+  constexpr int VEC = E::kVec;
+  constexpr int HALF = D / 2;
+  constexpr int TPR = HALF / VEC;              // threads per rotated row
+  constexpr int HALF_B = HALF * E::kBytes;
+  constexpr int CPR = D * E::kBytes / 16;      // 16-byte chunks per copied row
+  static_assert(HALF % VEC == 0 && kRopeThreads >= HALF, "head_dim out of range");
+
+  __shared__ float2 cs_tab[HALF];
+
+  const int t = blockIdx.x;
+  const int64_t p = pos[t];
+  const int64_t row = rows != nullptr ? rows[t] : t;
+  if (p < INT32_MIN || p > INT32_MAX || row < 0 || row >= n_out) {  // uniform per workgroup
+    if (threadIdx.x == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+    return;
+  }
+  const int n_rot = (Hq + Hkv) * TPR;  // q heads then k heads
+
+  auto src_of = [&](int it) {
+    const int h = it / TPR, col = it % TPR;
+    return h < Hq ? q_in + h * qi_hs_b + t * qi_ts_b + col * 16
+                  : k_in + (h - Hq) * ki_hs_b + t * ki_ts_b + col * 16;
+  };
+  auto dst_of = [&](int it) {
+    const int h = it / TPR, col = it % TPR;
+    return h < Hq ? q_out + h * qo_hs_b + t * qo_ts_b + col * 16
+                  : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b + col * 16;
+  };
+
+  // First item's loads go out before the table is built (one item per thread at Hq+Hkv=32, D=128).
+  int it = threadIdx.x;
+  vec16 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+  if (it < n_rot) {
+    const char* s = src_of(it);
+    a = ld16(s);
+    b = ld16(s + HALF_B);
+  }
+  if (threadIdx.x < HALF) cs_tab[threadIdx.x] = rope_shift_cos_sin(threadIdx.x, D, theta, (int)p);
+  __syncthreads();
+
+  for (; it < n_rot; it += kRopeThreads) {
+    if (it != (int)threadIdx.x) {
+      const char* s = src_of(it);
+      a = ld16(s);
+      b = ld16(s + HALF_B);
+    }
+    const int col = it % TPR;
+    float c[VEC], sn[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float2 cs = cs_tab[col * VEC + e];
+      c[e] = cs.x;
+      sn[e] = cs.y;
+    }
+    vec16 y1, y2;
+    rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
+    char* d = dst_of(it);
+    st16(d, y1);
+    st16(d + HALF_B, y2);
+  }
+  if (v_out != nullptr) {
+    for (int i = threadIdx.x; i < Hkv * CPR; i += kRopeThreads) {
+      const int h = i / CPR, c = i % CPR;
+      st16(v_out + h * vo_hs_b + row * vo_ts_b + c * 16, ld16(v_in + h * vi_hs_b + t * vi_ts_b + c * 16));
+    }
+  }
+}
+
+template <int DTYPE, int D>
+static void launch_rope(int n, hipStream_t st, char* qo, int64_t qo_hs, int64_t qo_ts, char* ko, int64_t ko_hs,
+                        int64_t ko_ts, char* vo, int64_t vo_hs, int64_t vo_ts, const int64_t* rows, int n_out,
+                        const char* qi, int64_t qi_hs, int64_t qi_ts, const char* ki, int64_t ki_hs, int64_t ki_ts,
+                        const char* vi, int64_t vi_hs, int64_t vi_ts, const int64_t* pos, int Hq, int Hkv,
+                        double theta, int32_t* err) {
+  hipLaunchKernelGGL((rope_qkv_kernel<DTYPE, D>), dim3((unsigned)n), dim3(kRopeThreads), 0, st, qo, qo_hs, qo_ts, ko,
+                     ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, qi, qi_hs, qi_ts, ki, ki_hs, ki_ts, vi, vi_hs,
+                     vi_ts, pos, Hq, Hkv, theta, err);
+}
+
+typedef void (*RopeLaunch)(int, hipStream_t, char*, int64_t, int64_t, char*, int64_t, int64_t, char*, int64_t,
+                           int64_t, const int64_t*, int, const char*, int64_t, int64_t, const char*, int64_t, int64_t,
+                           const char*, int64_t, int64_t, const int64_t*, int, int, double, int32_t*);
+
+static RopeLaunch pick_rope(int dtype, int head_dim) {
+#define CKV_CASE(DT, HD) \
+  if (dtype == DT && head_dim == HD) return &launch_rope<DT, HD>;
+  CKV_CASE(CKV_DTYPE_BF16, 64)
+  CKV_CASE(CKV_DTYPE_BF16, 128)
+  CKV_CASE(CKV_DTYPE_BF16, 256)
+  CKV_CASE(CKV_DTYPE_F32, 64)
+  CKV_CASE(CKV_DTYPE_F32, 128)
+  CKV_CASE(CKV_DTYPE_F32, 256)
+#undef CKV_CASE
+  return nullptr;
+}
+
+}  // namespace ckv
+
+extern "C" int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_token_stride, void* k_out,
+                                int64_t ko_head_stride, int64_t ko_token_stride, void* v_out, int64_t vo_head_stride,
+                                int64_t vo_token_stride, const int64_t* rows, int32_t n_out_rows, const void* q_in,
+                                int64_t qi_head_stride, int64_t qi_token_stride, const void* k_in,
+                                int64_t ki_head_stride, int64_t ki_token_stride, const void* v_in,
+                                int64_t vi_head_stride, int64_t vi_token_stride, const int64_t* positions,
+                                int32_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                int32_t dtype, double theta, int32_t* err, void* stream) {
+  using namespace ckv;
+  RopeLaunch fn = pick_rope(dtype, head_dim);
+  if (fn == nullptr || q_out == nullptr || q_in == nullptr || k_out == nullptr || k_in == nullptr ||
+      positions == nullptr || (v_out == nullptr) != (v_in == nullptr))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_tokens < 0 || n_q_heads < 0 || n_kv_heads <= 0 || n_out_rows < 0 || !(theta > 0.0))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (rows == nullptr && n_out_rows < n_tokens) return CKV_ERR_OUT_OF_RANGE;
+  const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
+  const int64_t strides[] = {qo_head_stride, qo_token_stride, ko_head_stride, ko_token_stride, vo_head_stride,
+                             vo_token_stride, qi_head_stride, qi_token_stride, ki_head_stride, ki_token_stride,
+                             vi_head_stride, vi_token_stride};
+  for (int64_t s : strides)
+    if ((s * eb) % 16) return CKV_ERR_INVALID_ARGUMENT;  // every row starts on a 16-byte boundary
+  if (((uintptr_t)q_out | (uintptr_t)q_in | (uintptr_t)k_out | (uintptr_t)k_in | (uintptr_t)v_out | (uintptr_t)v_in) %
+      16)
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_tokens == 0) return CKV_OK;
+  if (n_tokens > 0x7fffffff) return CKV_ERR_TOO_LARGE;
+  fn(n_tokens, (hipStream_t)stream, (char*)q_out, qo_head_stride * eb, qo_token_stride * eb, (char*)k_out,
+     ko_head_stride * eb, ko_token_stride * eb, (char*)v_out, vo_head_stride * eb, vo_token_stride * eb, rows,
+     n_out_rows, (const char*)q_in, qi_head_stride * eb, qi_token_stride * eb, (const char*)k_in,
+     ki_head_stride * eb, ki_token_stride * eb, (const char*)v_in, vi_head_stride * eb, vi_token_stride * eb,
+     positions, n_q_heads, n_kv_heads, theta, err);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}

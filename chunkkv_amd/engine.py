@@ -4,28 +4,30 @@ hand-written gfx950 kernels.
 Public surface = src/chunkkv/engine/torch_engine.py:18-207: constructor ``(model, tokenizer)``,
 ``load(repo, dtype)``, ``prefill(tokens, placements, config, logits_from) -> PrefillResult``,
 ``generate``, ``last_logprobs``, ``sync``, ``clear_cache``, ``shift_keys``, ``tokenizer``.
-The model's GEMMs, RMSNorm, MLP and SDPA attention stay on PyTorch-ROCm (chunkkv_amd.model).
-The KV repair runs on the HIP kernels:
+The model's GEMMs, RMSNorm and MLP stay on PyTorch-ROCm (chunkkv_amd.model). The KV repair,
+the fresh-token RoPE and the attention run on the HIP kernels:
 
   reference (torch_engine.py)                        here
-  base_kv (:96-103; ~13 launches per placement and   layer 0: one ckv_assemble_layer launch that
-    layer, zero-filled cache) + K[:, :, active] = k    writes every row once (fresh if active, else
-    (:155-156), every layer                            the re-rotated cached row)
-                                                     layer 1: ckv_assemble_layer with no active set
-                                                       (the base cache), then the selection below,
-                                                       then ckv_scatter_rows of the kept rows
-                                                     layers 2..L-1: right after the selection, one
-                                                       ckv_rerope_gather_layers launch on a side
-                                                       stream writes the cached rows of every
-                                                       position the selection dropped, for all of
-                                                       them at once, while the main stream computes
-                                                       and scatters each layer's fresh rows (the
-                                                       two write disjoint rows); layer 2's attention
-                                                       waits for the side stream
+  _qkv + _rope/_rotate (:61-66, :53-54, :46-51)      one q|k|v GEMM (stacked weights), then
+    and K[:, :, active] = k, V[...] = v (:155-156)     ckv_rope_qkv: q rotated into the layout the
+                                                       attention reads, k rotated and v copied
+                                                       straight into the cache rows of the active
+                                                       positions (layer 1: into tensors, for the
+                                                       deviation; its kept rows then go through
+                                                       ckv_scatter_rows)
+  base_kv (:96-103; ~13 launches per placement and   ckv_rerope_gather_layers, on a side stream:
+    layer, zero-filled cache, every layer)             at the start, layer 1's base cache (and
+                                                       layer 0's rows of exact placements);
+                                                       right after the selection, one launch for
+                                                       the cached rows of every position the
+                                                       selection dropped, layers 2..L-1 at once.
+                                                       Rows the fresh K/V overwrite are never
+                                                       gathered; the main stream waits only
+                                                       before the attention that reads them
   deviation (:117-124)                               ckv_deviation (one wavefront per token)
   rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
     one .item() per chunk)                             nothing back unless a threshold is set
-  mask + SDPA (:157, :68-72)                          ckv_attention_active: matrix-core
+  mask + SDPA (:157, :68-72)                         ckv_attention_active: matrix-core
                                                        attention masked by the active positions
                                                        (bf16, head_dim 64/128)
 All layers' caches live in one (L, 1, H, N, D) slab; PrefillResult.keys/values are its views.
@@ -73,8 +75,8 @@ class HipEngine(DecoderPieces):
         if attention not in ("fused", "reference"):
             raise ValueError("attention must be 'fused' or 'reference'")
         self.attention = attention
-        # overlap=False builds layers 2..L-1 with one ckv_assemble_layer launch each on the main
-        # stream instead of the side-stream gather + per-layer scatters (same bytes, same rows).
+        # overlap=False issues the cached-row gathers on the main stream, in order, instead of on
+        # a side stream (same launches, same rows).
         self.overlap = overlap
         self._side: torch.cuda.Stream | None = None
         # Set to a dict to record the layer-1 selection inputs/outputs (device tensors) of the
@@ -89,6 +91,17 @@ class HipEngine(DecoderPieces):
         self.inv_freq = ops.inv_freq(self.head_dim, self.theta, self.device)
         # ckv_attention_active covers bf16 caches with head_dim 64 or 128; other models keep SDPA
         self._native_attention = self.kv_dtype == torch.bfloat16 and self.head_dim in (64, 128)
+        # One projection GEMM per layer for q, k and v (their weights stacked once, here); its
+        # token-major output feeds ckv_rope_qkv directly.
+        self._w_qkv, self._b_qkv = [], []
+        with torch.no_grad():
+            for layer in self.layers:
+                a = layer.self_attn
+                self._w_qkv.append(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0).contiguous())
+                biases = [a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]
+                self._b_qkv.append(None if all(b is None for b in biases) else torch.cat(
+                    [b if b is not None else torch.zeros(w.shape[0], dtype=w.dtype, device=w.device)
+                     for b, w in zip(biases, (a.q_proj.weight, a.k_proj.weight, a.v_proj.weight))]))
 
     @classmethod
     def load(cls, repo: str, dtype=torch.bfloat16) -> "HipEngine":
@@ -97,9 +110,11 @@ class HipEngine(DecoderPieces):
         model = AutoModelForCausalLM.from_pretrained(repo, dtype=dtype).to("cuda")
         return cls(model, AutoTokenizer.from_pretrained(repo))
 
-    def _attend_active(self, layer, h, q, K, V, active, ar, masks: dict, err=None):
-        """Attention of the active rows over the whole cache: row i sees positions <= active[i]."""
+    def _attend_active(self, layer, h, q_tm, K, V, active, ar, masks: dict, err=None):
+        """Attention of the active rows over the whole cache: row i sees positions <= active[i].
+        q_tm: (1, n, Hq, D) token-major, as ckv_rope_qkv writes it."""
         n_act, N = active.shape[0], ar.shape[0]
+        q = q_tm.transpose(1, 2)  # (1, Hq, n, D) view
         key = (active.data_ptr(), n_act)
         if self.attention == "reference":
             return self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :])
@@ -181,20 +196,30 @@ class HipEngine(DecoderPieces):
             for a, o in zip(parts, offs)
         ]
 
-    def _gather_dropped(self, k_slab, v_slab, tab_d, segs_d, n_segs, max_seg, keep_rank, err) -> torch.cuda.Event:
-        """Layers 2..L-1: cached rows of the positions the selection dropped, one launch on the
-        side stream, ordered after the selection. Returns the event that marks its end."""
+    def _project(self, li: int, x: torch.Tensor):
+        """q|k|v projection of layer li in one GEMM: views (1, n, H*D) of its token-major output."""
+        lin = F.linear(x, self._w_qkv[li], self._b_qkv[li])
+        qd, kd = self.n_heads * self.head_dim, self.n_kv * self.head_dim
+        return lin[..., :qd], lin[..., qd : qd + kd], lin[..., qd + kd :]
+
+    def _gather(self, k_slab, v_slab, tab_d, segs_d, n_segs, max_seg, layers, skip, err):
+        """Cached rows of layers [layers) that no fresh row of that layer overwrites (skip[p] >= 0
+        marks the active positions; skip None = every cached row), one launch. With overlap on, it
+        runs on the side stream, ordered after everything issued so far; the returned event marks
+        its end (None when it ran on the main stream)."""
+        if not self.overlap:
+            ops.rerope_gather(k_slab, v_slab, tab_d, segs_d, n_segs, max_seg, self.theta, err, layers=layers, skip=skip)
+            return None
         main = torch.cuda.current_stream(self.device)
         if self._side is None:
             self._side = torch.cuda.Stream(device=self.device)  # default priority
         side = self._side
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            ops.rerope_gather(k_slab, v_slab, tab_d, segs_d, n_segs, max_seg, self.theta, err,
-                              layers=(2, k_slab.shape[0]), skip=keep_rank)
+            ops.rerope_gather(k_slab, v_slab, tab_d, segs_d, n_segs, max_seg, self.theta, err, layers=layers, skip=skip)
             done = torch.cuda.Event()
             done.record(side)
-        for t in (k_slab, v_slab, tab_d, segs_d, keep_rank, err):
+        for t in (k_slab, v_slab, tab_d, segs_d, err) + ((skip,) if skip is not None else ()):
             t.record_stream(side)  # allocated on the main stream, read or written on the side stream
         return done
 
@@ -221,9 +246,10 @@ class HipEngine(DecoderPieces):
         flags_d, local_d, active_d, segs_d, spans_d, tab_d = self._upload(
             [plan.flags, local_np, active_np.astype(np.int64), plan.all_segments.reshape(-1), plan.spans.reshape(-1), tab]
         )
-        n_cached_segs, n_all_segs = len(plan.segments), len(plan.all_segments)
+        n_cached_segs = len(plan.segments)
 
-        # Every row of every layer is written by the assemble / gather + scatter below.
+        # Every row of every layer is written below: active rows by ckv_rope_qkv (layer 1: by
+        # ckv_scatter_rows), the other cached rows by the gathers.
         k_slab = torch.empty((n_layers, 1, H, N, D), dtype=self.kv_dtype, device=dev)
         v_slab = torch.empty_like(k_slab)
         err = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -231,26 +257,32 @@ class HipEngine(DecoderPieces):
         values_out = list(v_slab.unbind(0))
 
         active = active_d
-        local_cur = local_d  # local index map of the current active set
         h = self.inner.embed_tokens(torch.tensor([tokens], device=dev))[:, active]
         ar = torch.arange(N, device=dev)
         masks: dict = {}
         sel = None
-        gathered = None  # event: the side-stream gather of layers 2..L-1 has finished
-        for li, layer in enumerate(self.layers):
-            q, k, v = self._qkv(layer.self_attn, layer.input_layernorm(h), active)
-            K, V = keys_out[li], values_out[li]
-            if gathered is not None:
-                ops.scatter_rows(K, V, k, v, active, err)
-                if li == 2:
-                    torch.cuda.current_stream(dev).wait_event(gathered)
-            elif li != 1 or not select_layer:
-                ops.assemble_layer(K, V, tab_d, n_layers, li, segs_d, n_all_segs, plan.max_all_seg_tokens, k, v,
-                                   local_cur, self.theta, err)
+        ready: dict[int, torch.cuda.Event | None] = {}  # layer -> its cached rows are in place
+        gather = lambda layers, skip: self._gather(  # noqa: E731
+            k_slab, v_slab, tab_d, segs_d, n_cached_segs, plan.max_seg_tokens, layers, skip, err)
+        # Cached rows that do not depend on the model go out first, overlapped with layer 0:
+        # with the selection, layer 0's rows outside its active set (exact placements) and layer
+        # 1's base cache (every cached row); without it, every layer's rows outside the one
+        # active set. Layers 2.. follow right after the selection.
+        if n_cached_segs:
+            if select_layer:
+                if plan.exact.any():
+                    ready[0] = gather((0, 1), local_d)
+                ready[1] = gather((1, 2), None)
             else:
-                # base cache of layer 1 (cached rows re-rotated), compared with the fresh rows
-                ops.assemble_layer(K, V, tab_d, n_layers, li, segs_d, n_cached_segs, plan.max_seg_tokens, None, None,
-                                   None, self.theta, err)
+                ready[0] = gather((0, n_layers), local_d)
+        for li, layer in enumerate(self.layers):
+            q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
+            K, V = keys_out[li], values_out[li]
+            if li == 1 and select_layer:
+                q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, err=err)
+                v = v_in.view(1, -1, H, D).transpose(1, 2)
+                if ready.get(1) is not None:
+                    torch.cuda.current_stream(dev).wait_event(ready[1])
                 diff, norm = ops.deviation(k, v, K, V, flags_d, local_d, err)
                 sel = ops.select(diff, norm, flags_d, local_d, spans_d, config.escalate_threshold)
                 if config.escalate_threshold is None and not plan.has_overlap:
@@ -264,13 +296,17 @@ class HipEngine(DecoderPieces):
                     self.trace.update(k=k, v=v, K=K.clone(), V=V.clone(), flags=flags_d, local=local_d, spans=spans_d,
                                       diff=diff, norm=norm, sel=sel, n_keep=n_keep)
                 rows = sel.keep_local[:n_keep]
-                h, q, k, v = h.index_select(1, rows), q.index_select(2, rows), k.index_select(2, rows), v.index_select(2, rows)
+                h, q, k, v = h.index_select(1, rows), q.index_select(1, rows), k.index_select(2, rows), v.index_select(2, rows)
                 active = sel.keep_abs[:n_keep]
-                local_cur = sel.keep_rank
                 ops.scatter_rows(K, V, k, v, active, err)
-                if self.overlap and n_layers > 2 and n_cached_segs > 0:
-                    gathered = self._gather_dropped(k_slab, v_slab, tab_d, segs_d, n_cached_segs, plan.max_seg_tokens,
-                                                    sel.keep_rank, err)
+                if n_cached_segs and n_layers > 2:
+                    ready[2] = gather((2, n_layers), sel.keep_rank)
+            else:
+                # RoPE of q/k with k and v written straight into this layer's cache rows
+                q, _ = ops.rope_qkv(q_in, k_in, v_in, active, self.n_heads, H, D, self.theta, k_out=K, v_out=V,
+                                    rows=active, err=err)
+                if ready.get(li) is not None:
+                    torch.cuda.current_stream(dev).wait_event(ready[li])
             h = self._attend_active(layer, h, q, K, V, active, ar, masks, err)
 
         n_want = N - logits_from

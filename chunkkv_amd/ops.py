@@ -356,3 +356,79 @@ def attention_active(
         "ckv_attention_active",
     )
     return out
+
+
+def _heads_view(t: torch.Tensor, n_heads: int, head_dim: int) -> tuple:
+    """(pointer, head stride, token stride) of a (1, n, n_heads*D)-like token-major tensor or a
+    (1, H, n, D) tensor with contiguous rows."""
+    if t.dim() == 3:
+        if t.stride(2) != 1 or t.shape[2] != n_heads * head_dim:
+            raise ValueError("projection output must have contiguous rows of n_heads * head_dim")
+        return _ptr(t), head_dim, t.stride(1)
+    if t.dim() == 4 and t.shape[1] == n_heads and t.shape[3] == head_dim and t.stride(3) == 1:
+        return _ptr(t), t.stride(1), t.stride(2)
+    raise ValueError(f"unsupported layout {tuple(t.shape)} / {t.stride()}")
+
+
+def rope_qkv(
+    q_in: torch.Tensor,
+    k_in: torch.Tensor,
+    v_in: torch.Tensor | None,
+    positions: torch.Tensor,
+    n_q_heads: int,
+    n_kv_heads: int,
+    head_dim: int,
+    theta: float,
+    *,
+    q_out: torch.Tensor | None = None,
+    k_out: torch.Tensor | None = None,
+    v_out: torch.Tensor | None = None,
+    rows: torch.Tensor | None = None,
+    err: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fresh-token RoPE (torch_engine.py:61-66, :53-54, :46-51) of q and k, v copied alongside.
+
+    q_in/k_in/v_in: projection outputs, token-major (1, n, H*D) views or (1, H, n, D) tensors.
+    Returns (q_out, k_out): q_out (1, n, Hq, D) token-major (the layout attention_active reads)
+    unless given; k_out (1, Hkv, n, D) unless given. With rows (int64 (n,)), k/v land in rows
+    rows[t] of k_out/v_out, e.g. the layer's cache (1, Hkv, N, D): the fresh-row scatter fused in.
+    """
+    _dev(q_in, k_in, positions)
+    n = positions.numel()
+    dev = q_in.device
+    if positions.dtype != torch.int64:
+        raise ValueError("positions must be int64")
+    positions = positions.contiguous()
+    if q_out is None:
+        q_out = torch.empty((1, n, n_q_heads, head_dim), dtype=q_in.dtype, device=dev)
+    if k_out is None:
+        if rows is not None:
+            raise ValueError("rows needs k_out (the cache)")
+        k_out = torch.empty((1, n_kv_heads, n, head_dim), dtype=q_in.dtype, device=dev)
+    n_out = k_out.shape[2] if k_out.dim() == 4 else k_out.shape[1]
+    if rows is not None:
+        _dev(q_in, rows)
+        if rows.dtype != torch.int64 or rows.numel() != n:
+            raise ValueError("rows must be int64 (n,)")
+        rows = rows.contiguous()
+    if (v_in is None) != (v_out is None):
+        raise ValueError("v_in and v_out go together")
+    for t in (q_in, k_in, q_out, k_out) + ((v_in, v_out) if v_in is not None else ()):
+        if t.dtype != q_in.dtype:
+            raise TypeError("q/k/v and outputs must share a dtype")
+    if q_out.shape != (1, n, n_q_heads, head_dim) or not q_out.is_contiguous():
+        raise ValueError("q_out must be contiguous (1, n, Hq, D), token-major")
+    qo = _heads_view(q_out.view(1, n, n_q_heads * head_dim), n_q_heads, head_dim)
+    qi, ki = _heads_view(q_in, n_q_heads, head_dim), _heads_view(k_in, n_kv_heads, head_dim)
+    ko = _heads_view(k_out, n_kv_heads, head_dim)
+    vi = _heads_view(v_in, n_kv_heads, head_dim) if v_in is not None else (None, 0, 0)
+    vo = _heads_view(v_out, n_kv_heads, head_dim) if v_out is not None else (None, 0, 0)
+    check(
+        lib().ckv_rope_qkv(
+            qo[0], qo[1], qo[2], ko[0], ko[1], ko[2], vo[0], vo[1], vo[2], _ptr(rows), n_out, qi[0], qi[1], qi[2],
+            ki[0], ki[1], ki[2], vi[0], vi[1], vi[2], _ptr(positions), n, n_q_heads, n_kv_heads, head_dim,
+            dtype_code(q_in.dtype), float(theta), _ptr(err), _stream(dev),
+        ),
+        "ckv_rope_qkv",
+    )
+    return q_out, k_out

@@ -242,6 +242,29 @@ int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride,
                          void* stream);
 
 /*
+ * Fresh-token RoPE of projected q/k rows, with the v rows copied alongside:
+ *   q_out[h, t] = rope(q_in[h, t], positions[t])                 h < n_q_heads
+ *   k_out[h, r] = rope(k_in[h, t], positions[t]),  v_out[h, r] = v_in[h, t]      h < n_kv_heads
+ * with r = rows[t] (rows != NULL: e.g. straight into the cache rows of the active positions,
+ * r < n_out_rows) or r = t (rows == NULL). rope(x, p) rotates the halves of x by the fp32 angles
+ * fl32(fl32(p) * inv_freq_i) with correctly rounded fp32 cos/sin, fp32 products and sums each
+ * rounded once, one rounding to dtype: the rotation ckv_shift_keys applies for a shift by p.
+ * Element (h, t, d) of each tensor is at base + h*head_stride + t*token_stride + d (elements;
+ * rows contiguous and 16-byte aligned), so projection outputs can be passed as token-major views.
+ * v_out and v_in are both NULL to skip the copy. dtype bf16 or f32, head_dim 64, 128 or 256.
+ * Replaces: _qkv/_rope/_rotate (torch_engine.py:61-66, :53-54, :46-51) and the scatter of k/v
+ * into the cache (:155-156).
+ */
+int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_token_stride, void* k_out,
+                     int64_t ko_head_stride, int64_t ko_token_stride, void* v_out, int64_t vo_head_stride,
+                     int64_t vo_token_stride, const int64_t* rows, int32_t n_out_rows, const void* q_in,
+                     int64_t qi_head_stride, int64_t qi_token_stride, const void* k_in,
+                     int64_t ki_head_stride, int64_t ki_token_stride, const void* v_in,
+                     int64_t vi_head_stride, int64_t vi_token_stride, const int64_t* positions,
+                     int32_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                     int32_t dtype, double theta, int32_t* err, void* stream);
+
+/*
  * Attention of the active rows over the whole cache with the causal mask given by positions:
  *   out[i, h, :] = softmax_j( scale * q[h, i, :] . K[h / G, j, :] ) V[h / G, j, :],
  *   j ranging over [0, positions[i]], G = n_q_heads / n_kv_heads.

@@ -7,6 +7,7 @@
  *   ckvo_inv_freq        src/chunkkv/engine/torch_engine.py:33 (rerope.py:31-33)
  *   ckvo_rerope_gather   torch_engine.py:46-51 (_rotate), :56-59 (shift_keys), :96-103 (base_kv)
  *   ckvo_shift_keys      torch_engine.py:56-59
+ *   ckvo_rope            torch_engine.py:53-54 with :46-51
  *   ckvo_deviation       torch_engine.py:117-124
  *   ckvo_select          torch_engine.py:125-153
  *   ckvo_scatter_rows    torch_engine.py:155-156
@@ -26,6 +27,7 @@
  * one bf16 ulp), fp64 brute force for the deviation, an independent numpy lexsort and torch's
  * stable argsort for the selection, and the reference's closed-form stats.
  */
+#include <limits.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -115,6 +117,31 @@ static void shift_tables(int D, double theta, int32_t delta, float* c, float* s)
     c[i] = (float)cos((double)ang); /* correctly rounded fp32 cos/sin of the fp32 angle */
     s[i] = (float)sin((double)ang);
   }
+}
+
+/* Fresh-token RoPE: torch_engine.py:53-54 (_rope, angles = positions.float()[:, None] *
+ * inv_freq[None, :]) with _rotate (:46-51). Row t of every head is rotated by the fp32 angle
+ * fl32(fl32(pos[t]) * inv_freq_i), i.e. the rotation of a shift by pos[t]; the formula is applied
+ * at every position (no shortcut at 0, as torch). Element (h, t, d) at h*hs + t*ts + d. */
+int ckvo_rope(void* dst, int64_t dst_hs, int64_t dst_ts, const void* src, int64_t src_hs, int64_t src_ts,
+              const int64_t* pos, int n_heads, int n_rows, int D, int dt, double theta) {
+  if (D <= 0 || D > 2048 || (D & 1)) return 1;
+  float c[1024], s[1024];
+  const int half = D / 2;
+  for (int t = 0; t < n_rows; ++t) {
+    if (pos[t] < INT32_MIN || pos[t] > INT32_MAX) return 2;
+    shift_tables(D, theta, (int32_t)pos[t], c, s);
+    for (int h = 0; h < n_heads; ++h) {
+      const int64_t so = (int64_t)h * src_hs + (int64_t)t * src_ts, dof = (int64_t)h * dst_hs + (int64_t)t * dst_ts;
+      for (int i = 0; i < half; ++i) {
+        const float x1 = ld(src, so + i, dt), x2 = ld(src, so + half + i, dt);
+        const float a = x1 * c[i], b = x2 * s[i], d = x1 * s[i], e = x2 * c[i];
+        st(dst, dof + i, dt, a - b);
+        st(dst, dof + half + i, dt, d + e);
+      }
+    }
+  }
+  return 0;
 }
 
 /* keys (n_heads, n_rows, D) with head strides in elements; dst may equal src. */

@@ -14,6 +14,9 @@ Parity status of each function (how it is pinned is in tests/test_oracle.py):
   select          pinned: numpy lexsort and torch stable argsort of the reference expression,
                   closed-form budgets/stats of tests/test_mlx_engine.py
   scatter_rows    pinned: brute-force Python loop on small shapes
+  rope            pinned: equal positions = shift_keys by that position (bit-exact), torch's
+                  own _rope/_rotate expression on the CPU within one bf16 ulp, fp64 rotation
+                  within one bf16 ulp, composition rope(rope(x, a), b) ~ rope(x, a + b)
   attention_active pinned: torch's CPU scaled_dot_product_attention with the reference's boolean
                   mask and enable_gqa (the reference call itself), fp32, on small shapes
 """
@@ -48,6 +51,7 @@ def lib() -> ctypes.CDLL:
             "ckvo_deviation": [P, L, L, P, L, L, P, P, L, P, P, I, I, I, I, I, P, P],
             "ckvo_select": [P, P, P, P, I, P, I, I, D, P, P, P, P, P],
             "ckvo_scatter_rows": [P, P, L, P, L, L, P, L, L, P, I, I, I, I, I],
+            "ckvo_rope": [P, L, L, P, L, L, P, I, I, I, I, D],
         }
         for name, args in sig.items():
             fn = getattr(_lib, name)
@@ -147,6 +151,17 @@ def rerope_gather(
     return lib().ckvo_rerope_gather(
         _p(k_dst), _p(v_dst), H * N * D, N * D, _p(tab), _p(segs), len(segs), n_layers, H, N, D, dt_of(k_dst), float(theta)
     )
+
+
+def rope(x: np.ndarray, positions: np.ndarray, theta: float) -> np.ndarray:
+    """x (H, n, D) -> rows rotated to their positions (torch_engine.py:53-54, :46-51)."""
+    x = np.ascontiguousarray(x)
+    H, n, D = x.shape
+    pos = np.ascontiguousarray(positions, dtype=np.int64)
+    out = np.empty_like(x)
+    rc = lib().ckvo_rope(_p(out), n * D, D, _p(x), n * D, D, _p(pos), H, n, D, dt_of(x), float(theta))
+    assert rc == 0
+    return out
 
 
 def deviation(k: np.ndarray, v: np.ndarray, K: np.ndarray, V: np.ndarray, flags: np.ndarray, local: np.ndarray):

@@ -1,0 +1,89 @@
+"""GPU parity of the fused fresh-token RoPE kernel (ckv_rope_qkv) against the oracle: q and k
+rotated bit-exactly (same correctly rounded cos/sin, same fp32 operation order), v copied, rows
+placed where `rows` says, other cache rows untouched."""
+
+import numpy as np
+import pytest
+import torch
+
+from chunkkv_amd import _native, ops
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+THETA = 1e6
+
+
+def _proj(rng, n, Hq, Hkv, D, bf16):
+    """A fused q|k|v projection output (1, n, (Hq + 2 Hkv) D), token-major like F.linear's."""
+    a = rng.standard_normal((1, n, (Hq + 2 * Hkv) * D)).astype(np.float32) * 3
+    return O.f32_to_bf16_bits(a) if bf16 else a
+
+
+def _split(lin, Hq, Hkv, D):
+    q = lin[..., : Hq * D]
+    k = lin[..., Hq * D : (Hq + Hkv) * D]
+    v = lin[..., (Hq + Hkv) * D :]
+    return q, k, v
+
+
+def _heads(a, H, D):  # (1, n, H*D) -> (H, n, D)
+    return np.ascontiguousarray(a[0].reshape(a.shape[1], H, D).transpose(1, 0, 2))
+
+
+@pytest.mark.parametrize("bf16,D,Hq,Hkv", [(True, 128, 28, 4), (True, 64, 14, 2), (False, 128, 8, 2), (True, 256, 4, 1)])
+def test_rope_qkv_tensor_mode_bit_exact(bf16, D, Hq, Hkv):
+    rng = np.random.default_rng(D + Hq)
+    n = 333
+    lin = _proj(rng, n, Hq, Hkv, D, bf16)
+    pos = rng.integers(0, 40000, n)
+    pos[0] = 0
+    lt = O.from_numpy(lin, DEV)
+    q_in, k_in, v_in = _split(lt, Hq, Hkv, D)
+    q_out, k_out = ops.rope_qkv(q_in, k_in, None, torch.from_numpy(pos).to(DEV), Hq, Hkv, D, THETA)
+    torch.cuda.synchronize()
+    qn, kn, _ = _split(lin, Hq, Hkv, D)
+    want_q = O.rope(_heads(qn, Hq, D), pos, THETA)  # (Hq, n, D)
+    want_k = O.rope(_heads(kn, Hkv, D), pos, THETA)
+    np.testing.assert_array_equal(O.to_numpy(q_out)[0].transpose(1, 0, 2), want_q)
+    np.testing.assert_array_equal(O.to_numpy(k_out)[0], want_k)
+
+
+def test_rope_qkv_scatter_into_cache():
+    """k and v land in the cache rows of their positions; every other row keeps its value."""
+    rng = np.random.default_rng(7)
+    Hq, Hkv, D, N, n = 28, 4, 128, 1000, 297
+    lin = _proj(rng, n, Hq, Hkv, D, True)
+    pos = np.sort(rng.choice(N, n, replace=False))
+    lt = O.from_numpy(lin, DEV)
+    q_in, k_in, v_in = _split(lt, Hq, Hkv, D)
+    K = torch.full((1, Hkv, N, D), -3.0, dtype=torch.bfloat16, device=DEV)
+    V = torch.full_like(K, -3.0)
+    pt = torch.from_numpy(pos).to(DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    q_out, _ = ops.rope_qkv(q_in, k_in, v_in, pt, Hq, Hkv, D, THETA, k_out=K, v_out=V, rows=pt, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    qn, kn, vn = _split(lin, Hq, Hkv, D)
+    Kw = np.full((Hkv, N, D), O.f32_to_bf16_bits(np.float32([-3.0]))[0], dtype=np.uint16)
+    Vw = Kw.copy()
+    Kw[:, pos] = O.rope(_heads(kn, Hkv, D), pos, THETA)
+    Vw[:, pos] = _heads(vn, Hkv, D)
+    np.testing.assert_array_equal(O.to_numpy(K)[0], Kw)
+    np.testing.assert_array_equal(O.to_numpy(V)[0], Vw)
+    np.testing.assert_array_equal(O.to_numpy(q_out)[0].transpose(1, 0, 2), O.rope(_heads(qn, Hq, D), pos, THETA))
+
+
+def test_rope_qkv_flags_bad_row():
+    rng = np.random.default_rng(8)
+    Hq, Hkv, D, N, n = 4, 2, 64, 50, 5
+    lt = O.from_numpy(_proj(rng, n, Hq, Hkv, D, True), DEV)
+    q_in, k_in, v_in = _split(lt, Hq, Hkv, D)
+    K = torch.zeros((1, Hkv, N, D), dtype=torch.bfloat16, device=DEV)
+    V = torch.zeros_like(K)
+    rows = torch.tensor([0, 1, 2, 3, N], dtype=torch.int64, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.rope_qkv(q_in, k_in, v_in, rows.clone(), Hq, Hkv, D, THETA, k_out=K, v_out=V, rows=rows, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == _native.DEVICE_ERR_RANGE
+    assert int(K[0, :, 4:].count_nonzero()) == 0

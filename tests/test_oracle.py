@@ -383,3 +383,48 @@ def test_attention_active_closed_forms():
     q[0, 2, 0] = 1.0
     out = O.attention_active(q, K, V, np.array([0, 4, 9]))
     np.testing.assert_allclose(out[2, 0], V[0, 7])
+
+
+def test_rope_equal_positions_is_shift_keys():
+    """Every row at position p is a shift by p (the same fp32 angle, the same rotation)."""
+    rng = np.random.default_rng(31)
+    x = O.f32_to_bf16_bits(rng.standard_normal((3, 20, 128)).astype(np.float32))
+    for p in (1, 37, 4096, 32767, -5):
+        got = O.rope(x, np.full(20, p), 1e6)
+        np.testing.assert_array_equal(got, O.shift_keys(x, p, 1e6))
+
+
+def test_rope_matches_reference_torch_expression():
+    """torch_engine.py:53-54 + :46-51 on the CPU in torch (its own fp32 cos/sin): within one bf16
+    ulp; position 0 goes through the formula (signed zeros included) like torch."""
+    rng = np.random.default_rng(32)
+    H, n, D, theta = 4, 300, 128, 1e6
+    x = O.f32_to_bf16_bits(rng.standard_normal((H, n, D)).astype(np.float32))
+    x[0, 0, :4] = O.f32_to_bf16_bits(np.float32([-0.0, 0.0, -0.0, 1.0]))
+    pos = np.concatenate([[0], np.sort(rng.choice(np.arange(1, 32768), n - 1, replace=False))])
+    got = O.rope(x, pos, theta)
+    inv = torch.from_numpy(O.inv_freq(D, theta))
+    xt = O.from_numpy(x)
+    ang = torch.from_numpy(pos).float()[:, None] * inv[None, :]
+    cos, sin = ang.cos(), ang.sin()
+    x32 = xt.float()
+    x1, x2 = x32[..., : D // 2], x32[..., D // 2 :]
+    want = O.to_numpy(torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1).to(torch.bfloat16))
+    assert bf16_ulp_distance(got, want).max() <= 1
+    np.testing.assert_array_equal(got[:, 0], want[:, 0])  # position 0: cos 1, sin 0 exactly
+
+
+def test_rope_fp64_rotation_and_composition():
+    rng = np.random.default_rng(33)
+    H, n, D, theta = 2, 64, 64, 1e4
+    x = rng.standard_normal((H, n, D)).astype(np.float32)
+    pos = rng.integers(0, 20000, n)
+    got = O.rope(x, pos, theta)
+    inv = O.inv_freq(D, theta).astype(np.float64)
+    ang = (pos.astype(np.float32)[:, None] * O.inv_freq(D, theta)[None, :]).astype(np.float64)
+    x1, x2 = x[..., : D // 2].astype(np.float64), x[..., D // 2 :].astype(np.float64)
+    want = np.concatenate([x1 * np.cos(ang) - x2 * np.sin(ang), x1 * np.sin(ang) + x2 * np.cos(ang)], -1)
+    np.testing.assert_allclose(got, want, atol=2e-5, rtol=0)
+    del inv
+    a, b = rng.integers(0, 500, n), rng.integers(0, 500, n)
+    np.testing.assert_allclose(O.rope(O.rope(x, a, theta), b, theta), O.rope(x, a + b, theta), atol=1e-4, rtol=0)
