@@ -8,27 +8,30 @@ shuffled positions (each chunk computed at its own original offset, so every pla
 its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
 
 A step is one request's whole KV repair with every input already resident in HBM, issued as
-HipEngine issues it (31 launches): layer 0 in one assemble launch (every cache row written once,
-fresh if the position is active, else the re-rotated cached row); layer 1 as the base cache, the
-deviation and the selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows) and the
-scatter of the kept rows; then, forked onto a second stream, one gather launch for the cached
-rows of the 5280 dropped positions of layers 2-27, while the first stream scatters the kept rows
-of layers 2-27 (disjoint rows; the streams join at the end of the step). The unit of work is one
-request's KV repair as the reference's op sequence moves it (re-RoPE + gather of every cached
-row of all 28 layers, the layer-0 scatter of all 8256 rows, the deviation, the scatters of layers
-1-27):
+HipEngine issues it (32 launches on two streams): layer 1's base cache gathered on the second
+stream while the first writes layer 0's fresh rows into its cache; the layer-1 deviation, the
+selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows) and the scatter of the kept
+rows; then the gather of the cached rows of the 5280 dropped positions of layers 2-27 in one
+launch on the second stream while the first writes the fresh rows of layers 2-27 (disjoint rows;
+the streams join at the end). The fresh rows are written by ckv_rope_qkv as in the engine (k
+rotated to its position, v copied, straight into the cache rows); the engine's launch also
+rotates q for the attention, which the step leaves out as the reference's KV-repair bytes do.
+The unit of work is one request's KV repair as the reference's op sequence moves it (re-RoPE +
+gather of every cached row of all 28 layers, the layer-0 scatter of all 8256 rows, the
+deviation, the scatters of layers 1-27):
     gather          28 x 24 x 320 x 4 heads x 128 x 2 B x 2 (K,V) x 2 (r+w) =   880,803,840
     deviation       8256 x (4 rows x 1 KiB) + 8256 x 8 B                       =    33,882,624
     scatter L0      8256 x 4096 B                                              =    33,816,576
     scatter L1-27   27 x 2976 x 4096 B                                         =   329,121,792
     total                                                                      = 1,277,624,832
 `value` = that total / measured time per step (GB/s), the step replayed from a HIP graph (the
-eager time, launch-bound from Python, is reported as ms_per_step_eager, and the same rows built
-on one stream with an assemble launch per layer as ms_per_step_one_stream); the fused flow
-itself moves 990,577,152 B per step (moved_bytes_per_step, moved_gbs). `roofline` is the
-dominant kernel (the gather of the dropped rows of layers 2-27, 562,298,880 B per launch) timed
-live with HIP events around a burst of back-to-back launches on the launch stream. Inputs rotate
-between two independent copies so consecutive steps do not hit in the 256 MB MALL.
+eager time, launch-bound from Python, is reported as ms_per_step_eager, the same launches on one
+stream as ms_per_step_one_stream, and layers 0 and 2-27 built by one assemble launch each as
+ms_per_step_assemble_variant); the fused flow itself moves 990,577,152 B per step
+(moved_bytes_per_step, moved_gbs). `roofline` is the dominant kernel (the gather of the dropped
+rows of layers 2-27, 562,298,880 B per launch) timed live with HIP events around a burst of
+back-to-back launches on the launch stream. Inputs rotate between two independent copies so
+consecutive steps do not hit in the 256 MB MALL.
 
 Besides the bandwidth line, the run measures blend-prefill TTFT p50 (prefill + last_logprobs,
 the bracket of the reference's bench/replay.py:32-35) over seeded requests of the same shape on
@@ -169,8 +172,15 @@ class RepairWorkload:
             k = k.to(torch.bfloat16).to(dev)
             v = v.to(torch.bfloat16).transpose(1, 2).contiguous().to(dev).transpose(1, 2)
             self.fresh.append((k, v))
+        # k/v projection outputs (token-major (1, n, H*D), before RoPE) of layers 0 and 2..27:
+        # what ckv_rope_qkv turns into cache rows in the engine.
+        self.proj = [None if li == 1 else tuple(
+            torch.randn((1, N_TOKENS if li == 0 else plan.n_keep, N_KV * HEAD_DIM), generator=gen).to(torch.bfloat16)
+            .to(dev) for _ in range(2)) for li in range(N_LAYERS)]
         self.sel = None
         self.side = torch.cuda.Stream(device=dev)  # default priority
+        # the engine's per-position (cos, sin) table, built once per engine (not per request)
+        self.rope_tab = ops.rope_table(N_TOKENS, HEAD_DIM, THETA, dev)
 
     def gather(self):
         from chunkkv_amd import ops
@@ -209,26 +219,61 @@ class RepairWorkload:
         ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(self.plan.segments),
                           self.plan.max_seg_tokens, THETA, self.err, layers=(2, N_LAYERS), skip=self.sel.keep_rank)
 
-    def step(self):
-        """One request's KV repair exactly as HipEngine issues it (31 launches): assemble L0; base
-        cache of L1, deviation, selection, scatter of the kept rows of L1; then, forked onto a side
-        stream, one gather of the dropped cached rows of L2..L27, while the main stream scatters
-        the kept (fresh) rows of L2..L27; the two write disjoint rows and join at the end."""
+    def kv_rows(self, li: int):
+        """Layer li's fresh rows into its cache as the engine writes them: the k/v part of
+        ckv_rope_qkv (k rotated to its position, v copied, straight into the cache rows). The
+        engine's launch also rotates q for the attention; the step leaves q out, as the
+        reference's KV-repair bytes do."""
         from chunkkv_amd import ops
 
-        self._head()
-        main = torch.cuda.current_stream()
-        self.side.wait_stream(main)
-        with torch.cuda.stream(self.side):
-            self.gather_dropped()
+        pos = self.layer0 if li == 0 else self.sel.keep_abs[: self.plan.n_keep]
+        k_in, v_in = self.proj[li]
+        ops.rope_qkv(None, k_in, v_in, pos, 0, N_KV, HEAD_DIM, THETA, k_out=self.k_slab[li], v_out=self.v_slab[li],
+                     rows=pos, table=self.rope_tab, err=self.err)
+
+    def step(self, two_streams: bool = True):
+        """One request's KV repair as HipEngine issues it (32 launches). Layer 1's base cache is
+        gathered on a second stream while layer 0's fresh rows are written; then the layer-1
+        deviation, selection and scatter of the kept rows; then the gather of the dropped rows of
+        layers 2-27 on the second stream while the first writes those layers' fresh rows (the
+        two write disjoint rows). two_streams=False issues the same launches on one stream."""
+        from chunkkv_amd import ops
+
+        plan = self.plan
         K, V = self.k_slab.unbind(0), self.v_slab.unbind(0)
-        rows = self.sel.keep_abs[: self.plan.n_keep]
+        main = torch.cuda.current_stream()
+
+        def fork(fn):
+            if not two_streams:
+                return fn()
+            self.side.wait_stream(main)
+            with torch.cuda.stream(self.side):
+                fn()
+
+        fork(lambda: ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(plan.segments),
+                                       plan.max_seg_tokens, THETA, self.err, layers=(1, 2)))
+        self.kv_rows(0)
+        if two_streams:
+            main.wait_stream(self.side)
+        k1, v1 = self.fresh[1]
+        diff, norm = ops.deviation(k1, v1, K[1], V[1], self.flags, self.local, self.err)
+        self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
+        ops.scatter_rows(K[1], V[1], k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep], self.sel.keep_abs[: plan.n_keep],
+                         self.err)
+        fork(self.gather_dropped)
         for li in range(2, N_LAYERS):
-            ops.scatter_rows(K[li], V[li], *self.fresh[li], rows, self.err)
-        main.wait_stream(self.side)
+            self.kv_rows(li)
+        if two_streams:
+            main.wait_stream(self.side)
 
     def step_serial(self):
-        """The same rows on one stream: assemble L0; layer 1 as in step(); assemble L2..L27."""
+        """The same launches on one stream."""
+        self.step(two_streams=False)
+
+    def step_assemble(self):
+        """Layer 0 and layers 2-27 with one assemble launch each (every row written once, fresh
+        rows from k/v tensors), one stream: the alternative when the caller's fresh rows already
+        exist as tensors."""
         self._head()
         for li in range(2, N_LAYERS):
             self.assemble(li)
@@ -280,22 +325,28 @@ def _graph_of(fn):
 
 
 def bench_repair(steps: int, warmup: int, dev) -> dict:
-    """Time the KV-repair step as HipEngine issues it (31 launches on two streams, captured once
-    per input set in a HIP graph and replayed; the eager time, launch-bound from Python, and the
-    one-stream variant are reported too), and the dominant kernel (the gather of the dropped rows
-    of layers 2..27) from a burst of back-to-back launches."""
+    """Time the KV-repair step as HipEngine issues it (32 launches on two streams, captured once
+    per input set in a HIP graph and replayed; the eager time, launch-bound from Python, the
+    one-stream issue of the same launches and the assemble-per-layer variant are reported too),
+    and the dominant kernel (the gather of the dropped rows of layers 2..27) from a burst of
+    back-to-back launches."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
     for i in range(max(warmup, 2)):
         wls[i % 2].step()
         wls[i % 2].step_serial()
+        wls[i % 2].step_assemble()
     torch.cuda.synchronize()
     graphs = [_graph_of(w.step) for w in wls]
     serial = [_graph_of(w.step_serial) for w in wls]
+    asm_graphs = [_graph_of(w.step_assemble) for w in wls]
     stream = torch.cuda.current_stream(dev)
-    for g in graphs + serial:
+    for g in graphs + serial + asm_graphs:
         g.replay()
     ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
     ms_serial = _timed(lambda i: serial[i % 2].replay(), steps, stream)
+    ms_asm = _timed(lambda i: asm_graphs[i % 2].replay(), steps, stream)
+    for w in wls:  # the selection state of the two-stream step again
+        w.step()
     ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
     gd_ms = _timed(lambda i: wls[i % 2].gather_dropped(), steps, stream)
     n_asm = N_LAYERS - 2
@@ -306,7 +357,7 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     assert int(wls[0].sel.counts[0].item()) == n_keep
     nbytes = repair_bytes(n_keep)
     gd_bytes = dropped_bytes(plan)
-    return dict(ms_per_step=ms, ms_serial=ms_serial, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(plan),
+    return dict(ms_per_step=ms, ms_serial=ms_serial, ms_asm=ms_asm, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
                 asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep)
 
@@ -655,13 +706,72 @@ def traffic_probe(steps: int, warmup: int, dev) -> dict:
 COPY_BYTES = 512 << 20
 
 
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix-core peak
+
+
+def bench_attention(steps: int, warmup: int, dev) -> dict:
+    """ckv_attention_active at the Qwen2.5-7B shape (28 query / 4 KV heads, head_dim 128, bf16)
+    over an 8256-row cache: the 2976 active rows of layers 2-27 of the 8k request (2400 cached
+    positions kept at random + the 576 uncached tail) and all 8256 rows (layers 0-1, plain
+    causal). Work = 4 * D flops per visible (query, key) pair and query head (the two products);
+    the torch SDPA formulations the engine used before (expanded KV heads + boolean mask;
+    is_causal with enable_gqa) are timed beside it."""
+    import torch.nn.functional as F
+
+    from chunkkv_amd import ops
+
+    gen = torch.Generator().manual_seed(5)
+    Hq = 28
+    K = torch.randn((1, N_KV, N_TOKENS, HEAD_DIM), generator=gen).to(torch.bfloat16).to(dev)
+    V = torch.randn((1, N_KV, N_TOKENS, HEAD_DIM), generator=gen).to(torch.bfloat16).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    n_cached = N_CHUNKS * CHUNK_LEN
+    cases = {
+        "active_2976": torch.cat([torch.randperm(n_cached, generator=gen)[:2400].sort().values,
+                                  torch.arange(n_cached, N_TOKENS)]),
+        "causal_8256": torch.arange(N_TOKENS),
+    }
+    out = {}
+    for name, active in cases.items():
+        active = active.to(dev)
+        n = active.numel()
+        q = torch.randn((1, Hq, n, HEAD_DIM), generator=gen).to(torch.bfloat16).to(dev)
+        flops = 4.0 * HEAD_DIM * Hq * float((active + 1).sum().item())
+        for _ in range(warmup):
+            ops.attention_active(q, K, V, active)
+        ms = _timed(lambda i: ops.attention_active(q, K, V, active), steps, stream)
+        if n == N_TOKENS:
+            sdpa = lambda i: F.scaled_dot_product_attention(q, K, V, is_causal=True, enable_gqa=True)  # noqa: E731
+        else:
+            mask = active[:, None] >= torch.arange(N_TOKENS, device=dev)[None, :]
+            Ke, Ve = K.repeat_interleave(Hq // N_KV, 1), V.repeat_interleave(Hq // N_KV, 1)
+            sdpa = lambda i: F.scaled_dot_product_attention(q, Ke, Ve, attn_mask=mask)  # noqa: E731
+        sdpa(0)
+        ms_sdpa = _timed(sdpa, steps, stream)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "sdpa_ms": round(ms_sdpa, 4), "flops": flops}
+    main_case = out["active_2976"]
+    return {
+        "metric": "positions-masked GQA attention, TFLOP/s", "value": main_case["tflops"], "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": main_case["ms"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "Qwen2.5-7B attention shape: 28 q / 4 KV heads, head_dim 128, 8256-row cache; "
+                               "2976 active rows (layers 2-27) and 8256 (layers 0-1)"},
+        "roofline": {"kernel": "attn_active_kernel<128>", "bound": "mfma", "achieved": main_case["tflops"],
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": main_case["frac"], "traffic": None,
+                     "flops_per_launch": main_case["flops"], "avg_launch_us": round(main_case["ms"] * 1e3, 2)},
+        "cases": out,
+    }
+
+
 def bench_dropped(steps: int, warmup: int, dev) -> dict:
     """The dominant kernel alone: `steps` back-to-back gathers of the dropped rows of layers 2-27
     (alternating two input sets), timed with HIP events on the launch stream. Its rocprofv3
     kernel average is the same quantity (no other gather launch runs in this workload)."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
     for w in wls:
-        w.step_serial()  # selection output, without a gather of the dropped rows
+        w.step_assemble()  # selection output, without a gather of the dropped rows
     for i in range(warmup):
         wls[i % 2].gather_dropped()
     stream = torch.cuda.current_stream(dev)
@@ -695,7 +805,7 @@ def main() -> None:
     ap.add_argument("--ttft-requests", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload", default="request",
-                    choices=["request", "gather", "deviation", "replay", "traffic", "dropped"],
+                    choices=["request", "gather", "deviation", "replay", "traffic", "dropped", "attention"],
                     help="request: the 8k Qwen2.5-7B blend-prefill KV repair (default); gather / deviation / replay: "
                          "the re-RoPE+gather, deviation+top-k+scatter and 4x32k replay microbenchmarks")
     args = ap.parse_args()
@@ -706,13 +816,14 @@ def main() -> None:
     torch.cuda.set_device(dev)
     if args.workload != "request":
         fn = {"gather": bench_gather_only, "deviation": bench_deviation_topk, "replay": bench_replay,
-              "traffic": traffic_probe, "dropped": bench_dropped}[args.workload]
+              "traffic": traffic_probe, "dropped": bench_dropped, "attention": bench_attention}[args.workload]
         print(json.dumps(fn(args.steps, args.warmup, dev)), flush=True)
         return
 
     r = bench_repair(args.steps, args.warmup, dev)
     log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_serial']:.3f} ms one "
-        f"stream, {r['ms_eager']:.3f} ms eager); dropped-row gather {r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
+        f"stream, {r['ms_asm']:.3f} ms assemble variant, {r['ms_eager']:.3f} ms eager); dropped-row gather "
+        f"{r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
         f"assemble {r['asm_gbs']:.1f} GB/s ({r['asm_ms'] * 1e3:.2f} us)")
     ttft = bench_ttft(args.ttft_requests, dev) if args.ttft_requests > 0 else None
     cpu = bench_cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None
@@ -745,6 +856,7 @@ def main() -> None:
         "pct_of_peak": round(100.0 * r["gbs"] / PEAK_GBS, 2),
         "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
         "ms_per_step_one_stream": round(r["ms_serial"], 4),
+        "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
         "roofline": {
             "kernel": "rerope_gather_kernel<bf16,128> (layers 2-27, dropped rows)",
             "bound": "hbm",
@@ -753,7 +865,7 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(r["gd_gbs"] / PEAK_GBS, 4),
             "traffic": DROPPED_TRAFFIC_BYTES,
-            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_rerope_gather_qwen25_7b_8k.md",
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_gather_dropped_rows_qwen25_7b_8k.md",
             "bytes_per_launch": r["gd_bytes"],
             "avg_launch_us": round(r["gd_ms"] * 1e3, 2),
         },

@@ -10,11 +10,15 @@
 // rounded fp32 cos/sin of that angle (evaluated in fp64), the same rotation ckv_shift_keys
 // applies for a shift by pos[t]; products and sums are separately rounded fp32 operations.
 //
-// Design (gfx950): one workgroup per token. Its D/2 cos/sin pairs are built in LDS while the
-// token's first 16-byte loads are in flight; then every (head, 16-byte column) pair of q and k
+// Design (gfx950): with a per-position cos/sin table (built once by ckv_rope_table and kept by
+// the caller) one thread handles one (token, 16-byte item), grid-stride. Without a table, one
+// workgroup per token builds its D/2 cos/sin pairs in LDS while the token's first 16-byte loads
+// are in flight; then every (head, 16-byte column) pair of q and k
 // is rotated and stored, and the v row copied, with 16-byte accesses. The ~20 elementwise torch
 // launches of the reference's RoPE (fp32 temporaries, cat, cast) and the separate scatter of k/v
 // into the cache become one pass over the projection output.
+#include <algorithm>
+
 #include "ckv_common.hpp"
 
 namespace ckv {
@@ -27,7 +31,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
     int64_t ko_ts_b, char* __restrict__ v_out, int64_t vo_hs_b, int64_t vo_ts_b, const int64_t* __restrict__ rows,
     int n_out, const char* __restrict__ q_in, int64_t qi_hs_b, int64_t qi_ts_b, const char* __restrict__ k_in,
     int64_t ki_hs_b, int64_t ki_ts_b, const char* __restrict__ v_in, int64_t vi_hs_b, int64_t vi_ts_b,
-    const int64_t* __restrict__ pos, int Hq, int Hkv, double theta, int32_t* __restrict__ err) {
+    const int64_t* __restrict__ pos, const float2* __restrict__ cs_table, int64_t n_table, int Hq, int Hkv,
+    double theta, int32_t* __restrict__ err) {
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
   constexpr int HALF = D / 2;
@@ -41,7 +46,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
   const int t = blockIdx.x;
   const int64_t p = pos[t];
   const int64_t row = rows != nullptr ? rows[t] : t;
-  if (p < INT32_MIN || p > INT32_MAX || row < 0 || row >= n_out) {  // uniform per workgroup
+  if (p < INT32_MIN || p > INT32_MAX || row < 0 || row >= n_out ||
+      (cs_table != nullptr && (p < 0 || p >= n_table))) {  // uniform per workgroup
     if (threadIdx.x == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
     return;
   }
@@ -58,7 +64,9 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
                   : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b + col * 16;
   };
 
-  // First item's loads go out before the table is built (one item per thread at Hq+Hkv=32, D=128).
+  // First item's loads go out before the cos/sin are fetched or built (one item per thread at
+  // Hq+Hkv=32, D=128). With a table the pairs come straight from it (the row of position p, in
+  // L2 for all heads of the token); without one the workgroup builds them in LDS.
   int it = threadIdx.x;
   vec16 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
   if (it < n_rot) {
@@ -66,8 +74,11 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
     a = ld16(s);
     b = ld16(s + HALF_B);
   }
-  if (threadIdx.x < HALF) cs_tab[threadIdx.x] = rope_shift_cos_sin(threadIdx.x, D, theta, (int)p);
-  __syncthreads();
+  const float2* trow = cs_table != nullptr ? cs_table + p * HALF : nullptr;
+  if (trow == nullptr) {  // uniform
+    if (threadIdx.x < HALF) cs_tab[threadIdx.x] = rope_shift_cos_sin(threadIdx.x, D, theta, (int)p);
+    __syncthreads();
+  }
 
   for (; it < n_rot; it += kRopeThreads) {
     if (it != (int)threadIdx.x) {
@@ -79,7 +90,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
     float c[VEC], sn[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float2 cs = cs_tab[col * VEC + e];
+      const float2 cs = trow != nullptr ? trow[col * VEC + e] : cs_tab[col * VEC + e];
       c[e] = cs.x;
       sn[e] = cs.y;
     }
@@ -97,20 +108,87 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
   }
 }
 
+// With a cos/sin table a token needs no shared state, so the work is flattened: one thread per
+// (token, item), item = a rotated 16-byte column pair of a q/k head or a copied 16-byte chunk of
+// a v row, grid-stride over all of them (every thread busy, whatever the head counts).
+template <int DTYPE, int D>
+__global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
+    char* __restrict__ q_out, int64_t qo_hs_b, int64_t qo_ts_b, char* __restrict__ k_out, int64_t ko_hs_b,
+    int64_t ko_ts_b, char* __restrict__ v_out, int64_t vo_hs_b, int64_t vo_ts_b, const int64_t* __restrict__ rows,
+    int n_out, const char* __restrict__ q_in, int64_t qi_hs_b, int64_t qi_ts_b, const char* __restrict__ k_in,
+    int64_t ki_hs_b, int64_t ki_ts_b, const char* __restrict__ v_in, int64_t vi_hs_b, int64_t vi_ts_b,
+    const int64_t* __restrict__ pos, const float2* __restrict__ cs_table, int64_t n_table, int n, int Hq, int Hkv,
+    int32_t* __restrict__ err) {
+  using E = Elem<DTYPE>;
+  constexpr int VEC = E::kVec;
+  constexpr int HALF = D / 2;
+  constexpr int TPR = HALF / VEC;
+  constexpr int HALF_B = HALF * E::kBytes;
+  constexpr int CPR = D * E::kBytes / 16;
+  typedef __attribute__((address_space(1))) const int64_t gi64;
+  const int n_rot = (Hq + Hkv) * TPR;
+  const unsigned per_tok = (unsigned)(n_rot + (v_out != nullptr ? Hkv * CPR : 0));
+  const unsigned total = (unsigned)n * per_tok;  // < 2^31, checked by the host
+  for (unsigned idx = blockIdx.x * kRopeThreads + threadIdx.x; idx < total; idx += gridDim.x * kRopeThreads) {
+    const int t = (int)(idx / per_tok), it = (int)(idx - (unsigned)t * per_tok);
+    const int64_t p = *(gi64*)(pos + t);
+    const int64_t row = rows != nullptr ? *(gi64*)(rows + t) : t;
+    if (p < 0 || p >= n_table || row < 0 || row >= n_out) {
+      if (it == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+      continue;
+    }
+    if (it < n_rot) {
+      const int h = it / TPR, col = it % TPR;
+      const char* s = h < Hq ? q_in + h * qi_hs_b + t * qi_ts_b : k_in + (h - Hq) * ki_hs_b + t * ki_ts_b;
+      char* d = h < Hq ? q_out + h * qo_hs_b + t * qo_ts_b : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b;
+      s += col * 16;
+      d += col * 16;
+      const vec16 a = ld16(s), b = ld16(s + HALF_B);
+      const float2* tr = cs_table + p * HALF + col * VEC;  // VEC pairs = VEC/2 16-byte loads
+      float c[VEC], sn[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; e += 2) {
+        const vec16 w = ld16(tr + e);
+        c[e] = __uint_as_float(w[0]);
+        sn[e] = __uint_as_float(w[1]);
+        c[e + 1] = __uint_as_float(w[2]);
+        sn[e + 1] = __uint_as_float(w[3]);
+      }
+      vec16 y1, y2;
+      rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
+      st16(d, y1);
+      st16(d + HALF_B, y2);
+    } else {
+      const int i = it - n_rot, h = i / CPR, c = i % CPR;
+      st16(v_out + h * vo_hs_b + row * vo_ts_b + c * 16, ld16(v_in + h * vi_hs_b + t * vi_ts_b + c * 16));
+    }
+  }
+}
+
 template <int DTYPE, int D>
 static void launch_rope(int n, hipStream_t st, char* qo, int64_t qo_hs, int64_t qo_ts, char* ko, int64_t ko_hs,
                         int64_t ko_ts, char* vo, int64_t vo_hs, int64_t vo_ts, const int64_t* rows, int n_out,
                         const char* qi, int64_t qi_hs, int64_t qi_ts, const char* ki, int64_t ki_hs, int64_t ki_ts,
-                        const char* vi, int64_t vi_hs, int64_t vi_ts, const int64_t* pos, int Hq, int Hkv,
-                        double theta, int32_t* err) {
+                        const char* vi, int64_t vi_hs, int64_t vi_ts, const int64_t* pos, const float2* tab,
+                        int64_t n_tab, int Hq, int Hkv, double theta, int32_t* err) {
+  if (tab != nullptr) {
+    using E = Elem<DTYPE>;
+    const int64_t per_tok = (int64_t)(Hq + Hkv) * (D / 2 / E::kVec) + (vo != nullptr ? Hkv * (D * E::kBytes / 16) : 0);
+    const int64_t blocks = std::min<int64_t>((n * per_tok + kRopeThreads - 1) / kRopeThreads, 1 << 20);
+    hipLaunchKernelGGL((rope_qkv_flat_kernel<DTYPE, D>), dim3((unsigned)blocks), dim3(kRopeThreads), 0, st, qo, qo_hs,
+                       qo_ts, ko, ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, qi, qi_hs, qi_ts, ki, ki_hs, ki_ts, vi,
+                       vi_hs, vi_ts, pos, tab, n_tab, n, Hq, Hkv, err);
+    return;
+  }
   hipLaunchKernelGGL((rope_qkv_kernel<DTYPE, D>), dim3((unsigned)n), dim3(kRopeThreads), 0, st, qo, qo_hs, qo_ts, ko,
                      ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, qi, qi_hs, qi_ts, ki, ki_hs, ki_ts, vi, vi_hs,
-                     vi_ts, pos, Hq, Hkv, theta, err);
+                     vi_ts, pos, tab, n_tab, Hq, Hkv, theta, err);
 }
 
 typedef void (*RopeLaunch)(int, hipStream_t, char*, int64_t, int64_t, char*, int64_t, int64_t, char*, int64_t,
                            int64_t, const int64_t*, int, const char*, int64_t, int64_t, const char*, int64_t, int64_t,
-                           const char*, int64_t, int64_t, const int64_t*, int, int, double, int32_t*);
+                           const char*, int64_t, int64_t, const int64_t*, const float2*, int64_t, int, int, double,
+                           int32_t*);
 
 static RopeLaunch pick_rope(int dtype, int head_dim) {
 #define CKV_CASE(DT, HD) \
@@ -125,7 +203,27 @@ static RopeLaunch pick_rope(int dtype, int head_dim) {
   return nullptr;
 }
 
+// table[p][i] = (cos, sin) of the fp32 angle fl32(fl32(p) * inv_freq_i), correctly rounded.
+__global__ void rope_table_kernel(float2* __restrict__ tab, int64_t n_pos, int head_dim, double theta) {
+  const int half = head_dim / 2;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n_pos * half) tab[i] = rope_shift_cos_sin((int)(i % half), head_dim, theta, (int)(i / half));
+}
+
 }  // namespace ckv
+
+extern "C" int32_t ckv_rope_table(void* table, int64_t n_positions, int32_t head_dim, double theta, void* stream) {
+  using namespace ckv;
+  if (table == nullptr || n_positions < 0 || head_dim <= 0 || (head_dim & 1) || head_dim > 512 || !(theta > 0.0))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_positions > 0x7fffffff) return CKV_ERR_TOO_LARGE;
+  const int64_t total = n_positions * (head_dim / 2);
+  if (total == 0) return CKV_OK;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (float2*)table, n_positions, (int)head_dim, theta);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}
 
 extern "C" int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_token_stride, void* k_out,
                                 int64_t ko_head_stride, int64_t ko_token_stride, void* v_out, int64_t vo_head_stride,
@@ -133,16 +231,20 @@ extern "C" int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_
                                 int64_t qi_head_stride, int64_t qi_token_stride, const void* k_in,
                                 int64_t ki_head_stride, int64_t ki_token_stride, const void* v_in,
                                 int64_t vi_head_stride, int64_t vi_token_stride, const int64_t* positions,
-                                int32_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
-                                int32_t dtype, double theta, int32_t* err, void* stream) {
+                                const void* cs_table, int64_t n_table, int32_t n_tokens, int32_t n_q_heads,
+                                int32_t n_kv_heads, int32_t head_dim, int32_t dtype, double theta, int32_t* err,
+                                void* stream) {
   using namespace ckv;
   RopeLaunch fn = pick_rope(dtype, head_dim);
-  if (fn == nullptr || q_out == nullptr || q_in == nullptr || k_out == nullptr || k_in == nullptr ||
-      positions == nullptr || (v_out == nullptr) != (v_in == nullptr))
+  if (fn == nullptr || k_out == nullptr || k_in == nullptr || positions == nullptr ||
+      (v_out == nullptr) != (v_in == nullptr) || (n_q_heads > 0 && (q_out == nullptr || q_in == nullptr)))
     return CKV_ERR_INVALID_ARGUMENT;
   if (n_tokens < 0 || n_q_heads < 0 || n_kv_heads <= 0 || n_out_rows < 0 || !(theta > 0.0))
     return CKV_ERR_INVALID_ARGUMENT;
   if (rows == nullptr && n_out_rows < n_tokens) return CKV_ERR_OUT_OF_RANGE;
+  if (cs_table != nullptr && (n_table < 0 || (uintptr_t)cs_table % 16)) return CKV_ERR_INVALID_ARGUMENT;
+  if (cs_table != nullptr && (int64_t)n_tokens * ((n_q_heads + n_kv_heads) * 64 + n_kv_heads * 64) >= (1ll << 31))
+    return CKV_ERR_TOO_LARGE;  // the flattened (token, item) index stays below 2^31
   const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
   const int64_t strides[] = {qo_head_stride, qo_token_stride, ko_head_stride, ko_token_stride, vo_head_stride,
                              vo_token_stride, qi_head_stride, qi_token_stride, ki_head_stride, ki_token_stride,
@@ -158,7 +260,7 @@ extern "C" int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_
      ko_head_stride * eb, ko_token_stride * eb, (char*)v_out, vo_head_stride * eb, vo_token_stride * eb, rows,
      n_out_rows, (const char*)q_in, qi_head_stride * eb, qi_token_stride * eb, (const char*)k_in,
      ki_head_stride * eb, ki_token_stride * eb, (const char*)v_in, vi_head_stride * eb, vi_token_stride * eb,
-     positions, n_q_heads, n_kv_heads, theta, err);
+     positions, (const float2*)cs_table, n_table, n_q_heads, n_kv_heads, theta, err);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

@@ -79,6 +79,7 @@ class HipEngine(DecoderPieces):
         # a side stream (same launches, same rows).
         self.overlap = overlap
         self._side: torch.cuda.Stream | None = None
+        self._rope_tab: torch.Tensor | None = None  # (cos, sin) per position, grown on demand
         # Set to a dict to record the layer-1 selection inputs/outputs (device tensors) of the
         # next prefill, for parity checks; None (default) records nothing.
         self.trace: dict | None = None
@@ -196,6 +197,14 @@ class HipEngine(DecoderPieces):
             for a, o in zip(parts, offs)
         ]
 
+    def _table(self, n: int) -> torch.Tensor:
+        """Per-position (cos, sin) table covering positions [0, n), kept across requests."""
+        if self._rope_tab is None or self._rope_tab.shape[0] < n:
+            size = max(n, 4096)
+            size = (size + 4095) // 4096 * 4096
+            self._rope_tab = ops.rope_table(size, self.head_dim, self.theta, self.device)
+        return self._rope_tab
+
     def _project(self, li: int, x: torch.Tensor):
         """q|k|v projection of layer li in one GEMM: views (1, n, H*D) of its token-major output."""
         lin = F.linear(x, self._w_qkv[li], self._b_qkv[li])
@@ -262,6 +271,7 @@ class HipEngine(DecoderPieces):
         masks: dict = {}
         sel = None
         ready: dict[int, torch.cuda.Event | None] = {}  # layer -> its cached rows are in place
+        tab = self._table(N)
         gather = lambda layers, skip: self._gather(  # noqa: E731
             k_slab, v_slab, tab_d, segs_d, n_cached_segs, plan.max_seg_tokens, layers, skip, err)
         # Cached rows that do not depend on the model go out first, overlapped with layer 0:
@@ -279,7 +289,7 @@ class HipEngine(DecoderPieces):
             q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
             K, V = keys_out[li], values_out[li]
             if li == 1 and select_layer:
-                q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, err=err)
+                q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, table=tab, err=err)
                 v = v_in.view(1, -1, H, D).transpose(1, 2)
                 if ready.get(1) is not None:
                     torch.cuda.current_stream(dev).wait_event(ready[1])
@@ -304,7 +314,7 @@ class HipEngine(DecoderPieces):
             else:
                 # RoPE of q/k with k and v written straight into this layer's cache rows
                 q, _ = ops.rope_qkv(q_in, k_in, v_in, active, self.n_heads, H, D, self.theta, k_out=K, v_out=V,
-                                    rows=active, err=err)
+                                    rows=active, table=tab, err=err)
                 if ready.get(li) is not None:
                     torch.cuda.current_stream(dev).wait_event(ready[li])
             h = self._attend_active(layer, h, q, K, V, active, ar, masks, err)

@@ -371,7 +371,7 @@ def _heads_view(t: torch.Tensor, n_heads: int, head_dim: int) -> tuple:
 
 
 def rope_qkv(
-    q_in: torch.Tensor,
+    q_in: torch.Tensor | None,
     k_in: torch.Tensor,
     v_in: torch.Tensor | None,
     positions: torch.Tensor,
@@ -384,22 +384,30 @@ def rope_qkv(
     k_out: torch.Tensor | None = None,
     v_out: torch.Tensor | None = None,
     rows: torch.Tensor | None = None,
+    table: torch.Tensor | None = None,
     err: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Fresh-token RoPE (torch_engine.py:61-66, :53-54, :46-51) of q and k, v copied alongside.
 
-    q_in/k_in/v_in: projection outputs, token-major (1, n, H*D) views or (1, H, n, D) tensors.
+    n_q_heads = 0 (q_in ignored) rotates and writes k/v only. q_in/k_in/v_in: projection outputs, token-major (1, n, H*D) views or (1, H, n, D) tensors.
     Returns (q_out, k_out): q_out (1, n, Hq, D) token-major (the layout attention_active reads)
     unless given; k_out (1, Hkv, n, D) unless given. With rows (int64 (n,)), k/v land in rows
     rows[t] of k_out/v_out, e.g. the layer's cache (1, Hkv, N, D): the fresh-row scatter fused in.
+    table: a rope_table() covering every position (same results, no per-call cos/sin evaluation).
     """
-    _dev(q_in, k_in, positions)
+    if table is not None:
+        _dev(k_in, table)
+        if table.dtype != torch.float32 or table.dim() != 3 or table.shape[1:] != (head_dim // 2, 2):
+            raise ValueError("table must be a rope_table() output (n, D/2, 2) float32")
+    _dev(k_in, positions)
     n = positions.numel()
-    dev = q_in.device
+    dev = k_in.device
+    if n_q_heads == 0:  # k/v only
+        q_in = k_in
     if positions.dtype != torch.int64:
         raise ValueError("positions must be int64")
     positions = positions.contiguous()
-    if q_out is None:
+    if q_out is None and n_q_heads:
         q_out = torch.empty((1, n, n_q_heads, head_dim), dtype=q_in.dtype, device=dev)
     if k_out is None:
         if rows is not None:
@@ -413,22 +421,36 @@ def rope_qkv(
         rows = rows.contiguous()
     if (v_in is None) != (v_out is None):
         raise ValueError("v_in and v_out go together")
-    for t in (q_in, k_in, q_out, k_out) + ((v_in, v_out) if v_in is not None else ()):
+    for t in (q_in, k_in, k_out) + ((q_out,) if n_q_heads else ()) + ((v_in, v_out) if v_in is not None else ()):
         if t.dtype != q_in.dtype:
             raise TypeError("q/k/v and outputs must share a dtype")
-    if q_out.shape != (1, n, n_q_heads, head_dim) or not q_out.is_contiguous():
-        raise ValueError("q_out must be contiguous (1, n, Hq, D), token-major")
-    qo = _heads_view(q_out.view(1, n, n_q_heads * head_dim), n_q_heads, head_dim)
-    qi, ki = _heads_view(q_in, n_q_heads, head_dim), _heads_view(k_in, n_kv_heads, head_dim)
+    if n_q_heads:
+        if q_out.shape != (1, n, n_q_heads, head_dim) or not q_out.is_contiguous():
+            raise ValueError("q_out must be contiguous (1, n, Hq, D), token-major")
+        qo = _heads_view(q_out.view(1, n, n_q_heads * head_dim), n_q_heads, head_dim)
+        qi = _heads_view(q_in, n_q_heads, head_dim)
+    else:
+        qo = qi = (None, 0, 0)
+    ki = _heads_view(k_in, n_kv_heads, head_dim)
     ko = _heads_view(k_out, n_kv_heads, head_dim)
     vi = _heads_view(v_in, n_kv_heads, head_dim) if v_in is not None else (None, 0, 0)
     vo = _heads_view(v_out, n_kv_heads, head_dim) if v_out is not None else (None, 0, 0)
     check(
         lib().ckv_rope_qkv(
             qo[0], qo[1], qo[2], ko[0], ko[1], ko[2], vo[0], vo[1], vo[2], _ptr(rows), n_out, qi[0], qi[1], qi[2],
-            ki[0], ki[1], ki[2], vi[0], vi[1], vi[2], _ptr(positions), n, n_q_heads, n_kv_heads, head_dim,
+            ki[0], ki[1], ki[2], vi[0], vi[1], vi[2], _ptr(positions), _ptr(table),
+            0 if table is None else table.shape[0], n, n_q_heads, n_kv_heads, head_dim,
             dtype_code(q_in.dtype), float(theta), _ptr(err), _stream(dev),
         ),
         "ckv_rope_qkv",
     )
     return q_out, k_out
+
+
+def rope_table(n_positions: int, head_dim: int, theta: float, device) -> torch.Tensor:
+    """(n_positions, head_dim/2, 2) float32: the correctly rounded (cos, sin) ckv_rope_qkv uses for
+    each position (fp32 angle fl32(fl32(p) * inv_freq_i))."""
+    out = torch.empty((n_positions, head_dim // 2, 2), dtype=torch.float32, device=device)
+    _dev(out)
+    check(lib().ckv_rope_table(_ptr(out), n_positions, head_dim, float(theta), _stream(out.device)), "ckv_rope_table")
+    return out

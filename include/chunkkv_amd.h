@@ -251,7 +251,9 @@ int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride,
  * rounded once, one rounding to dtype: the rotation ckv_shift_keys applies for a shift by p.
  * Element (h, t, d) of each tensor is at base + h*head_stride + t*token_stride + d (elements;
  * rows contiguous and 16-byte aligned), so projection outputs can be passed as token-major views.
- * v_out and v_in are both NULL to skip the copy. dtype bf16 or f32, head_dim 64, 128 or 256.
+ * v_out and v_in are both NULL to skip the copy; with n_q_heads = 0, q_out and q_in may be NULL
+ * (k/v only). cs_table: optional ckv_rope_table output with n_table positions (NULL: the kernel
+ * evaluates the cos/sin itself). dtype bf16 or f32, head_dim 64, 128 or 256.
  * Replaces: _qkv/_rope/_rotate (torch_engine.py:61-66, :53-54, :46-51) and the scatter of k/v
  * into the cache (:155-156).
  */
@@ -261,8 +263,18 @@ int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_token_strid
                      int64_t qi_head_stride, int64_t qi_token_stride, const void* k_in,
                      int64_t ki_head_stride, int64_t ki_token_stride, const void* v_in,
                      int64_t vi_head_stride, int64_t vi_token_stride, const int64_t* positions,
-                     int32_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
-                     int32_t dtype, double theta, int32_t* err, void* stream);
+                     const void* cs_table, int64_t n_table, int32_t n_tokens, int32_t n_q_heads,
+                     int32_t n_kv_heads, int32_t head_dim, int32_t dtype, double theta, int32_t* err,
+                     void* stream);
+
+/*
+ * The (cos, sin) pairs ckv_rope_qkv uses, for positions [0, n_positions): table[p][i] =
+ * (cos, sin) of fl32(fl32(p) * inv_freq_i), correctly rounded fp32, i < head_dim/2; float2
+ * entries, n_positions * head_dim/2 of them. Passed to ckv_rope_qkv as cs_table (positions
+ * must then lie in [0, n_table)); the results are identical with or without it. No counterpart
+ * in the reference (it recomputes cos/sin per call, torch_engine.py:53-54, :47).
+ */
+int32_t ckv_rope_table(void* table, int64_t n_positions, int32_t head_dim, double theta, void* stream);
 
 /*
  * Attention of the active rows over the whole cache with the causal mask given by positions:

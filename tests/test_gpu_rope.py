@@ -87,3 +87,58 @@ def test_rope_qkv_flags_bad_row():
     torch.cuda.synchronize()
     assert int(err.item()) == _native.DEVICE_ERR_RANGE
     assert int(K[0, :, 4:].count_nonzero()) == 0
+
+
+def test_rope_qkv_kv_only():
+    """n_q_heads = 0: k rotated and v copied into the cache rows, no q touched."""
+    rng = np.random.default_rng(9)
+    Hkv, D, N, n = 4, 128, 500, 123
+    lin = _proj(rng, n, 0, Hkv, D, True)
+    pos = np.sort(rng.choice(N, n, replace=False))
+    lt = O.from_numpy(lin, DEV)
+    _, k_in, v_in = _split(lt, 0, Hkv, D)
+    K = torch.zeros((1, Hkv, N, D), dtype=torch.bfloat16, device=DEV)
+    V = torch.zeros_like(K)
+    pt = torch.from_numpy(pos).to(DEV)
+    q_out, _ = ops.rope_qkv(None, k_in, v_in, pt, 0, Hkv, D, THETA, k_out=K, v_out=V, rows=pt)
+    torch.cuda.synchronize()
+    assert q_out is None
+    _, kn, vn = _split(lin, 0, Hkv, D)
+    np.testing.assert_array_equal(O.to_numpy(K)[0][:, pos], O.rope(_heads(kn, Hkv, D), pos, THETA))
+    np.testing.assert_array_equal(O.to_numpy(V)[0][:, pos], _heads(vn, Hkv, D))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_rope_table_matches_oracle(D):
+    """ckv_rope_table equals the oracle's cos/sin (read off a rotation of unit vectors: x1 = 1,
+    x2 = 0 gives y1 = cos, y2 = sin exactly)."""
+    N = 5000
+    tab = O.to_numpy(ops.rope_table(N, D, THETA, DEV))
+    x = np.zeros((1, N, D), np.float32)
+    x[..., : D // 2] = 1.0
+    y = O.rope(x, np.arange(N), THETA)[0]
+    np.testing.assert_array_equal(tab[..., 0].view(np.uint32), y[:, : D // 2].view(np.uint32))
+    np.testing.assert_array_equal(tab[..., 1].view(np.uint32), y[:, D // 2 :].view(np.uint32))
+
+
+def test_rope_qkv_with_table_identical_and_bounds():
+    rng = np.random.default_rng(10)
+    Hq, Hkv, D, N, n = 28, 4, 128, 900, 400
+    lt = O.from_numpy(_proj(rng, n, Hq, Hkv, D, True), DEV)
+    q_in, k_in, v_in = _split(lt, Hq, Hkv, D)
+    pt = torch.from_numpy(np.sort(rng.choice(N, n, replace=False))).to(DEV)
+    tab = ops.rope_table(N, D, THETA, DEV)
+    outs = []
+    for t in (None, tab):
+        K = torch.zeros((1, Hkv, N, D), dtype=torch.bfloat16, device=DEV)
+        V = torch.zeros_like(K)
+        q, _ = ops.rope_qkv(q_in, k_in, v_in, pt, Hq, Hkv, D, THETA, k_out=K, v_out=V, rows=pt, table=t)
+        outs.append((q, K, V))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    short = ops.rope_table(int(pt.max().item()), D, THETA, DEV)  # one position short
+    ops.rope_qkv(q_in, k_in, None, pt, Hq, Hkv, D, THETA, table=short, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == _native.DEVICE_ERR_RANGE
