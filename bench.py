@@ -706,6 +706,120 @@ def traffic_probe(steps: int, warmup: int, dev) -> dict:
 COPY_BYTES = 512 << 20
 
 
+def bench_extract(steps: int, warmup: int, dev) -> dict:
+    """Store-put extraction after the 8k Qwen2.5-7B-shape request: the 24 reusable chunk segments
+    (320 tokens each) of all 28 layers' K and V copied out of the request slabs, one
+    ckv_extract_chunks launch (the reference: PrefillResult.chunk per segment, 2 x 28 `.contiguous()`
+    copies each, timed beside it). Bytes per launch = 24 x 320 x 28 x 2 x 1024 x 2 = 880,803,840."""
+    from chunkkv_amd import ops
+
+    gen = torch.Generator().manual_seed(9)
+    slabs = [tuple(torch.randn((N_LAYERS, 1, N_KV, N_TOKENS, HEAD_DIM), generator=gen).to(torch.bfloat16).to(dev)
+                   for _ in range(2)) for _ in range(2)]
+    perm = torch.randperm(N_CHUNKS, generator=gen).tolist()
+    spans = [(i * CHUNK_LEN, (i + 1) * CHUNK_LEN) for i in perm]
+    stream = torch.cuda.current_stream(dev)
+    keep = []
+
+    def ours(i):
+        K, V = slabs[i % 2]
+        keep.append(ops.extract_chunks(K, V, spans))
+        if len(keep) > 2:
+            keep.pop(0)
+
+    def reference(i):
+        K, V = slabs[i % 2]
+        keep.append([[K[l][:, :, s:e].contiguous() for l in range(N_LAYERS)] + [V[l][:, :, s:e].contiguous()
+                      for l in range(N_LAYERS)] for s, e in spans])
+        if len(keep) > 2:
+            keep.pop(0)
+
+    # the kernel alone: fixed destination buffers and descriptors, back-to-back launches
+    from chunkkv_amd._native import lib
+
+    fixed = [ops.extract_chunks(K, V, spans) for K, V in slabs]
+    desc = []
+    for bufs in fixed:
+        host = np.zeros(N_CHUNKS * 4, dtype=np.int32)
+        host[: 2 * N_CHUNKS].view(np.uint64)[:] = [b.data_ptr() for b in bufs]
+        host[2 * N_CHUNKS :] = [v for s_, e_ in spans for v in (s_, e_ - s_)]
+        desc.append(torch.from_numpy(host).to(dev))
+
+    def kernel_only(i):
+        K, V = slabs[i % 2]
+        d = desc[i % 2]
+        lib().ckv_extract_chunks(K.data_ptr(), V.data_ptr(), N_KV * N_TOKENS * HEAD_DIM, N_TOKENS * HEAD_DIM,
+                                 d.data_ptr(), d.data_ptr() + 8 * N_CHUNKS, N_CHUNKS, CHUNK_LEN, N_LAYERS, N_KV,
+                                 N_TOKENS, HEAD_DIM, 1, None, torch.cuda.current_stream(dev).cuda_stream)
+
+    for i in range(max(warmup, 2)):
+        ours(i)
+        reference(i)
+        kernel_only(i)
+    ms = _timed(ours, steps, stream)
+    ms_ref = _timed(reference, steps, stream)
+    ms_k = _timed(kernel_only, steps, stream)
+    for (K, V), bufs in zip(slabs, fixed):
+        for b, (s_, e_) in zip(bufs, spans):
+            assert torch.equal(b[0, 5], K[5][:, :, s_:e_]) and torch.equal(b[1, 27], V[27][:, :, s_:e_])
+    nb = N_CHUNKS * CHUNK_LEN * N_LAYERS * 2 * ROW_BYTES * 2
+    line = _workload_line(
+        "store-put extraction, HBM GB/s", nb / (ms * 1e-3) / 1e9, ms, steps, warmup,
+        {"workload": "24 reusable segments x 320 tokens of the 8256-token request, 28 layers, 4 KV heads, "
+                     "head_dim 128, bf16, one launch (value: the whole PrefillResult.chunks call, incl. the 24 "
+                     "buffer allocations and the descriptor copy)"},
+        _rooffor("extract_kernel", nb, ms_k))
+    line["reference_per_layer_copies_ms"] = round(ms_ref, 4)
+    return line
+
+
+def bench_decode(steps: int, warmup: int, dev) -> dict:
+    """Greedy decode after the 8k blend prefill on a random-init Qwen2.5-7B-architecture bf16
+    model: 32 new tokens per request (EOS disabled), HipEngine.generate (preallocated slabs,
+    in-place k/v rows, positions-masked attention) vs the reference's torch.cat-per-token decode
+    (torch_engine.py:180-198) run on the same engine and prefill. Metric: decode tokens/s."""
+    from chunkkv_amd.engine import HipEngine
+    from chunkkv_amd.model import DecoderPieces
+    from chunkkv_amd.types import BlendConfig
+
+    model = random_qwen25_7b(dev)
+    hip = HipEngine(model, _Tok())
+    hip.eos = set()
+    gen = torch.Generator().manual_seed(11)
+    vocab = model.config.vocab_size
+    pool = []
+    for _ in range(N_CHUNKS):
+        toks = torch.randint(0, vocab, (CHUNK_LEN,), generator=gen).tolist()
+        pool.append((toks, hip.prefill(toks).chunk(0, CHUNK_LEN)))
+    tokens, placements = [], []
+    for c in torch.randperm(len(pool), generator=gen).tolist():
+        placements.append(Place(pool[c][1], len(tokens)))
+        tokens += pool[c][0]
+    tokens += torch.randint(0, vocab, (TAIL + QUERY,), generator=gen).tolist()
+    res = hip.prefill(tokens, placements, BlendConfig(recompute_ratio=RATIO, n_sink=N_SINK))
+    n_new = 32
+    out = {}
+    for name, fn in (("hip", lambda: hip.generate(res, n_new)), ("concat", lambda: DecoderPieces.generate(hip, res, n_new))):
+        for _ in range(max(1, warmup)):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks_out = [fn() for _ in range(max(1, steps))]
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / max(1, steps)
+        out[name] = (dt, toks_out[0])
+    agree = sum(a == b for a, b in zip(out["hip"][1], out["concat"][1]))
+    tps = n_new / out["hip"][0]
+    return {
+        "metric": "decode tokens/s after the 8k blend prefill", "value": round(tps, 2), "unit": "tokens/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(out["hip"][0] * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"random-init Qwen2.5-7B architecture, 8256-token blend prefill, {n_new} greedy tokens"},
+        "concat_decode_tokens_per_s": round(n_new / out["concat"][0], 2),
+        "tokens_equal_to_concat_decode": f"{agree}/{n_new}",
+    }
+
+
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix-core peak
 
 
@@ -805,7 +919,8 @@ def main() -> None:
     ap.add_argument("--ttft-requests", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload", default="request",
-                    choices=["request", "gather", "deviation", "replay", "traffic", "dropped", "attention"],
+                    choices=["request", "gather", "deviation", "replay", "traffic", "dropped", "attention", "extract",
+                             "decode"],
                     help="request: the 8k Qwen2.5-7B blend-prefill KV repair (default); gather / deviation / replay: "
                          "the re-RoPE+gather, deviation+top-k+scatter and 4x32k replay microbenchmarks")
     args = ap.parse_args()
@@ -816,7 +931,8 @@ def main() -> None:
     torch.cuda.set_device(dev)
     if args.workload != "request":
         fn = {"gather": bench_gather_only, "deviation": bench_deviation_topk, "replay": bench_replay,
-              "traffic": traffic_probe, "dropped": bench_dropped, "attention": bench_attention}[args.workload]
+              "traffic": traffic_probe, "dropped": bench_dropped, "attention": bench_attention,
+              "extract": bench_extract, "decode": bench_decode}[args.workload]
         print(json.dumps(fn(args.steps, args.warmup, dev)), flush=True)
         return
 

@@ -71,6 +71,10 @@ SIGNATURES = {
          _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p],
     ),
     "ckv_rope_table": (_i32, [_p, _i64, _i32, _f64, _p]),
+    "ckv_extract_chunks": (
+        _i32,
+        [_p, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p],
+    ),
     "ckv_attention_active": (
         _i32,
         [_p, _p, _i64, _i64, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p],

@@ -232,6 +232,56 @@ class HipEngine(DecoderPieces):
             t.record_stream(side)  # allocated on the main stream, read or written on the side stream
         return done
 
+    # -- decode ---------------------------------------------------------------------------
+
+    @torch.inference_mode()
+    def generate(self, result: PrefillResult, max_tokens: int = 32) -> list[int]:
+        """Greedy decode continuing a prefill (torch_engine.py:180-198) on preallocated caches.
+
+        The reference appends each new token with a torch.cat of every layer's whole cache
+        (:190-191), re-copying the cache once per token. Here one (L, 1, H, N + max_tokens, D) slab
+        per tensor is filled once from the prefill's caches; each step writes the token's rotated
+        k and its v into row pos in place (ckv_rope_qkv) and attends over the slab with the
+        position as the mask (rows past pos are never read)."""
+        out: list[int] = []
+        nxt = int(result.logits[-1].argmax().item())
+        if max_tokens <= 0 or nxt in self.eos:
+            return out
+        dev, H, D, L = self.device, self.n_kv, self.head_dim, len(self.layers)
+        N = result.keys[0].shape[2]
+        cap = N + max_tokens
+        Ks = torch.empty((L, 1, H, cap, D), dtype=self.kv_dtype, device=dev)
+        Vs = torch.empty_like(Ks)
+        for li in range(L):
+            Ks[li, :, :, :N].copy_(result.keys[li])
+            Vs[li, :, :, :N].copy_(result.values[li])
+        tab = self._table(cap)
+        positions = torch.arange(N, cap, device=dev)
+        err = torch.zeros(1, dtype=torch.int32, device=dev)
+        pos = N
+        while len(out) < max_tokens and nxt not in self.eos:
+            out.append(nxt)
+            h = self.inner.embed_tokens(torch.tensor([[nxt]], device=dev))
+            where = positions[pos - N : pos - N + 1]
+            for li, layer in enumerate(self.layers):
+                q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
+                K, V = Ks[li], Vs[li]
+                q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=K, v_out=V,
+                                    rows=where, table=tab, err=err)
+                attn = layer.self_attn
+                if self._native_attention and self.attention == "fused":
+                    o = ops.attention_active(q.transpose(1, 2), K, V, where, err=err)
+                else:
+                    o = F.scaled_dot_product_attention(q.transpose(1, 2), K[:, :, : pos + 1], V[:, :, : pos + 1],
+                                                       enable_gqa=True).transpose(1, 2)
+                h = h + attn.o_proj(o.reshape(1, 1, -1))
+                h = h + layer.mlp(layer.post_attention_layernorm(h))
+            nxt = int(self._logits(h)[0, -1].argmax().item())
+            pos += 1
+        if int(err.item()) != 0:
+            raise RuntimeError("a decode kernel reported an out-of-range position")
+        return out
+
     # -- main entry -----------------------------------------------------------------------
 
     @torch.inference_mode()
@@ -345,4 +395,5 @@ class HipEngine(DecoderPieces):
 
         layer0 = len(plan.layer0_idx) if config.full_first_layer else N - plan.n_cached
         stats = stats_dict(N, plan.n_cached, n_layers, layer0, selected_cached, chunk_stats)
-        return PrefillResult(logits, torch.arange(logits_from, N), keys_out, values_out, stats, copy=lambda t: t.contiguous())
+        return PrefillResult(logits, torch.arange(logits_from, N), keys_out, values_out, stats,
+                             copy=lambda t: t.contiguous(), extract=lambda spans: ops.extract_chunks(k_slab, v_slab, spans))

@@ -454,3 +454,45 @@ def rope_table(n_positions: int, head_dim: int, theta: float, device) -> torch.T
     _dev(out)
     check(lib().ckv_rope_table(_ptr(out), n_positions, head_dim, float(theta), _stream(out.device)), "ckv_rope_table")
     return out
+
+
+def extract_chunks(
+    k_slab: torch.Tensor, v_slab: torch.Tensor, spans: list, err: torch.Tensor | None = None
+) -> list[torch.Tensor]:
+    """Copies of token rows [start, end) of every layer's K and V for each (start, end) in spans,
+    one launch for all of them (base.py:55-60 per layer and segment in the reference).
+
+    k_slab/v_slab: (L, 1, H, N, D) contiguous. Returns one (2, L, 1, H, end - start, D) tensor per
+    span (index 0 = keys, 1 = values), each its own allocation so a store can free it alone.
+    """
+    _dev(k_slab, v_slab)
+    if not (k_slab.is_contiguous() and v_slab.is_contiguous() and k_slab.shape == v_slab.shape):
+        raise ValueError("K/V slabs must be contiguous and of equal shape")
+    L, _, H, N, D = k_slab.shape
+    dev = k_slab.device
+    bufs, meta = [], []
+    for start, end in spans:
+        start, end = int(start), int(end)
+        if not 0 <= start <= end <= N:
+            raise ValueError(f"span [{start}, {end}) outside the request of {N} tokens")
+        b = torch.empty((2, L, 1, H, end - start, D), dtype=k_slab.dtype, device=dev)
+        bufs.append(b)
+        meta.append((b.data_ptr(), start, end - start))
+    live = [(p, s, n) for p, s, n in meta if n > 0]
+    if not live:
+        return bufs
+    # descriptors: [ptr lo, ptr hi] per span, then (start, len) pairs; pinned, one async copy
+    # (torch's pinned allocator keeps the host block until the copy has run)
+    pinned = torch.empty(len(live) * 4, dtype=torch.int32, pin_memory=True)
+    host = pinned.numpy()
+    host[: 2 * len(live)].view("<u8")[:] = [p for p, _, _ in live]
+    host[2 * len(live) :] = [v for _, s, n in live for v in (s, n)]
+    d = pinned.to(dev, non_blocking=True)
+    check(
+        lib().ckv_extract_chunks(
+            _ptr(k_slab), _ptr(v_slab), H * N * D, N * D, _ptr(d), d.data_ptr() + 8 * len(live), len(live),
+            max(n for _, _, n in live), L, H, N, D, dtype_code(k_slab.dtype), _ptr(err), _stream(dev),
+        ),
+        "ckv_extract_chunks",
+    )
+    return bufs

@@ -57,13 +57,21 @@ class PrefillResult:
     values: list[Any]
     stats: dict = field(default_factory=dict)
     copy: Callable[[Any], Any] = lambda a: a  # backend copy, so stored chunks don't pin request buffers
+    # Batched extraction hook (spans -> one (2, L, 1, H, len, D) buffer per span); set by HipEngine
+    # to its one-launch kernel. None: the per-layer `copy` path of the reference.
+    extract: Callable[[list], list] | None = None
 
     def chunk(self, start: int, end: int) -> ChunkKV:
-        return ChunkKV(
-            keys=[self.copy(k[:, :, start:end, :]) for k in self.keys],
-            values=[self.copy(v[:, :, start:end, :]) for v in self.values],
-            start=start,
-        )
+        return self.chunks([(start, end)])[0]
+
+    def chunks(self, spans: list) -> list[ChunkKV]:
+        """ChunkKV copies of several (start, end) segments; with an extraction hook, one launch
+        for all layers of all of them."""
+        if self.extract is None:
+            return [ChunkKV(keys=[self.copy(k[:, :, s:e, :]) for k in self.keys],
+                            values=[self.copy(v[:, :, s:e, :]) for v in self.values], start=s) for s, e in spans]
+        return [ChunkKV(keys=list(b[0].unbind(0)), values=list(b[1].unbind(0)), start=int(s))
+                for b, (s, _) in zip(self.extract(spans), spans)]
 
 
 def plan_positions(n: int, placements: list, n_sink: int):

@@ -277,6 +277,23 @@ int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_token_strid
 int32_t ckv_rope_table(void* table, int64_t n_positions, int32_t head_dim, double theta, void* stream);
 
 /*
+ * Store-put extraction: for each of n_spans segments (spans[2s] = start, spans[2s+1] = len),
+ * copy token rows [start, start + len) of every layer's K and V out of the request slabs
+ * (layer l, head h, token t at base + l*layer_stride + h*head_stride + t*head_dim, elements)
+ * into the buffer dst_tab[s] (device address), laid out [2][n_layers][n_heads][len][head_dim]:
+ * K layers then V layers, so each layer's keys/values are a contiguous (1, H, len, D) block. The
+ * buffer must hold 2 * n_layers * n_heads * len * head_dim elements. max_len >= every len.
+ * A span outside [0, n_tokens) is skipped and flagged in *err. Bit copies (bf16 or f32).
+ * Replaces: PrefillResult.chunk's per-layer copies (base.py:55-60, torch_engine.py:177), called
+ * per reusable segment by the runtime (runtime.py:83-92): 2 x n_layers launches per segment.
+ */
+int32_t ckv_extract_chunks(const void* k_slab, const void* v_slab, int64_t layer_stride,
+                           int64_t head_stride, const uint64_t* dst_tab, const int32_t* spans,
+                           int32_t n_spans, int32_t max_len, int32_t n_layers, int32_t n_heads,
+                           int32_t n_tokens, int32_t head_dim, int32_t dtype, int32_t* err,
+                           void* stream);
+
+/*
  * Attention of the active rows over the whole cache with the causal mask given by positions:
  *   out[i, h, :] = softmax_j( scale * q[h, i, :] . K[h / G, j, :] ) V[h / G, j, :],
  *   j ranging over [0, positions[i]], G = n_q_heads / n_kv_heads.

@@ -231,6 +231,25 @@ def test_generate_matches_hf_greedy(models, parts):
     assert ours == ref[: len(ours)] and len(ours) > 0
 
 
+@pytest.mark.parametrize("heads,kv", [(4, 4), (8, 2)])
+def test_bf16_generate_on_preallocated_cache_matches_concat_decode(heads, kv):
+    """bf16 decode on the preallocated slab (in-place row writes, positions-masked attention)
+    gives the same greedy tokens as the reference-style torch.cat decode over the same prefill
+    (logits sharpened so greedy picks are not near-ties)."""
+    from chunkkv_amd.model import DecoderPieces
+
+    gpu = tiny_qwen2(layers=3, hidden=512, heads=heads, kv=kv, inter=1024, vocab=512, seed=6, dtype=torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        gpu.model.norm.weight.mul_(20.0)
+    eng = HipEngine(gpu, StubTokenizer())
+    assert eng._native_attention
+    rng = np.random.default_rng(6)
+    res = eng.prefill(rng.integers(1, 511, 300).tolist())
+    ours = eng.generate(res, max_tokens=12)
+    ref = DecoderPieces.generate(eng, res, max_tokens=12)
+    assert len(ours) > 0 and ours == ref
+
+
 @pytest.mark.parametrize("attention,heads,kv", [("reference", 4, 4), ("fused", 4, 4), ("fused", 8, 2)])
 def test_bf16_blend_matches_rocm_reference_ops(attention, heads, kv):
     """bf16 model: HipEngine (reference SDPA call, or the fused path with the positions-masked
