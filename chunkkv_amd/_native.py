@@ -77,8 +77,9 @@ SIGNATURES = {
     ),
     "ckv_attention_active": (
         _i32,
-        [_p, _p, _i64, _i64, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p],
+        [_p, _p, _i64, _i64, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f64, _p, _i64, _p, _p],
     ),
+    "ckv_attention_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _p, _p]),
     "ckv_scatter_rows": (
         _i32,
         [_p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p, _p],

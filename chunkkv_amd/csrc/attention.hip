@@ -17,8 +17,13 @@
 // max/sum and the output rows live in that lane and only two xor-shuffles per tile combine the
 // four lane groups. K rows are stored in LDS in the order the fragment reads want (conflict-free
 // 16-byte reads) and V is transposed on its way into LDS. Scores and the output accumulate in
-// fp32; P is rounded to bf16 for the second product (as fused SDPA kernels do). Built with the
+// fp32; P is rounded to bf16 for the second product (as fused SDPA kernels do). When a launch
+// would have too few workgroups to fill the chip (decode: one query, long cache) the cache range
+// is split over more workgroups (flash-decoding): each writes unnormalised fp32 rows with their
+// running max and sum to a caller-provided workspace, and a small kernel merges the splits. Built with the
 // MFMA VGPR form (no accumulator-register copies around the online-softmax rescale).
+#include <algorithm>
+
 #include "ckv_common.hpp"
 
 namespace ckv {
@@ -59,8 +64,8 @@ __attribute__((amdgpu_waves_per_eu(CKV_ATTN_OCC)))
 void attn_active_kernel(
     char* __restrict__ out, const char* __restrict__ q, int64_t q_hs_b, int64_t q_ts_b,
     const char* __restrict__ kc, const char* __restrict__ vc, int64_t kv_hs_b,
-    const int64_t* __restrict__ pos, int n, int N, int Hq, int group, float scale_log2,
-    int32_t* __restrict__ err) {
+    const int64_t* __restrict__ pos, int n, int N, int Hq, int group, float scale_log2, int split_tiles,
+    float* __restrict__ ws, int32_t* __restrict__ err) {
   constexpr int DS = D / 32;          // k-steps of S^T = K Q^T
   constexpr int DT = D / 16;          // 16-row tiles of O^T
   constexpr int CPR = D / 8;          // 16-byte chunks per cache row
@@ -112,7 +117,11 @@ void attn_active_kernel(
   int bmax = blk_max_s[0];
 #pragma unroll
   for (int w = 1; w < kAttnWaves; ++w) bmax = max(bmax, blk_max_s[w]);
-  const int n_tiles = bmax < 0 ? 0 : bmax / kAttnBN + 1;
+  // This workgroup's share of the cache tiles: all of them, or split z of the key range when the
+  // launch is split (flash-decoding: few queries, long cache) and partials go to ws.
+  const int all_tiles = bmax < 0 ? 0 : bmax / kAttnBN + 1;
+  const int tile_begin = ws != nullptr ? (int)blockIdx.z * split_tiles : 0;
+  const int n_tiles = ws != nullptr ? min(all_tiles, tile_begin + split_tiles) : all_tiles;
 
   // Q fragments (B operand of S^T): query q0 + 16 qg + lm, head-dim 32 s + 8 g .. + 8.
   bf16x8 qf[kAttnQG][DS];
@@ -159,9 +168,9 @@ void attn_active_kernel(
       if (r + 1 < N) vb[i] = ld16(vh + (int64_t)(r + 1) * (D * 2) + col * 16);
     }
   };
-  if (kAttnPrefetch && n_tiles > 0) load_tile(0);
+  if (kAttnPrefetch && tile_begin < n_tiles) load_tile(tile_begin * kAttnBN);
 
-  for (int tile = 0; tile < n_tiles; ++tile) {
+  for (int tile = tile_begin; tile < n_tiles; ++tile) {
     const int n0 = tile * kAttnBN;
     if (!kAttnPrefetch) load_tile(n0);
     __syncthreads();  // previous tile's LDS reads are done
@@ -260,6 +269,8 @@ void attn_active_kernel(
   }
 
   // Normalise and write: lane (g, lm) holds O[query][dt*16 + 4g + e], 4 bf16 = 8 bytes per tile.
+  // A split launch writes the unnormalised fp32 rows with their (max, sum) instead; the combine
+  // kernel merges the splits.
 #pragma unroll
   for (int qg = 0; qg < kAttnQG; ++qg) {
     float l = l_run[qg];
@@ -267,6 +278,17 @@ void attn_active_kernel(
     l += __shfl_xor(l, 32, 64);
     const int m = q0 + qg * 16 + lm;
     if (m >= n) continue;
+    if (ws != nullptr) {
+      float* prow = ws + (((int64_t)blockIdx.z * Hq + hq) * n + m) * (D + 4);  // 16-byte aligned rows
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *(float4*)(prow + dt * 16 + 4 * g) = make_float4(o[qg][dt][0], o[qg][dt][1],
+                                                                                    o[qg][dt][2], o[qg][dt][3]);
+      if (g == 0) {
+        prow[D] = m_run[qg];
+        prow[D + 1] = l;
+      }
+      continue;
+    }
     const float inv = 1.f / l;
     char* orow = out + ((int64_t)m * Hq + hq) * (D * 2);
 #pragma unroll
@@ -282,13 +304,64 @@ void attn_active_kernel(
   }
 }
 
+// Merge the splits of a split launch: for query m and head h, with (M_z, L_z, O_z) the partials
+// of split z (max in the log2 domain, sum and unnormalised rows relative to M_z):
+//   out = sum_z 2^(M_z - M) O_z / sum_z 2^(M_z - M) L_z,  M = max_z M_z  (splits with M_z = -inf
+// saw no visible row and weigh 0). One 64-lane wavefront per (query, head); lane d covers
+// head-dim columns d, d + 64.
+template <int D>
+__global__ __launch_bounds__(64) void attn_combine_kernel(char* __restrict__ out, const float* __restrict__ ws,
+                                                          int n, int Hq, int splits) {
+  const int m = blockIdx.x, hq = blockIdx.y, lane = threadIdx.x;
+  const int64_t stride = (int64_t)Hq * n * (D + 4);
+  const float* base = ws + ((int64_t)hq * n + m) * (D + 4);
+  float M = -INFINITY;
+  for (int z = 0; z < splits; ++z) M = fmaxf(M, base[z * stride + D]);
+  float L = 0.f, acc[D / 64];
+#pragma unroll
+  for (int j = 0; j < D / 64; ++j) acc[j] = 0.f;
+  for (int z = 0; z < splits; ++z) {
+    const float* pz = base + z * stride;
+    const float mz = pz[D];
+    if (mz == -INFINITY) continue;
+    const float w = __builtin_amdgcn_exp2f(mz - M);
+    L += w * pz[D + 1];
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) acc[j] += w * pz[lane + 64 * j];
+  }
+  const float inv = 1.f / L;
+  uint16_t* orow = reinterpret_cast<uint16_t*>(out + ((int64_t)m * Hq + hq) * (D * 2));
+#pragma unroll
+  for (int j = 0; j < D / 64; ++j) orow[lane + 64 * j] = (uint16_t)f32_to_bf16_bits(acc[j] * inv);
+}
+
 }  // namespace ckv
+
+extern "C" int64_t ckv_attention_workspace_bytes(int32_t n_queries, int32_t n_tokens, int32_t n_q_heads,
+                                                 int32_t head_dim, int32_t* splits_out, int32_t* split_tiles_out) {
+  using namespace ckv;
+  int splits = 1, split_tiles = 0;
+  if (n_queries > 0 && n_tokens > 0 && n_q_heads > 0 && head_dim > 0) {
+    const int64_t blocks = (int64_t)((n_queries + kAttnBM - 1) / kAttnBM) * n_q_heads;
+    const int tiles = (n_tokens + kAttnBN - 1) / kAttnBN;
+    constexpr int64_t kTarget = 1024;  // workgroups that fill the 256 CUs a few times over
+    if (blocks < kTarget / 2 && tiles >= 8) {
+      const int want = (int)std::min<int64_t>((kTarget + blocks - 1) / blocks, tiles / 4);
+      split_tiles = (tiles + want - 1) / want;
+      splits = (tiles + split_tiles - 1) / split_tiles;
+    }
+  }
+  if (splits_out != nullptr) *splits_out = splits;
+  if (split_tiles_out != nullptr) *split_tiles_out = split_tiles;
+  return splits > 1 ? (int64_t)splits * n_q_heads * n_queries * (head_dim + 4) * 4 : 0;
+}
 
 extern "C" int32_t ckv_attention_active(void* out, const void* q, int64_t q_head_stride, int64_t q_token_stride,
                                         const void* k_cache, const void* v_cache, int64_t kv_head_stride,
                                         const int64_t* positions, int32_t n_queries, int32_t n_tokens,
                                         int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
-                                        double scale, int32_t* err, void* stream) {
+                                        double scale, void* workspace, int64_t workspace_bytes, int32_t* err,
+                                        void* stream) {
   using namespace ckv;
   if (out == nullptr || q == nullptr || k_cache == nullptr || v_cache == nullptr || positions == nullptr)
     return CKV_ERR_INVALID_ARGUMENT;
@@ -303,18 +376,34 @@ extern "C" int32_t ckv_attention_active(void* out, const void* q, int64_t q_head
   const int blocks = (n_queries + kAttnBM - 1) / kAttnBM;
   if (n_q_heads > 65535) return CKV_ERR_TOO_LARGE;
   const float scale_log2 = (float)(scale * 1.4426950408889634);  // exp(x) = exp2(x log2 e)
-  dim3 grid((unsigned)blocks, (unsigned)n_q_heads);
+  int splits = 1, split_tiles = 0;
+  const int64_t need = ckv_attention_workspace_bytes(n_queries, n_tokens, n_q_heads, head_dim, &splits, &split_tiles);
+  float* ws = nullptr;
+  if (splits > 1 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0) {
+    ws = (float*)workspace;
+  } else {
+    splits = 1;
+  }
+  dim3 grid((unsigned)blocks, (unsigned)n_q_heads, (unsigned)splits);
   const int group = n_q_heads / n_kv_heads;
-  if (head_dim == 128)
-    hipLaunchKernelGGL((attn_active_kernel<128>), grid, dim3(kAttnWaves * 64), 0, (hipStream_t)stream, (char*)out,
-                       (const char*)q, q_head_stride * 2, q_token_stride * 2, (const char*)k_cache,
-                       (const char*)v_cache, kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group,
-                       scale_log2, err);
-  else
-    hipLaunchKernelGGL((attn_active_kernel<64>), grid, dim3(kAttnWaves * 64), 0, (hipStream_t)stream, (char*)out,
-                       (const char*)q, q_head_stride * 2, q_token_stride * 2, (const char*)k_cache,
-                       (const char*)v_cache, kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group,
-                       scale_log2, err);
+  hipStream_t st = (hipStream_t)stream;
+  if (head_dim == 128) {
+    hipLaunchKernelGGL((attn_active_kernel<128>), grid, dim3(kAttnWaves * 64), 0, st, (char*)out, (const char*)q,
+                       q_head_stride * 2, q_token_stride * 2, (const char*)k_cache, (const char*)v_cache,
+                       kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group, scale_log2, split_tiles,
+                       ws, err);
+    if (ws != nullptr)
+      hipLaunchKernelGGL((attn_combine_kernel<128>), dim3((unsigned)n_queries, (unsigned)n_q_heads), dim3(64), 0, st,
+                         (char*)out, ws, n_queries, n_q_heads, splits);
+  } else {
+    hipLaunchKernelGGL((attn_active_kernel<64>), grid, dim3(kAttnWaves * 64), 0, st, (char*)out, (const char*)q,
+                       q_head_stride * 2, q_token_stride * 2, (const char*)k_cache, (const char*)v_cache,
+                       kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group, scale_log2, split_tiles,
+                       ws, err);
+    if (ws != nullptr)
+      hipLaunchKernelGGL((attn_combine_kernel<64>), dim3((unsigned)n_queries, (unsigned)n_q_heads), dim3(64), 0, st,
+                         (char*)out, ws, n_queries, n_q_heads, splits);
+  }
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

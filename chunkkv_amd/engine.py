@@ -80,6 +80,8 @@ class HipEngine(DecoderPieces):
         self.overlap = overlap
         self._side: torch.cuda.Stream | None = None
         self._rope_tab: torch.Tensor | None = None  # (cos, sin) per position, grown on demand
+        # generate(): replay each decode step after the first from a HIP graph (device-side loop)
+        self.decode_graphs = True
         # Set to a dict to record the layer-1 selection inputs/outputs (device tensors) of the
         # next prefill, for parity checks; None (default) records nothing.
         self.trace: dict | None = None
@@ -242,7 +244,10 @@ class HipEngine(DecoderPieces):
         (:190-191), re-copying the cache once per token. Here one (L, 1, H, N + max_tokens, D) slab
         per tensor is filled once from the prefill's caches; each step writes the token's rotated
         k and its v into row pos in place (ckv_rope_qkv) and attends over the slab with the
-        position as the mask (rows past pos are never read)."""
+        position as the mask (rows past pos are never read). With the positions-masked attention
+        kernel a step reads its token and position from device tensors and writes the next greedy
+        token back, so after the first (eager) step every step is one HIP graph replay; the host
+        only reads the token, for the EOS test."""
         out: list[int] = []
         nxt = int(result.logits[-1].argmax().item())
         if max_tokens <= 0 or nxt in self.eos:
@@ -256,31 +261,57 @@ class HipEngine(DecoderPieces):
             Ks[li, :, :, :N].copy_(result.keys[li])
             Vs[li, :, :, :N].copy_(result.values[li])
         tab = self._table(cap)
-        positions = torch.arange(N, cap, device=dev)
         err = torch.zeros(1, dtype=torch.int32, device=dev)
-        pos = N
+        device_loop = self._native_attention and self.attention == "fused"
+        tok = torch.tensor([[nxt]], dtype=torch.int64, device=dev)
+        where = torch.tensor([N], dtype=torch.int64, device=dev)
+        graph = None
         while len(out) < max_tokens and nxt not in self.eos:
             out.append(nxt)
-            h = self.inner.embed_tokens(torch.tensor([[nxt]], device=dev))
-            where = positions[pos - N : pos - N + 1]
-            for li, layer in enumerate(self.layers):
-                q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
-                K, V = Ks[li], Vs[li]
-                q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=K, v_out=V,
-                                    rows=where, table=tab, err=err)
-                attn = layer.self_attn
-                if self._native_attention and self.attention == "fused":
-                    o = ops.attention_active(q.transpose(1, 2), K, V, where, err=err)
-                else:
-                    o = F.scaled_dot_product_attention(q.transpose(1, 2), K[:, :, : pos + 1], V[:, :, : pos + 1],
-                                                       enable_gqa=True).transpose(1, 2)
-                h = h + attn.o_proj(o.reshape(1, 1, -1))
-                h = h + layer.mlp(layer.post_attention_layernorm(h))
-            nxt = int(self._logits(h)[0, -1].argmax().item())
-            pos += 1
+            if not device_loop:
+                self._decode_step_sdpa(tok, N + len(out) - 1, Ks, Vs, tab, err)
+            elif graph is not None:
+                graph.replay()
+            else:
+                self._decode_step(tok, where, Ks, Vs, tab, err)  # also the warm-up of the capture
+                if max_tokens - len(out) >= 2 and self.decode_graphs:
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        self._decode_step(tok, where, Ks, Vs, tab, err)
+            nxt = int(tok.item())
         if int(err.item()) != 0:
             raise RuntimeError("a decode kernel reported an out-of-range position")
         return out
+
+    def _decode_step(self, tok, where, Ks, Vs, tab, err) -> None:
+        """One token (tok: (1, 1) int64 at position where: (1,) int64) through every layer; writes
+        the next greedy token into tok and advances where. No host values are read."""
+        H, D = self.n_kv, self.head_dim
+        h = self.inner.embed_tokens(tok)
+        for li, layer in enumerate(self.layers):
+            q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
+            q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=Ks[li], v_out=Vs[li],
+                                rows=where, table=tab, err=err)
+            o = ops.attention_active(q.transpose(1, 2), Ks[li], Vs[li], where, err=err)
+            h = h + layer.self_attn.o_proj(o.view(1, 1, -1))
+            h = h + layer.mlp(layer.post_attention_layernorm(h))
+        tok.copy_(self._logits(h)[0, -1].argmax().view(1, 1))
+        where.add_(1)
+
+    def _decode_step_sdpa(self, tok, pos: int, Ks, Vs, tab, err) -> None:
+        """_decode_step for models outside the attention kernel's range (SDPA over rows <= pos)."""
+        H, D = self.n_kv, self.head_dim
+        where = torch.tensor([pos], dtype=torch.int64, device=self.device)
+        h = self.inner.embed_tokens(tok)
+        for li, layer in enumerate(self.layers):
+            q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
+            q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=Ks[li], v_out=Vs[li],
+                                rows=where, table=tab, err=err)
+            o = F.scaled_dot_product_attention(q.transpose(1, 2), Ks[li][:, :, : pos + 1], Vs[li][:, :, : pos + 1],
+                                               enable_gqa=True)
+            h = h + layer.self_attn.o_proj(o.transpose(1, 2).reshape(1, 1, -1))
+            h = h + layer.mlp(layer.post_attention_layernorm(h))
+        tok.copy_(self._logits(h)[0, -1].argmax().view(1, 1))
 
     # -- main entry -----------------------------------------------------------------------
 

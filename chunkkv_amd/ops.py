@@ -324,12 +324,15 @@ def attention_active(
     scale: float | None = None,
     err: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    split: bool = True,
 ) -> torch.Tensor:
     """Attention of the active query rows over the cache, query i seeing positions <= positions[i]
     (the reference's boolean-mask SDPA with enable_gqa, torch_engine.py:157 and :68-72).
 
     q: (1, Hq, n, D) bf16 with contiguous rows; K/V: (1, Hkv, N, D) contiguous; positions: int64
     (n,). Returns (1, n, Hq, D) bf16, token-major (``.view(1, n, Hq * D)`` feeds o_proj).
+    split: let launches too small to fill the chip split the cache range (a workspace is
+    allocated for the partial results).
     """
     _dev(q, K, V, positions)
     _, Hq, n, D = q.shape
@@ -348,10 +351,12 @@ def attention_active(
     elif out.shape != (1, n, Hq, D) or not out.is_contiguous() or out.dtype != q.dtype:
         raise ValueError("out must be contiguous (1, n, Hq, D) bf16")
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    ws_bytes = lib().ckv_attention_workspace_bytes(n, N, Hq, D, None, None) if split else 0
+    ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
     check(
         lib().ckv_attention_active(
             _ptr(out), _ptr(q), q.stride(1), q.stride(2), _ptr(K), _ptr(V), N * D, _ptr(positions), n, N, Hq, Hkv,
-            D, dtype_code(q.dtype), scale, _ptr(err), _stream(q.device),
+            D, dtype_code(q.dtype), scale, _ptr(ws), ws_bytes, _ptr(err), _stream(q.device),
         ),
         "ckv_attention_active",
     )

@@ -310,13 +310,29 @@ int32_t ckv_extract_chunks(const void* k_slab, const void* v_slab, int64_t layer
  *              output projection reads
  * dtype must be CKV_DTYPE_BF16 and head_dim 64 or 128. Scores and the output accumulate in
  * fp32; the softmax weights are rounded to bf16 before they multiply V.
- * Replaces: the mask construction and SDPA call of torch_engine.py:157, :68-72.
+ *   workspace  optional device buffer of workspace_bytes >= ckv_attention_workspace_bytes(...)
+ *              (16-byte aligned): with it, launches that are too small to fill the chip (few
+ *              queries over a long cache, e.g. decode) split the cache range over more
+ *              workgroups and merge the partial results; without it they run unsplit. The
+ *              result is the same up to fp32 rounding of the merge.
+ * Replaces: the mask construction and SDPA call of torch_engine.py:157, :68-72 (and the decode
+ * step's SDPA, :192).
  */
 int32_t ckv_attention_active(void* out, const void* q, int64_t q_head_stride, int64_t q_token_stride,
                              const void* k_cache, const void* v_cache, int64_t kv_head_stride,
                              const int64_t* positions, int32_t n_queries, int32_t n_tokens,
                              int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t dtype,
-                             double scale, int32_t* err, void* stream);
+                             double scale, void* workspace, int64_t workspace_bytes, int32_t* err,
+                             void* stream);
+
+/*
+ * Bytes of workspace ckv_attention_active uses to split a launch of this shape (0: it never
+ * splits this shape); the split count and cache tiles per split go to *splits and
+ * *split_tiles when those are not NULL. Host-only, no device work. No counterpart in the
+ * reference.
+ */
+int64_t ckv_attention_workspace_bytes(int32_t n_queries, int32_t n_tokens, int32_t n_q_heads,
+                                      int32_t head_dim, int32_t* splits, int32_t* split_tiles);
 
 #ifdef __cplusplus
 }

@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "chunkkv_amd.h"
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int32_t|const char\*)\s+(ckv_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int32_t|int64_t|const char\*)\s+(ckv_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -125,3 +125,13 @@ def test_struct_layouts_match_header(tmp_path):
     assert SEG_FIELDS * 4 == 24 and SPAN_FIELDS * 4 == 16
     assert np.dtype(np.int32).itemsize == 4
     assert ctypes.sizeof(ctypes.c_void_p) == 8
+
+
+def test_attention_workspace_sizing_is_host_only():
+    """The split decision for the attention: decode-like shapes split, big launches do not."""
+    lib = _native.lib()
+    s, t = ctypes.c_int32(0), ctypes.c_int32(0)
+    nb = lib.ckv_attention_workspace_bytes(1, 8256, 28, 128, ctypes.byref(s), ctypes.byref(t))
+    assert s.value > 1 and t.value * s.value >= (8256 + 63) // 64 and nb == s.value * 28 * 1 * 132 * 4
+    assert lib.ckv_attention_workspace_bytes(2976, 8256, 28, 128, None, None) == 0
+    assert lib.ckv_attention_workspace_bytes(1, 100, 28, 128, None, None) == 0  # short cache: no split

@@ -93,3 +93,18 @@ def test_attention_strided_query_view():
     out = ops.attention_active(qt, O.from_numpy(K, DEV)[None], O.from_numpy(V, DEV)[None], torch.from_numpy(pos).to(DEV))
     ref, _ = _run(q, K, V, pos)
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,N,n", [(28, 4, 128, 8256, 1), (28, 4, 128, 5000, 3), (14, 2, 64, 3000, 40)])
+def test_attention_split_launch_matches_oracle_and_unsplit(Hq, Hkv, D, N, n):
+    """Decode-like shapes split the cache range over workgroups and merge: same result as the
+    unsplit launch (up to the merge's fp32 rounding) and the oracle."""
+    q, K, V, pos = _case(N + n, Hq, Hkv, D, N, n, with_ends=False)
+    pos[-1] = N - 1
+    assert _native.lib().ckv_attention_workspace_bytes(n, N, Hq, D, None, None) > 0
+    args = (O.from_numpy(q, DEV)[None], O.from_numpy(K, DEV)[None], O.from_numpy(V, DEV)[None], torch.from_numpy(pos).to(DEV))
+    split = ops.attention_active(*args)
+    whole = ops.attention_active(*args, split=False)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(split.float(), whole.float(), atol=4e-3, rtol=0)
+    np.testing.assert_allclose(split[0].float().cpu().numpy(), O.attention_active(q, K, V, pos), atol=ATOL, rtol=0)

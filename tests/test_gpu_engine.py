@@ -245,9 +245,11 @@ def test_bf16_generate_on_preallocated_cache_matches_concat_decode(heads, kv):
     assert eng._native_attention
     rng = np.random.default_rng(6)
     res = eng.prefill(rng.integers(1, 511, 300).tolist())
-    ours = eng.generate(res, max_tokens=12)
+    ours = eng.generate(res, max_tokens=12)  # device loop, HIP graph replays
     ref = DecoderPieces.generate(eng, res, max_tokens=12)
     assert len(ours) > 0 and ours == ref
+    eng.decode_graphs = False
+    assert eng.generate(res, max_tokens=12) == ours  # the same steps issued eagerly
 
 
 @pytest.mark.parametrize("attention,heads,kv", [("reference", 4, 4), ("fused", 4, 4), ("fused", 8, 2)])
