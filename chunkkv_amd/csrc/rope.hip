@@ -110,7 +110,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
 
 // With a cos/sin table a token needs no shared state, so the work is flattened: one thread per
 // (token, item), item = a rotated 16-byte column pair of a q/k head or a copied 16-byte chunk of
-// a v row, grid-stride over all of them (every thread busy, whatever the head counts).
+// a v row, grid-stride over all of them (every thread busy, whatever the head counts), rotation
+// items first.
 template <int DTYPE, int D>
 __global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
     char* __restrict__ q_out, int64_t qo_hs_b, int64_t qo_ts_b, char* __restrict__ k_out, int64_t ko_hs_b,
@@ -126,18 +127,24 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
   constexpr int HALF_B = HALF * E::kBytes;
   constexpr int CPR = D * E::kBytes / 16;
   typedef __attribute__((address_space(1))) const int64_t gi64;
-  const int n_rot = (Hq + Hkv) * TPR;
-  const unsigned per_tok = (unsigned)(n_rot + (v_out != nullptr ? Hkv * CPR : 0));
-  const unsigned total = (unsigned)n * per_tok;  // < 2^31, checked by the host
+  const unsigned n_rot = (unsigned)((Hq + Hkv) * TPR);       // rotation items per token
+  const unsigned n_cp = v_out != nullptr ? (unsigned)(Hkv * CPR) : 0u;  // copy items per token
+  const unsigned rot_total = (unsigned)n * n_rot;
+  const unsigned total = rot_total + (unsigned)n * n_cp;  // < 2^31, checked by the host
+  // Items are ordered by kind (every rotation item, then every copy item) so that a wavefront
+  // runs one kind only.
   for (unsigned idx = blockIdx.x * kRopeThreads + threadIdx.x; idx < total; idx += gridDim.x * kRopeThreads) {
-    const int t = (int)(idx / per_tok), it = (int)(idx - (unsigned)t * per_tok);
+    const bool rot = idx < rot_total;
+    const unsigned j = rot ? idx : idx - rot_total;
+    const unsigned per = rot ? n_rot : n_cp;
+    const int t = (int)(j / per), it = (int)(j - (unsigned)t * per);
     const int64_t p = *(gi64*)(pos + t);
     const int64_t row = rows != nullptr ? *(gi64*)(rows + t) : t;
     if (p < 0 || p >= n_table || row < 0 || row >= n_out) {
-      if (it == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+      if (it == 0 && rot) flag_error(err, CKV_DEVICE_ERR_RANGE);
       continue;
     }
-    if (it < n_rot) {
+    if (rot) {
       const int h = it / TPR, col = it % TPR;
       const char* s = h < Hq ? q_in + h * qi_hs_b + t * qi_ts_b : k_in + (h - Hq) * ki_hs_b + t * ki_ts_b;
       char* d = h < Hq ? q_out + h * qo_hs_b + t * qo_ts_b : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b;
@@ -159,7 +166,7 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
       st16(d, y1);
       st16(d + HALF_B, y2);
     } else {
-      const int i = it - n_rot, h = i / CPR, c = i % CPR;
+      const int h = it / CPR, c = it % CPR;
       st16(v_out + h * vo_hs_b + row * vo_ts_b + c * 16, ld16(v_in + h * vi_hs_b + t * vi_ts_b + c * 16));
     }
   }
