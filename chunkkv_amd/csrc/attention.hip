@@ -152,20 +152,39 @@ void attn_active_kernel(
   constexpr int KL = (kAttnBN * CPR) / NT;        // 16-byte K loads per thread and tile
   constexpr int VL = ((kAttnBN / 2) * CPR) / NT;  // V row-pair loads per thread and tile
   vec16 kr[KL], va[VL], vb[VL];
+  // Per-thread offsets of its K chunks and V row pairs inside a tile (tile-invariant).
+  int k_off[KL], k_row[KL], v_off[VL], v_row[VL];
+#pragma unroll
+  for (int i = 0; i < KL; ++i) {
+    const int c = threadIdx.x + i * NT;
+    k_row[i] = c / CPR;
+    k_off[i] = k_row[i] * (D * 2) + (c % CPR) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < VL; ++i) {
+    const int c = threadIdx.x + i * NT;
+    v_row[i] = 2 * (c % (kAttnBN / 2));
+    v_off[i] = v_row[i] * (D * 2) + (c / (kAttnBN / 2)) * 16;
+  }
   auto load_tile = [&](int n0) {  // global -> registers; rows past the cache read as zero
+    const char* kt = kh + (int64_t)n0 * (D * 2);
+    const char* vt = vh + (int64_t)n0 * (D * 2);
+    if (n0 + kAttnBN <= N) {  // uniform: a full tile needs no row checks
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int c = threadIdx.x + i * NT, r = c / CPR, col = c % CPR;
-      kr[i] = vec16{0, 0, 0, 0};
-      if (n0 + r < N) kr[i] = ld16(kh + (int64_t)(n0 + r) * (D * 2) + col * 16);
-    }
+      for (int i = 0; i < KL; ++i) kr[i] = ld16(kt + k_off[i]);
 #pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int c = threadIdx.x + i * NT, pr = c % (kAttnBN / 2), col = c / (kAttnBN / 2);
-      const int r = n0 + 2 * pr;
-      va[i] = vb[i] = vec16{0, 0, 0, 0};
-      if (r < N) va[i] = ld16(vh + (int64_t)r * (D * 2) + col * 16);
-      if (r + 1 < N) vb[i] = ld16(vh + (int64_t)(r + 1) * (D * 2) + col * 16);
+      for (int i = 0; i < VL; ++i) {
+        va[i] = ld16(vt + v_off[i]);
+        vb[i] = ld16(vt + v_off[i] + D * 2);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < KL; ++i) kr[i] = n0 + k_row[i] < N ? ld16(kt + k_off[i]) : vec16{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < VL; ++i) {
+        va[i] = n0 + v_row[i] < N ? ld16(vt + v_off[i]) : vec16{0, 0, 0, 0};
+        vb[i] = n0 + v_row[i] + 1 < N ? ld16(vt + v_off[i] + D * 2) : vec16{0, 0, 0, 0};
+      }
     }
   };
   if (kAttnPrefetch && tile_begin < n_tiles) load_tile(tile_begin * kAttnBN);
@@ -183,10 +202,9 @@ void attn_active_kernel(
     for (int i = 0; i < VL; ++i) {
       const int c = threadIdx.x + i * NT, pr = c % (kAttnBN / 2), col = c / (kAttnBN / 2);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {  // (V[2pr][d], V[2pr+1][d]) for d = 8 col + e, packed
-        const unsigned lo = (e & 1) ? (va[i][e >> 1] >> 16) : (va[i][e >> 1] & 0xffffu);
-        const unsigned hi = (e & 1) ? (vb[i][e >> 1] >> 16) : (vb[i][e >> 1] & 0xffffu);
-        *(unsigned*)(v_lds + (8 * col + e) * VROW + pr * 4) = lo | (hi << 16);
+      for (int e = 0; e < 8; ++e) {  // (V[2pr][d], V[2pr+1][d]) for d = 8 col + e: one byte permute
+        const unsigned w = __builtin_amdgcn_perm(vb[i][e >> 1], va[i][e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
+        *(unsigned*)(v_lds + (8 * col + e) * VROW + pr * 4) = w;
       }
     }
     __syncthreads();
@@ -220,20 +238,29 @@ void attn_active_kernel(
     bf16x8 pb[kAttnQG][KB];
 #pragma unroll
     for (int qg = 0; qg < kAttnQG; ++qg) {
+      // Raw scores of this lane (query lm, rows n0 + 32 kb + 8 g + 4 t + e); rows past the query's
+      // position become -inf, on the tiles that reach past the lowest position only (uniform).
       float x[KB][8];
-      float bm = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float v = s[qg][kb][t][e] * scale_log2;
-            if (need_mask && n0 + 32 * kb + 8 * g + 4 * t + e > my_pos[qg]) v = -INFINITY;
-            x[kb][4 * t + e] = v;
-            bm = fmaxf(bm, v);
-          }
-      bm = wave_xor_max(wave_xor_max(bm, 16), 32);
+          for (int e = 0; e < 4; ++e) x[kb][4 * t + e] = s[qg][kb][t][e];
+      if (need_mask) {
+        const int lim = my_pos[qg] - n0 - 8 * g;  // row offset 32 kb + 4 t + e must stay <= lim
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (32 * kb + j > lim) x[kb][j] = -INFINITY;
+      }
+      float bm = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bm = fmaxf(bm, x[kb][j]);
+      bm = wave_xor_max(wave_xor_max(bm, 16), 32) * scale_log2;  // the scale is > 0: max commutes
       const bool raise = bm > m_run[qg] + 8.f;  // also true on the first visible tile (m_run = -inf)
       if (__builtin_amdgcn_ballot_w64(raise)) {  // uniform branch
         const float m_new = raise ? bm : m_run[qg];
@@ -243,13 +270,15 @@ void attn_active_kernel(
         for (int dt = 0; dt < DT; ++dt) o[qg][dt] *= alpha;
         m_run[qg] = m_new;
       }
-      const bool none = m_run[qg] == -INFINITY;  // no visible row yet (absent queries only)
+      // p = 2^(score * scale - max) in one fma; with no visible row yet (absent queries) every
+      // score is -inf and subtracting 0 keeps p = 0.
+      const float msub = m_run[qg] == -INFINITY ? 0.f : m_run[qg];
       float psum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p = none ? 0.f : __builtin_amdgcn_exp2f(x[kb][e] - m_run[qg]);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kb][e], scale_log2, -msub));
           psum += p;
           pb[qg][kb][e] = (__bf16)p;
         }
