@@ -37,7 +37,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #ifndef CKV_ATTN_PREFETCH
 #define CKV_ATTN_PREFETCH 1
 #endif
-constexpr int kAttnWaves = 4;
+#ifndef CKV_ATTN_WAVES
+#define CKV_ATTN_WAVES 4
+#endif
+constexpr int kAttnWaves = CKV_ATTN_WAVES;
 constexpr int kAttnQG = CKV_ATTN_QG;                // 16-query groups per wavefront
 constexpr int kAttnBM = kAttnWaves * kAttnQG * 16;  // queries per workgroup
 constexpr int kAttnBN = 64;                         // cache rows per tile
@@ -52,6 +55,9 @@ __device__ __forceinline__ int kslot(int r) {
   return blk + ((k >> 2) & 1) * 16 + (k >> 3) * 4 + (k & 3);
 }
 
+#ifndef CKV_ATTN_PRIO
+#define CKV_ATTN_PRIO 1  // raise the wavefront's issue priority around its matrix-core sections
+#endif
 #ifndef CKV_ATTN_OCC
 #define CKV_ATTN_OCC 0
 #endif
@@ -216,20 +222,21 @@ void attn_active_kernel(
     // S^T for the tile: lane (g, lm) gets query lm, rows n0 + 32 kb + 8 g + 4 t + e.
     constexpr int KB = kAttnBN / 32;
     f32x4 s[kAttnQG][KB][2];
+    if (CKV_ATTN_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int qg = 0; qg < kAttnQG; ++qg) s[qg][kb][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
           const bf16x8 a = *(const bf16x8*)(k_lds + (kb * 32 + 16 * t + lm) * KROW + (32 * ds + 8 * g) * 2);
 #pragma unroll
           for (int qg = 0; qg < kAttnQG; ++qg)
-            s[qg][kb][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[qg][ds], s[qg][kb][t], 0, 0, 0);
+            s[qg][kb][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[qg][ds], ds == 0 ? f32x4{0.f, 0.f, 0.f, 0.f}
+                                                                                       : s[qg][kb][t], 0, 0, 0);
         }
       }
+    if (CKV_ATTN_PRIO) __builtin_amdgcn_s_setprio(0);
 
     // Online softmax over the tile. The running max is only raised when a query's tile max
     // exceeds it by more than 2^8 (log2 domain): weights stay <= 256, the output rescale is
@@ -286,6 +293,7 @@ void attn_active_kernel(
     }
 
     // O^T += V^T P^T: A = V^T rows dt*16 + lm, columns 32 kb + 8 g .. + 8.
+    if (CKV_ATTN_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -295,6 +303,7 @@ void attn_active_kernel(
         for (int qg = 0; qg < kAttnQG; ++qg)
           o[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qg][kb], o[qg][dt], 0, 0, 0);
       }
+    if (CKV_ATTN_PRIO) __builtin_amdgcn_s_setprio(0);
   }
 
   // Normalise and write: lane (g, lm) holds O[query][dt*16 + 4g + e], 4 bf16 = 8 bytes per tile.
