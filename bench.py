@@ -603,11 +603,15 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
     return line
 
 
-def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4) -> dict:
+def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests: int = 6) -> dict:
     """Long-context multi-request replay at the Qwen2.5-7B shape: an HBM-resident store of 256
     chunks x 256 tokens x 2 context variants (7.0 GiB); 4 concurrent requests of 128 chunks
     sampled with replacement (Zipf s=1.1) at random order + a 64-token query (32832 tokens), 15%
-    recompute + 4 sinks; each request's whole KV repair runs on its own HIP stream."""
+    recompute + 4 sinks. Each request's KV repair is the engine's launch sequence (layer 1's base
+    cache, layer 0's fresh rows, deviation, selection, scatter of the kept rows, the gather of the
+    dropped rows of layers 2-27, the fresh rows of layers 2-27) on its own HIP stream. Then TTFT
+    p50/p99 of HipEngine.prefill + last_logprobs on requests of the same shape (random-init
+    Qwen2.5-7B architecture, bf16; the store's K/V serve as the cached chunks), one at a time."""
     from chunkkv_amd import ops
     from chunkkv_amd.planner import local_index, plan_request
 
@@ -622,38 +626,48 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4) -> dict:
     zipf = 1.0 / np.arange(1, POOL + 1) ** 1.1
     zipf /= zipf.sum()
     rng = np.random.default_rng(11)
-    reqs = []
+    cs_tab = ops.rope_table(N, HEAD_DIM, THETA, dev)
+    row = N_KV * HEAD_DIM
+    reqs, placements_of = [], []
     for r in range(2 * n_streams):
         ids = rng.choice(POOL, PER_REQ, p=zipf) * VARIANTS + rng.integers(0, VARIANTS, PER_REQ)
         pl = [Place(store[i], j * L) for j, i in enumerate(ids)]
+        placements_of.append(pl)
         plan = plan_request(N, pl, N_SINK, 0.15)
         tab = np.concatenate([np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(ch.keys, ch.values)],
                                        dtype=np.uint64).reshape(-1) for ch in plan.chunks])
         K = torch.empty((N_LAYERS, 1, N_KV, N, HEAD_DIM), dtype=torch.bfloat16, device=dev)
-        fresh = [(torch.randn((1, N_KV, N if li < 2 else plan.n_keep, HEAD_DIM), device=dev).bfloat16(),
-                  torch.randn((1, N_KV, N if li < 2 else plan.n_keep, HEAD_DIM), device=dev).bfloat16())
-                 for li in range(N_LAYERS)]
+        proj = [None if li == 1 else (torch.randn((1, N if li == 0 else plan.n_keep, row), device=dev).bfloat16(),
+                                      torch.randn((1, N if li == 0 else plan.n_keep, row), device=dev).bfloat16())
+                for li in range(N_LAYERS)]
         reqs.append(dict(plan=plan, tab=torch.from_numpy(tab.view(np.int64)).to(dev),
                          segs=torch.from_numpy(plan.segments.reshape(-1)).to(dev), K=K, V=torch.empty_like(K),
                          flags=torch.from_numpy(plan.flags).to(dev),
                          local=torch.from_numpy(local_index(N, plan.layer0_idx)).to(dev),
                          spans=torch.from_numpy(plan.spans.reshape(-1)).to(dev),
-                         layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), fresh=fresh, sel=None))
+                         layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), proj=proj,
+                         fresh1=(torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16(),
+                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None))
     assert reqs[0]["plan"].budget == 4864
     streams = [torch.cuda.Stream() for _ in range(n_streams)]
 
     def repair(rq):
         plan = rq["plan"]
-        ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], len(plan.segments), plan.max_seg_tokens, THETA)
         K, V = rq["K"].unbind(0), rq["V"].unbind(0)
-        ops.scatter_rows(K[0], V[0], *rq["fresh"][0], rq["layer0"])
-        k1, v1 = rq["fresh"][1]
+        nseg, mseg = len(plan.segments), plan.max_seg_tokens
+        ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(1, 2))
+        ops.rope_qkv(None, *rq["proj"][0], rq["layer0"], 0, N_KV, HEAD_DIM, THETA, k_out=K[0], v_out=V[0],
+                     rows=rq["layer0"], table=cs_tab)
+        k1, v1 = rq["fresh1"]
         d, n = ops.deviation(k1, v1, K[1], V[1], rq["flags"], rq["local"])
         rq["sel"] = ops.select(d, n, rq["flags"], rq["local"], rq["spans"], None, rq["sel"])
         rows = rq["sel"].keep_abs[: plan.n_keep]
-        for li in range(1, N_LAYERS):
-            k, v = rq["fresh"][li] if li > 1 else (k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep])
-            ops.scatter_rows(K[li], V[li], k, v, rows)
+        ops.scatter_rows(K[1], V[1], k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep], rows)
+        ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(2, N_LAYERS),
+                          skip=rq["sel"].keep_rank)
+        for li in range(2, N_LAYERS):
+            ops.rope_qkv(None, *rq["proj"][li], rows, 0, N_KV, HEAD_DIM, THETA, k_out=K[li], v_out=V[li], rows=rows,
+                         table=cs_tab)
 
     def round_(i):
         base = (i % 2) * n_streams
@@ -679,6 +693,36 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4) -> dict:
          "bytes_per_step": int(nbytes), "requests_per_step": n_streams},
         None)
     line["store_gib"] = round(len(store) * N_LAYERS * 2 * N_KV * L * HEAD_DIM * 2 / 2**30, 2)
+    for rq in reqs:  # free the repair buffers before the model comes in
+        rq.clear()
+    del reqs
+    torch.cuda.empty_cache()
+    if ttft_requests > 0:
+        from chunkkv_amd.engine import HipEngine
+        from chunkkv_amd.types import BlendConfig
+
+        model = random_qwen25_7b(dev)
+        hip = HipEngine(model, _Tok())
+        cfg = BlendConfig(recompute_ratio=0.15, n_sink=N_SINK)
+        vocab = model.config.vocab_size
+        times = []
+        for i in range(ttft_requests + 1):
+            tokens = torch.randint(0, vocab, (N,), generator=torch.Generator().manual_seed(100 + i)).tolist()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            res = hip.prefill(tokens, placements_of[i % len(placements_of)], cfg)
+            hip.last_logprobs(res)
+            dt = time.perf_counter() - t0
+            if i:
+                times.append(dt * 1e3)
+            del res
+        line["ttft_p50_ms"] = round(float(np.percentile(times, 50)), 2)
+        line["ttft_p99_ms"] = round(float(np.percentile(times, 99)), 2)
+        line["ttft_requests"] = len(times)
+        line["ttft_note"] = ("HipEngine, one request at a time; the reference op sequence is not timed at 32k "
+                             "(its math-path SDPA would hold ~120 GB of fp32 scores per layer)")
+        del hip, model
+        torch.cuda.empty_cache()
     return line
 
 
