@@ -55,3 +55,22 @@ def bf16_ulp_distance(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
         return np.where(u & 0x8000, 0x8000 - (u & 0x7FFF), 0x8000 + (u & 0x7FFF))
 
     return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+def random_qwen25_7b(device, layers: int = 28):
+    """Random-init Qwen2.5-7B architecture in bf16 on `device` (28 layers, hidden 3584, 28 query
+    / 4 KV heads, head_dim 128, intermediate 18944, vocab 152064, theta 1e6)."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(vocab_size=152064, hidden_size=3584, intermediate_size=18944, num_hidden_layers=layers,
+                      num_attention_heads=28, num_key_value_heads=4, max_position_embeddings=32768,
+                      rope_theta=1e6, tie_word_embeddings=False, rms_norm_eps=1e-6)
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = Qwen2ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    return model.eval()
