@@ -109,9 +109,14 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
 }
 
 // With a cos/sin table a token needs no shared state, so the work is flattened: one thread per
-// (token, item), item = a rotated 16-byte column pair of a q/k head or a copied 16-byte chunk of
-// a v row, grid-stride over all of them (every thread busy, whatever the head counts), rotation
-// items first.
+// (token, item), item = a rotated 16-byte column pair of kRopeHG consecutive q/k heads (one load
+// of the column's cos/sin for all of them) or a copied 16-byte chunk of a v row, grid-stride over
+// all of them (every thread busy, whatever the head counts), rotation items first.
+#ifndef CKV_ROPE_HG
+#define CKV_ROPE_HG 2
+#endif
+constexpr int kRopeHG = CKV_ROPE_HG;  // heads per rotation item (one cos/sin load for all of them)
+
 template <int DTYPE, int D>
 __global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
     char* __restrict__ q_out, int64_t qo_hs_b, int64_t qo_ts_b, char* __restrict__ k_out, int64_t ko_hs_b,
@@ -127,7 +132,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
   constexpr int HALF_B = HALF * E::kBytes;
   constexpr int CPR = D * E::kBytes / 16;
   typedef __attribute__((address_space(1))) const int64_t gi64;
-  const unsigned n_rot = (unsigned)((Hq + Hkv) * TPR);       // rotation items per token
+  const int n_heads = Hq + Hkv;
+  const unsigned n_rot = (unsigned)((n_heads + kRopeHG - 1) / kRopeHG * TPR);  // rotation items per token
   const unsigned n_cp = v_out != nullptr ? (unsigned)(Hkv * CPR) : 0u;  // copy items per token
   const unsigned rot_total = (unsigned)n * n_rot;
   const unsigned total = rot_total + (unsigned)n * n_cp;  // < 2^31, checked by the host
@@ -145,12 +151,18 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
       continue;
     }
     if (rot) {
-      const int h = it / TPR, col = it % TPR;
-      const char* s = h < Hq ? q_in + h * qi_hs_b + t * qi_ts_b : k_in + (h - Hq) * ki_hs_b + t * ki_ts_b;
-      char* d = h < Hq ? q_out + h * qo_hs_b + t * qo_ts_b : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b;
-      s += col * 16;
-      d += col * 16;
-      const vec16 a = ld16(s), b = ld16(s + HALF_B);
+      const int h0 = (it / TPR) * kRopeHG, col = it % TPR;
+      vec16 a[kRopeHG], b[kRopeHG];
+#pragma unroll
+      for (int j = 0; j < kRopeHG; ++j) {  // the heads' loads first, all in flight together
+        const int h = h0 + j;
+        if (h < n_heads) {
+          const char* s = (h < Hq ? q_in + h * qi_hs_b + t * qi_ts_b : k_in + (h - Hq) * ki_hs_b + t * ki_ts_b) +
+                          col * 16;
+          a[j] = ld16(s);
+          b[j] = ld16(s + HALF_B);
+        }
+      }
       const float2* tr = cs_table + p * HALF + col * VEC;  // VEC pairs = VEC/2 16-byte loads
       float c[VEC], sn[VEC];
 #pragma unroll
@@ -161,10 +173,18 @@ __global__ __launch_bounds__(kRopeThreads) void rope_qkv_flat_kernel(
         c[e + 1] = __uint_as_float(w[2]);
         sn[e + 1] = __uint_as_float(w[3]);
       }
-      vec16 y1, y2;
-      rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
-      st16(d, y1);
-      st16(d + HALF_B, y2);
+#pragma unroll
+      for (int j = 0; j < kRopeHG; ++j) {
+        const int h = h0 + j;
+        if (h < n_heads) {
+          char* d = (h < Hq ? q_out + h * qo_hs_b + t * qo_ts_b : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b) +
+                    col * 16;
+          vec16 y1, y2;
+          rotate_pairs<DTYPE>(a[j], b[j], c, sn, y1, y2);
+          st16(d, y1);
+          st16(d + HALF_B, y2);
+        }
+      }
     } else {
       const int h = it / CPR, c = it % CPR;
       st16(v_out + h * vo_hs_b + row * vo_ts_b + c * 16, ld16(v_in + h * vi_hs_b + t * vi_ts_b + c * 16));
@@ -180,7 +200,8 @@ static void launch_rope(int n, hipStream_t st, char* qo, int64_t qo_hs, int64_t 
                         int64_t n_tab, int Hq, int Hkv, double theta, int32_t* err) {
   if (tab != nullptr) {
     using E = Elem<DTYPE>;
-    const int64_t per_tok = (int64_t)(Hq + Hkv) * (D / 2 / E::kVec) + (vo != nullptr ? Hkv * (D * E::kBytes / 16) : 0);
+    const int64_t per_tok = (int64_t)(Hq + Hkv + kRopeHG - 1) / kRopeHG * (D / 2 / E::kVec) +
+                            (vo != nullptr ? Hkv * (D * E::kBytes / 16) : 0);
     const int64_t blocks = std::min<int64_t>((n * per_tok + kRopeThreads - 1) / kRopeThreads, 1 << 20);
     hipLaunchKernelGGL((rope_qkv_flat_kernel<DTYPE, D>), dim3((unsigned)blocks), dim3(kRopeThreads), 0, st, qo, qo_hs,
                        qo_ts, ko, ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, qi, qi_hs, qi_ts, ki, ki_hs, ki_ts, vi,
