@@ -188,21 +188,6 @@ class RepairWorkload:
         ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(self.plan.segments),
                           self.plan.max_seg_tokens, THETA, self.err)
 
-    def rest(self):
-        """Everything after the gather: scatter L0, deviation + selection at L1, scatters L1-27
-        (the reference's op order, kept for comparison; HipEngine runs step())."""
-        from chunkkv_amd import ops
-
-        K, V = self.k_slab.unbind(0), self.v_slab.unbind(0)
-        ops.scatter_rows(K[0], V[0], *self.fresh[0], self.layer0, self.err)
-        k1, v1 = self.fresh[1]
-        diff, norm = ops.deviation(k1, v1, K[1], V[1], self.flags, self.local, self.err)
-        self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
-        rows = self.sel.keep_abs[: self.plan.n_keep]
-        for li in range(1, N_LAYERS):
-            k, v = self.fresh[li] if li > 1 else (k1[:, :, : self.plan.n_keep], v1[:, :, : self.plan.n_keep])
-            ops.scatter_rows(K[li], V[li], k, v, rows, self.err)
-
     def assemble(self, li: int):
         """One layer li >= 2 (or 0) as HipEngine builds it: every row written once."""
         from chunkkv_amd import ops

@@ -37,10 +37,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #ifndef CKV_ATTN_PREFETCH
 #define CKV_ATTN_PREFETCH 1
 #endif
-#ifndef CKV_ATTN_WAVES
-#define CKV_ATTN_WAVES 4
-#endif
-constexpr int kAttnWaves = CKV_ATTN_WAVES;
+constexpr int kAttnWaves = 4;
 constexpr int kAttnQG = CKV_ATTN_QG;                // 16-query groups per wavefront
 constexpr int kAttnBM = kAttnWaves * kAttnQG * 16;  // queries per workgroup
 constexpr int kAttnBN = 64;                         // cache rows per tile
@@ -58,16 +55,8 @@ __device__ __forceinline__ int kslot(int r) {
 #ifndef CKV_ATTN_PRIO
 #define CKV_ATTN_PRIO 1  // raise the wavefront's issue priority around its matrix-core sections
 #endif
-#ifndef CKV_ATTN_OCC
-#define CKV_ATTN_OCC 0
-#endif
-
 template <int D>
-__global__ __launch_bounds__(kAttnWaves * 64)
-#if CKV_ATTN_OCC > 0
-__attribute__((amdgpu_waves_per_eu(CKV_ATTN_OCC)))
-#endif
-void attn_active_kernel(
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
     char* __restrict__ out, const char* __restrict__ q, int64_t q_hs_b, int64_t q_ts_b,
     const char* __restrict__ kc, const char* __restrict__ vc, int64_t kv_hs_b,
     const int64_t* __restrict__ pos, int n, int N, int Hq, int group, float scale_log2, int split_tiles,
