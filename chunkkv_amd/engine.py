@@ -157,10 +157,12 @@ class HipEngine(DecoderPieces):
         keys, values = chunk.keys, chunk.values
         if len(keys) != n_layers or len(values) != n_layers:
             raise ValueError(f"chunk has {len(keys)} key / {len(values)} value layers, model has {n_layers}")
-        sig = (id(keys), id(values), keys[0].data_ptr(), values[-1].data_ptr(), self.kv_dtype, self.device)
+        # The memo holds the very tensor objects it was built from and is reused only while every
+        # per-layer tensor is still the same object (a replaced layer invalidates it).
         memo = getattr(chunk, "_ckv_ptrs", None)
-        if memo is not None and memo[0] == sig:
-            return memo[1]
+        if (memo is not None and memo[0] == (self.kv_dtype, self.device) and len(memo[1]) == 2 * n_layers
+                and all(a is b for a, b in zip(memo[1], (*keys, *values)))):
+            return memo[2]
         want = (1, self.n_kv, keys[0].shape[2], self.head_dim)
         ptrs = np.empty((n_layers, 2), dtype=np.uint64)
         converted = False
@@ -175,7 +177,7 @@ class HipEngine(DecoderPieces):
                 ptrs[li, j] = t.data_ptr()
         if not converted:
             try:
-                chunk._ckv_ptrs = (sig, ptrs)
+                chunk._ckv_ptrs = ((self.kv_dtype, self.device), (*keys, *values), ptrs)
             except AttributeError:
                 pass
         return ptrs

@@ -410,3 +410,20 @@ def test_config1_qwen25_05b_shape_matches_oracle(attention):
     np.testing.assert_array_equal(got, want["keep_abs"])
     assert_same_selection(got, ref, tokens, pl, bc)
     assert _kl(ref["logits"], out.logits.cpu()) < 1e-4
+
+
+def test_chunk_address_memo_follows_replaced_layers(models, parts):
+    """A stored chunk whose layer tensor is replaced must not be gathered from the old address."""
+    _, gpu = models
+    eng = HipEngine(gpu, StubTokenizer())
+    toks2, pl = _swap_setup(eng, parts)
+    cfg = BlendConfig(recompute_ratio=0.3, n_sink=2)
+    first = eng.prefill(toks2, pl, cfg)
+    ch = pl[0].chunk
+    old = ch.keys[2]
+    ch.keys[2] = old.clone() * 0.5  # a new tensor object with different contents
+    second = eng.prefill(toks2, pl, cfg)
+    ch.keys[2] = old
+    third = eng.prefill(toks2, pl, cfg)
+    assert not torch.equal(first.keys[2], second.keys[2])
+    assert torch.equal(first.keys[2], third.keys[2]) and torch.equal(first.logits, third.logits)
