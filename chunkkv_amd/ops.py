@@ -8,7 +8,6 @@ Every wrapper launches a HIP kernel; none computes anything on the CPU.
 from __future__ import annotations
 
 import math
-
 from dataclasses import dataclass
 
 import torch

@@ -268,6 +268,16 @@ def test_bf16_blend_matches_rocm_reference_ops(attention, heads, kv):
     a, b = hip.prefill(toks2, pl, cfg), ref.prefill(toks2, pl, cfg)
     assert a.stats["recomputed_cached_tokens"] == b.stats["recomputed_cached_tokens"]
     assert _kl(b.logits, a.logits) < 1e-3
+    # with an exact placement (its rows never recomputed, gathered at layer 0 as well) and an
+    # escalation threshold (the kept count read back from the device)
+    sys_chunk = hip.prefill(parts["sys"]).chunk(0, len(parts["sys"]))
+    pl2 = [Placement(sys_chunk, 0, exact=True)] + pl
+    cfg2 = BlendConfig(recompute_ratio=0.3, n_sink=4, escalate_threshold=0.05)
+    a2, b2 = hip.prefill(toks2, pl2, cfg2), ref.prefill(toks2, pl2, cfg2)
+    for key in ("cached_tokens", "recomputed_cached_tokens", "prefill_token_equiv"):
+        assert a2.stats[key] == b2.stats[key], key
+    assert [c["escalated"] for c in a2.stats["chunks"]] == [c["escalated"] for c in b2.stats["chunks"]]
+    assert _kl(b2.logits, a2.logits) < 1e-3
 
 
 def test_shift_keys_api(models):
