@@ -51,6 +51,8 @@ import time
 import numpy as np
 import torch
 
+from chunkkv_amd.gemm_tuning import use_tuned_gemms
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -389,7 +391,8 @@ class _Tok:
 
 
 def bench_ttft(n_requests: int, dev) -> dict:
-    """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests."""
+    """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests. Both run
+    the model's library GEMMs with the same committed TunableOp selection table (when present)."""
     from chunkkv_amd.baseline import TorchOpsEngine
     from chunkkv_amd.engine import HipEngine
     from chunkkv_amd.types import BlendConfig
@@ -397,6 +400,9 @@ def bench_ttft(n_requests: int, dev) -> dict:
     t = time.perf_counter()
     model = random_qwen25_7b(dev)
     log(f"[bench] random-init Qwen2.5-7B architecture ready in {time.perf_counter() - t:.1f}s")
+    tuned = use_tuned_gemms()
+    log(f"[bench] library GEMMs: {'tuned table (TunableOp, lookup only)' if tuned else 'default heuristics'} "
+        "for both engines")
     hip, ref = HipEngine(model, _Tok()), TorchOpsEngine(model, _Tok())
     gen = torch.Generator().manual_seed(7)
     vocab = model.config.vocab_size
@@ -430,7 +436,8 @@ def bench_ttft(n_requests: int, dev) -> dict:
                 times.append(dt * 1e3)
             stats = res.stats
             del res
-        out[name] = dict(p50=float(np.percentile(times, 50)), p99=float(np.percentile(times, 99)), stats=stats)
+        out[name] = dict(p50=float(np.percentile(times, 50)), p99=float(np.percentile(times, 99)), stats=stats,
+                         tuned_gemms=tuned)
         log(f"[bench] TTFT {name}: p50 {out[name]['p50']:.2f} ms  p99 {out[name]['p99']:.2f} ms")
     del hip, ref, model
     torch.cuda.empty_cache()
@@ -687,6 +694,7 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         from chunkkv_amd.types import BlendConfig
 
         model = random_qwen25_7b(dev)
+        use_tuned_gemms()
         hip = HipEngine(model, _Tok())
         cfg = BlendConfig(recompute_ratio=0.15, n_sink=N_SINK)
         vocab = model.config.vocab_size
@@ -812,6 +820,7 @@ def bench_decode(steps: int, warmup: int, dev) -> dict:
     from chunkkv_amd.types import BlendConfig
 
     model = random_qwen25_7b(dev)
+    use_tuned_gemms()
     hip = HipEngine(model, _Tok())
     hip.eos = set()
     gen = torch.Generator().manual_seed(11)
@@ -1022,6 +1031,7 @@ def main() -> None:
         line["ttft_p50_ms"] = round(ttft["hip"]["p50"], 2)
         line["ttft_p99_ms"] = round(ttft["hip"]["p99"], 2)
         line["ttft_p50_ms_torch_ops"] = round(ttft["torch_ops"]["p50"], 2)
+        line["ttft_gemm_selection"] = "committed TunableOp table" if ttft["hip"]["tuned_gemms"] else "default heuristics"
         line["ttft_p99_ms_torch_ops"] = round(ttft["torch_ops"]["p99"], 2)
         line["ttft_requests"] = args.ttft_requests
     print(json.dumps(line), flush=True)
