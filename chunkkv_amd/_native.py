@@ -40,6 +40,7 @@ _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f64 = ctypes.c_double
+_f32 = ctypes.c_float
 
 # name -> (restype, argtypes); must match include/chunkkv_amd.h
 SIGNATURES = {
@@ -80,6 +81,8 @@ SIGNATURES = {
         [_p, _p, _i64, _i64, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f64, _p, _i64, _p, _p],
     ),
     "ckv_attention_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _p, _p]),
+    "ckv_add_rmsnorm": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _f32, _i32, _p]),
+    "ckv_silu_mul": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i64, _i32, _i32, _p]),
     "ckv_scatter_rows": (
         _i32,
         [_p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p, _p],

@@ -105,6 +105,58 @@ class HipEngine(DecoderPieces):
                 self._b_qkv.append(None if all(b is None for b in biases) else torch.cat(
                     [b if b is not None else torch.zeros(w.shape[0], dtype=w.dtype, device=w.device)
                      for b, w in zip(biases, (a.q_proj.weight, a.k_proj.weight, a.v_proj.weight))]))
+        # The elementwise steps between the GEMMs (residual adds, RMSNorms, the SiLU-gated product)
+        # run as ckv_add_rmsnorm / ckv_silu_mul for RMSNorm + SiLU-MLP models; the MLP's output is
+        # then added by the next norm (or the final one) instead of right away.
+        self._fused_mlp = attention == "fused" and self._fusable(model)
+        if self._fused_mlp:
+            norm = lambda m: (m.weight, float(m.variance_epsilon))  # noqa: E731
+            self._norm_in = [norm(layer.input_layernorm) for layer in self.layers]
+            self._norm_post = [norm(layer.post_attention_layernorm) for layer in self.layers]
+            self._norm_final = norm(self.inner.norm)
+
+    _RMSNORMS = ("Qwen2RMSNorm", "LlamaRMSNorm", "MistralRMSNorm")
+
+    def _fusable(self, model) -> bool:
+        """RMSNorm modules of weight * (x * rsqrt(mean(x^2) + eps)).to(dtype) and a SiLU-gated MLP,
+        in a dtype and width the fused kernels take."""
+        if getattr(model.config, "hidden_act", None) != "silu" or self.kv_dtype not in (torch.bfloat16, torch.float32):
+            return False
+        hidden = model.config.hidden_size
+        if hidden % 8 or hidden > (8192 if self.kv_dtype == torch.bfloat16 else 4096):
+            return False
+        norms = [self.inner.norm] + [m for layer in self.layers for m in (layer.input_layernorm, layer.post_attention_layernorm)]
+        if any(type(m).__name__ not in self._RMSNORMS or m.weight.dtype != self.kv_dtype for m in norms):
+            return False
+        mlps = [layer.mlp for layer in self.layers]
+        return all(hasattr(m, "gate_proj") and hasattr(m, "up_proj") and hasattr(m, "down_proj")
+                   and m.gate_proj.out_features % 8 == 0 for m in mlps)
+
+    def _norm(self, li: int, layer, h, pending):
+        """Input of layer li: (h + pending, input_layernorm(h + pending)); pending is the previous
+        layer's MLP output when the fused kernels defer its residual add (updated in place)."""
+        if not self._fused_mlp:
+            return h, layer.input_layernorm(h)
+        w, eps = self._norm_in[li]
+        return ops.add_rmsnorm(h, pending, w, eps, h_out=h if pending is not None else None)
+
+    def _mlp(self, li: int, layer, h, a):
+        """h + a (the attention output after o_proj), then the MLP block. Returns (h, pending): the
+        fused kernels leave the MLP's output in pending for the next norm to add."""
+        if not self._fused_mlp:
+            h = h + a
+            return h + layer.mlp(layer.post_attention_layernorm(h)), None
+        w, eps = self._norm_post[li]
+        h, x = ops.add_rmsnorm(h, a, w, eps, h_out=h)
+        mlp = layer.mlp
+        return h, mlp.down_proj(ops.silu_mul(mlp.gate_proj(x), mlp.up_proj(x)))
+
+    def _final_logits(self, h, pending):
+        """lm_head(norm(h + pending)) of the given rows (torch_engine.py:75)."""
+        if pending is None:
+            return self._logits(h)
+        w, eps = self._norm_final
+        return self.model.lm_head(ops.add_rmsnorm(h.contiguous(), pending.contiguous(), w, eps)[1])
 
     @classmethod
     def load(cls, repo: str, dtype=torch.bfloat16) -> "HipEngine":
@@ -113,20 +165,20 @@ class HipEngine(DecoderPieces):
         model = AutoModelForCausalLM.from_pretrained(repo, dtype=dtype).to("cuda")
         return cls(model, AutoTokenizer.from_pretrained(repo))
 
-    def _attend_active(self, layer, h, q_tm, K, V, active, ar, masks: dict, err=None):
-        """Attention of the active rows over the whole cache: row i sees positions <= active[i].
-        q_tm: (1, n, Hq, D) token-major, as ckv_rope_qkv writes it."""
+    def _attend_active(self, li, layer, h, q_tm, K, V, active, ar, masks: dict, err=None):
+        """Attention of the active rows over the whole cache (row i sees positions <= active[i]),
+        then the MLP block; returns (h, pending) as _mlp does. q_tm: (1, n, Hq, D) token-major, as
+        ckv_rope_qkv writes it."""
         n_act, N = active.shape[0], ar.shape[0]
         q = q_tm.transpose(1, 2)  # (1, Hq, n, D) view
         key = (active.data_ptr(), n_act)
         if self.attention == "reference":
-            return self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :])
+            return self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :]), None
         attn = layer.self_attn
         if self._native_attention:
             # positions-only mask on the matrix-core kernel; output already token-major
             o = ops.attention_active(q, K, V, active, err=err)
-            h = h + attn.o_proj(o.view(h.shape[0], h.shape[1], -1))
-            return h + layer.mlp(layer.post_attention_layernorm(h))
+            return self._mlp(li, layer, h, attn.o_proj(o.view(h.shape[0], h.shape[1], -1)))
         if n_act == N:  # active == arange(N): the mask is exactly the causal mask
             o = F.scaled_dot_product_attention(q, K, V, is_causal=True, enable_gqa=True)
         else:
@@ -137,8 +189,7 @@ class HipEngine(DecoderPieces):
             if group > 1:
                 K, V = K.repeat_interleave(group, dim=1), V.repeat_interleave(group, dim=1)
             o = F.scaled_dot_product_attention(q, K, V, attn_mask=masks[key])
-        h = h + attn.o_proj(o.transpose(1, 2).reshape(h.shape[0], h.shape[1], -1))
-        return h + layer.mlp(layer.post_attention_layernorm(h))
+        return self._mlp(li, layer, h, attn.o_proj(o.transpose(1, 2).reshape(h.shape[0], h.shape[1], -1)))
 
     def shift_keys(self, keys: torch.Tensor, delta: int) -> torch.Tensor:
         """Move post-RoPE keys by `delta` positions on the HIP kernel (torch_engine.py:56-59)."""
@@ -289,31 +340,31 @@ class HipEngine(DecoderPieces):
         """One token (tok: (1, 1) int64 at position where: (1,) int64) through every layer; writes
         the next greedy token into tok and advances where. No host values are read."""
         H, D = self.n_kv, self.head_dim
-        h = self.inner.embed_tokens(tok)
+        h, pending = self.inner.embed_tokens(tok), None
         for li, layer in enumerate(self.layers):
-            q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
+            h, x = self._norm(li, layer, h, pending)
+            q_in, k_in, v_in = self._project(li, x)
             q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=Ks[li], v_out=Vs[li],
                                 rows=where, table=tab, err=err)
             o = ops.attention_active(q.transpose(1, 2), Ks[li], Vs[li], where, err=err)
-            h = h + layer.self_attn.o_proj(o.view(1, 1, -1))
-            h = h + layer.mlp(layer.post_attention_layernorm(h))
-        tok.copy_(self._logits(h)[0, -1].argmax().view(1, 1))
+            h, pending = self._mlp(li, layer, h, layer.self_attn.o_proj(o.view(1, 1, -1)))
+        tok.copy_(self._final_logits(h, pending)[0, -1].argmax().view(1, 1))
         where.add_(1)
 
     def _decode_step_sdpa(self, tok, pos: int, Ks, Vs, tab, err) -> None:
         """_decode_step for models outside the attention kernel's range (SDPA over rows <= pos)."""
         H, D = self.n_kv, self.head_dim
         where = torch.tensor([pos], dtype=torch.int64, device=self.device)
-        h = self.inner.embed_tokens(tok)
+        h, pending = self.inner.embed_tokens(tok), None
         for li, layer in enumerate(self.layers):
-            q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
+            h, x = self._norm(li, layer, h, pending)
+            q_in, k_in, v_in = self._project(li, x)
             q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=Ks[li], v_out=Vs[li],
                                 rows=where, table=tab, err=err)
             o = F.scaled_dot_product_attention(q.transpose(1, 2), Ks[li][:, :, : pos + 1], Vs[li][:, :, : pos + 1],
                                                enable_gqa=True)
-            h = h + layer.self_attn.o_proj(o.transpose(1, 2).reshape(1, 1, -1))
-            h = h + layer.mlp(layer.post_attention_layernorm(h))
-        tok.copy_(self._logits(h)[0, -1].argmax().view(1, 1))
+            h, pending = self._mlp(li, layer, h, layer.self_attn.o_proj(o.transpose(1, 2).reshape(1, 1, -1)))
+        tok.copy_(self._final_logits(h, pending)[0, -1].argmax().view(1, 1))
 
     # -- main entry -----------------------------------------------------------------------
 
@@ -368,8 +419,10 @@ class HipEngine(DecoderPieces):
                 ready[1] = gather((1, 2), None)
             else:
                 ready[0] = gather((0, n_layers), local_d)
+        pending = None  # the previous layer's MLP output, when its residual add is deferred
         for li, layer in enumerate(self.layers):
-            q_in, k_in, v_in = self._project(li, layer.input_layernorm(h))
+            h, x = self._norm(li, layer, h, pending)
+            q_in, k_in, v_in = self._project(li, x)
             K, V = keys_out[li], values_out[li]
             if li == 1 and select_layer:
                 q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, table=tab, err=err)
@@ -400,18 +453,19 @@ class HipEngine(DecoderPieces):
                                     rows=active, table=tab, err=err)
                 if ready.get(li) is not None:
                     torch.cuda.current_stream(dev).wait_event(ready[li])
-            h = self._attend_active(layer, h, q, K, V, active, ar, masks, err)
+            h, pending = self._attend_active(li, layer, h, q, K, V, active, ar, masks, err)
 
         n_want = N - logits_from
         if 0 <= logits_from <= N and not plan.cached[logits_from:].any():
             # Uncached positions are in every active set, and active sets are sorted, so the
             # requested positions are the last n_want rows.
-            logits = self._logits(h[:, h.shape[1] - n_want :])[0]
+            tail = slice(h.shape[1] - n_want, None)
+            logits = self._final_logits(h[:, tail], None if pending is None else pending[:, tail])[0]
         else:
             want = (active >= logits_from).nonzero().squeeze(1)
             if len(want) != n_want:
                 raise ValueError("logits requested for positions that were not recomputed")
-            logits = self._logits(h[:, want])[0]
+            logits = self._final_logits(h[:, want], None if pending is None else pending[:, want])[0]
 
         chunk_stats: list[dict] = []
         selected_cached = 0

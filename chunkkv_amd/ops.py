@@ -500,3 +500,77 @@ def extract_chunks(
         "ckv_extract_chunks",
     )
     return bufs
+
+
+def _row_major(t: torch.Tensor, width: int, what: str) -> int:
+    """Row stride (elements) of a (..., width) tensor whose rows are contiguous and evenly spaced."""
+    if t.shape[-1] != width or t.stride(-1) != 1 or t.data_ptr() % 16 != 0:
+        raise ValueError(f"{what} must have contiguous, 16-byte aligned rows of {width} elements")
+    rows = t.reshape(-1, width) if t.dim() != 2 else t
+    if rows.data_ptr() != t.data_ptr() or (rows.shape[0] > 1 and rows.stride(1) != 1):
+        raise ValueError(f"{what} rows must be evenly spaced")
+    return rows.stride(0) if rows.shape[0] > 1 else width
+
+
+def add_rmsnorm(
+    h: torch.Tensor,
+    delta: torch.Tensor | None,
+    weight: torch.Tensor,
+    eps: float,
+    *,
+    h_out: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Residual add and RMSNorm: (h + delta, RMSNorm(h + delta)), or (h, RMSNorm(h)) with delta None.
+
+    The Hugging Face Qwen2/Llama RMSNorm module's steps (fp32 math, the normalised row rounded to
+    h.dtype before the weight multiplies it) after the decoder's residual add (torch_engine.py:71-72,
+    :113, :75). h, delta: (..., hidden) contiguous; h_out defaults to a new tensor and may be h
+    itself (in place).
+    """
+    _dev(h, weight, *(() if delta is None else (delta,)))
+    hidden = h.shape[-1]
+    if not h.is_contiguous() or (delta is not None and (not delta.is_contiguous() or delta.shape != h.shape)):
+        raise ValueError("h and delta must be contiguous and of one shape")
+    if weight.shape != (hidden,) or weight.dtype != h.dtype or (delta is not None and delta.dtype != h.dtype):
+        raise ValueError("weight must be (hidden,) and every operand of h's dtype")
+    if out is None:
+        out = torch.empty_like(h)
+    elif out.shape != h.shape or not out.is_contiguous() or out.dtype != h.dtype:
+        raise ValueError("out must be contiguous, of h's shape and dtype")
+    if delta is not None and h_out is None:
+        h_out = torch.empty_like(h)
+    elif h_out is not None and (h_out.shape != h.shape or not h_out.is_contiguous() or h_out.dtype != h.dtype):
+        raise ValueError("h_out must be contiguous, of h's shape and dtype")
+    n_rows = h.numel() // hidden if hidden else 0
+    check(
+        lib().ckv_add_rmsnorm(
+            _ptr(h_out), _ptr(h), _ptr(delta), _ptr(out), _ptr(weight.contiguous()), n_rows, hidden, float(eps),
+            dtype_code(h.dtype), _stream(h.device),
+        ),
+        "ckv_add_rmsnorm",
+    )
+    return (h if delta is None else h_out), out
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up with the MLP's roundings (torch_engine.py:72 via the SiLU-gated Qwen2/Llama
+    MLP). gate/up: (..., width) with evenly spaced contiguous rows (e.g. the halves of one
+    stacked GEMM output); returns a contiguous (..., width) tensor."""
+    _dev(gate, up)
+    width = gate.shape[-1]
+    if up.shape != gate.shape or up.dtype != gate.dtype:
+        raise ValueError("gate and up must have one shape and dtype")
+    gs, us = _row_major(gate, width, "gate"), _row_major(up, width, "up")
+    if out is None:
+        out = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+    elif out.shape != gate.shape or not out.is_contiguous() or out.dtype != gate.dtype:
+        raise ValueError("out must be contiguous, of gate's shape and dtype")
+    n_rows = gate.numel() // width if width else 0
+    check(
+        lib().ckv_silu_mul(
+            _ptr(out), width, _ptr(gate), gs, _ptr(up), us, n_rows, width, dtype_code(gate.dtype), _stream(gate.device),
+        ),
+        "ckv_silu_mul",
+    )
+    return out

@@ -334,6 +334,35 @@ int32_t ckv_attention_active(void* out, const void* q, int64_t q_head_stride, in
 int64_t ckv_attention_workspace_bytes(int32_t n_queries, int32_t n_tokens, int32_t n_q_heads,
                                       int32_t head_dim, int32_t* splits, int32_t* split_tiles);
 
+/*
+ * Residual add and RMSNorm of each row, the elementwise steps around a decoder layer's GEMMs:
+ *   s = h_in + delta, rounded to dtype and written to h_out       (delta != NULL)
+ *   s = h_in                                                       (delta == NULL; h_out unused)
+ *   y = dtype( weight * dtype( s * rsqrt(fl32(sum(s^2)) * fl32(1/hidden) + eps) ) )
+ * in fp32 with each product rounded once: the Hugging Face Qwen2/Llama RMSNorm module
+ * (x.to(fp32); x * rsqrt(x.pow(2).mean(-1) + eps); weight * x.to(dtype)) after the residual add.
+ * The fp32 order of the sum of squares is the kernel's own (a fixed tree). h_out may equal h_in.
+ * Rows contiguous: element (r, c) at base + r*hidden + c. hidden a multiple of 8 (bf16) or 4
+ * (f32) and at most 8192 (bf16) or 4096 (f32); dtype bf16 or f32.
+ * Replaces: `h + attn.o_proj(out)` and `layer.post_attention_layernorm(h)` (torch_engine.py:71-72),
+ * the next layer's `layer.input_layernorm(h)` after the MLP's residual add (:72, :113, :191) and
+ * `self.inner.norm(h)` (:75).
+ */
+int32_t ckv_add_rmsnorm(void* h_out, const void* h_in, const void* delta, void* y, const void* weight,
+                        int64_t n_rows, int32_t hidden, float eps, int32_t dtype, void* stream);
+
+/*
+ * SiLU-gated product of the MLP: out = dtype( dtype(gate / (1 + exp(-gate))) * up ), fp32 math
+ * with each step rounded once. Row r of each operand starts at base + r*row_stride (elements,
+ * multiples of 8 for bf16 or 4 for f32; base 16-byte aligned), so the halves of one stacked
+ * gate|up GEMM output can be passed as two views. dtype bf16 or f32.
+ * Replaces: `act_fn(gate_proj(x)) * up_proj(x)` inside layer.mlp (torch_engine.py:72; the Hugging
+ * Face Qwen2/Llama MLP with SiLU).
+ */
+int32_t ckv_silu_mul(void* out, int64_t out_row_stride, const void* gate, int64_t gate_row_stride,
+                     const void* up, int64_t up_row_stride, int64_t n_rows, int32_t width, int32_t dtype,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

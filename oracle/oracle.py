@@ -19,6 +19,10 @@ Parity status of each function (how it is pinned is in tests/test_oracle.py):
                   within one bf16 ulp, composition rope(rope(x, a), b) ~ rope(x, a + b)
   attention_active pinned: torch's CPU scaled_dot_product_attention with the reference's boolean
                   mask and enable_gqa (the reference call itself), fp32, on small shapes
+  add_rmsnorm     pinned: the transformers Qwen2RMSNorm module on the CPU after torch's own
+                  residual add (bf16 and fp32, within one ulp), closed form of a constant row
+  silu_mul        pinned: torch's CPU F.silu(gate) * up in bf16 (within one bf16 ulp), fp64
+                  silu closed forms (silu(0) = 0, odd part x/2)
 """
 
 from __future__ import annotations
@@ -237,3 +241,41 @@ def attention_active(q: np.ndarray, K: np.ndarray, V: np.ndarray, positions: np.
         p = np.exp(s)
         out[:, h] = (p @ V[h // G]) / p.sum(axis=1, keepdims=True)
     return out
+
+
+def _round_to(x: np.ndarray, bf16: bool) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(x)) if bf16 else x
+
+
+def add_rmsnorm(h: np.ndarray, delta: np.ndarray | None, weight: np.ndarray, eps: float):
+    """Residual add + RMSNorm of the rows of h (torch_engine.py:71-72 and :113 / :75 through the
+    model's RMSNorm modules): s = dtype(h + delta); y = dtype(w * dtype(s * rsqrt(mean(s^2) + eps))).
+
+    h, delta: (rows, hidden) float32 or uint16 bf16 bits; weight (hidden,) of the same kind.
+    The sum of squares is taken in fp64 and rounded once to fp32, then scaled by fl32(1/hidden)
+    in fp32, eps added in fp32, and rsqrt evaluated in fp64 and rounded once.
+    Returns (s, y) in the input representation."""
+    bf16 = h.dtype == np.uint16
+    s = as_f32(h)
+    if delta is not None:
+        s = _round_to(s + as_f32(delta), bf16)
+    ss = np.float32(np.sum(s.astype(np.float64) ** 2, axis=-1, keepdims=True))
+    var = (ss * np.float32(1.0 / np.float32(h.shape[-1]))).astype(np.float32)
+    r = (1.0 / np.sqrt((var + np.float32(eps)).astype(np.float32).astype(np.float64))).astype(np.float32)
+    y = _round_to(as_f32(weight)[None, :] * _round_to(s * r, bf16), bf16)
+    if bf16:
+        return f32_to_bf16_bits(s), f32_to_bf16_bits(y)
+    return s, y
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """dtype(dtype(silu(gate)) * up), silu(x) = x / (1 + exp(-x)) in fp64 rounded once to fp32,
+    the SiLU-gated MLP product (torch_engine.py:72 via the model's MLP). Inputs and output in the
+    input representation (float32 or uint16 bf16 bits)."""
+    bf16 = gate.dtype == np.uint16
+    g = as_f32(gate).astype(np.float64)
+    with np.errstate(over="ignore"):
+        silu = (g / (1.0 + np.exp(-g))).astype(np.float32)
+    out = _round_to(_round_to(silu, bf16) * as_f32(up), bf16)
+    return f32_to_bf16_bits(out) if bf16 else out

@@ -135,3 +135,23 @@ def test_attention_workspace_sizing_is_host_only():
     assert s.value > 1 and t.value * s.value >= (8256 + 63) // 64 and nb == s.value * 28 * 1 * 132 * 4
     assert lib.ckv_attention_workspace_bytes(2976, 8256, 28, 128, None, None) == 0
     assert lib.ckv_attention_workspace_bytes(1, 100, 28, 128, None, None) == 0  # short cache: no split
+
+
+def test_norm_and_gate_validation_never_launches():
+    lib = _native.lib()
+    bf16, f32 = 1, 0
+    norm = lambda *a: lib.ckv_add_rmsnorm(*a)  # noqa: E731
+    assert norm(1, 1, 1, 1, 1, 4, 8200, 1e-6, bf16, None) == _native.CKV_ERR_TOO_LARGE  # > 8192 elements
+    assert norm(1, 1, 1, 1, 1, 4, 4100, 1e-6, f32, None) == _native.CKV_ERR_TOO_LARGE  # > 4096 fp32
+    assert norm(1, 1, 1, 1, 1, 4, 100, 1e-6, bf16, None) == _native.CKV_ERR_INVALID_ARGUMENT  # not a multiple of 8
+    assert norm(1, 1, 1, 1, 1, 4, 128, 1e-6, 7, None) == _native.CKV_ERR_INVALID_ARGUMENT  # dtype
+    assert norm(None, 1, 1, 1, 1, 4, 128, 1e-6, bf16, None) == _native.CKV_ERR_INVALID_ARGUMENT  # add needs h_out
+    assert norm(1, 1, 1, 1, 1, 4, 128, -1.0, bf16, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert norm(1, 1, 1, 1, 1, -1, 128, 1e-6, bf16, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert norm(None, None, None, None, None, 0, 128, 1e-6, bf16, None) == _native.CKV_OK  # no rows
+    gate = lambda *a: lib.ckv_silu_mul(*a)  # noqa: E731
+    assert gate(1, 64, 1, 32, 1, 64, 4, 64, bf16, None) == _native.CKV_ERR_OUT_OF_RANGE  # row stride < width
+    assert gate(1, 64, 1, 68, 1, 64, 4, 64, bf16, None) == _native.CKV_ERR_INVALID_ARGUMENT  # unaligned stride
+    assert gate(1, 60, 1, 60, 1, 60, 4, 60, bf16, None) == _native.CKV_ERR_INVALID_ARGUMENT  # width % 8
+    assert gate(None, 64, 1, 64, 1, 64, 4, 64, bf16, None) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert gate(None, 64, None, 64, None, 64, 0, 64, bf16, None) == _native.CKV_OK

@@ -280,6 +280,33 @@ def test_bf16_blend_matches_rocm_reference_ops(attention, heads, kv):
     assert _kl(b2.logits, a2.logits) < 1e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fused_decoder_steps_match_the_model_modules(dtype):
+    """The fused residual-add + RMSNorm and gated-product kernels (with the MLP's residual add
+    deferred to the next norm) against the same engine running the model's own modules: same
+    selection and stats, logits and decode within floating-point rounding."""
+    gpu = tiny_qwen2(layers=3, hidden=512, heads=8, kv=2, inter=1024, vocab=512, seed=8, dtype=dtype).to(DEV)
+    with torch.no_grad():
+        gpu.model.norm.weight.mul_(20.0)
+    fused, plain = HipEngine(gpu, StubTokenizer()), HipEngine(gpu, StubTokenizer())
+    assert fused._fused_mlp
+    plain._fused_mlp = False
+    rng = np.random.default_rng(8)
+    t = lambda n: rng.integers(1, 511, n).tolist()  # noqa: E731
+    parts = dict(sys=t(20), a=t(64), b=t(48), q=t(8))
+    toks2, pl = _swap_setup(plain, parts)
+    cfg = BlendConfig(recompute_ratio=0.3, n_sink=4)
+    a, b = fused.prefill(toks2, pl, cfg, logits_from=len(toks2) - 5), plain.prefill(toks2, pl, cfg, logits_from=len(toks2) - 5)
+    for key in ("cached_tokens", "recomputed_cached_tokens", "prefill_token_equiv"):
+        assert a.stats[key] == b.stats[key], key
+    for ca, cb in zip(a.stats["chunks"], b.stats["chunks"]):
+        assert ca["rel_dev"] == pytest.approx(cb["rel_dev"], rel=1e-2 if dtype == torch.bfloat16 else 1e-5)
+    assert _kl(b.logits, a.logits) < (1e-4 if dtype == torch.bfloat16 else 1e-8)
+    # layer 0 recomputes a fixed set of rows from the embeddings through the first norm
+    torch.testing.assert_close(a.keys[0], b.keys[0], atol=0.05 if dtype == torch.bfloat16 else 1e-5, rtol=0)
+    assert fused.generate(a, max_tokens=8) == plain.generate(a, max_tokens=8)
+
+
 def test_shift_keys_api(models):
     _, gpu = models
     eng = HipEngine(gpu, StubTokenizer())

@@ -428,3 +428,74 @@ def test_rope_fp64_rotation_and_composition():
     del inv
     a, b = rng.integers(0, 500, n), rng.integers(0, 500, n)
     np.testing.assert_allclose(O.rope(O.rope(x, a, theta), b, theta), O.rope(x, a + b, theta), atol=1e-4, rtol=0)
+
+
+def _hf_rmsnorm(hidden, weight, eps, dtype):
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
+
+    m = Qwen2RMSNorm(hidden, eps=eps).to(dtype)
+    with torch.no_grad():
+        m.weight.copy_(weight)
+    return m
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_add_rmsnorm_matches_hf_module(bf16):
+    """The model's own module (transformers Qwen2RMSNorm) after torch's residual add, on the CPU:
+    the residual sum is bit-exact, the normalised row within one ulp (sum order and rsqrt are
+    torch's there)."""
+    rng = np.random.default_rng(41)
+    rows, hidden, eps = 33, 896, 1e-6
+    dt = torch.bfloat16 if bf16 else torch.float32
+    ht = torch.from_numpy(rng.standard_normal((rows, hidden)).astype(np.float32) * 3).to(dt)
+    dt_ = torch.from_numpy(rng.standard_normal((rows, hidden)).astype(np.float32)).to(dt)
+    wt = torch.from_numpy(rng.uniform(0.5, 2.0, hidden).astype(np.float32)).to(dt)
+    s_want = ht + dt_
+    y_want = _hf_rmsnorm(hidden, wt, eps, dt)(s_want).detach()
+    s, y = O.add_rmsnorm(O.to_numpy(ht), O.to_numpy(dt_), O.to_numpy(wt), eps)
+    np.testing.assert_array_equal(s, O.to_numpy(s_want))
+    if bf16:
+        dist = bf16_ulp_distance(y, O.to_numpy(y_want))
+        assert dist.max() <= 1 and (dist > 0).mean() < 0.01
+    else:
+        np.testing.assert_allclose(y, y_want.numpy(), rtol=2e-6, atol=0)
+    # no residual: the norm of h alone
+    s0, y0 = O.add_rmsnorm(O.to_numpy(ht), None, O.to_numpy(wt), eps)
+    np.testing.assert_array_equal(s0, O.to_numpy(ht))
+    y0_want = O.to_numpy(_hf_rmsnorm(hidden, wt, eps, dt)(ht).detach())
+    if bf16:
+        assert bf16_ulp_distance(y0, y0_want).max() <= 1
+    else:
+        np.testing.assert_allclose(y0, y0_want, rtol=2e-6, atol=0)
+
+
+def test_add_rmsnorm_closed_form():
+    """A constant row c normalises to c / sqrt(c^2 + eps) (times the weight); the weight is
+    applied per column, not per row; rows are independent."""
+    hidden, eps = 256, 1e-6
+    h = np.full((3, hidden), 2.0, dtype=np.float32)
+    h[1] *= -1
+    h[2] = np.arange(hidden, dtype=np.float32) - 100
+    w = np.linspace(0.5, 1.5, hidden).astype(np.float32)
+    _, y = O.add_rmsnorm(h, None, w, eps)
+    np.testing.assert_allclose(y[0], w * 2.0 / np.sqrt(4.0 + eps), rtol=1e-6)
+    np.testing.assert_allclose(y[1], -y[0], rtol=0, atol=0)
+    x = h[2].astype(np.float64)
+    np.testing.assert_allclose(y[2], w * x / np.sqrt((x**2).mean() + eps), rtol=1e-6)
+
+
+def test_silu_mul_matches_torch_and_closed_forms():
+    rng = np.random.default_rng(42)
+    g = torch.from_numpy(rng.standard_normal((17, 512)).astype(np.float32) * 4).to(torch.bfloat16)
+    u = torch.from_numpy(rng.standard_normal((17, 512)).astype(np.float32)).to(torch.bfloat16)
+    g[0, :4] = torch.tensor([0.0, -0.0, 80.0, -80.0])
+    got = O.silu_mul(O.to_numpy(g), O.to_numpy(u))
+    want = O.to_numpy(torch.nn.functional.silu(g) * u)
+    dist = bf16_ulp_distance(got, want)
+    assert dist.max() <= 1 and (dist > 0).mean() < 0.01
+    x = np.linspace(-6, 6, 101).astype(np.float32)
+    one = np.ones_like(x)
+    s = O.silu_mul(x, one)
+    assert s[50] == 0.0
+    np.testing.assert_allclose(s - O.silu_mul(-x, one), x, rtol=1e-6, atol=1e-6)  # silu(x) - silu(-x) = x
+    np.testing.assert_allclose(O.silu_mul(x, 2 * one), 2 * s, rtol=0, atol=0)
