@@ -55,6 +55,41 @@ __device__ __forceinline__ int kslot(int r) {
 #ifndef CKV_ATTN_PRIO
 #define CKV_ATTN_PRIO 1  // raise the wavefront's issue priority around its matrix-core sections
 #endif
+#ifndef CKV_ATTN_XCD
+#define CKV_ATTN_XCD 1  // place the workgroups of one KV head on the same XCDs
+#endif
+constexpr int kXcds = 8;  // MI355X: workgroups go round-robin to 8 XCDs, each with its own L2
+
+// Work item (query block qb, query head hq) of this workgroup. The hardware hands workgroup L
+// (x fastest) to XCD L % 8, so items are assigned through L: the XCDs split evenly over the KV
+// heads (8 / Hkv XCDs each), every item of one KV head lands on that head's XCDs (its K/V stay
+// in their L2s and are read there by all `group` query heads together), consecutive items of
+// an XCD cycle through the group's query heads on one query block, and query blocks go latest
+// position first, alternating between the head's XCDs so their work stays balanced. Items that
+// do not fill a last round of 8 are dealt to the workgroups of that round. A bijection of the
+// grid; with a KV-head count that does not divide 8 the plain order is kept.
+__device__ __forceinline__ void attn_work_item(int nqb, int Hq, int group, int& qb, int& hq) {
+  qb = nqb - 1 - (int)blockIdx.x;  // latest positions (most keys) first
+  hq = (int)blockIdx.y;
+  const int Hkv = Hq / group;
+  if (!CKV_ATTN_XCD || gridDim.z != 1 || kXcds % Hkv != 0) return;
+  const int L = (int)blockIdx.x + (int)blockIdx.y * nqb;
+  const int xpk = kXcds / Hkv, P = group * nqb;     // XCDs per KV head, items per KV head
+  const int per = P * Hkv / kXcds, full = per * kXcds;  // complete rounds of 8 workgroups
+  int kv, j;
+  if (L < full) {
+    const int xcd = L % kXcds, idx = L / kXcds;
+    kv = xcd / xpk;
+    j = idx * xpk + xcd % xpk;
+  } else {
+    const int left = P - xpk * per;  // items per KV head past the complete rounds (> 0 here)
+    const int t = L - full;
+    kv = t / left;
+    j = xpk * per + t % left;
+  }
+  qb = nqb - 1 - j / group;
+  hq = kv * group + j % group;
+}
 template <int D>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
     char* __restrict__ out, const char* __restrict__ q, int64_t q_hs_b, int64_t q_ts_b,
@@ -76,9 +111,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int g = lane / 16, lm = lane % 16;
-  const int hq = blockIdx.y;
+  int qb, hq;
+  attn_work_item((int)gridDim.x, Hq, group, qb, hq);
   const int hk = hq / group;
-  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // latest positions (most keys) first
   const int q0 = qb * kAttnBM + wave * kAttnQG * 16;
 
   // Positions of this lane's queries (-1 = no query); out-of-range positions are flagged and
