@@ -53,29 +53,31 @@ __device__ __forceinline__ int kslot(int r) {
 }
 
 #ifndef CKV_ATTN_PRIO
-#define CKV_ATTN_PRIO 1  // raise the wavefront's issue priority around its matrix-core sections
+#define CKV_ATTN_PRIO 0  // 1: raise the wavefront's issue priority around its matrix-core sections
 #endif
 #ifndef CKV_ATTN_XCD
 #define CKV_ATTN_XCD 1  // place the workgroups of one KV head on the same XCDs
 #endif
 constexpr int kXcds = 8;  // MI355X: workgroups go round-robin to 8 XCDs, each with its own L2
 
-// Work item (query block qb, query head hq) of this workgroup. The hardware hands workgroup L
-// (x fastest) to XCD L % 8, so items are assigned through L: the XCDs split evenly over the KV
-// heads (8 / Hkv XCDs each), every item of one KV head lands on that head's XCDs (its K/V stay
-// in their L2s and are read there by all `group` query heads together), consecutive items of
-// an XCD cycle through the group's query heads on one query block, and query blocks go latest
-// position first, alternating between the head's XCDs so their work stays balanced. Items that
-// do not fill a last round of 8 are dealt to the workgroups of that round. A bijection of the
-// grid; with a KV-head count that does not divide 8 the plain order is kept.
-__device__ __forceinline__ void attn_work_item(int nqb, int Hq, int group, int& qb, int& hq) {
+// Work item (query block qb, query head hq, cache split z) of this workgroup. The hardware hands
+// workgroup L (x fastest, then y, then z) to XCD L % 8, so items are assigned through L: the
+// XCDs split evenly over the KV heads (8 / Hkv XCDs each), every item of one KV head lands on
+// that head's XCDs (its K/V stay in their L2s and are read there by all `group` query heads
+// together), consecutive items of an XCD cycle through the group's query heads on one query
+// block and split, and query blocks go latest position first, alternating between the head's
+// XCDs so their work stays balanced. Items that do not fill a last round of 8 are dealt to the
+// workgroups of that round. A bijection of the grid; with a KV-head count that does not divide 8
+// the plain order is kept.
+__device__ __forceinline__ void attn_work_item(int nqb, int Hq, int group, int& qb, int& hq, int& z) {
   qb = nqb - 1 - (int)blockIdx.x;  // latest positions (most keys) first
   hq = (int)blockIdx.y;
+  z = (int)blockIdx.z;
   const int Hkv = Hq / group;
-  if (!CKV_ATTN_XCD || gridDim.z != 1 || kXcds % Hkv != 0) return;
-  const int L = (int)blockIdx.x + (int)blockIdx.y * nqb;
-  const int xpk = kXcds / Hkv, P = group * nqb;     // XCDs per KV head, items per KV head
-  const int per = P * Hkv / kXcds, full = per * kXcds;  // complete rounds of 8 workgroups
+  if (!CKV_ATTN_XCD || kXcds % Hkv != 0) return;
+  const int L = (int)blockIdx.x + ((int)blockIdx.y + (int)blockIdx.z * Hq) * nqb;
+  const int xpk = kXcds / Hkv, P = group * nqb * (int)gridDim.z;  // XCDs, items per KV head
+  const int per = P * Hkv / kXcds, full = per * kXcds;              // complete rounds of 8 workgroups
   int kv, j;
   if (L < full) {
     const int xcd = L % kXcds, idx = L / kXcds;
@@ -87,9 +89,12 @@ __device__ __forceinline__ void attn_work_item(int nqb, int Hq, int group, int& 
     kv = t / left;
     j = xpk * per + t % left;
   }
-  qb = nqb - 1 - j / group;
+  const int rest = j / group;
   hq = kv * group + j % group;
+  qb = nqb - 1 - rest % nqb;
+  z = rest / nqb;
 }
+
 template <int D>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
     char* __restrict__ out, const char* __restrict__ q, int64_t q_hs_b, int64_t q_ts_b,
@@ -111,8 +116,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int g = lane / 16, lm = lane % 16;
-  int qb, hq;
-  attn_work_item((int)gridDim.x, Hq, group, qb, hq);
+  int qb, hq, z;
+  attn_work_item((int)gridDim.x, Hq, group, qb, hq, z);
   const int hk = hq / group;
   const int q0 = qb * kAttnBM + wave * kAttnQG * 16;
 
@@ -150,7 +155,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   // This workgroup's share of the cache tiles: all of them, or split z of the key range when the
   // launch is split (flash-decoding: few queries, long cache) and partials go to ws.
   const int all_tiles = bmax < 0 ? 0 : bmax / kAttnBN + 1;
-  const int tile_begin = ws != nullptr ? (int)blockIdx.z * split_tiles : 0;
+  const int tile_begin = ws != nullptr ? z * split_tiles : 0;
   const int n_tiles = ws != nullptr ? min(all_tiles, tile_begin + split_tiles) : all_tiles;
 
   // Q fragments (B operand of S^T): query q0 + 16 qg + lm, head-dim 32 s + 8 g .. + 8.
@@ -341,7 +346,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
     const int m = q0 + qg * 16 + lm;
     if (m >= n) continue;
     if (ws != nullptr) {
-      float* prow = ws + (((int64_t)blockIdx.z * Hq + hq) * n + m) * (D + 4);  // 16-byte aligned rows
+      float* prow = ws + (((int64_t)z * Hq + hq) * n + m) * (D + 4);  // 16-byte aligned rows
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) *(float4*)(prow + dt * 16 + 4 * g) = make_float4(o[qg][dt][0], o[qg][dt][1],
                                                                                     o[qg][dt][2], o[qg][dt][3]);
