@@ -45,6 +45,13 @@ constexpr bool kAttnPrefetch = CKV_ATTN_PREFETCH;   // next tile's loads in flig
 
 __device__ __forceinline__ float wave_xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
 
+// V row r of a 16-row block goes to LDS slot vslot(r) (bits 2 and 3 of r swapped): the four rows
+// one 16-lane group reads with a transposing load, and the four the next group reads, then sit
+// in eight distinct 8-dword bank ranges (row stride 8 x odd dwords).
+__device__ __forceinline__ int vslot(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
 // Cache row r of a 32-row block goes to LDS slot kslot(r): the 16 rows that lanes 0-15 read for
 // one S^T tile are then 16 consecutive slots (distinct banks with the padded row stride).
 __device__ __forceinline__ int kslot(int r) {
@@ -105,13 +112,14 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   constexpr int DT = D / 16;          // 16-row tiles of O^T
   constexpr int CPR = D / 8;          // 16-byte chunks per cache row
   constexpr int KROW = D * 2 + 16;    // padded LDS row of the K tile (bytes)
-  constexpr int VROW = kAttnBN * 2 + 16;  // padded LDS row of V^T: one row per head-dim index
+  constexpr int VROW = D * 2 + 32;     // padded LDS row of V: 8 x an odd number of dwords
   constexpr int NT = kAttnWaves * 64;
   static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
-  static_assert((kAttnBN * CPR) % NT == 0 && ((kAttnBN / 2) * CPR) % NT == 0, "tile loads must tile the workgroup");
+  static_assert((kAttnBN * CPR) % NT == 0, "tile loads must tile the workgroup");
+  static_assert((VROW / 4) % 16 == 8, "V row stride must be 8 x an odd number of dwords");
 
   __shared__ __attribute__((aligned(16))) char k_lds[kAttnBN * KROW];
-  __shared__ __attribute__((aligned(16))) char v_lds[D * VROW];
+  __shared__ __attribute__((aligned(16))) char v_lds[kAttnBN * VROW];
   __shared__ int blk_max_s[kAttnWaves];
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -184,44 +192,42 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   const char* kh = kc + (int64_t)hk * kv_hs_b;
   const char* vh = vc + (int64_t)hk * kv_hs_b;
 
-  constexpr int KL = (kAttnBN * CPR) / NT;        // 16-byte K loads per thread and tile
-  constexpr int VL = ((kAttnBN / 2) * CPR) / NT;  // V row-pair loads per thread and tile
-  vec16 kr[KL], va[VL], vb[VL];
-  // Per-thread offsets of its K chunks and V row pairs inside a tile (tile-invariant).
-  int k_off[KL], k_row[KL], v_off[VL], v_row[VL];
+  constexpr int KL = (kAttnBN * CPR) / NT;  // 16-byte K (and V) loads per thread and tile
+  vec16 kr[KL], vr[KL];
+  // Per-thread offsets of its K/V chunks inside a tile (tile-invariant; same for K and V).
+  int k_off[KL], k_row[KL];
 #pragma unroll
   for (int i = 0; i < KL; ++i) {
     const int c = threadIdx.x + i * NT;
     k_row[i] = c / CPR;
     k_off[i] = k_row[i] * (D * 2) + (c % CPR) * 16;
   }
-#pragma unroll
-  for (int i = 0; i < VL; ++i) {
-    const int c = threadIdx.x + i * NT;
-    v_row[i] = 2 * (c % (kAttnBN / 2));
-    v_off[i] = v_row[i] * (D * 2) + (c / (kAttnBN / 2)) * 16;
-  }
   auto load_tile = [&](int n0) {  // global -> registers; rows past the cache read as zero
     const char* kt = kh + (int64_t)n0 * (D * 2);
     const char* vt = vh + (int64_t)n0 * (D * 2);
     if (n0 + kAttnBN <= N) {  // uniform: a full tile needs no row checks
 #pragma unroll
-      for (int i = 0; i < KL; ++i) kr[i] = ld16(kt + k_off[i]);
-#pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        va[i] = ld16(vt + v_off[i]);
-        vb[i] = ld16(vt + v_off[i] + D * 2);
+      for (int i = 0; i < KL; ++i) {
+        kr[i] = ld16(kt + k_off[i]);
+        vr[i] = ld16(vt + k_off[i]);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < KL; ++i) kr[i] = n0 + k_row[i] < N ? ld16(kt + k_off[i]) : vec16{0, 0, 0, 0};
-#pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        va[i] = n0 + v_row[i] < N ? ld16(vt + v_off[i]) : vec16{0, 0, 0, 0};
-        vb[i] = n0 + v_row[i] + 1 < N ? ld16(vt + v_off[i] + D * 2) : vec16{0, 0, 0, 0};
+      for (int i = 0; i < KL; ++i) {
+        const bool in = n0 + k_row[i] < N;
+        kr[i] = in ? ld16(kt + k_off[i]) : vec16{0, 0, 0, 0};
+        vr[i] = in ? ld16(vt + k_off[i]) : vec16{0, 0, 0, 0};
       }
     }
   };
+  // O^T's A operand (V^T rows) comes from row-major V through transposing 64-bit LDS loads:
+  // in each 16-lane group, lane m names row 4h + m / 4 (of the group's 8 keys 8 g ..) at column
+  // 4 (m % 4) of the 16-column tile, and lane 4a + b receives column 4a + b of rows 4h + 0..3.
+  // So lane (g, lm) holds V[8 g + 4 h + e][16 dt + lm], e = 0..3: two loads (h = 0, 1) give the
+  // eight keys 8 g + e' the B operand (P^T) pairs with that lane.
+  int v_rd[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) v_rd[h] = vslot(8 * g + 4 * h + lm / 4) * VROW + 4 * (lm % 4) * 2;
   if (kAttnPrefetch && tile_begin < n_tiles) load_tile(tile_begin * kAttnBN);
 
   for (int tile = tile_begin; tile < n_tiles; ++tile) {
@@ -234,13 +240,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
       *(vec16*)(k_lds + kslot(r) * KROW + col * 16) = kr[i];
     }
 #pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int c = threadIdx.x + i * NT, pr = c % (kAttnBN / 2), col = c / (kAttnBN / 2);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {  // (V[2pr][d], V[2pr+1][d]) for d = 8 col + e: one byte permute
-        const unsigned w = __builtin_amdgcn_perm(vb[i][e >> 1], va[i][e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
-        *(unsigned*)(v_lds + (8 * col + e) * VROW + pr * 4) = w;
-      }
+    for (int i = 0; i < KL; ++i) {
+      const int c = threadIdx.x + i * NT, r = c / CPR, col = c % CPR;
+      *(vec16*)(v_lds + vslot(r) * VROW + col * 16) = vr[i];
     }
     __syncthreads();
     if (kAttnPrefetch && tile + 1 < n_tiles) load_tile(n0 + kAttnBN);  // lands during the MFMAs below
@@ -327,7 +329,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 a = *(const bf16x8*)(v_lds + (dt * 16 + lm) * VROW + (kb * 32 + 8 * g) * 2);
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        const char* vb = v_lds + kb * 32 * VROW + dt * 16 * 2;
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + v_rd[0]));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + v_rd[1]));
+        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int qg = 0; qg < kAttnQG; ++qg)
           o[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qg][kb], o[qg][dt], 0, 0, 0);
