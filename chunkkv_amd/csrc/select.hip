@@ -178,6 +178,28 @@ __device__ __forceinline__ int block_scan_1b(int v, int* slots, int& total) {
   return before + x - v;
 }
 
+// block_scan_1b for a 64-bit value (several counts packed in disjoint bit fields).
+__device__ __forceinline__ uint64_t block_scan_1b_u64(uint64_t v, uint64_t* slots, uint64_t& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  uint64_t x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint64_t y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) slots[wave] = x;
+  __syncthreads();
+  uint64_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const uint64_t t = slots[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  total = all;
+  return before + x - v;
+}
+
 // Register-resident selection for n_tokens <= KPT * 1024: thread t owns positions
 // [t*KPT, (t+1)*KPT); their keys stay in registers through the four radix passes.
 // Barrier budget: chunk phase 2, candidate count 1, 2 per radix pass (double-buffered
@@ -193,7 +215,8 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
   constexpr int kBatch = 8;            // chunk-sum loads in flight per lane
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
   __shared__ uint32_t hist[2][kSelWaves][256];
-  __shared__ int slots[5][kSelWaves];
+  __shared__ int slots[2][kSelWaves];
+  __shared__ uint64_t slots64[kSelWaves];
   __shared__ int s_budget_req, s_bad_span;
 
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
@@ -206,13 +229,38 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
   constexpr int kFlagWords = (KPT + 3) / 4;
   uint32_t key[KPT];        // order-preserving deviation keys of the owned positions
   uint32_t fl[kFlagWords];  // their flag bytes, four per register
+  int lv[KPT];              // their local indices (the compaction's keep_local)
 #pragma unroll
   for (int w = 0; w < kFlagWords; ++w) fl[w] = 0u;
+  // A thread's run is contiguous, so lanes are KPT elements apart: with KPT % 4 == 0 and aligned
+  // arrays, 16-byte (4-byte for flags) loads cut the load instructions and cache-line requests
+  // four-fold.
+  const bool vec_ok = KPT % 4 == 0 && (((uintptr_t)diff | (uintptr_t)local) % 16 == 0) &&
+                      ((uintptr_t)flags % 4 == 0) && (keep_rank == nullptr || (uintptr_t)keep_rank % 16 == 0);
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int p = p0 + i;
-    key[i] = p < n_tokens ? dev_key(diff[p]) : 0u;
-    if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
+  for (int i0 = 0; i0 < KPT; i0 += 4) {
+    if (vec_ok && p0 + i0 + 4 <= n_tokens) {
+      const float4 d = *(const float4*)(diff + p0 + i0);
+      const int4 l = *(const int4*)(local + p0 + i0);
+      const uint32_t f = *(const uint32_t*)(flags + p0 + i0);
+      key[i0] = dev_key(d.x);
+      key[i0 + 1] = dev_key(d.y);
+      key[i0 + 2] = dev_key(d.z);
+      key[i0 + 3] = dev_key(d.w);
+      lv[i0] = l.x;
+      lv[i0 + 1] = l.y;
+      lv[i0 + 2] = l.z;
+      lv[i0 + 3] = l.w;
+      fl[i0 / 4] = f;  // i0 % 4 == 0 here: the word holds flags i0 .. i0 + 3
+    } else {
+#pragma unroll
+      for (int i = i0; i < i0 + 4 && i < KPT; ++i) {
+        const int p = p0 + i;
+        key[i] = p < n_tokens ? dev_key(diff[p]) : 0u;
+        lv[i] = p < n_tokens ? local[p] : 0;
+        if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
+      }
+    }
   }
   // this wavefront's first chunk: span and the first batch of its deviations
   ckv_chunk_span sp0{0, 0, 0, 0};
@@ -303,6 +351,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
   // Phase 3: radix select of the budget-th largest candidate key.
   uint32_t prefix = 0u, pmask = 0u;
   int need = budget;
+  int tie_count = 0;  // candidates with key == T (the last pass's bin of T)
   if (budget > 0) {
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
@@ -366,6 +415,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
       need -= (int)__shfl(my_above, src, kWave);
       prefix |= (uint32_t)digit << shift;
       pmask |= 255u << shift;
+      if (pass == 3) tie_count = (int)h[0][digit];
     }
   }
   const uint32_t T = prefix;
@@ -381,37 +431,58 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
       }
     }
   }
-  int lv[KPT];  // the keys are dead now; their registers carry local[] through the scans
+  if (need < tie_count) {  // uniform: only then do ties need ranking (lowest positions first)
+    int tie_total = 0;
+    int tie_rank = block_scan_1b(__popcll(tie), slots[1], tie_total);
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) lv[i] = (p0 + i < n_tokens) ? local[p0 + i] : 0;
-  int tie_total = 0;
-  int tie_rank = block_scan_1b(__popcll(tie), slots[1], tie_total);
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    if ((tie >> i) & 1ull) {
-      take |= (uint64_t)(tie_rank < need) << i;
-      ++tie_rank;
+    for (int i = 0; i < KPT; ++i) {
+      if ((tie >> i) & 1ull) {
+        take |= (uint64_t)(tie_rank < need) << i;
+        ++tie_rank;
+      }
     }
+  } else {
+    take |= tie;  // every tie at T is taken
   }
   const uint64_t kept = kept_static | take;
-  int n_keep = 0;
-  int rank = block_scan_1b(__popcll(kept), slots[2], n_keep);
-  int my_cached = 0, my_bad = 0;
+  // One scan for three counts in 21-bit fields (each total <= n_tokens < 2^21): kept positions
+  // (the rank of each), kept cached positions, kept positions absent from the active set.
+  uint64_t mine = (uint64_t)__popcll(kept);
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    if (keep_rank != nullptr && p0 + i < n_tokens) keep_rank[p0 + i] = ((kept >> i) & 1ull) ? rank : -1;
+    if ((kept >> i) & 1ull) {
+      mine += (((fl[i / 4] >> (8 * (i % 4))) & CKV_POS_CACHED) ? 1ull : 0ull) << 21;
+      mine += (uint64_t)(lv[i] < 0) << 42;
+    }
+  }
+  uint64_t all = 0;
+  int rank = (int)(block_scan_1b_u64(mine, slots64, all) & 0x1fffffu);
+  const int n_keep = (int)(all & 0x1fffffu);
+  const int sel_cached = (int)((all >> 21) & 0x1fffffu);
+  const int uncomputed = (int)((all >> 42) & 0x1fffffu);
+  int kr[KPT];  // keep_rank of the owned positions
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    kr[i] = ((kept >> i) & 1ull) ? rank : -1;
     if ((kept >> i) & 1ull) {
       const int p = p0 + i;
       keep_abs[rank] = p;
       keep_local[rank] = lv[i] < 0 ? 0 : lv[i];
-      my_bad += lv[i] < 0;
-      my_cached += ((fl[i / 4] >> (8 * (i % 4))) & CKV_POS_CACHED) ? 1 : 0;
       ++rank;
     }
   }
-  int sel_cached = 0, uncomputed = 0;
-  block_scan_1b(my_cached, slots[3], sel_cached);
-  block_scan_1b(my_bad, slots[4], uncomputed);
+  if (keep_rank != nullptr) {
+#pragma unroll
+    for (int i0 = 0; i0 < KPT; i0 += 4) {
+      if (vec_ok && p0 + i0 + 4 <= n_tokens) {
+        *(int4*)(keep_rank + p0 + i0) = make_int4(kr[i0], kr[i0 + 1], kr[i0 + 2], kr[i0 + 3]);
+      } else {
+#pragma unroll
+        for (int i = i0; i < i0 + 4 && i < KPT; ++i)
+          if (p0 + i < n_tokens) keep_rank[p0 + i] = kr[i];
+      }
+    }
+  }
   if (tid == 0) {
     counts[CKV_COUNT_KEEP] = n_keep;
     counts[CKV_COUNT_SELECTED_CACHED] = sel_cached;

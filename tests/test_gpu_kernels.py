@@ -171,6 +171,48 @@ def test_rerope_gather_layer_range_with_skip_map(layers):
     np.testing.assert_array_equal(Vg, want_v)
 
 
+@pytest.mark.parametrize("lens,pattern", [
+    ([300, 700, 257, 1, 64], "per_segment"),  # several 256-token ranking rounds per segment
+    ([40, 70, 33, 64, 1, 97], "all_or_none"),  # whole segments kept or gathered
+    ([5000, 30], "per_segment"),               # past the compacted path's segment limit
+])
+def test_rerope_gather_skip_map_uneven_selection(lens, pattern):
+    """Skip maps as a selection leaves them: the kept share differs per segment (0% to 100%), so
+    the gathered rows of a segment are ranked across several rounds, some segments gather
+    nothing and some everything. Every remaining row equals the oracle's full gather; kept rows
+    stay untouched."""
+    bf16, D, layers = True, 64, (1, 3)
+    rng = np.random.default_rng(sum(lens))
+    n_layers, H = 3, 2
+    N = sum(lens) + 5 * len(lens)
+    plan, ks, vs = _gather_case(rng, bf16, n_layers, H, D, lens, N, False)
+    _, _, Ko, Vo, src = _run_gather(plan, ks, vs, n_layers, H, D, N, bf16)
+    keep = rng.random(N) < 0.5  # uncached positions are irrelevant to the gather
+    for i, (s0, n, *_rest) in enumerate(plan.segments):
+        share = rng.choice([0.0, 0.05, 0.5, 0.95, 1.0]) if pattern == "per_segment" else float(i % 2)
+        keep[s0 : s0 + n] = rng.random(n) < share
+    skip = np.where(keep, 0, -1).astype(np.int32)
+    tab = np.zeros((len(plan.chunks), n_layers, 2), dtype=np.uint64)
+    for ci, ch in enumerate(plan.chunks):
+        for l in range(n_layers):
+            tab[ci, l] = src[ch.idx][0][l].data_ptr(), src[ch.idx][1][l].data_ptr()
+    K = torch.full((n_layers, 1, H, N, D), -7.0, dtype=torch.bfloat16, device=DEV)
+    V = torch.full_like(K, -7.0)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.rerope_gather(K, V, torch.from_numpy(tab.view(np.int64)).to(DEV), dev(plan.segments.reshape(-1)),
+                      len(plan.segments), plan.max_seg_tokens, THETA, err, layers=layers, skip=dev(skip))
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    Kg, Vg = host(K).reshape(n_layers, H, N, D), host(V).reshape(n_layers, H, N, D)
+    sent = O.f32_to_bf16_bits(np.float32([-7.0]))[0]
+    want_k, want_v = np.full_like(Ko, sent), np.full_like(Vo, sent)
+    rows = np.flatnonzero(skip < 0)
+    for l in range(*layers):
+        want_k[l][:, rows], want_v[l][:, rows] = Ko[l][:, rows], Vo[l][:, rows]
+    np.testing.assert_array_equal(Kg, want_k)
+    np.testing.assert_array_equal(Vg, want_v)
+
+
 def test_rerope_gather_config2_full_size():
     """Re-RoPE + gather at the Qwen2.5-7B KV shape: 28 layers, 4 heads, D=128, bf16,
     16 chunks x 256 tokens moved by delta ~ U[-4096, 4096] into a 4096-token cache."""
