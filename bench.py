@@ -286,8 +286,19 @@ def repair_bytes(n_keep: int) -> int:
     return GATHER_BYTES + DEVIATION_BYTES + N_TOKENS * scatter_row + (N_LAYERS - 1) * n_keep * scatter_row
 
 
+PREWARM_S = 0.2  # untimed calls before each timed burst: MI355X clocks ramp up over tens of ms of load
+
+
 def _timed(fn, n: int, stream) -> float:
-    """Average ms of n calls of fn(i), HIP events on `stream` around the whole burst."""
+    """Average ms of n calls of fn(i), HIP events on `stream` around the whole burst. The burst
+    follows PREWARM_S seconds of untimed calls of the same fn, so it is timed at the clocks a
+    loaded GPU runs at rather than while they are still rising from idle."""
+    t_end, i = time.perf_counter() + PREWARM_S, 0
+    while time.perf_counter() < t_end:
+        fn(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
