@@ -684,7 +684,12 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
     for i in range(max(warmup, 2)):
         round_(i)
     torch.cuda.synchronize()
-    ms = _timed(round_, steps, torch.cuda.current_stream(dev))
+    ms_eager = _timed(round_, steps, torch.cuda.current_stream(dev))
+    # the same rounds replayed from HIP graphs (one per input set), as a serving loop would issue them
+    graphs = [_graph_of(lambda i=i: round_(i)) for i in range(2)]
+    for g in graphs:
+        g.replay()
+    ms = _timed(lambda i: graphs[i % 2].replay(), steps, torch.cuda.current_stream(dev))
     per_req = sum(repair_bytes_for(rq["plan"]) for rq in reqs[:n_streams]) / n_streams
     nbytes = per_req * n_streams
     assert all(int(rq["sel"].counts[0].item()) == rq["plan"].n_keep for rq in reqs)
@@ -696,9 +701,10 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
          "bytes_per_step": int(nbytes), "requests_per_step": n_streams},
         None)
     line["store_gib"] = round(len(store) * N_LAYERS * 2 * N_KV * L * HEAD_DIM * 2 / 2**30, 2)
+    line["ms_per_step_eager"] = round(ms_eager, 4)
     for rq in reqs:  # free the repair buffers before the model comes in
         rq.clear()
-    del reqs
+    del reqs, graphs
     torch.cuda.empty_cache()
     if ttft_requests > 0:
         from chunkkv_amd.engine import HipEngine
