@@ -355,9 +355,43 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     assert int(wls[0].sel.counts[0].item()) == n_keep
     nbytes = repair_bytes(n_keep)
     gd_bytes = dropped_bytes(plan)
+    ms_conc = _concurrent_steps(wls, steps, dev)
     return dict(ms_per_step=ms, ms_serial=ms_serial, ms_asm=ms_asm, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
-                asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep)
+                asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep, ms_conc=ms_conc,
+                conc_gbs=CONCURRENT * nbytes / (ms_conc * 1e-3) / 1e9)
+
+
+CONCURRENT = 4  # requests in flight for the serving-loop variant of the step
+
+
+def _concurrent_steps(wls, steps: int, dev) -> float:
+    """ms per round of CONCURRENT requests' KV repairs, each request's launches on its own stream
+    (one stream per request, as a server with concurrent requests issues them), replayed from a
+    HIP graph. The single request's step is a chain of dependent launches, most of them too small
+    to fill the GPU; independent requests overlap each other's latency."""
+    reqs = list(wls) + [RepairWorkload(1234 + len(wls) + i, dev) for i in range(CONCURRENT - len(wls))]
+    streams = [torch.cuda.Stream(device=dev) for _ in reqs]  # default priority
+
+    def round_():
+        main = torch.cuda.current_stream(dev)
+        for w, st in zip(reqs, streams):
+            st.wait_stream(main)
+            with torch.cuda.stream(st):
+                w.step_serial()
+        for st in streams:
+            main.wait_stream(st)
+
+    round_()
+    torch.cuda.synchronize()
+    g = _graph_of(round_)
+    g.replay()
+    ms = _timed(lambda i: g.replay(), steps, torch.cuda.current_stream(dev))
+    assert all(int(w.err.item()) == 0 for w in reqs)
+    for w in wls:  # leave the two-stream step's selection state as it was
+        w.step()
+    torch.cuda.synchronize()
+    return ms
 
 
 def dropped_bytes(plan) -> int:
@@ -1028,6 +1062,10 @@ def main() -> None:
         "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
         "ms_per_step_one_stream": round(r["ms_serial"], 4),
         "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
+        "concurrent_requests": {"requests": CONCURRENT, "ms_per_round": round(r["ms_conc"], 4),
+                                "gbs": round(r["conc_gbs"], 1), "pct_of_peak": round(100.0 * r["conc_gbs"] / PEAK_GBS, 2),
+                                "note": "the same request's KV repair, CONCURRENT independent requests in flight on "
+                                        "their own streams (one HIP graph per round); value is the single-request step"},
         "roofline": {
             "kernel": "rerope_gather_kernel<bf16,128> (layers 2-27, dropped rows)",
             "bound": "hbm",
