@@ -43,7 +43,21 @@ constexpr int kAttnBM = kAttnWaves * kAttnQG * 16;  // queries per workgroup
 constexpr int kAttnBN = 64;                         // cache rows per tile
 constexpr bool kAttnPrefetch = CKV_ATTN_PREFETCH;   // next tile's loads in flight during the MFMAs
 
-__device__ __forceinline__ float wave_xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
+// Combine a lane's value with the lanes 16 and 32 away (the four lane groups of one query), with
+// gfx950's row-swap permutes (VALU, no LDS round trip): each returns the lane's own value and
+// its partner's, in an order that depends on the lane, so only order-free combinations are used.
+__device__ __forceinline__ float group_max(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group_sum(float v) {  // fp32 addition commutes: every lane agrees
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // V row r of a 16-row block goes to LDS slot vslot(r) (bits 2 and 3 of r swapped): the four rows
 // one 16-lane group reads with a transposing load, and the four the next group reads, then sit
@@ -298,7 +312,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int j = 0; j < 8; ++j) bm = fmaxf(bm, x[kb][j]);
-      bm = wave_xor_max(wave_xor_max(bm, 16), 32) * scale_log2;  // the scale is > 0: max commutes
+      bm = group_max(bm) * scale_log2;  // the scale is > 0: max commutes
       const bool raise = bm > m_run[qg] + 8.f;  // also true on the first visible tile (m_run = -inf)
       if (__builtin_amdgcn_ballot_w64(raise)) {  // uniform branch
         const float m_new = raise ? bm : m_run[qg];
@@ -346,9 +360,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   // kernel merges the splits.
 #pragma unroll
   for (int qg = 0; qg < kAttnQG; ++qg) {
-    float l = l_run[qg];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = group_sum(l_run[qg]);
     const int m = q0 + qg * 16 + lm;
     if (m >= n) continue;
     if (ws != nullptr) {
