@@ -76,6 +76,9 @@ __device__ __forceinline__ int kslot(int r) {
 #ifndef CKV_ATTN_PRIO
 #define CKV_ATTN_PRIO 0  // 1: raise the wavefront's issue priority around its matrix-core sections
 #endif
+#ifndef CKV_ATTN_MFMA_SUM
+#define CKV_ATTN_MFMA_SUM 1  // softmax row sums on the matrix cores (a ones operand) instead of VALU adds
+#endif
 #ifndef CKV_ATTN_XCD
 #define CKV_ATTN_XCD 1  // place the workgroups of one KV head on the same XCDs
 #endif
@@ -195,10 +198,17 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
 
   f32x4 o[kAttnQG][DT];
   float m_run[kAttnQG], l_run[kAttnQG];
+  // With CKV_ATTN_MFMA_SUM the row sums come from one more MFMA per key block with an all-ones A
+  // operand: every row of its output is sum_k P^T[k][query], the sum of the bf16 weights that
+  // multiply V (lane (g, lm) gets query lm's sum in each of its four values).
+  f32x4 l_acc[kAttnQG];
+  const bf16x8 ones = {(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+                       (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
 #pragma unroll
   for (int qg = 0; qg < kAttnQG; ++qg) {
     m_run[qg] = -INFINITY;
     l_run[qg] = 0.f;
+    l_acc[qg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[qg][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -318,6 +328,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
         const float m_new = raise ? bm : m_run[qg];
         const float alpha = m_run[qg] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[qg] - m_new);
         l_run[qg] *= alpha;
+        l_acc[qg] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[qg][dt] *= alpha;
         m_run[qg] = m_new;
@@ -331,10 +342,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kb][e], scale_log2, -msub));
-          psum += p;
+          if (!CKV_ATTN_MFMA_SUM) psum += p;
           pb[qg][kb][e] = (__bf16)p;
         }
-      l_run[qg] += psum;
+      if (!CKV_ATTN_MFMA_SUM) l_run[qg] += psum;
     }
 
     // O^T += V^T P^T: A = V^T rows dt*16 + lm, columns 32 kb + 8 g .. + 8.
@@ -351,6 +362,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
 #pragma unroll
         for (int qg = 0; qg < kAttnQG; ++qg)
           o[qg][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qg][kb], o[qg][dt], 0, 0, 0);
+        if (CKV_ATTN_MFMA_SUM && dt == DT - 1) {
+#pragma unroll
+          for (int qg = 0; qg < kAttnQG; ++qg)
+            l_acc[qg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qg][kb], l_acc[qg], 0, 0, 0);
+        }
       }
     if (CKV_ATTN_PRIO) __builtin_amdgcn_s_setprio(0);
   }
@@ -360,7 +376,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   // kernel merges the splits.
 #pragma unroll
   for (int qg = 0; qg < kAttnQG; ++qg) {
-    const float l = group_sum(l_run[qg]);
+    const float l = CKV_ATTN_MFMA_SUM ? l_acc[qg][0] : group_sum(l_run[qg]);
     const int m = q0 + qg * 16 + lm;
     if (m >= n) continue;
     if (ws != nullptr) {
