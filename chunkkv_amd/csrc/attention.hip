@@ -119,7 +119,11 @@ __device__ __forceinline__ void attn_work_item(int nqb, int Hq, int group, int& 
   z = rest / nqb;
 }
 
-template <int D>
+// GROUPED (few queries, decode): a workgroup's query rows are (token, query head) pairs of ONE KV
+// head, row r = token r / group, head hk * group + r % group, so the group's query heads share
+// every K/V tile the workgroup loads (grid y = KV heads); otherwise rows are tokens of one query
+// head (grid y = query heads).
+template <int D, bool GROUPED>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
     char* __restrict__ out, const char* __restrict__ q, int64_t q_hs_b, int64_t q_ts_b,
     const char* __restrict__ kc, const char* __restrict__ vc, int64_t kv_hs_b,
@@ -142,9 +146,24 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int g = lane / 16, lm = lane % 16;
   int qb, hq, z;
-  attn_work_item((int)gridDim.x, Hq, group, qb, hq, z);
+  if (GROUPED) {
+    int hk0;
+    attn_work_item((int)gridDim.x, Hq / group, 1, qb, hk0, z);
+    hq = hk0 * group;  // the group's first query head
+  } else {
+    attn_work_item((int)gridDim.x, Hq, group, qb, hq, z);
+  }
   const int hk = hq / group;
   const int q0 = qb * kAttnBM + wave * kAttnQG * 16;
+  const int n_rows = GROUPED ? n * group : n;
+  // This lane's query rows: token row_m and query head row_h (row_m >= n: no query).
+  int row_m[kAttnQG], row_h[kAttnQG];
+#pragma unroll
+  for (int qg = 0; qg < kAttnQG; ++qg) {
+    const int r = q0 + qg * 16 + lm;
+    row_m[qg] = r < n_rows ? (GROUPED ? r / group : r) : n;
+    row_h[qg] = GROUPED ? hq + r % group : hq;
+  }
 
   // Positions of this lane's queries (-1 = no query); out-of-range positions are flagged and
   // clamped so that every read stays inside the cache.
@@ -152,7 +171,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   int wmax = -1, wmin = N;
 #pragma unroll
   for (int qg = 0; qg < kAttnQG; ++qg) {
-    const int m = q0 + qg * 16 + lm;
+    const int m = row_m[qg];
     int p = -1;
     if (m < n) {
       const int64_t p64 = pos[m];
@@ -187,11 +206,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
   bf16x8 qf[kAttnQG][DS];
 #pragma unroll
   for (int qg = 0; qg < kAttnQG; ++qg) {
-    const int m = q0 + qg * 16 + lm;
+    const int m = row_m[qg];
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
       vec16 v = {0, 0, 0, 0};
-      if (m < n) v = ld16(q + (int64_t)hq * q_hs_b + (int64_t)m * q_ts_b + (32 * s + 8 * g) * 2);
+      if (m < n) v = ld16(q + (int64_t)row_h[qg] * q_hs_b + (int64_t)m * q_ts_b + (32 * s + 8 * g) * 2);
       qf[qg][s] = __builtin_bit_cast(bf16x8, v);
     }
   }
@@ -377,10 +396,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
 #pragma unroll
   for (int qg = 0; qg < kAttnQG; ++qg) {
     const float l = CKV_ATTN_MFMA_SUM ? l_acc[qg][0] : group_sum(l_run[qg]);
-    const int m = q0 + qg * 16 + lm;
+    const int m = row_m[qg], h = row_h[qg];
     if (m >= n) continue;
     if (ws != nullptr) {
-      float* prow = ws + (((int64_t)z * Hq + hq) * n + m) * (D + 4);  // 16-byte aligned rows
+      float* prow = ws + (((int64_t)z * Hq + h) * n + m) * (D + 4);  // 16-byte aligned rows
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) *(float4*)(prow + dt * 16 + 4 * g) = make_float4(o[qg][dt][0], o[qg][dt][1],
                                                                                     o[qg][dt][2], o[qg][dt][3]);
@@ -391,7 +410,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
       continue;
     }
     const float inv = 1.f / l;
-    char* orow = out + ((int64_t)m * Hq + hq) * (D * 2);
+    char* orow = out + ((int64_t)m * Hq + h) * (D * 2);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       unsigned w[2];
@@ -438,23 +457,50 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(char* __restrict__ out
 
 }  // namespace ckv
 
+namespace ckv {
+
+#ifndef CKV_ATTN_GSPLIT
+#define CKV_ATTN_GSPLIT 6
+#endif
+constexpr int kGroupedSplitTiles = CKV_ATTN_GSPLIT;  // cache tiles per split of a grouped launch
+
+// Split plan of a launch whose rows are tokens of one query head: split only launches too small
+// to fill the chip (decode-like), into about 1024 workgroups of >= 4 tiles each.
+static void row_split_plan(int n_queries, int n_tokens, int n_q_heads, int& splits, int& split_tiles) {
+  splits = 1;
+  split_tiles = 0;
+  const int64_t blocks = (int64_t)((n_queries + kAttnBM - 1) / kAttnBM) * n_q_heads;
+  const int tiles = (n_tokens + kAttnBN - 1) / kAttnBN;
+  constexpr int64_t kTarget = 1024;  // workgroups that fill the 256 CUs a few times over
+  if (blocks < kTarget / 2 && tiles >= 8) {
+    const int want = (int)std::min<int64_t>((kTarget + blocks - 1) / blocks, tiles / 4);
+    split_tiles = (tiles + want - 1) / want;
+    splits = (tiles + split_tiles - 1) / split_tiles;
+  }
+}
+
+// Grouped launches (queries that share KV heads fit one workgroup's rows): every
+// kGroupedSplitTiles cache tiles are one split. Usable when n_queries * group <= kAttnBM.
+static void grouped_split_plan(int n_queries, int n_tokens, int& splits) {
+  const int tiles = (n_tokens + kAttnBN - 1) / kAttnBN;
+  splits = (2 * n_queries <= kAttnBM && tiles >= 2) ? (tiles + kGroupedSplitTiles - 1) / kGroupedSplitTiles : 1;
+}
+
+}  // namespace ckv
+
 extern "C" int64_t ckv_attention_workspace_bytes(int32_t n_queries, int32_t n_tokens, int32_t n_q_heads,
                                                  int32_t head_dim, int32_t* splits_out, int32_t* split_tiles_out) {
   using namespace ckv;
-  int splits = 1, split_tiles = 0;
+  int splits = 1, split_tiles = 0, gsplits = 1;
   if (n_queries > 0 && n_tokens > 0 && n_q_heads > 0 && head_dim > 0) {
-    const int64_t blocks = (int64_t)((n_queries + kAttnBM - 1) / kAttnBM) * n_q_heads;
-    const int tiles = (n_tokens + kAttnBN - 1) / kAttnBN;
-    constexpr int64_t kTarget = 1024;  // workgroups that fill the 256 CUs a few times over
-    if (blocks < kTarget / 2 && tiles >= 8) {
-      const int want = (int)std::min<int64_t>((kTarget + blocks - 1) / blocks, tiles / 4);
-      split_tiles = (tiles + want - 1) / want;
-      splits = (tiles + split_tiles - 1) / split_tiles;
-    }
+    row_split_plan(n_queries, n_tokens, n_q_heads, splits, split_tiles);
+    grouped_split_plan(n_queries, n_tokens, gsplits);
   }
   if (splits_out != nullptr) *splits_out = splits;
   if (split_tiles_out != nullptr) *split_tiles_out = split_tiles;
-  return splits > 1 ? (int64_t)splits * n_q_heads * n_queries * (head_dim + 4) * 4 : 0;
+  const int64_t row = (int64_t)n_q_heads * n_queries * (head_dim + 4) * 4;
+  const int64_t most = std::max(splits > 1 ? splits : 0, gsplits > 1 ? gsplits : 0);
+  return most * row;
 }
 
 extern "C" int32_t ckv_attention_active(void* out, const void* q, int64_t q_head_stride, int64_t q_token_stride,
@@ -474,37 +520,43 @@ extern "C" int32_t ckv_attention_active(void* out, const void* q, int64_t q_head
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16) return CKV_ERR_INVALID_ARGUMENT;
   if (q_token_stride < head_dim || kv_head_stride < (int64_t)n_tokens * head_dim) return CKV_ERR_OUT_OF_RANGE;
   if (n_queries == 0) return CKV_OK;
-  const int blocks = (n_queries + kAttnBM - 1) / kAttnBM;
   if (n_q_heads > 65535) return CKV_ERR_TOO_LARGE;
   const float scale_log2 = (float)(scale * 1.4426950408889634);  // exp(x) = exp2(x log2 e)
-  int splits = 1, split_tiles = 0;
-  const int64_t need = ckv_attention_workspace_bytes(n_queries, n_tokens, n_q_heads, head_dim, &splits, &split_tiles);
-  float* ws = nullptr;
-  if (splits > 1 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 16 == 0) {
-    ws = (float*)workspace;
-  } else {
-    splits = 1;
-  }
-  dim3 grid((unsigned)blocks, (unsigned)n_q_heads, (unsigned)splits);
   const int group = n_q_heads / n_kv_heads;
   hipStream_t st = (hipStream_t)stream;
-  if (head_dim == 128) {
-    hipLaunchKernelGGL((attn_active_kernel<128>), grid, dim3(kAttnWaves * 64), 0, st, (char*)out, (const char*)q,
-                       q_head_stride * 2, q_token_stride * 2, (const char*)k_cache, (const char*)v_cache,
-                       kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group, scale_log2, split_tiles,
-                       ws, err);
+  const int64_t row_b = (int64_t)n_q_heads * n_queries * (head_dim + 4) * 4;
+  const bool ws_ok = workspace != nullptr && (uintptr_t)workspace % 16 == 0;
+  auto launch = [&](auto kernel, auto combine, dim3 grid, int split_tiles, float* ws, int splits) {
+    hipLaunchKernelGGL(kernel, grid, dim3(kAttnWaves * 64), 0, st, (char*)out, (const char*)q, q_head_stride * 2,
+                       q_token_stride * 2, (const char*)k_cache, (const char*)v_cache, kv_head_stride * 2, positions,
+                       n_queries, n_tokens, n_q_heads, group, scale_log2, split_tiles, ws, err);
     if (ws != nullptr)
-      hipLaunchKernelGGL((attn_combine_kernel<128>), dim3((unsigned)n_queries, (unsigned)n_q_heads), dim3(64), 0, st,
-                         (char*)out, ws, n_queries, n_q_heads, splits);
-  } else {
-    hipLaunchKernelGGL((attn_active_kernel<64>), grid, dim3(kAttnWaves * 64), 0, st, (char*)out, (const char*)q,
-                       q_head_stride * 2, q_token_stride * 2, (const char*)k_cache, (const char*)v_cache,
-                       kv_head_stride * 2, positions, n_queries, n_tokens, n_q_heads, group, scale_log2, split_tiles,
-                       ws, err);
-    if (ws != nullptr)
-      hipLaunchKernelGGL((attn_combine_kernel<64>), dim3((unsigned)n_queries, (unsigned)n_q_heads), dim3(64), 0, st,
-                         (char*)out, ws, n_queries, n_q_heads, splits);
+      hipLaunchKernelGGL(combine, dim3((unsigned)n_queries, (unsigned)n_q_heads), dim3(64), 0, st, (char*)out, ws,
+                         n_queries, n_q_heads, splits);
+  };
+  // Queries that share KV heads and fit one workgroup's rows (decode): one workgroup per
+  // (KV head, split), all of the group's query heads on each loaded K/V tile.
+  int gsplits = 1;
+  grouped_split_plan(n_queries, n_tokens, gsplits);
+  if (group > 1 && (int64_t)n_queries * group <= kAttnBM && gsplits > 1 && ws_ok &&
+      workspace_bytes >= gsplits * row_b) {
+    const dim3 grid(1u, (unsigned)n_kv_heads, (unsigned)gsplits);
+    if (head_dim == 128)
+      launch(attn_active_kernel<128, true>, attn_combine_kernel<128>, grid, kGroupedSplitTiles, (float*)workspace, gsplits);
+    else
+      launch(attn_active_kernel<64, true>, attn_combine_kernel<64>, grid, kGroupedSplitTiles, (float*)workspace, gsplits);
+    CKV_RETURN_IF_LAUNCH_FAILED();
+    return CKV_OK;
   }
+  int splits = 1, split_tiles = 0;
+  row_split_plan(n_queries, n_tokens, n_q_heads, splits, split_tiles);
+  float* ws = (splits > 1 && ws_ok && workspace_bytes >= splits * row_b) ? (float*)workspace : nullptr;
+  if (ws == nullptr) splits = 1;
+  const dim3 grid((unsigned)((n_queries + kAttnBM - 1) / kAttnBM), (unsigned)n_q_heads, (unsigned)splits);
+  if (head_dim == 128)
+    launch(attn_active_kernel<128, false>, attn_combine_kernel<128>, grid, split_tiles, ws, splits);
+  else
+    launch(attn_active_kernel<64, false>, attn_combine_kernel<64>, grid, split_tiles, ws, splits);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

@@ -327,9 +327,11 @@ int32_t ckv_attention_active(void* out, const void* q, int64_t q_head_stride, in
 
 /*
  * Bytes of workspace ckv_attention_active uses to split a launch of this shape (0: it never
- * splits this shape); the split count and cache tiles per split go to *splits and
- * *split_tiles when those are not NULL. Host-only, no device work. No counterpart in the
- * reference.
+ * splits this shape), enough for either plan it may take: query heads that share a KV head with
+ * n_queries * group <= 128 (decode) go into one workgroup per (KV head, split of 6 cache tiles);
+ * other launches split into about 1024 workgroups when they would not fill the chip. The latter
+ * plan's split count and cache tiles per split go to *splits and *split_tiles when those are
+ * not NULL. Host-only, no device work. No counterpart in the reference.
  */
 int64_t ckv_attention_workspace_bytes(int32_t n_queries, int32_t n_tokens, int32_t n_q_heads,
                                       int32_t head_dim, int32_t* splits, int32_t* split_tiles);

@@ -95,10 +95,17 @@ def test_attention_strided_query_view():
     assert torch.equal(out, ref)
 
 
-@pytest.mark.parametrize("Hq,Hkv,D,N,n", [(28, 4, 128, 8256, 1), (28, 4, 128, 5000, 3), (14, 2, 64, 3000, 40)])
+@pytest.mark.parametrize("Hq,Hkv,D,N,n", [
+    (28, 4, 128, 8256, 1),  # decode: grouped rows (7 query heads of a KV head per workgroup)
+    (28, 4, 128, 5000, 3),  # grouped, 21 rows
+    (16, 2, 128, 777, 16),  # grouped, exactly one workgroup of rows (16 x 8), ragged last split
+    (14, 2, 64, 3000, 40),  # 280 rows: token rows per query head, split
+    (8, 8, 64, 3000, 2),    # no grouping (one query head per KV head): token rows, split
+])
 def test_attention_split_launch_matches_oracle_and_unsplit(Hq, Hkv, D, N, n):
     """Decode-like shapes split the cache range over workgroups and merge: same result as the
-    unsplit launch (up to the merge's fp32 rounding) and the oracle."""
+    unsplit launch (up to the merge's fp32 rounding) and the oracle. Launches whose queries share
+    KV heads and fit one workgroup put the group's query heads in one workgroup's rows."""
     q, K, V, pos = _case(N + n, Hq, Hkv, D, N, n, with_ends=False)
     pos[-1] = N - 1
     assert _native.lib().ckv_attention_workspace_bytes(n, N, Hq, D, None, None) > 0
