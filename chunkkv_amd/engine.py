@@ -114,6 +114,17 @@ class HipEngine(DecoderPieces):
             self._norm_in = [norm(layer.input_layernorm) for layer in self.layers]
             self._norm_post = [norm(layer.post_attention_layernorm) for layer in self.layers]
             self._norm_final = norm(self.inner.norm)
+            # gate and up as one GEMM per layer (weights stacked once, here): one launch of twice
+            # the width fills the CUs better than two at the prefill shapes; ckv_silu_mul reads
+            # the two halves of its output in place.
+            self._w_gu, self._b_gu = [], []
+            with torch.no_grad():
+                for layer in self.layers:
+                    g, u = layer.mlp.gate_proj, layer.mlp.up_proj
+                    self._w_gu.append(torch.cat([g.weight, u.weight], 0).contiguous())
+                    self._b_gu.append(None if g.bias is None and u.bias is None else torch.cat(
+                        [m.bias if m.bias is not None else torch.zeros(m.out_features, dtype=m.weight.dtype,
+                                                                       device=m.weight.device) for m in (g, u)]))
 
     _RMSNORMS = ("Qwen2RMSNorm", "LlamaRMSNorm", "MistralRMSNorm")
 
@@ -130,7 +141,8 @@ class HipEngine(DecoderPieces):
             return False
         mlps = [layer.mlp for layer in self.layers]
         return all(hasattr(m, "gate_proj") and hasattr(m, "up_proj") and hasattr(m, "down_proj")
-                   and m.gate_proj.out_features % 8 == 0 for m in mlps)
+                   and m.gate_proj.out_features % 8 == 0 and m.up_proj.out_features == m.gate_proj.out_features
+                   and m.up_proj.weight.shape == m.gate_proj.weight.shape for m in mlps)
 
     def _norm(self, li: int, layer, h, pending):
         """Input of layer li: (h + pending, input_layernorm(h + pending)); pending is the previous
@@ -141,15 +153,17 @@ class HipEngine(DecoderPieces):
         return ops.add_rmsnorm(h, pending, w, eps, h_out=h if pending is not None else None)
 
     def _mlp(self, li: int, layer, h, a):
-        """h + a (the attention output after o_proj), then the MLP block. Returns (h, pending): the
-        fused kernels leave the MLP's output in pending for the next norm to add."""
+        """h + a (the attention output after o_proj), then the MLP block (gate and up as one stacked
+        GEMM). Returns (h, pending): the fused kernels leave the MLP's output in pending for the
+        next norm to add."""
         if not self._fused_mlp:
             h = h + a
             return h + layer.mlp(layer.post_attention_layernorm(h)), None
         w, eps = self._norm_post[li]
         h, x = ops.add_rmsnorm(h, a, w, eps, h_out=h)
-        mlp = layer.mlp
-        return h, mlp.down_proj(ops.silu_mul(mlp.gate_proj(x), mlp.up_proj(x)))
+        gu = F.linear(x, self._w_gu[li], self._b_gu[li])
+        width = gu.shape[-1] // 2
+        return h, layer.mlp.down_proj(ops.silu_mul(gu[..., :width], gu[..., width:]))
 
     def _final_logits(self, h, pending):
         """lm_head(norm(h + pending)) of the given rows (torch_engine.py:75)."""

@@ -38,9 +38,12 @@ def use_tuned_gemms(table: Path = TABLE, scratch: str | None = None) -> bool:
 
 def tune(out: Path = TABLE) -> None:
     """Tune the GEMM shapes of the 8k blend request (prefill, chunk prefills, last-token logits)
-    and of greedy decode on a random-init Qwen2.5-7B architecture; write the table to `out`."""
+    and of greedy decode on a random-init Qwen2.5-7B architecture, for HipEngine (stacked q|k|v
+    and gate|up projections) and for the reference op sequence (TorchOpsEngine, the model's own
+    projections), so both run from tuned entries; write the table to `out`."""
     sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
     import bench  # the workload definitions (request shape, model) live with the benchmark
+    from chunkkv_amd.baseline import TorchOpsEngine
     from chunkkv_amd.engine import HipEngine
     from chunkkv_amd.types import BlendConfig
 
@@ -63,7 +66,9 @@ def tune(out: Path = TABLE) -> None:
         placements.append(bench.Place(pool[c][1], len(tokens)))
         tokens += pool[c][0]
     tokens += torch.randint(0, vocab, (bench.TAIL + bench.QUERY,), generator=gen).tolist()
-    res = eng.prefill(tokens, placements, BlendConfig(recompute_ratio=bench.RATIO, n_sink=bench.N_SINK))
+    cfg = BlendConfig(recompute_ratio=bench.RATIO, n_sink=bench.N_SINK)
+    res = eng.prefill(tokens, placements, cfg)
+    TorchOpsEngine(model, bench._Tok()).prefill(tokens, placements, cfg)
     eng.last_logprobs(res)
     eng.eos = set()
     eng.generate(res, 2)
