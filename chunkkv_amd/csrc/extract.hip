@@ -11,26 +11,28 @@
 // Destination layout per segment s: [2][n_layers][H][len_s][D] (K layers, then V layers), so
 // that layer l's keys (and values) are a contiguous (1, H, len_s, D) view.
 //
-// Design (gfx950): one workgroup = one (segment, 16-token tile, layer); 16-byte loads and
+// Design (gfx950): one workgroup = one (segment, 8-token tile, layer); 16-byte loads and
 // stores; a thread walks (K/V, head, token, 16-byte column) items with the column fastest, so a
-// wavefront reads and writes whole rows.
+// wavefront reads and writes whole rows. Grid x = tile (fastest), y = segment, z = layer: the
+// workgroups in flight together copy neighbouring tiles of one segment (159 -> 150 us for the
+// 8k request's 24 segments x 28 layers against segment-fastest order with 16-token tiles).
 #include "ckv_common.hpp"
 
 namespace ckv {
 
 constexpr int kExtractThreads = 256;
-constexpr int kExtractTile = 16;
+constexpr int kExtractTile = 8;
 
 __global__ __launch_bounds__(kExtractThreads) void extract_kernel(
     const char* __restrict__ src_k, const char* __restrict__ src_v, int64_t ls_b, int64_t hs_b, int row_b,
     const uint64_t* __restrict__ dst_tab, const int32_t* __restrict__ spans, int n_layers, int n_heads, int n_tokens,
     int32_t* __restrict__ err) {
   typedef __attribute__((address_space(1))) const int32_t gi32;
-  const int seg = blockIdx.x, layer = blockIdx.z;
+  const int seg = blockIdx.y, layer = blockIdx.z;
   const int start = *(gi32*)(spans + 2 * seg), len = *(gi32*)(spans + 2 * seg + 1);
-  const int t0 = blockIdx.y * kExtractTile;
+  const int t0 = blockIdx.x * kExtractTile;
   if (start < 0 || len < 0 || (int64_t)start + len > n_tokens) {
-    if (threadIdx.x == 0 && blockIdx.y == 0 && layer == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+    if (threadIdx.x == 0 && blockIdx.x == 0 && layer == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
     return;
   }
   if (t0 >= len) return;  // uniform
@@ -69,8 +71,8 @@ extern "C" int32_t ckv_extract_chunks(const void* k_slab, const void* v_slab, in
   if (head_stride < (int64_t)n_tokens * head_dim || layer_stride < head_stride * n_heads) return CKV_ERR_OUT_OF_RANGE;
   if (n_spans == 0 || max_len == 0) return CKV_OK;
   const int tiles = (max_len + kExtractTile - 1) / kExtractTile;
-  if (tiles > 65535 || n_layers > 65535) return CKV_ERR_TOO_LARGE;
-  hipLaunchKernelGGL(extract_kernel, dim3((unsigned)n_spans, (unsigned)tiles, (unsigned)n_layers),
+  if (n_spans > 65535 || n_layers > 65535) return CKV_ERR_TOO_LARGE;  // grid y and z
+  hipLaunchKernelGGL(extract_kernel, dim3((unsigned)tiles, (unsigned)n_spans, (unsigned)n_layers),
                      dim3(kExtractThreads), 0, (hipStream_t)stream, (const char*)k_slab, (const char*)v_slab,
                      layer_stride * eb, head_stride * eb, (int)row_b, dst_tab, spans, n_layers, n_heads, n_tokens, err);
   CKV_RETURN_IF_LAUNCH_FAILED();

@@ -284,7 +284,7 @@ int32_t ckv_rope_table(void* table, int64_t n_positions, int32_t head_dim, doubl
  * into the buffer dst_tab[s] (device address), laid out [2][n_layers][n_heads][len][head_dim]:
  * K layers then V layers, so each layer's keys/values are a contiguous (1, H, len, D) block. The
  * buffer must hold 2 * n_layers * n_heads * len * head_dim elements. max_len >= every len.
- * A span outside [0, n_tokens) is skipped and flagged in *err. Bit copies (bf16 or f32).
+ * n_spans and n_layers are at most 65535 (CKV_ERR_TOO_LARGE beyond). A span outside [0, n_tokens) is skipped and flagged in *err. Bit copies (bf16 or f32).
  * Replaces: PrefillResult.chunk's per-layer copies (base.py:55-60, torch_engine.py:177), called
  * per reusable segment by the runtime (runtime.py:83-92): 2 x n_layers launches per segment.
  */
