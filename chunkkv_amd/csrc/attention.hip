@@ -427,32 +427,80 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
 // Merge the splits of a split launch: for query m and head h, with (M_z, L_z, O_z) the partials
 // of split z (max in the log2 domain, sum and unnormalised rows relative to M_z):
 //   out = sum_z 2^(M_z - M) O_z / sum_z 2^(M_z - M) L_z,  M = max_z M_z  (splits with M_z = -inf
-// saw no visible row and weigh 0). One 64-lane wavefront per (query, head); lane d covers
+// saw no visible row and weigh 0). One workgroup of kCombineWaves wavefronts per (query, head):
+// wavefront w folds splits w*4 .. w*4+3, then every (4 x kCombineWaves)-th group after them,
+// loading each group's four partials together and merging them into a running (max, sum, row)
+// with the online rescale; the wavefronts' results are merged through LDS. Lane d covers
 // head-dim columns d, d + 64.
+constexpr int kCombineWaves = 4;
+
 template <int D>
-__global__ __launch_bounds__(64) void attn_combine_kernel(char* __restrict__ out, const float* __restrict__ ws,
-                                                          int n, int Hq, int splits) {
-  const int m = blockIdx.x, hq = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(kCombineWaves * 64) void attn_combine_kernel(char* __restrict__ out,
+                                                                          const float* __restrict__ ws, int n, int Hq,
+                                                                          int splits) {
+  constexpr int CW = D / 64;  // columns per lane
+  constexpr int U = 4;        // partials in flight per wavefront
+  const int m = blockIdx.x, hq = blockIdx.y, lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int64_t stride = (int64_t)Hq * n * (D + 4);
   const float* base = ws + ((int64_t)hq * n + m) * (D + 4);
-  float M = -INFINITY;
-  for (int z = 0; z < splits; ++z) M = fmaxf(M, base[z * stride + D]);
-  float L = 0.f, acc[D / 64];
+  float M = -INFINITY, L = 0.f, acc[CW];
 #pragma unroll
-  for (int j = 0; j < D / 64; ++j) acc[j] = 0.f;
-  for (int z = 0; z < splits; ++z) {
-    const float* pz = base + z * stride;
-    const float mz = pz[D];
-    if (mz == -INFINITY) continue;
-    const float w = __builtin_amdgcn_exp2f(mz - M);
-    L += w * pz[D + 1];
+  for (int j = 0; j < CW; ++j) acc[j] = 0.f;
+  for (int z0 = wave * U; z0 < splits; z0 += U * kCombineWaves) {
+    float mz[U], lz[U], oz[U][CW];
 #pragma unroll
-    for (int j = 0; j < D / 64; ++j) acc[j] += w * pz[lane + 64 * j];
+    for (int u = 0; u < U; ++u) {
+      mz[u] = -INFINITY;
+      lz[u] = 0.f;
+#pragma unroll
+      for (int j = 0; j < CW; ++j) oz[u][j] = 0.f;
+      if (z0 + u < splits) {
+        const float* pz = base + (int64_t)(z0 + u) * stride;
+        mz[u] = pz[D];
+        lz[u] = pz[D + 1];
+#pragma unroll
+        for (int j = 0; j < CW; ++j) oz[u][j] = pz[lane + 64 * j];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (mz[u] == -INFINITY) continue;  // uniform: the same partial for every lane
+      const float mn = fmaxf(M, mz[u]);
+      const float a = __builtin_amdgcn_exp2f(M - mn);  // 0 while M is still -inf
+      const float b = __builtin_amdgcn_exp2f(mz[u] - mn);
+      L = L * a + lz[u] * b;
+#pragma unroll
+      for (int j = 0; j < CW; ++j) acc[j] = acc[j] * a + oz[u][j] * b;
+      M = mn;
+    }
   }
-  const float inv = 1.f / L;
+  __shared__ float s_m[kCombineWaves], s_l[kCombineWaves], s_o[kCombineWaves][D];
+  if (lane == 0) {
+    s_m[wave] = M;
+    s_l[wave] = L;
+  }
+#pragma unroll
+  for (int j = 0; j < CW; ++j) s_o[wave][lane + 64 * j] = acc[j];
+  __syncthreads();
+  if (wave != 0) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kCombineWaves; ++w) mx = fmaxf(mx, s_m[w]);
+  float lt = 0.f, o[CW];
+#pragma unroll
+  for (int j = 0; j < CW; ++j) o[j] = 0.f;
+#pragma unroll
+  for (int w = 0; w < kCombineWaves; ++w) {
+    if (s_m[w] == -INFINITY) continue;
+    const float sw = __builtin_amdgcn_exp2f(s_m[w] - mx);
+    lt += sw * s_l[w];
+#pragma unroll
+    for (int j = 0; j < CW; ++j) o[j] += sw * s_o[w][lane + 64 * j];
+  }
+  const float inv = 1.f / lt;
   uint16_t* orow = reinterpret_cast<uint16_t*>(out + ((int64_t)m * Hq + hq) * (D * 2));
 #pragma unroll
-  for (int j = 0; j < D / 64; ++j) orow[lane + 64 * j] = (uint16_t)f32_to_bf16_bits(acc[j] * inv);
+  for (int j = 0; j < CW; ++j) orow[lane + 64 * j] = (uint16_t)f32_to_bf16_bits(o[j] * inv);
 }
 
 }  // namespace ckv
@@ -460,7 +508,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(char* __restrict__ out
 namespace ckv {
 
 #ifndef CKV_ATTN_GSPLIT
-#define CKV_ATTN_GSPLIT 6
+#define CKV_ATTN_GSPLIT 3
 #endif
 constexpr int kGroupedSplitTiles = CKV_ATTN_GSPLIT;  // cache tiles per split of a grouped launch
 
@@ -531,7 +579,8 @@ extern "C" int32_t ckv_attention_active(void* out, const void* q, int64_t q_head
                        q_token_stride * 2, (const char*)k_cache, (const char*)v_cache, kv_head_stride * 2, positions,
                        n_queries, n_tokens, n_q_heads, group, scale_log2, split_tiles, ws, err);
     if (ws != nullptr)
-      hipLaunchKernelGGL(combine, dim3((unsigned)n_queries, (unsigned)n_q_heads), dim3(64), 0, st, (char*)out, ws,
+      hipLaunchKernelGGL(combine, dim3((unsigned)n_queries, (unsigned)n_q_heads), dim3(kCombineWaves * 64), 0, st,
+                         (char*)out, ws,
                          n_queries, n_q_heads, splits);
   };
   // Queries that share KV heads and fit one workgroup's rows (decode): one workgroup per
