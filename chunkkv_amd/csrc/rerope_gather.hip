@@ -34,17 +34,29 @@ namespace ckv {
 #define CKV_GATHER_NT_STORE 1
 #endif
 
-// Workgroup shapes (threads, tokens per tile, row slots in flight per thread), measured on MI355X
-// at the Qwen2.5-7B KV shape (4 heads x 128, bf16). Dense gathers (every row of a segment):
-// 256 threads x 8 tokens, 2 slots. Gathers with a skip map, where a selection leaves about a
-// third of the rows out at scattered positions: 512 threads x 16 tokens, 1 slot (96 us against
-// 100 us for the dense shape on the 8k request's dropped rows of 26 layers).
+// Launch shapes (threads, tokens per tile, row slots in flight per thread, grid order), measured
+// on MI355X at the Qwen2.5-7B KV shape (4 heads x 128, bf16).
+//  - Tile-fastest grid (x = tile, y = segment): the workgroups in flight together stream
+//    neighbouring tiles of one segment. Dense gathers (every row of a segment): 256 threads x 8
+//    tokens x 2 slots. Gathers with a skip map (a selection leaves rows out at scattered
+//    positions): 512 x 16 x 1; the 8k request's dropped rows of 26 layers (24 segments) take
+//    95 us, against 112 us with the segment-fastest grid.
+//  - Segment-fastest grid (x = segment, y = tile), 256 x 16 x 4, for launches of 64 segments or
+//    more: the replay's 4 concurrent 32k requests (128 segments each) reach 75.0 % of HBM peak
+//    with it, 68.2 % with the tile-fastest shapes above.
 struct GatherDense {
   static constexpr int kThreads = 256, kTile = 8, kUnroll = 2;
+  static constexpr bool kSegFastest = false;
 };
 struct GatherSkip {
   static constexpr int kThreads = 512, kTile = 16, kUnroll = 1;
+  static constexpr bool kSegFastest = false;
 };
+struct GatherWide {
+  static constexpr int kThreads = 256, kTile = 16, kUnroll = 4;
+  static constexpr bool kSegFastest = true;
+};
+constexpr int kGatherWideSegs = 64;  // segment count from which GatherWide is used
 
 __device__ __forceinline__ vec16 gather_ld(const void* p) {
   if constexpr (CKV_GATHER_NT_LOAD) return ld16_stream(p);
@@ -55,10 +67,7 @@ __device__ __forceinline__ void gather_st(void* p, const vec16& v) {
   else st16(p, v);
 }
 
-// Grid: x = token tile (fastest), y = segment, z = layer. Workgroups are dispatched in that order,
-// so the ones in flight together stream neighbouring tiles of one segment (contiguous source and
-// destination rows) rather than one tile of many segments: 112 -> 96 us for the dropped rows of
-// the 8k request.
+// Grid: (tile, segment) in the order of S (x fastest), z = layer.
 template <int DTYPE, int D, class S>
 __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
     char* __restrict__ dst_k, char* __restrict__ dst_v, int64_t dst_layer_stride_b,
@@ -83,11 +92,11 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
   ckv_segment s = one_seg;
   if (segs != nullptr) {
     typedef __attribute__((address_space(1))) const int32_t gi32;
-    gi32* f = (gi32*)(segs + blockIdx.y);
+    gi32* f = (gi32*)(segs + (S::kSegFastest ? blockIdx.x : blockIdx.y));
     s = ckv_segment{f[0], f[1], f[2], f[3], f[4], f[5]};
   }
   const int layer = layer_begin + (int)blockIdx.z;
-  const int t0 = blockIdx.x * kGatherTile;
+  const int t0 = (int)(S::kSegFastest ? blockIdx.y : blockIdx.x) * kGatherTile;
   if (t0 >= s.n_tokens) return;  // uniform: tile past this segment's end
   if (s.dst_start < 0 || s.src_start < 0 || s.chunk < 0 || s.chunk >= n_chunks ||
       (int64_t)s.dst_start + s.n_tokens > n_tokens ||
@@ -210,11 +219,14 @@ static void launch_gather(char* dk, char* dv, int64_t ls_b, int64_t hs_b, const 
   auto go = [&](auto shape) {
     using S = decltype(shape);
     const unsigned tiles = (unsigned)((max_seg_tokens + S::kTile - 1) / S::kTile);
-    hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D, S>), dim3(tiles, (unsigned)n_segs, (unsigned)layer_count),
-                       dim3(S::kThreads), 0, st, dk, dv, ls_b, hs_b, tab, n_chunks, segs, one, one_k, one_v,
-                       one_hs_b, n_layers, layer_begin, n_heads, n_tokens, skip, theta, err);
+    const dim3 grid = S::kSegFastest ? dim3((unsigned)n_segs, tiles, (unsigned)layer_count)
+                                     : dim3(tiles, (unsigned)n_segs, (unsigned)layer_count);
+    hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D, S>), grid, dim3(S::kThreads), 0, st, dk, dv, ls_b, hs_b, tab,
+                       n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, layer_begin, n_heads, n_tokens, skip,
+                       theta, err);
   };
-  if (skip != nullptr) go(GatherSkip{});
+  if (n_segs >= kGatherWideSegs) go(GatherWide{});
+  else if (skip != nullptr) go(GatherSkip{});
   else go(GatherDense{});
 }
 
@@ -265,7 +277,8 @@ extern "C" int32_t ckv_rerope_gather_layers(void* dst_k, void* dst_v, int64_t ds
   if (dst_head_stride < (int64_t)n_tokens * head_dim || dst_layer_stride < dst_head_stride * n_heads)
     return CKV_ERR_OUT_OF_RANGE;
   if (n_segs == 0 || max_seg_tokens == 0 || layer_end == layer_begin) return CKV_OK;
-  if (n_segs > 65535 || layer_end - layer_begin > 65535) return CKV_ERR_TOO_LARGE;  // grid y and z
+  // grid y (tiles of the segment-fastest shape, segments below kGatherWideSegs) and z (layers)
+  if ((max_seg_tokens + 15) / 16 > 65535 || layer_end - layer_begin > 65535) return CKV_ERR_TOO_LARGE;
   const int64_t eb = elem_bytes(dtype);
   fn((char*)dst_k, (char*)dst_v, dst_layer_stride * eb, dst_head_stride * eb, src_tab, n_chunks, segs, ckv_segment{},
      0, 0, 0, n_segs, max_seg_tokens, n_layers, layer_begin, layer_end - layer_begin, n_heads, n_tokens, skip, theta, err,

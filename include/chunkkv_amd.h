@@ -120,7 +120,8 @@ int32_t ckv_inv_freq(float* out, int32_t head_dim, double theta, void* stream);
  *                (H, src_len, D) tensor of dtype `dtype`. n_chunks = table rows; a segment
  *                naming a chunk outside [0, n_chunks) is skipped and flagged.
  *   segs         n_segs device descriptors; max_seg_tokens >= every segs[i].n_tokens.
- *                n_segs and the layer count are at most 65535 (CKV_ERR_TOO_LARGE beyond).
+ *                max_seg_tokens is at most 1,048,560 and the layer count at most 65535
+ *                (CKV_ERR_TOO_LARGE beyond).
  *   Keys are re-rotated by delta (delta == 0 copies bit-for-bit); values are copied.
  * Destination rows covered by no segment are left untouched (the engine always overwrites
  * them with freshly computed rows).
