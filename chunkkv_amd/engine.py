@@ -391,17 +391,30 @@ class HipEngine(DecoderPieces):
         logits_from = N - 1 if logits_from is None else logits_from
         dev, H, D = self.device, self.n_kv, self.head_dim
 
+        tokens_np = np.asarray(tokens, dtype=np.int64).reshape(-1)
+        # When layer 0's active set is every position (no exact placement), the embedding and
+        # layer 0's input norm and q|k|v GEMM need nothing from the request plan: they go out
+        # first and run while the host builds the plan.
+        first = None
+        if config.full_first_layer and not any(getattr(p, "exact", False) for p in placements) or not placements:
+            tok_d = torch.from_numpy(tokens_np).to(dev)
+            h, x = self._norm(0, self.layers[0], self.inner.embed_tokens(tok_d[None]), None)
+            first = self._project(0, x)
+
         plan: RequestPlan = plan_request(N, placements, config.n_sink, config.recompute_ratio)
         select_layer = bool(placements) and config.full_first_layer and n_layers > 1
         active_np = plan.layer0_idx if config.full_first_layer else plan.fresh_idx
         local_np = local_index(N, active_np)
+        if first is not None and len(active_np) != N:
+            raise AssertionError("layer 0's active set is not every position")
 
         keepalive: list = []
         tab = np.zeros(0, dtype=np.uint64)
         if plan.chunks:
             tab = np.concatenate([self._chunk_pointers(c, keepalive).reshape(-1) for c in plan.chunks])
-        flags_d, local_d, active_d, segs_d, spans_d, tab_d = self._upload(
-            [plan.flags, local_np, active_np.astype(np.int64), plan.all_segments.reshape(-1), plan.spans.reshape(-1), tab]
+        flags_d, local_d, active_d, segs_d, spans_d, tab_d, tok_up = self._upload(
+            [plan.flags, local_np, active_np.astype(np.int64), plan.all_segments.reshape(-1), plan.spans.reshape(-1), tab,
+             tokens_np if first is None else tokens_np[:0]]
         )
         n_cached_segs = len(plan.segments)
 
@@ -414,7 +427,8 @@ class HipEngine(DecoderPieces):
         values_out = list(v_slab.unbind(0))
 
         active = active_d
-        h = self.inner.embed_tokens(torch.tensor([tokens], device=dev))[:, active]
+        if first is None:
+            h = self.inner.embed_tokens(tok_up[None])[:, active]
         ar = torch.arange(N, device=dev)
         masks: dict = {}
         sel = None
@@ -435,8 +449,11 @@ class HipEngine(DecoderPieces):
                 ready[0] = gather((0, n_layers), local_d)
         pending = None  # the previous layer's MLP output, when its residual add is deferred
         for li, layer in enumerate(self.layers):
-            h, x = self._norm(li, layer, h, pending)
-            q_in, k_in, v_in = self._project(li, x)
+            if li == 0 and first is not None:
+                q_in, k_in, v_in = first
+            else:
+                h, x = self._norm(li, layer, h, pending)
+                q_in, k_in, v_in = self._project(li, x)
             K, V = keys_out[li], values_out[li]
             if li == 1 and select_layer:
                 q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, table=tab, err=err)
