@@ -213,6 +213,50 @@ def test_rerope_gather_skip_map_uneven_selection(lens, pattern):
     np.testing.assert_array_equal(Vg, want_v)
 
 
+@pytest.mark.parametrize("bf16,D", [(True, 128), (False, 64)])
+def test_rerope_gather_many_segments(bf16, D):
+    """Launches of 64 or more segments take the segment-fastest launch shape: 80 ragged segments
+    (1-40 tokens), every layer without a skip map and layers 1-2 with one, against the oracle."""
+    rng = np.random.default_rng(640 + D)
+    n_layers, H = 3, 2
+    lens = [int(x) for x in rng.integers(1, 41, 80)]
+    N = sum(lens) + 5 * len(lens)
+    plan, ks, vs = _gather_case(rng, bf16, n_layers, H, D, lens, N, False)
+    assert len(plan.segments) >= 64
+    Kg, Vg, Ko, Vo, src = _run_gather(plan, ks, vs, n_layers, H, D, N, bf16)
+    np.testing.assert_array_equal(Vg, Vo)
+    rot = np.zeros(N, dtype=bool)
+    for s0, n, c, _s, _L, delta in plan.segments:
+        if delta != 0:
+            rot[s0 : s0 + n] = True
+    np.testing.assert_array_equal(Kg[:, :, ~rot], Ko[:, :, ~rot])
+    assert_keys_close(Kg[:, :, rot], Ko[:, :, rot], bf16)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    skip = np.where(rng.random(N) < 0.3, 0, -1).astype(np.int32)
+    tab = np.zeros((len(plan.chunks), n_layers, 2), dtype=np.uint64)
+    for ci, ch in enumerate(plan.chunks):
+        for l in range(n_layers):
+            tab[ci, l] = src[ch.idx][0][l].data_ptr(), src[ch.idx][1][l].data_ptr()
+    K = torch.full((n_layers, 1, H, N, D), -7.0, dtype=dt, device=DEV)
+    V = torch.full_like(K, -7.0)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.rerope_gather(K, V, torch.from_numpy(tab.view(np.int64)).to(DEV), dev(plan.segments.reshape(-1)),
+                      len(plan.segments), plan.max_seg_tokens, THETA, err, layers=(1, 3), skip=dev(skip))
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    Ks, Vs = host(K).reshape(n_layers, H, N, D), host(V).reshape(n_layers, H, N, D)
+    rows = np.flatnonzero(skip < 0)
+    sent = O.f32_to_bf16_bits(np.float32([-7.0]))[0] if bf16 else np.float32(-7.0)
+    for l in range(n_layers):
+        if l == 0:
+            assert (Ks[0] == sent).all() and (Vs[0] == sent).all()
+            continue
+        np.testing.assert_array_equal(Ks[l][:, rows], Kg[l][:, rows])
+        np.testing.assert_array_equal(Vs[l][:, rows], Vg[l][:, rows])
+        kept = np.flatnonzero(skip >= 0)
+        assert (Ks[l][:, kept] == sent).all() and (Vs[l][:, kept] == sent).all()
+
+
 def test_rerope_gather_config2_full_size():
     """Re-RoPE + gather at the Qwen2.5-7B KV shape: 28 layers, 4 heads, D=128, bf16,
     16 chunks x 256 tokens moved by delta ~ U[-4096, 4096] into a 4096-token cache."""
