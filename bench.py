@@ -622,9 +622,13 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         for i in range(max(warmup, 1)):
             dev_sel(i)
             scat(i)
-        g_dev, g_sc = _graph_of(lambda: dev_sel(0)), _graph_of(lambda: scat(0))  # small kernels: no launch overhead
-        t_dev = _timed(lambda i: g_dev.replay(), steps, stream)
-        t_sc = _timed(lambda i: g_sc.replay(), steps, stream)
+        # small kernels: REPS back-to-back repetitions per graph, so a replay's own launch cost is
+        # spread over them (what remains per repetition is the kernels' time and their gaps)
+        reps = 16
+        g_dev = _graph_of(lambda: [dev_sel(0) for _ in range(reps)])
+        g_sc = _graph_of(lambda: [scat(0) for _ in range(reps)])
+        t_dev = _timed(lambda i: g_dev.replay(), steps, stream) / reps
+        t_sc = _timed(lambda i: g_sc.replay(), steps, stream) / reps
         assert int(st["sel"].counts[0].item()) == plan.n_keep
         out[ratio] = dict(n_keep=plan.n_keep, dev_sel_ms=t_dev, scatter_ms=t_sc, scatter_bytes=plan.n_keep * ROW_BYTES * 4)
     dev_bytes = N * 4 * ROW_BYTES
