@@ -99,6 +99,7 @@ def test_attention_strided_query_view():
     (28, 4, 128, 8256, 1),  # decode: grouped rows (7 query heads of a KV head per workgroup)
     (28, 4, 128, 5000, 3),  # grouped, 21 rows
     (16, 2, 128, 777, 16),  # grouped, exactly one workgroup of rows (16 x 8), ragged last split
+    (14, 2, 64, 3001, 1),   # grouped at head_dim 64 (Qwen2.5-0.5B decode), ragged last tile
     (14, 2, 64, 3000, 40),  # 280 rows: token rows per query head, split
     (8, 8, 64, 3000, 2),    # no grouping (one query head per KV head): token rows, split
 ])
