@@ -8,12 +8,11 @@ shuffled positions (each chunk computed at its own original offset, so every pla
 its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
 
 A step is one request's whole KV repair with every input already resident in HBM, issued as
-HipEngine issues it (32 launches on two streams): layer 1's base cache gathered on the second
-stream while the first writes layer 0's fresh rows into its cache; the layer-1 deviation, the
-selection (2304 pooled + 96 sinks + 576 uncached = 2976 kept rows) and the scatter of the kept
-rows; then the gather of the cached rows of the 5280 dropped positions of layers 2-27 in one
-launch on the second stream while the first writes the fresh rows of layers 2-27 (disjoint rows;
-the streams join at the end). The fresh rows are written by ckv_rope_qkv as in the engine (k
+HipEngine issues it (32 launches in order on one stream): layer 1's base cache gathered, layer
+0's fresh rows written into its cache; the layer-1 deviation, the selection (2304 pooled + 96
+sinks + 576 uncached = 2976 kept rows) and the scatter of the kept rows; then the gather of the
+cached rows of the 5280 dropped positions of layers 2-27 in one launch, and the fresh rows of
+layers 2-27 (disjoint rows). The fresh rows are written by ckv_rope_qkv as in the engine (k
 rotated to its position, v copied, straight into the cache rows); the engine's launch also
 rotates q for the attention, which the step leaves out as the reference's KV-repair bytes do.
 The unit of work is one request's KV repair as the reference's op sequence moves it (re-RoPE +
@@ -25,8 +24,9 @@ deviation, the scatters of layers 1-27):
     scatter L1-27   27 x 2976 x 4096 B                                         =   329,121,792
     total                                                                      = 1,277,624,832
 `value` = that total / measured time per step (GB/s), the step replayed from a HIP graph (the
-eager time, launch-bound from Python, is reported as ms_per_step_eager, the same launches on one
-stream as ms_per_step_one_stream, and layers 0 and 2-27 built by one assemble launch each as
+eager time, launch-bound from Python, is reported as ms_per_step_eager, the same launches with
+both gathers on a second stream (HipEngine(overlap=True)) as ms_per_step_two_streams, and layers
+0 and 2-27 built by one assemble launch each as
 ms_per_step_assemble_variant); the fused flow itself moves 990,577,152 B per step
 (moved_bytes_per_step, moved_gbs). `roofline` is the dominant kernel (the gather of the dropped
 rows of layers 2-27, 562,298,880 B per launch) timed live with HIP events around a burst of
@@ -218,12 +218,13 @@ class RepairWorkload:
         ops.rope_qkv(None, k_in, v_in, pos, 0, N_KV, HEAD_DIM, THETA, k_out=self.k_slab[li], v_out=self.v_slab[li],
                      rows=pos, table=self.rope_tab, err=self.err)
 
-    def step(self, two_streams: bool = True):
-        """One request's KV repair as HipEngine issues it (32 launches). Layer 1's base cache is
-        gathered on a second stream while layer 0's fresh rows are written; then the layer-1
-        deviation, selection and scatter of the kept rows; then the gather of the dropped rows of
-        layers 2-27 on the second stream while the first writes those layers' fresh rows (the
-        two write disjoint rows). two_streams=False issues the same launches on one stream."""
+    def step(self, two_streams: bool = False):
+        """One request's KV repair as HipEngine issues it (32 launches, in order on one stream):
+        layer 1's base cache, layer 0's fresh rows, the layer-1 deviation, selection and scatter of
+        the kept rows, the gather of the dropped rows of layers 2-27, those layers' fresh rows.
+        two_streams=True issues the two gathers on a second stream instead, as
+        HipEngine(overlap=True) does (the base cache beside layer 0's rows, the dropped rows beside
+        the fresh rows of layers 2-27: disjoint rows)."""
         from chunkkv_amd import ops
 
         plan = self.plan
@@ -253,9 +254,9 @@ class RepairWorkload:
         if two_streams:
             main.wait_stream(self.side)
 
-    def step_serial(self):
-        """The same launches on one stream."""
-        self.step(two_streams=False)
+    def step_two_streams(self):
+        """The same launches with the gathers on a second stream."""
+        self.step(two_streams=True)
 
     def step_assemble(self):
         """Layer 0 and layers 2-27 with one assemble launch each (every row written once, fresh
@@ -323,27 +324,27 @@ def _graph_of(fn):
 
 
 def bench_repair(steps: int, warmup: int, dev) -> dict:
-    """Time the KV-repair step as HipEngine issues it (32 launches on two streams, captured once
+    """Time the KV-repair step as HipEngine issues it (32 launches on one stream, captured once
     per input set in a HIP graph and replayed; the eager time, launch-bound from Python, the
-    one-stream issue of the same launches and the assemble-per-layer variant are reported too),
+    two-stream issue of the same launches and the assemble-per-layer variant are reported too),
     and the dominant kernel (the gather of the dropped rows of layers 2..27) from a burst of
     back-to-back launches."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
     for i in range(max(warmup, 2)):
         wls[i % 2].step()
-        wls[i % 2].step_serial()
+        wls[i % 2].step_two_streams()
         wls[i % 2].step_assemble()
     torch.cuda.synchronize()
     graphs = [_graph_of(w.step) for w in wls]
-    serial = [_graph_of(w.step_serial) for w in wls]
+    two = [_graph_of(w.step_two_streams) for w in wls]
     asm_graphs = [_graph_of(w.step_assemble) for w in wls]
     stream = torch.cuda.current_stream(dev)
-    for g in graphs + serial + asm_graphs:
+    for g in graphs + two + asm_graphs:
         g.replay()
     ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
-    ms_serial = _timed(lambda i: serial[i % 2].replay(), steps, stream)
+    ms_two = _timed(lambda i: two[i % 2].replay(), steps, stream)
     ms_asm = _timed(lambda i: asm_graphs[i % 2].replay(), steps, stream)
-    for w in wls:  # the selection state of the two-stream step again
+    for w in wls:  # the selection state of the one-stream step again
         w.step()
     ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
     gd_ms = _timed(lambda i: wls[i % 2].gather_dropped(), steps, stream)
@@ -356,7 +357,7 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     nbytes = repair_bytes(n_keep)
     gd_bytes = dropped_bytes(plan)
     ms_conc = _concurrent_steps(wls, steps, dev)
-    return dict(ms_per_step=ms, ms_serial=ms_serial, ms_asm=ms_asm, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(plan),
+    return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
                 asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep, ms_conc=ms_conc,
                 conc_gbs=CONCURRENT * nbytes / (ms_conc * 1e-3) / 1e9)
@@ -378,7 +379,7 @@ def _concurrent_steps(wls, steps: int, dev) -> float:
         for w, st in zip(reqs, streams):
             st.wait_stream(main)
             with torch.cuda.stream(st):
-                w.step_serial()
+                w.step()
         for st in streams:
             main.wait_stream(st)
 
@@ -388,7 +389,7 @@ def _concurrent_steps(wls, steps: int, dev) -> float:
     g.replay()
     ms = _timed(lambda i: g.replay(), steps, torch.cuda.current_stream(dev))
     assert all(int(w.err.item()) == 0 for w in reqs)
-    for w in wls:  # leave the two-stream step's selection state as it was
+    for w in wls:  # leave the step's selection state as it was
         w.step()
     torch.cuda.synchronize()
     return ms
@@ -1030,8 +1031,8 @@ def main() -> None:
         return
 
     r = bench_repair(args.steps, args.warmup, dev)
-    log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_serial']:.3f} ms one "
-        f"stream, {r['ms_asm']:.3f} ms assemble variant, {r['ms_eager']:.3f} ms eager); dropped-row gather "
+    log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_two']:.3f} ms two "
+        f"streams, {r['ms_asm']:.3f} ms assemble variant, {r['ms_eager']:.3f} ms eager); dropped-row gather "
         f"{r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
         f"assemble {r['asm_gbs']:.1f} GB/s ({r['asm_ms'] * 1e3:.2f} us)")
     ttft = bench_ttft(args.ttft_requests, dev) if args.ttft_requests > 0 else None
@@ -1064,7 +1065,7 @@ def main() -> None:
         },
         "pct_of_peak": round(100.0 * r["gbs"] / PEAK_GBS, 2),
         "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
-        "ms_per_step_one_stream": round(r["ms_serial"], 4),
+        "ms_per_step_two_streams": round(r["ms_two"], 4),
         "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
         "concurrent_requests": {"requests": CONCURRENT, "ms_per_round": round(r["ms_conc"], 4),
                                 "gbs": round(r["conc_gbs"], 1), "pct_of_peak": round(100.0 * r["conc_gbs"] / PEAK_GBS, 2),

@@ -15,15 +15,17 @@ the fresh-token RoPE and the attention run on the HIP kernels:
                                                        positions (layer 1: into tensors, for the
                                                        deviation; its kept rows then go through
                                                        ckv_scatter_rows)
-  base_kv (:96-103; ~13 launches per placement and   ckv_rerope_gather_layers, on a side stream:
-    layer, zero-filled cache, every layer)             at the start, layer 1's base cache (and
-                                                       layer 0's rows of exact placements);
+  base_kv (:96-103; ~13 launches per placement and   ckv_rerope_gather_layers (overlap=True: on
+    layer, zero-filled cache, every layer)             a side stream): at the start, layer 1's
+                                                       base cache (and layer 0's rows of exact
+                                                       placements);
                                                        right after the selection, one launch for
                                                        the cached rows of every position the
                                                        selection dropped, layers 2..L-1 at once.
                                                        Rows the fresh K/V overwrite are never
-                                                       gathered; the main stream waits only
-                                                       before the attention that reads them
+                                                       gathered; with the side stream the main
+                                                       stream waits only before the attention
+                                                       that reads them
   deviation (:117-124)                               ckv_deviation (one wavefront per token)
   rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
     one .item() per chunk)                             nothing back unless a threshold is set
@@ -71,12 +73,14 @@ _TORCH_OF = {
 
 
 class HipEngine(DecoderPieces):
-    def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = True):
+    def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = False):
         if attention not in ("fused", "reference"):
             raise ValueError("attention must be 'fused' or 'reference'")
         self.attention = attention
-        # overlap=False issues the cached-row gathers on the main stream, in order, instead of on
-        # a side stream (same launches, same rows).
+        # overlap=True issues the cached-row gathers on a side stream, joined by events where a
+        # layer needs its rows, instead of in order on the main stream (same launches, same rows).
+        # Off by default: on MI355X the side stream did not shorten the 8k request's TTFT (42.47 vs
+        # 42.38 ms p50) and it lengthens the KV-repair launches' own span (0.320 vs 0.314 ms).
         self.overlap = overlap
         self._side: torch.cuda.Stream | None = None
         self._rope_tab: torch.Tensor | None = None  # (cos, sin) per position, grown on demand
@@ -436,7 +440,7 @@ class HipEngine(DecoderPieces):
         tab = self._table(N)
         gather = lambda layers, skip: self._gather(  # noqa: E731
             k_slab, v_slab, tab_d, segs_d, n_cached_segs, plan.max_seg_tokens, layers, skip, err)
-        # Cached rows that do not depend on the model go out first, overlapped with layer 0:
+        # Cached rows that do not depend on the model go out first (overlap=True: beside layer 0):
         # with the selection, layer 0's rows outside its active set (exact placements) and layer
         # 1's base cache (every cached row); without it, every layer's rows outside the one
         # active set. Layers 2.. follow right after the selection.

@@ -120,8 +120,8 @@ def test_side_stream_and_one_stream_builds_identical(models, parts, ratio):
     """Layers 2..L-1 built by the side-stream gather of dropped rows + per-layer scatters, or by
     one assemble launch per layer on the main stream: the same caches, bit for bit."""
     _, gpu = models
-    a = HipEngine(gpu, StubTokenizer())
-    b = HipEngine(gpu, StubTokenizer(), overlap=False)
+    a = HipEngine(gpu, StubTokenizer(), overlap=True)
+    b = HipEngine(gpu, StubTokenizer())
     assert a.overlap and not b.overlap
     toks2, pl = _swap_setup(a, parts)
     cfg = BlendConfig(recompute_ratio=ratio, n_sink=4)
