@@ -41,6 +41,16 @@ __device__ __forceinline__ uint32_t dev_key(float f) {
 
 __device__ __forceinline__ bool bit_of(const uint32_t* w, int p) { return (w[p >> 5] >> (p & 31)) & 1u; }
 
+// Workgroup barrier that orders LDS only: waits for this wavefront's LDS operations (lgkmcnt 0),
+// not for its global loads and stores, which __syncthreads() would also drain. Values loaded
+// from global memory are still waited for where they are used.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt at their maxima (no wait)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Exclusive prefix count of `pred` over the workgroup in thread order, plus the total.
 __device__ __forceinline__ int block_excl_count(bool pred, int* wave_tot, int& total) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
     int has_thr, double thr, int64_t* __restrict__ keep_abs, int64_t* __restrict__ keep_local,
     int32_t* __restrict__ keep_rank, float* __restrict__ rel_out, uint8_t* __restrict__ esc_out,
     int32_t* __restrict__ counts) {
-  static_assert(KPT <= 64, "per-thread position bits live in one 64-bit word");
+  static_assert(KPT <= 33, "a run of KPT positions spans at most two mask words and one 64-bit word");
   constexpr int kBatch = 8;            // chunk-sum loads in flight per lane
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
   __shared__ uint32_t hist[2][kSelWaves][256];
@@ -281,7 +291,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
   }
   for (int w = tid; w < 2 * W; w += kSelThreads) masks[w] = 0u;
   for (int b = tid; b < 2 * kSelWaves * 256; b += kSelThreads) (&hist[0][0][0])[b] = 0u;
-  __syncthreads();
+  lds_barrier();  // the loads above stay in flight
 
   // Phase 1: per-chunk rel / escalation / budget, one wavefront per chunk, summed in the
   // contract's order (lane-strided, ascending, then the xor butterfly).
@@ -329,18 +339,27 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(
       if (lane == 0) atomicAdd(&s_budget_req, sp.budget);
     }
   }
-  __syncthreads();
+  lds_barrier();  // the rel/escalation stores above need no acknowledgement here
 
   // Phase 2: keep = ~cached | sink | escalated span; candidates = pooled span minus keep.
+  // The run [p0, p0 + KPT) lies in mask words p0 / 32 and p0 / 32 + 1 ((p0 % 32) + KPT <= 64):
+  // two reads per mask, bit i of the shifted window is position p0 + i.
+  uint64_t esc_bits = 0u, pool_bits = 0u;
+  if (p0 < n_tokens) {
+    const int w0 = p0 >> 5;
+    const bool two = w0 + 1 < W;
+    esc_bits = ((uint64_t)escw[w0] | (two ? (uint64_t)escw[w0 + 1] << 32 : 0ull)) >> (p0 & 31);
+    pool_bits = ((uint64_t)poolw[w0] | (two ? (uint64_t)poolw[w0 + 1] << 32 : 0ull)) >> (p0 & 31);
+  }
   uint64_t cand = 0u, kept_static = 0u;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     const int p = p0 + i;
     if (p < n_tokens) {
       const uint32_t f = (fl[i / 4] >> (8 * (i % 4))) & 0xffu;
-      const bool k = !(f & CKV_POS_CACHED) || (f & CKV_POS_SINK) || bit_of(escw, p);
+      const bool k = !(f & CKV_POS_CACHED) || (f & CKV_POS_SINK) || ((esc_bits >> i) & 1u);
       kept_static |= (uint64_t)k << i;
-      if (!k && bit_of(poolw, p)) cand |= 1ull << i;
+      if (!k && ((pool_bits >> i) & 1u)) cand |= 1ull << i;
     }
   }
   int n_cand = 0;
