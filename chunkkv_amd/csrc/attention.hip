@@ -425,10 +425,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_active_kernel(
     for (int dt = 0; dt < DT; ++dt) {
       unsigned w[2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const unsigned lo = f32_to_bf16_bits(o[qg][dt][2 * h] * inv), hi = f32_to_bf16_bits(o[qg][dt][2 * h + 1] * inv);
-        w[h] = lo | (hi << 16);
-      }
+      for (int h = 0; h < 2; ++h) w[h] = f32x2_to_bf16x2_bits(o[qg][dt][2 * h] * inv, o[qg][dt][2 * h + 1] * inv);
       *(uint2*)(orow + (dt * 16 + 4 * g) * 2) = uint2{w[0], w[1]};
     }
   }

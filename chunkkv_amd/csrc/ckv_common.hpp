@@ -18,14 +18,23 @@ typedef unsigned int vec16 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16 round-to-nearest-even; NaN becomes the canonical quiet NaN 0x7fc0, which is
+// Two fp32 -> bf16, round-to-nearest-even, packed (lo in bits 0-15): gfx950's packed hardware
+// conversion (v_cvt_pk_bf16_f32), which rounds every non-NaN input (denormals, ties, overflow
+// to infinity) exactly as adding 0x7fff + lsb to the bit pattern and truncating does, checked
+// over all 2^32 inputs in both slots; a NaN becomes the canonical quiet NaN 0x7fc0, which is
 // what torch's BFloat16 conversion produces.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
+typedef float f32x2_cvt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  const f32x2_cvt v = {lo, hi};
+  uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_cvt));
+  r = lo != lo ? (r & 0xffff0000u) | 0x7fc0u : r;
+  r = hi != hi ? (r & 0x0000ffffu) | 0x7fc00000u : r;
+  return r;
 }
+
+// fp32 -> bf16 bits, round-to-nearest-even, NaN -> 0x7fc0.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return f32x2_to_bf16x2_bits(f, 0.0f) & 0xffffu; }
 
 // Element traits: VEC elements per 16-byte vector, unpack to fp32, pack with rounding.
 template <int DTYPE>
@@ -46,7 +55,7 @@ struct Elem<CKV_DTYPE_BF16> {
   __device__ __forceinline__ static vec16 pack(const float (&f)[kVec]) {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = f32_to_bf16_bits(f[2 * i]) | (f32_to_bf16_bits(f[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) w[i] = f32x2_to_bf16x2_bits(f[2 * i], f[2 * i + 1]);
     return vec16{w[0], w[1], w[2], w[3]};
   }
   // value after rounding to the element type, back in fp32
