@@ -72,6 +72,46 @@ _TORCH_OF = {
 }
 
 
+def _adjacent_rows(ts: list[torch.Tensor]) -> torch.Tensor | None:
+    """The tensors as one (sum of rows, ...) view when they already lie back to back in one
+    storage (contiguous, same dtype and trailing shape), else None."""
+    t0 = ts[0]
+    if not all(t.is_contiguous() and t.dtype == t0.dtype and t.shape[1:] == t0.shape[1:] and t.device == t0.device
+               and t.untyped_storage().data_ptr() == t0.untyped_storage().data_ptr() for t in ts):
+        return None
+    for a, b in zip(ts, ts[1:]):
+        if b.data_ptr() != a.data_ptr() + a.numel() * a.element_size():
+            return None
+    rows = sum(t.shape[0] for t in ts)
+    return t0.new_empty(0).set_(t0.untyped_storage(), t0.storage_offset(), (rows, *t0.shape[1:]),
+                                (t0.stride(0), *t0.stride()[1:]) if t0.dim() > 1 else (1,))
+
+
+def _stack_params(mods: list, name: str) -> torch.Tensor | None:
+    """getattr(m, name) of the given modules stacked along dim 0, stored once: the modules'
+    parameters are re-pointed at their rows of the stacked tensor (so the model keeps working and
+    its weights are not held twice). Modules without the parameter get zero rows in the stack;
+    None when no module has it. Weights that already lie back to back (a previous stacking of
+    the same model) are viewed, not copied."""
+    ps = [getattr(m, name) for m in mods]
+    if all(p is None for p in ps):
+        return None
+    if all(p is not None for p in ps):
+        view = _adjacent_rows([p.data for p in ps])
+        if view is not None:
+            return view
+    ref = next(p for p in ps if p is not None)
+    parts = [p.data if p is not None else ref.new_zeros((m.weight.shape[0], *ref.shape[1:])) for p, m in zip(ps, mods)]
+    stacked = torch.cat(parts, 0).contiguous()
+    row = 0
+    for m, p, part in zip(mods, ps, parts):
+        n = part.shape[0]
+        if p is not None:
+            setattr(m, name, torch.nn.Parameter(stacked[row : row + n], requires_grad=p.requires_grad))
+        row += n
+    return stacked
+
+
 class HipEngine(DecoderPieces):
     def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = False):
         if attention not in ("fused", "reference"):
@@ -98,17 +138,16 @@ class HipEngine(DecoderPieces):
         self.inv_freq = ops.inv_freq(self.head_dim, self.theta, self.device)
         # ckv_attention_active covers bf16 caches with head_dim 64 or 128; other models keep SDPA
         self._native_attention = self.kv_dtype == torch.bfloat16 and self.head_dim in (64, 128)
-        # One projection GEMM per layer for q, k and v (their weights stacked once, here); its
-        # token-major output feeds ckv_rope_qkv directly.
+        # One projection GEMM per layer for q, k and v (their weights stacked once, here; the
+        # model's own q/k/v parameters become row views of the stack); its token-major output
+        # feeds ckv_rope_qkv directly.
         self._w_qkv, self._b_qkv = [], []
         with torch.no_grad():
             for layer in self.layers:
                 a = layer.self_attn
-                self._w_qkv.append(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0).contiguous())
-                biases = [a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]
-                self._b_qkv.append(None if all(b is None for b in biases) else torch.cat(
-                    [b if b is not None else torch.zeros(w.shape[0], dtype=w.dtype, device=w.device)
-                     for b, w in zip(biases, (a.q_proj.weight, a.k_proj.weight, a.v_proj.weight))]))
+                lin = [a.q_proj, a.k_proj, a.v_proj]
+                self._w_qkv.append(_stack_params(lin, "weight"))
+                self._b_qkv.append(_stack_params(lin, "bias"))
         # The elementwise steps between the GEMMs (residual adds, RMSNorms, the SiLU-gated product)
         # run as ckv_add_rmsnorm / ckv_silu_mul for RMSNorm + SiLU-MLP models; the MLP's output is
         # then added by the next norm (or the final one) instead of right away.
@@ -120,15 +159,14 @@ class HipEngine(DecoderPieces):
             self._norm_final = norm(self.inner.norm)
             # gate and up as one GEMM per layer (weights stacked once, here): one launch of twice
             # the width fills the CUs better than two at the prefill shapes; ckv_silu_mul reads
-            # the two halves of its output in place.
+            # the two halves of its output in place. As for q|k|v, the model's gate/up parameters
+            # become row views of the stack, so the weights are held once.
             self._w_gu, self._b_gu = [], []
             with torch.no_grad():
                 for layer in self.layers:
-                    g, u = layer.mlp.gate_proj, layer.mlp.up_proj
-                    self._w_gu.append(torch.cat([g.weight, u.weight], 0).contiguous())
-                    self._b_gu.append(None if g.bias is None and u.bias is None else torch.cat(
-                        [m.bias if m.bias is not None else torch.zeros(m.out_features, dtype=m.weight.dtype,
-                                                                       device=m.weight.device) for m in (g, u)]))
+                    lin = [layer.mlp.gate_proj, layer.mlp.up_proj]
+                    self._w_gu.append(_stack_params(lin, "weight"))
+                    self._b_gu.append(_stack_params(lin, "bias"))
 
     _RMSNORMS = ("Qwen2RMSNorm", "LlamaRMSNorm", "MistralRMSNorm")
 
@@ -473,6 +511,7 @@ class HipEngine(DecoderPieces):
                     if int(counts[_native.COUNT_UNCOMPUTED]) > 0:
                         raise AssertionError("selected a token that was never computed")
                     n_keep = int(counts[_native.COUNT_KEEP])
+                n_keep_used = n_keep
                 if self.trace is not None:
                     self.trace.update(k=k, v=v, K=K.clone(), V=V.clone(), flags=flags_d, local=local_d, spans=spans_d,
                                       diff=diff, norm=norm, sel=sel, n_keep=n_keep)
@@ -508,6 +547,11 @@ class HipEngine(DecoderPieces):
             counts = sel.counts.cpu()
             if int(counts[_native.COUNT_UNCOMPUTED]) > 0:
                 raise AssertionError("selected a token that was never computed")
+            # Without a device read-back the layers after the selection used the host plan's n_keep:
+            # the kernel's own count must agree, or the rows sliced above were the wrong ones.
+            if int(counts[_native.COUNT_KEEP]) != n_keep_used:
+                raise AssertionError(f"selection kept {int(counts[_native.COUNT_KEEP])} tokens, the plan "
+                                     f"{n_keep_used}")
             selected_cached = int(counts[_native.COUNT_SELECTED_CACHED])
             for (s, L, _, _), r, e in zip(plan.spans.tolist(), sel.rel_dev.cpu().tolist(), sel.escalated.cpu().tolist()):
                 chunk_stats.append({"start": s, "length": L, "rel_dev": r, "escalated": bool(e)})

@@ -397,6 +397,36 @@ def test_select_planted_ties_and_escalation(seed):
     _check_select(diff, norm, flags, local, spans, thr)
 
 
+@pytest.mark.parametrize("N_chunks", [4, 40, 130])
+def test_select_nan_candidates_rank_after_finite(N_chunks):
+    """A budget that reaches past the finite candidates into NaN ones. The kernels' rule: NaN
+    ranks below every finite deviation (0 included) and NaN candidates are taken lowest index
+    first, so every finite candidate is kept, then the lowest-index NaN candidates. (The
+    reference's argsort(-where(cand, diff, -1)) would instead reach the non-candidates' +1
+    entries before any NaN, in an unstable order, and keep arbitrary non-candidates.)"""
+    rng = np.random.default_rng(77 + N_chunks)
+    L = 64
+    N = N_chunks * L + 16
+    flags, spans = _spans(N_chunks, L, 0.9, 4, N)  # budget 58 of 60 candidates per chunk
+    diff = rng.gamma(2.0, 1.0, N).astype(np.float32)
+    cand = np.zeros(N, dtype=bool)
+    for s0, ln, _, _ in spans:
+        cand[s0 + 4 : s0 + ln] = True
+    cand_pos = np.flatnonzero(cand)
+    nan_pos = np.sort(rng.choice(cand_pos, 5 * N_chunks, replace=False))
+    diff[nan_pos] = np.nan
+    diff[rng.choice(np.setdiff1d(cand_pos, nan_pos), N_chunks, replace=False)] = 0.0
+    norm = (np.nan_to_num(diff) + 1).astype(np.float32)
+    local = np.arange(N, dtype=np.int32)
+    want = _check_select(diff, norm, flags, local, spans, None)
+    budget = int(want["counts"][2])
+    n_finite = int(cand.sum()) - len(nan_pos)
+    assert budget > n_finite  # the budget reaches into the NaN candidates
+    kept = set(want["keep_abs"].tolist())
+    assert set(np.setdiff1d(cand_pos, nan_pos).tolist()) <= kept
+    assert [p for p in nan_pos.tolist() if p in kept] == nan_pos[: budget - n_finite].tolist()
+
+
 @pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 1023, 1024, 1025, 8256, 33792, 33793, 131072])
 def test_select_sizes(N):
     rng = np.random.default_rng(N)
