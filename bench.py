@@ -180,6 +180,9 @@ class RepairWorkload:
             torch.randn((1, N_TOKENS if li == 0 else plan.n_keep, N_KV * HEAD_DIM), generator=gen).to(torch.bfloat16)
             .to(dev) for _ in range(2)) for li in range(N_LAYERS)]
         self.sel = None
+        self.ws = ops.deviation_select_workspace(dev)
+        self.dn = (torch.empty(N_TOKENS, dtype=torch.float32, device=dev),
+                   torch.empty(N_TOKENS, dtype=torch.float32, device=dev))
         self.side = torch.cuda.Stream(device=dev)  # default priority
         # the engine's per-position (cos, sin) table, built once per engine (not per request)
         self.rope_tab = ops.rope_table(N_TOKENS, HEAD_DIM, THETA, dev)
@@ -243,16 +246,38 @@ class RepairWorkload:
         self.kv_rows(0)
         if two_streams:
             main.wait_stream(self.side)
-        k1, v1 = self.fresh[1]
-        diff, norm = ops.deviation(k1, v1, K[1], V[1], self.flags, self.local, self.err)
-        self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
-        ops.scatter_rows(K[1], V[1], k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep], self.sel.keep_abs[: plan.n_keep],
-                         self.err)
+        self.layer1()
         fork(self.gather_dropped)
         for li in range(2, N_LAYERS):
             self.kv_rows(li)
         if two_streams:
             main.wait_stream(self.side)
+
+    fused_select = False  # as HipEngine: deviation and selection as two launches by default
+
+    def layer1(self):
+        """Layer 1 after its base cache: the deviation and the selection (two launches, or one
+        with fused_select), then the kept rows compacted and scattered into the cache."""
+        from chunkkv_amd import ops
+
+        n = self.plan.n_keep
+        K, V = self.k_slab[1], self.v_slab[1]
+        k1, v1 = self.fresh[1]
+        if self.fused_select:
+            _, _, self.sel = ops.deviation_select(k1, v1, K, V, self.flags, self.local, self.spans, None, self.ws,
+                                                  self.err, self.sel, self.dn)
+        else:
+            diff, norm = ops.deviation(k1, v1, K, V, self.flags, self.local, self.err)
+            self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
+        ops.scatter_kept_rows(K, V, k1, v1, self.sel.keep_abs[:n], self.sel.keep_local[:n], self.err)
+
+    def step_fused_select(self):
+        """The step with the layer-1 deviation and selection in one launch (ckv_deviation_select)."""
+        self.fused_select = True
+        try:
+            self.step()
+        finally:
+            self.fused_select = False
 
     def step_two_streams(self):
         """The same launches with the gathers on a second stream."""
@@ -274,11 +299,7 @@ class RepairWorkload:
         self.assemble(0)
         ops.assemble_layer(K[1], V[1], self.tab, N_LAYERS, 1, self.segs_all, len(plan.segments), plan.max_seg_tokens,
                            None, None, None, THETA, self.err)
-        k1, v1 = self.fresh[1]
-        diff, norm = ops.deviation(k1, v1, K[1], V[1], self.flags, self.local, self.err)
-        self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
-        ops.scatter_rows(K[1], V[1], k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep], self.sel.keep_abs[: plan.n_keep],
-                         self.err)
+        self.layer1()
 
 
 def repair_bytes(n_keep: int) -> int:
@@ -335,15 +356,20 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
         wls[i % 2].step_two_streams()
         wls[i % 2].step_assemble()
     torch.cuda.synchronize()
+    for w in wls:
+        w.step_fused_select()
+    torch.cuda.synchronize()
     graphs = [_graph_of(w.step) for w in wls]
     two = [_graph_of(w.step_two_streams) for w in wls]
     asm_graphs = [_graph_of(w.step_assemble) for w in wls]
+    fused = [_graph_of(w.step_fused_select) for w in wls]
     stream = torch.cuda.current_stream(dev)
-    for g in graphs + two + asm_graphs:
+    for g in graphs + two + asm_graphs + fused:
         g.replay()
     ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
     ms_two = _timed(lambda i: two[i % 2].replay(), steps, stream)
     ms_asm = _timed(lambda i: asm_graphs[i % 2].replay(), steps, stream)
+    ms_fused = _timed(lambda i: fused[i % 2].replay(), steps, stream)
     for w in wls:  # the selection state of the one-stream step again
         w.step()
     ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
@@ -357,7 +383,8 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     nbytes = repair_bytes(n_keep)
     gd_bytes = dropped_bytes(plan)
     ms_conc = _concurrent_steps(wls, steps, dev)
-    return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_eager=ms_eager, bytes=nbytes, moved=moved_bytes(plan),
+    return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_fused=ms_fused, ms_eager=ms_eager, bytes=nbytes,
+                moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
                 asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep, ms_conc=ms_conc,
                 conc_gbs=CONCURRENT * nbytes / (ms_conc * 1e-3) / 1e9)
@@ -583,65 +610,78 @@ def bench_gather_only(steps: int, warmup: int, dev) -> dict:
         _rooffor("rerope_gather_kernel<bf16,128>", nbytes, ms))
 
 
+DEV_SETS = 16  # config-3 input sets rotated per graph replay: 16 x 50 MB > 512 MB, past the 256 MB MALL
+
+
 def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
     """Deviation + pooled top-k + scatter microbenchmark: layer-1 fresh vs cached K/V for 32 chunks
     x 256 tokens (8192), 4 heads x 128, bf16; cached = fresh + sigma_c N(0,1), sigma_c ~
-    lognormal(-3, 1); pooled top-k at 15/30/50% plus 4 sinks per chunk, then the scatter of the
-    kept rows into one layer's cache."""
+    lognormal(-3, 1); pooled top-k at 15/30/50% plus 4 sinks per chunk (ckv_deviation_select, one
+    launch), then the kept rows compacted and scattered into the layer's cache
+    (ckv_scatter_kept_rows). DEV_SETS independent input sets (33.6 MB of K/V read and the kept
+    rows written per set, ~800 MB in all) are cycled through inside each graph replay, so every
+    launch reads HBM rather than the 256 MB MALL."""
     from chunkkv_amd import ops
     from chunkkv_amd.planner import local_index, plan_request
 
     N, C, L = 8192, 32, 256
-    gen = torch.Generator().manual_seed(3)
-    fk = torch.randn((1, N_KV, N, HEAD_DIM), generator=gen)
-    fv = torch.randn((1, N_KV, N, HEAD_DIM), generator=gen)
-    sigma = torch.exp(torch.randn(C, generator=gen) - 3.0).repeat_interleave(L)[None, None, :, None]
-    K = (fk + sigma * torch.randn(fk.shape, generator=gen)).bfloat16().to(dev)
-    V = (fv + sigma * torch.randn(fv.shape, generator=gen)).bfloat16().to(dev)
-    k = fk.bfloat16().to(dev)
-    v = fv.bfloat16().transpose(1, 2).contiguous().to(dev).transpose(1, 2)
+    g = torch.Generator(device=dev).manual_seed(3)
+    sets = []
+    for _ in range(DEV_SETS):
+        fk = torch.randn((1, N_KV, N, HEAD_DIM), generator=g, device=dev)
+        fv = torch.randn((1, N_KV, N, HEAD_DIM), generator=g, device=dev)
+        sigma = torch.exp(torch.randn(C, generator=g, device=dev) - 3.0).repeat_interleave(L)[None, None, :, None]
+        K = (fk + sigma * torch.randn(fk.shape, generator=g, device=dev)).bfloat16()
+        V = (fv + sigma * torch.randn(fv.shape, generator=g, device=dev)).bfloat16()
+        v = fv.bfloat16().transpose(1, 2).contiguous().transpose(1, 2)  # token-major, as v_proj leaves it
+        sets.append(dict(k=fk.bfloat16(), v=v, K=K, V=V, Kd=torch.empty_like(K), Vd=torch.empty_like(V),
+                         ws=ops.deviation_select_workspace(dev)))
     pl = [Place(Chunk(torch.empty((1, 1, N_KV, L, HEAD_DIM)), torch.empty((1, 1, N_KV, L, HEAD_DIM)), 0), c * L)
           for c in range(C)]
     out = {}
     stream = torch.cuda.current_stream(dev)
     for ratio in (0.15, 0.30, 0.50):
         plan = plan_request(N, pl, N_SINK, ratio)
+        n = plan.n_keep
         flags = torch.from_numpy(plan.flags).to(dev)
         local = torch.from_numpy(local_index(N, plan.layer0_idx)).to(dev)
         spans = torch.from_numpy(plan.spans.reshape(-1)).to(dev)
-        Kd, Vd = K.clone(), V.clone()
-        st = {}
+        sels = [None] * DEV_SETS
+        dns = [(torch.empty(N, device=dev), torch.empty(N, device=dev)) for _ in range(DEV_SETS)]
 
         def dev_sel(i):
-            d, n = ops.deviation(k, v, K, V, flags, local)
-            st["sel"] = ops.select(d, n, flags, local, spans, None, st.get("sel"))
+            st = sets[i]
+            sels[i] = ops.deviation_select(st["k"], st["v"], st["K"], st["V"], flags, local, spans, None, st["ws"],
+                                           out=sels[i], diff_norm=dns[i])[2]
 
         def scat(i):
-            rows = st["sel"].keep_abs[: plan.n_keep]
-            ops.scatter_rows(Kd, Vd, k[:, :, : plan.n_keep], v[:, :, : plan.n_keep], rows)
+            st = sets[i]
+            ops.scatter_kept_rows(st["Kd"], st["Vd"], st["k"], st["v"], sels[i].keep_abs[:n], sels[i].keep_local[:n])
 
-        for i in range(max(warmup, 1)):
+        for i in range(DEV_SETS):
             dev_sel(i)
             scat(i)
-        # small kernels: REPS back-to-back repetitions per graph, so a replay's own launch cost is
-        # spread over them (what remains per repetition is the kernels' time and their gaps)
-        reps = 16
-        g_dev = _graph_of(lambda: [dev_sel(0) for _ in range(reps)])
-        g_sc = _graph_of(lambda: [scat(0) for _ in range(reps)])
-        t_dev = _timed(lambda i: g_dev.replay(), steps, stream) / reps
-        t_sc = _timed(lambda i: g_sc.replay(), steps, stream) / reps
-        assert int(st["sel"].counts[0].item()) == plan.n_keep
-        out[ratio] = dict(n_keep=plan.n_keep, dev_sel_ms=t_dev, scatter_ms=t_sc, scatter_bytes=plan.n_keep * ROW_BYTES * 4)
-    dev_bytes = N * 4 * ROW_BYTES
+        # one graph = every input set once (DEV_SETS launches back to back: a replay's own launch
+        # cost is spread over them; what remains per launch is the kernel's time and its gaps)
+        g_dev = _graph_of(lambda: [dev_sel(i) for i in range(DEV_SETS)])
+        g_sc = _graph_of(lambda: [scat(i) for i in range(DEV_SETS)])
+        g_both = _graph_of(lambda: [(dev_sel(i), scat(i)) for i in range(DEV_SETS)])
+        t_dev = _timed(lambda i: g_dev.replay(), steps, stream) / DEV_SETS
+        t_sc = _timed(lambda i: g_sc.replay(), steps, stream) / DEV_SETS
+        t_both = _timed(lambda i: g_both.replay(), steps, stream) / DEV_SETS
+        assert all(int(sl.counts[0].item()) == n and int(sl.counts[7].item()) == 1 for sl in sels)
+        out[ratio] = dict(n_keep=n, dev_sel_ms=t_dev, scatter_ms=t_sc, both_ms=t_both, scatter_bytes=n * ROW_BYTES * 4)
+    dev_bytes = N * 4 * ROW_BYTES + N * 8
     r30 = out[0.30]
-    ms = r30["dev_sel_ms"] + r30["scatter_ms"]
+    nb = dev_bytes + r30["scatter_bytes"]
     line = _workload_line(
-        "deviation + pooled top-k + scatter HBM GB/s, Qwen2.5-7B KV shape", (dev_bytes + r30["scatter_bytes"]) / (ms * 1e-3) / 1e9,
-        ms, steps, warmup,
-        {"workload": "layer-1 deviation + pooled top-k (30%) + 4 sinks x 32 chunks x 256 + scatter, 4 KV heads, head_dim 128, bf16",
-         "bytes_per_step": dev_bytes + r30["scatter_bytes"]},
-        _rooffor("deviation_kernel<bf16> + select_reg_kernel", dev_bytes, r30["dev_sel_ms"]))
-    line["ratios"] = {str(r): {k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in o.items()} for r, o in out.items()}
+        "deviation + pooled top-k + scatter HBM GB/s, Qwen2.5-7B KV shape", nb / (r30["both_ms"] * 1e-3) / 1e9,
+        r30["both_ms"], steps, warmup,
+        {"workload": "layer-1 deviation + pooled top-k (30%) + 4 sinks x 32 chunks x 256 + scatter of the kept rows, "
+                     "4 KV heads, head_dim 128, bf16; 16 input sets rotated (cold HBM)", "bytes_per_step": nb},
+        _rooffor("deviation_select_kernel<bf16,8> (deviation + top-k, one launch)", dev_bytes, r30["dev_sel_ms"]))
+    line["ratios"] = {str(r): {k2: (round(v2, 5) if isinstance(v2, float) else v2) for k2, v2 in o.items()}
+                      for r, o in out.items()}
     return line
 
 
@@ -689,7 +729,8 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
                          spans=torch.from_numpy(plan.spans.reshape(-1)).to(dev),
                          layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), proj=proj,
                          fresh1=(torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16(),
-                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None))
+                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None,
+                         ws=ops.deviation_select_workspace(dev)))
     assert reqs[0]["plan"].budget == 4864
     streams = [torch.cuda.Stream() for _ in range(n_streams)]
 
@@ -701,10 +742,10 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         ops.rope_qkv(None, *rq["proj"][0], rq["layer0"], 0, N_KV, HEAD_DIM, THETA, k_out=K[0], v_out=V[0],
                      rows=rq["layer0"], table=cs_tab)
         k1, v1 = rq["fresh1"]
-        d, n = ops.deviation(k1, v1, K[1], V[1], rq["flags"], rq["local"])
-        rq["sel"] = ops.select(d, n, rq["flags"], rq["local"], rq["spans"], None, rq["sel"])
+        _, _, rq["sel"] = ops.deviation_select(k1, v1, K[1], V[1], rq["flags"], rq["local"], rq["spans"], None, rq["ws"],
+                                               out=rq["sel"])
         rows = rq["sel"].keep_abs[: plan.n_keep]
-        ops.scatter_rows(K[1], V[1], k1[:, :, : plan.n_keep], v1[:, :, : plan.n_keep], rows)
+        ops.scatter_kept_rows(K[1], V[1], k1, v1, rows, rq["sel"].keep_local[: plan.n_keep])
         ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(2, N_LAYERS),
                           skip=rq["sel"].keep_rank)
         for li in range(2, N_LAYERS):
@@ -1067,6 +1108,7 @@ def main() -> None:
         "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
         "ms_per_step_two_streams": round(r["ms_two"], 4),
         "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
+        "ms_per_step_fused_select": round(r["ms_fused"], 4),
         "concurrent_requests": {"requests": CONCURRENT, "ms_per_round": round(r["ms_conc"], 4),
                                 "gbs": round(r["conc_gbs"], 1), "pct_of_peak": round(100.0 * r["conc_gbs"] / PEAK_GBS, 2),
                                 "note": "the same request's KV repair, CONCURRENT independent requests in flight on "

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libchunkkv_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 CKV_OK = 0
 CKV_ERR_INVALID_ARGUMENT = 1
@@ -31,7 +31,12 @@ COUNT_BUDGET = 2
 COUNT_CANDIDATES = 3
 COUNT_UNCOMPUTED = 4
 COUNT_BUDGET_REQUESTED = 5
+COUNT_BAD_SPANS = 6
+COUNT_TOP_HISTOGRAM = 7
 COUNT_N = 8
+
+DEVIATION_SELECT_WORKSPACE_BYTES = 16640
+POS_POOLED = 8
 
 SELECT_MAX_TOKENS = 131072
 DEVICE_ERR_RANGE = 1
@@ -86,6 +91,15 @@ SIGNATURES = {
     "ckv_scatter_rows": (
         _i32,
         [_p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p, _p],
+    ),
+    "ckv_scatter_kept_rows": (
+        _i32,
+        [_p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p],
+    ),
+    "ckv_deviation_select": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f64,
+         _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p],
     ),
 }
 

@@ -19,8 +19,8 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 LIB_DIR = PKG / "_lib"
 LIB_NAME = "libchunkkv_amd.so"
-SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "scatter.hip", "attention.hip",
-           "rope.hip", "extract.hip", "norm.hip"]
+SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "deviation_select.hip",
+           "scatter.hip", "attention.hip", "rope.hip", "extract.hip", "norm.hip"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: products and sums stay separately rounded, like the reference's torch ops.

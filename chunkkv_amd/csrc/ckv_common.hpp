@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "chunkkv_amd.h"
 
 namespace ckv {
@@ -93,11 +95,62 @@ __device__ __forceinline__ void st16_stream(void* p, const vec16& v) { __builtin
 
 // ---- wavefront reductions -----------------------------------------------------------------
 
-// Butterfly sum over the 64 lanes (xor 32, 16, 8, 4, 2, 1). Every lane ends with the same
-// value because fp32 addition is commutative; the tree is part of the bit-exact contract.
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// x of another lane through a DPP row operation (VALU, no LDS round trip); lanes whose source
+// is outside the row, or whose row is not in ROW_MASK, read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t x) {
+  return __builtin_amdgcn_update_dpp(0u, x, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(x), CTRL, 0xf, 0xf, false));
+}
+
+// Butterfly sum over the 64 lanes: x_l + x_{l^m} for m = 32, 16, 8, 4, 2, 1, each lane adding
+// its own value first. Every lane ends with the same value because fp32 addition commutes; the
+// tree is part of the bit-exact contract. The partners come from gfx950's VALU permutes, not
+// LDS shuffles: xor 32 and 16 from the row-swap permutes (which return the lane's own value and
+// its partner in a lane-dependent order), xor 8 from rotating a 16-lane row by 8, xor 4 from
+// rotating it by 4 (lane l+4 of the row holds the same value as lane l^4 once the xor-8 step
+// has made lanes 8 apart equal), xor 2 and 1 from quad permutes. Checked against the xor-shuffle
+// tree bit for bit on the GPU.
 __device__ __forceinline__ float wave_butterfly_sum(float x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x = x + __shfl_xor(x, m, kWave);
+  const int l = lane_id();
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = x + __uint_as_float(l < 32 ? a[1] : a[0]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = x + __uint_as_float((l & 16) == 0 ? b[1] : b[0]);
+  x = x + dpp_f32<0x128>(x);  // row_ror:8
+  x = x + dpp_f32<0x124>(x);  // row_ror:4
+  x = x + dpp_f32<0x4e>(x);   // quad_perm [2, 3, 0, 1]
+  x = x + dpp_f32<0xb1>(x);   // quad_perm [1, 0, 3, 2]
+  return x;
+}
+
+// Inclusive prefix sum over the 64 lanes in lane order: shifts within 16-lane rows, then row 15
+// broadcast into rows 1 and 3 and lane 31 into rows 2 and 3 (integer sums: order-free).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += dpp_or_zero<0x111>(x);  // row_shr:1
+  x += dpp_or_zero<0x112>(x);  // row_shr:2
+  x += dpp_or_zero<0x114>(x);  // row_shr:4
+  x += dpp_or_zero<0x118>(x);  // row_shr:8
+  x += dpp_or_zero<0x142, 0xa>(x);  // row_bcast:15
+  x += dpp_or_zero<0x143, 0xc>(x);  // row_bcast:31
+  return x;
+}
+__device__ __forceinline__ uint64_t wave_incl_scan(uint64_t x) {
+  auto step = [](uint64_t v, auto ctrl) {
+    constexpr int C = decltype(ctrl)::value & 0xfff, RM = decltype(ctrl)::value >> 12;
+    return v + (((uint64_t)dpp_or_zero<C, RM>((uint32_t)(v >> 32)) << 32) | dpp_or_zero<C, RM>((uint32_t)v));
+  };
+  x = step(x, std::integral_constant<int, 0xf111>{});
+  x = step(x, std::integral_constant<int, 0xf112>{});
+  x = step(x, std::integral_constant<int, 0xf114>{});
+  x = step(x, std::integral_constant<int, 0xf118>{});
+  x = step(x, std::integral_constant<int, 0xa142>{});
+  x = step(x, std::integral_constant<int, 0xc143>{});
   return x;
 }
 

@@ -1,0 +1,120 @@
+// Layer-1 fresh-vs-cached K/V deviation of token positions, one 64-lane wavefront per position:
+// the arithmetic shared by ckv_deviation and ckv_deviation_select.
+//
+// Reference semantics (src/chunkkv/engine/torch_engine.py:117-124):
+//   d_act  = ((k - K[:, :, active]).float() ** 2).sum(dim=(0, 1, 3))
+//   d_act += ((v - V[:, :, active]).float() ** 2).sum(dim=(0, 1, 3))
+//   n_act  = (k.float() ** 2).sum(dim=(0, 1, 3)) + (v.float() ** 2).sum(dim=(0, 1, 3))
+//   diff[active] = d_act; norm[active] = n_act   (zeros elsewhere)
+// The subtraction happens in the element type (one rounding); squares and sums are fp32.
+// K/V rows outside every placement are zero in the reference (base_kv zero-fills them).
+//
+// Each lane loads 16 bytes of each of the four rows (fresh k, cached K, fresh v, cached V) of
+// every one of its tokens before any arithmetic, so a token's H*D elements (1 KiB per tensor at
+// H=4, D=128, bf16) arrive in one coalesced pass. 16-byte vector q of a tensor goes to lane
+// q mod 64, each lane adds in ascending q from +0, and four fp32 partial sums per lane are
+// combined by a xor butterfly: the summation contract the oracle restates bit for bit.
+#pragma once
+
+#include "ckv_common.hpp"
+
+namespace ckv {
+
+struct DevArgs {
+  const char* kf;  // fresh k rows: head stride kf_hs_b, token stride kf_ts_b (bytes)
+  int64_t kf_hs_b, kf_ts_b;
+  const char* vf;  // fresh v rows
+  int64_t vf_hs_b, vf_ts_b;
+  const char* kc;  // cached K, V: (H, N, D), head stride c_hs_b (bytes)
+  const char* vc;
+  int64_t c_hs_b;
+  const uint8_t* flags;
+  const int32_t* local;  // row of each position in the fresh tensors, -1 = not computed
+  int n_tokens, n_fresh, n_heads, head_dim;
+  int32_t* err;
+};
+
+// Deviation and norm of positions p_base .. p_base + T - 1, computed by the calling wavefront.
+// Every lane returns the totals; positions outside the active set (local < 0) or past n_tokens
+// give 0. fl[t] returns the position's flag byte (0 past n_tokens).
+template <int DTYPE, int T>
+__device__ __forceinline__ void deviation_wave(const DevArgs& a, int p_base, float (&diff)[T], float (&norm)[T],
+                                               uint32_t (&fl)[T]) {
+  using E = Elem<DTYPE>;
+  constexpr int VEC = E::kVec;
+  const int lane = threadIdx.x % kWave;
+  const int64_t row_b = (int64_t)a.head_dim * E::kBytes;
+  const int vecs_per_row = a.head_dim / VEC;
+  const int n_vecs = a.n_heads * vecs_per_row;
+
+  int jj[T];
+  bool cached[T];
+  float sk[T], sv[T], nk[T], nv[T];
+  // every position's index and flags first (all in flight together), then the checks
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int p = p_base + t;
+    jj[t] = p < a.n_tokens ? a.local[p] : -1;
+    fl[t] = p < a.n_tokens ? a.flags[p] : 0u;
+  }
+  bool bad = false;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    cached[t] = (fl[t] & CKV_POS_CACHED) != 0;
+    bad = bad || jj[t] >= a.n_fresh;
+    jj[t] = jj[t] >= a.n_fresh ? -1 : jj[t];
+    sk[t] = sv[t] = nk[t] = nv[t] = 0.0f;
+  }
+  for (int q = lane; q < n_vecs; q += kWave) {
+    const int h = q / vecs_per_row;
+    const int64_t cb = (int64_t)(q % vecs_per_row) * 16;
+    vec16 k16[T], v16[T], kc16[T], vc16[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (jj[t] >= 0) {
+        k16[t] = ld16(a.kf + h * a.kf_hs_b + jj[t] * a.kf_ts_b + cb);
+        v16[t] = ld16(a.vf + h * a.vf_hs_b + jj[t] * a.vf_ts_b + cb);
+        if (cached[t]) {
+          const int64_t co = h * a.c_hs_b + (int64_t)(p_base + t) * row_b + cb;
+          kc16[t] = ld16(a.kc + co);
+          vc16[t] = ld16(a.vc + co);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (jj[t] < 0) continue;
+      float kx[VEC], vx[VEC], kcx[VEC], vcx[VEC];
+      E::unpack(k16[t], kx);
+      E::unpack(v16[t], vx);
+      if (cached[t]) {
+        E::unpack(kc16[t], kcx);
+        E::unpack(vc16[t], vcx);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) kcx[e] = vcx[e] = 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float dk = E::round_trip(kx[e] - kcx[e]);
+        const float dv = E::round_trip(vx[e] - vcx[e]);
+        sk[t] = sk[t] + dk * dk;
+        sv[t] = sv[t] + dv * dv;
+        nk[t] = nk[t] + kx[e] * kx[e];
+        nv[t] = nv[t] + vx[e] * vx[e];
+      }
+    }
+  }
+  if (bad && lane == 0) flag_error(a.err, CKV_DEVICE_ERR_RANGE);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const float x = wave_butterfly_sum(sk[t]);
+    const float y = wave_butterfly_sum(sv[t]);
+    const float z = wave_butterfly_sum(nk[t]);
+    const float w = wave_butterfly_sum(nv[t]);
+    diff[t] = jj[t] < 0 ? 0.0f : x + y;
+    norm[t] = jj[t] < 0 ? 0.0f : z + w;
+  }
+}
+
+}  // namespace ckv

@@ -2,6 +2,8 @@
 //
 // Reference semantics (src/chunkkv/engine/torch_engine.py:155-156):
 //   K[:, :, active] = k;  V[:, :, active] = v      (row overwrite, bit-exact copy)
+// and, with a source row map (ckv_scatter_kept_rows), the compaction before it (:152):
+//   k, v = k[:, :, sel], v[:, :, sel]  folded into the same pass (k/v are read at rows sel[j]).
 //
 // Design (gfx950): each thread moves kScatterUnroll 16-byte vectors of K and the matching
 // vectors of V (all loads issued before any store; grid-stride so each load instruction of a
@@ -22,8 +24,8 @@ constexpr int kScatterUnroll = CKV_SCATTER_UNROLL;  // 16-byte K/V vector pairs 
 __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
     char* dst_k, char* dst_v, int64_t d_hs_b, const char* __restrict__ sk, int64_t sk_hs_b,
     int64_t sk_ts_b, const char* __restrict__ sv, int64_t sv_hs_b, int64_t sv_ts_b,
-    const int64_t* __restrict__ rows, int n_rows, int n_tokens, int n_heads, int vecs_per_row,
-    int64_t row_b, int32_t* __restrict__ err) {
+    const int64_t* __restrict__ rows, const int64_t* __restrict__ src_rows, int n_rows, int n_src, int n_tokens,
+    int n_heads, int vecs_per_row, int64_t row_b, int32_t* __restrict__ err) {
   const int64_t per_tok = (int64_t)n_heads * vecs_per_row;
   const int64_t total = (int64_t)n_rows * per_tok;
   const int64_t stride = (int64_t)gridDim.x * kScatterThreads;
@@ -40,9 +42,13 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
       const int h = rem / vecs_per_row;
       const int64_t cb = (int64_t)(rem % vecs_per_row) * 16;
       const int64_t t = rows[j];
-      a[u] = ld16(sk + h * sk_hs_b + j * sk_ts_b + cb);
-      b[u] = ld16(sv + h * sv_hs_b + j * sv_ts_b + cb);
-      if (t >= 0 && t < n_tokens) {
+      const int64_t js = src_rows != nullptr ? src_rows[j] : j;
+      const bool src_ok = js >= 0 && js < n_src;
+      if (src_ok) {
+        a[u] = ld16(sk + h * sk_hs_b + js * sk_ts_b + cb);
+        b[u] = ld16(sv + h * sv_hs_b + js * sv_ts_b + cb);
+      }
+      if (src_ok && t >= 0 && t < n_tokens) {
         dst_o[u] = h * d_hs_b + t * row_b + cb;
       } else if (rem == 0) {
         flag_error(err, CKV_DEVICE_ERR_RANGE);
@@ -60,15 +66,15 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
 
 }  // namespace ckv
 
-extern "C" int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
-                                    int64_t sk_head_stride, int64_t sk_token_stride, const void* src_v,
-                                    int64_t sv_head_stride, int64_t sv_token_stride, const int64_t* rows,
-                                    int32_t n_rows, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
-                                    int32_t dtype, int32_t* err, void* stream) {
+static int32_t scatter_launch(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
+                              int64_t sk_head_stride, int64_t sk_token_stride, const void* src_v,
+                              int64_t sv_head_stride, int64_t sv_token_stride, const int64_t* rows,
+                              const int64_t* src_rows, int32_t n_rows, int32_t n_src, int32_t n_tokens,
+                              int32_t n_heads, int32_t head_dim, int32_t dtype, int32_t* err, void* stream) {
   using namespace ckv;
   if (dtype != CKV_DTYPE_BF16 && dtype != CKV_DTYPE_F32) return CKV_ERR_INVALID_ARGUMENT;
   const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
-  if (head_dim <= 0 || (head_dim * eb) % 16 != 0 || n_heads <= 0 || n_rows < 0 || n_tokens < 0)
+  if (head_dim <= 0 || (head_dim * eb) % 16 != 0 || n_heads <= 0 || n_rows < 0 || n_tokens < 0 || n_src < 0)
     return CKV_ERR_INVALID_ARGUMENT;
   if (n_rows > 0 && (dst_k == nullptr || dst_v == nullptr || src_k == nullptr || src_v == nullptr || rows == nullptr))
     return CKV_ERR_INVALID_ARGUMENT;
@@ -82,7 +88,30 @@ extern "C" int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_s
   hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)blocks), dim3(kScatterThreads), 0, (hipStream_t)stream,
                      (char*)dst_k, (char*)dst_v, dst_head_stride * eb, (const char*)src_k, sk_head_stride * eb,
                      sk_token_stride * eb, (const char*)src_v, sv_head_stride * eb, sv_token_stride * eb, rows,
-                     (int)n_rows, (int)n_tokens, (int)n_heads, vecs_per_row, (int64_t)head_dim * eb, err);
+                     src_rows, (int)n_rows, (int)n_src, (int)n_tokens, (int)n_heads, vecs_per_row,
+                     (int64_t)head_dim * eb, err);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
+}
+
+extern "C" int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
+                                    int64_t sk_head_stride, int64_t sk_token_stride, const void* src_v,
+                                    int64_t sv_head_stride, int64_t sv_token_stride, const int64_t* rows,
+                                    int32_t n_rows, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
+                                    int32_t dtype, int32_t* err, void* stream) {
+  return scatter_launch(dst_k, dst_v, dst_head_stride, src_k, sk_head_stride, sk_token_stride, src_v, sv_head_stride,
+                        sv_token_stride, rows, nullptr, n_rows, n_rows, n_tokens, n_heads, head_dim, dtype, err,
+                        stream);
+}
+
+extern "C" int32_t ckv_scatter_kept_rows(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
+                                         int64_t sk_head_stride, int64_t sk_token_stride, const void* src_v,
+                                         int64_t sv_head_stride, int64_t sv_token_stride, const int64_t* dst_rows,
+                                         const int64_t* src_rows, int32_t n_rows, int32_t n_src, int32_t n_tokens,
+                                         int32_t n_heads, int32_t head_dim, int32_t dtype, int32_t* err,
+                                         void* stream) {
+  if (n_rows > 0 && src_rows == nullptr) return CKV_ERR_INVALID_ARGUMENT;
+  return scatter_launch(dst_k, dst_v, dst_head_stride, src_k, sk_head_stride, sk_token_stride, src_v, sv_head_stride,
+                        sv_token_stride, dst_rows, src_rows, n_rows, n_src, n_tokens, n_heads, head_dim, dtype, err,
+                        stream);
 }

@@ -1,0 +1,560 @@
+// Layer-1 selection machinery shared by ckv_select and ckv_deviation_select: per-chunk relative
+// deviation and escalation, pooled budget, pooled top-k with forced sinks, and compaction of the
+// new active set, run by one 1024-thread workgroup.
+//
+// Reference semantics (src/chunkkv/engine/torch_engine.py:125-153):
+//   keep = ~cached | sink
+//   for each non-exact placement p:                              (:128-140)
+//     rel = diff[span].sum() / norm[span].sum()                   (fp32, .item())
+//     escalated = thr is not None and rel > thr                   (Python float compare)
+//     if escalated: keep[span] = True
+//     elif ratio > 0: pool[span] = True; budget += int(round(ratio * len))
+//   budget = min(budget, (pool & ~keep).sum())                    (:142)
+//   top = argsort(-where(pool & ~keep, diff, -1))[:budget]; keep[top] = True   (:143-145)
+//   keep_abs = keep.nonzero(); sel = local[keep_abs]              (:146-152)
+// torch's argsort is not stable, so the reference leaves the order of equal deviations open;
+// these kernels fix it: larger diff first, then lower token index (NaN ranks last).
+//
+// Design (gfx950): 16 wavefronts; keep/pool spans live as N-bit masks in LDS. Chunk sums: one
+// wavefront per chunk, lane-strided fp32 partials + xor butterfly (the order the oracle
+// restates). Top-k: MSB-first radix select over order-preserving 32-bit keys, which yields the
+// exact threshold key T and how many ties at T to take; then key > T plus the lowest-index ties
+// are taken and the kept positions compacted in token order. Each thread owns a contiguous run
+// of KPT <= 33 positions whose keys stay in registers for every pass. A caller that already
+// counted the candidates' top 12 key bits (ckv_deviation_select does so while it computes the
+// deviations) hands that histogram in: the threshold's top 12 bits then come from one
+// workgroup scan over it, and only the remaining 20 bits go through radix passes, over the few
+// candidates in that bin.
+#pragma once
+
+#include "ckv_common.hpp"
+
+namespace ckv {
+
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / kWave;
+constexpr int kTopShift = 20;                    // top-digit histogram bin = key >> 20
+constexpr int kTopBins = 1 << (32 - kTopShift);  // 4096 bins
+static_assert(kTopBins == 4 * kSelThreads, "each thread owns four top-digit bins");
+
+// Order-preserving key of a deviation: larger float -> larger key; -0 == +0; NaN -> 0.
+__device__ __forceinline__ uint32_t dev_key(float f) {
+  if (f != f) return 0u;
+  if (f == 0.0f) f = 0.0f;
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ bool bit_of(const uint32_t* w, int p) { return (w[p >> 5] >> (p & 31)) & 1u; }
+
+// Workgroup barrier that orders LDS only: waits for this wavefront's LDS operations (lgkmcnt 0),
+// not for its global loads and stores, which __syncthreads() would also drain. Values loaded
+// from global memory are still waited for where they are used.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt at their maxima (no wait)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Exclusive prefix count of `pred` over the workgroup in thread order, plus the total.
+__device__ __forceinline__ int block_excl_count(bool pred, int* wave_tot, int& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const uint64_t m = __ballot(pred);
+  const int in_wave = __popcll(m & ((1ull << lane) - 1ull));
+  if (lane == 0) wave_tot[wave] = __popcll(m);
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const int t = wave_tot[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  __syncthreads();  // wave_tot is reused by the next call
+  total = all;
+  return before + in_wave;
+}
+
+// Set bits [a, b) of an LDS bitmask, spreading the words over the lanes of one wavefront.
+__device__ __forceinline__ void set_bit_range(uint32_t* w, int a, int b, int lane) {
+  if (a >= b) return;
+  for (int word = (a >> 5) + lane; word <= ((b - 1) >> 5); word += kWave) {
+    const int lo = max(a, word << 5) - (word << 5);
+    const int hi = min(b, (word << 5) + 32) - (word << 5);  // exclusive, 1..32
+    const uint32_t m = (hi - lo == 32) ? 0xffffffffu : (((1u << (hi - lo)) - 1u) << lo);
+    atomicOr(&w[word], m);
+  }
+}
+
+// Exclusive workgroup scan of one int per thread with ONE barrier: each call must get its own
+// `slots` array (kSelWaves ints) that no call in flight since the previous barrier reads.
+__device__ __forceinline__ int block_scan_1b(int v, int* slots, int& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int x = (int)wave_incl_scan((uint32_t)v);
+  if (lane == kWave - 1) slots[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const int t = slots[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  total = all;
+  return before + x - v;
+}
+
+// block_scan_1b for a 64-bit value (several counts packed in disjoint bit fields).
+__device__ __forceinline__ uint64_t block_scan_1b_u64(uint64_t v, uint64_t* slots, uint64_t& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const uint64_t x = wave_incl_scan(v);
+  if (lane == kWave - 1) slots[wave] = x;
+  __syncthreads();
+  uint64_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const uint64_t t = slots[w];
+    before += (w < wave) ? t : 0;
+    all += t;
+  }
+  total = all;
+  return before + x - v;
+}
+
+struct SelectArgs {
+  const float* diff;
+  const float* norm;
+  const uint8_t* flags;
+  const int32_t* local;
+  int n_tokens;
+  const ckv_chunk_span* chunks;
+  int n_chunks;
+  int has_thr;
+  double thr;
+  int64_t* keep_abs;
+  int64_t* keep_local;
+  int32_t* keep_rank;  // may be NULL
+  float* rel_out;
+  uint8_t* esc_out;
+  int32_t* counts;
+};
+
+constexpr uint64_t kField = 0x1fffffull;  // 21-bit count fields of the packed workgroup scans
+constexpr int kLightPass = 1024;          // candidates in the top bin up to which passes are light
+
+// The selection for n_tokens <= KPT * 1024, run by one whole 1024-thread workgroup: thread t owns
+// positions [t*KPT, (t+1)*KPT), whose keys stay in registers through every radix pass.
+//   ghist  NULL, or the 4096-bin histogram of key >> 20 over the positions flagged cached, pooled
+//          and not sink (what the candidates are when no chunk escalates). It is used when it
+//          matches the candidate set exactly (same positions, same total), else the selection
+//          runs its full four passes. Either way it is zeroed before the function returns.
+//   masks  2 * ceil(n_tokens / 32) words of LDS.
+// Barrier budget: chunk phase 1; candidate scan 1; top-bin broadcast 1 (histogram path);
+// 2 per radix pass (double-buffered histograms, every wavefront derives the digit itself); tie
+// scan 1 (only when ties at the threshold are split); compaction scan 1.
+// Chunks whose spans a wavefront loads before the selection (registers permitting).
+template <int KPT>
+constexpr int kSelPre = KPT <= 16 ? 2 : 1;
+
+// Spans of the chunks wavefront `wave` handles first (wave + r * 16, r < kSelPre), zero past the
+// last chunk: loaded by every workgroup of ckv_deviation_select at its start, so the selecting
+// workgroup has them without a dependent round trip.
+template <int KPT>
+__device__ __forceinline__ void load_first_spans(const ckv_chunk_span* chunks, int n_chunks, int wave,
+                                                 ckv_chunk_span (&sp)[kSelPre<KPT>]) {
+#pragma unroll
+  for (int r = 0; r < kSelPre<KPT>; ++r) {
+    const int c = wave + r * kSelWaves;
+    sp[r] = c < n_chunks ? chunks[c] : ckv_chunk_span{0, 0, 0, 0};
+  }
+}
+
+// Loads of diff/norm/histogram words another workgroup of the same launch wrote: device-scope
+// (global_load sc1, coherent across the XCDs' L2s) when COH, plain otherwise.
+template <bool COH>
+__device__ __forceinline__ float ld_val(const float* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+template <bool COH>
+__device__ __forceinline__ uint32_t ld_val(const uint32_t* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+
+template <int KPT, bool COH = false>
+__device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist, uint32_t* masks,
+                                           const ckv_chunk_span (&sp0)[kSelPre<KPT>]) {
+  static_assert(KPT <= 33, "a run of KPT positions spans at most two mask words and one 64-bit word");
+  constexpr int kBatch = 8;  // chunk-sum loads in flight per lane
+  __shared__ uint32_t hist[2][kSelWaves][256];
+  __shared__ uint32_t hl[3][256];  // one shared histogram per pass after the top digit (few candidates)
+  __shared__ int slots[2][kSelWaves];
+  __shared__ uint64_t slots64[2][kSelWaves];
+  __shared__ int s_budget_req, s_bad_span;
+  __shared__ int s_top[3];  // threshold top digit, ties still to take after it, its bin's count
+
+  const float* __restrict__ diff = a.diff;
+  const float* __restrict__ norm = a.norm;
+  const uint8_t* __restrict__ flags = a.flags;
+  const int32_t* __restrict__ local = a.local;
+  const int n_tokens = a.n_tokens;
+  const ckv_chunk_span* __restrict__ chunks = a.chunks;
+  const int n_chunks = a.n_chunks;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int W = (n_tokens + 31) >> 5;
+  uint32_t* escw = masks;
+  uint32_t* poolw = masks + W;
+
+  // Phase 0, no barrier before it: every global load this workgroup can issue up front, all in
+  // flight together (nothing loaded is used before the last load has gone out). The first chunks'
+  // spans come in with the call, so their deviation loads go out at once too.
+  const int p0 = tid * KPT;
+  constexpr int kFlagWords = (KPT + 3) / 4;
+  constexpr int kPre = kSelPre<KPT>;
+  float dv[KPT];            // the owned positions' deviations (their keys after phase 0)
+  uint32_t fl[kFlagWords];  // their flag bytes, four per register
+  int lv[KPT];              // their local indices (the compaction's keep_local)
+#pragma unroll
+  for (int w = 0; w < kFlagWords; ++w) fl[w] = 0u;
+  // A thread's run is contiguous, so lanes are KPT elements apart: with KPT % 4 == 0 and aligned
+  // arrays, 16-byte (4-byte for flags) loads cut the load instructions and cache-line requests
+  // four-fold.
+  int32_t* keep_rank = a.keep_rank;
+  const bool vec_ok = KPT % 4 == 0 && (((uintptr_t)diff | (uintptr_t)local) % 16 == 0) &&
+                      ((uintptr_t)flags % 4 == 0) && (keep_rank == nullptr || (uintptr_t)keep_rank % 16 == 0);
+#pragma unroll
+  for (int i0 = 0; i0 < KPT; i0 += 4) {
+    if (vec_ok && p0 + i0 + 4 <= n_tokens) {
+      float4 d;
+      if constexpr (COH) {
+        d = make_float4(ld_val<true>(diff + p0 + i0), ld_val<true>(diff + p0 + i0 + 1), ld_val<true>(diff + p0 + i0 + 2),
+                        ld_val<true>(diff + p0 + i0 + 3));
+      } else {
+        d = *(const float4*)(diff + p0 + i0);
+      }
+      const int4 l = *(const int4*)(local + p0 + i0);
+      fl[i0 / 4] = *(const uint32_t*)(flags + p0 + i0);  // i0 % 4 == 0: flags i0 .. i0 + 3
+      dv[i0] = d.x;
+      dv[i0 + 1] = d.y;
+      dv[i0 + 2] = d.z;
+      dv[i0 + 3] = d.w;
+      lv[i0] = l.x;
+      lv[i0 + 1] = l.y;
+      lv[i0 + 2] = l.z;
+      lv[i0 + 3] = l.w;
+    } else {
+#pragma unroll
+      for (int i = i0; i < i0 + 4 && i < KPT; ++i) {
+        const int p = p0 + i;
+        dv[i] = p < n_tokens ? ld_val<COH>(diff + p) : __uint_as_float(0x7fc00000u);  // NaN: key 0
+        lv[i] = p < n_tokens ? local[p] : 0;
+        if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
+      }
+    }
+  }
+  // the top-digit bins this thread owns: bins b0 .. b0 + 3, b0 = kTopBins - 4 (tid + 1), so that
+  // thread order is descending bin order
+  vec16 g4 = {0u, 0u, 0u, 0u};
+  uint32_t* gmine = ghist != nullptr ? ghist + (kTopBins - 4 * (tid + 1)) : nullptr;
+  if (gmine != nullptr) {
+    if constexpr (COH) {
+      g4 = vec16{ld_val<true>(gmine), ld_val<true>(gmine + 1), ld_val<true>(gmine + 2), ld_val<true>(gmine + 3)};
+    } else {
+      g4 = ld16(gmine);
+    }
+  }
+  // the first batch of this wavefront's first chunks' deviations
+  float bd0[kPre][kBatch], bn0[kPre][kBatch];
+#pragma unroll
+  for (int r = 0; r < kPre; ++r) {
+    const int c = wave + r * kSelWaves;
+    const bool ok0 = sp0[r].start >= 0 && sp0[r].length >= 0 && (int64_t)sp0[r].start + sp0[r].length <= n_tokens;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int q = j * kWave + lane;
+      const bool in = c < n_chunks && ok0 && q < sp0[r].length;
+      bd0[r][j] = in ? ld_val<COH>(diff + sp0[r].start + q) : 0.0f;
+      bn0[r][j] = in ? ld_val<COH>(norm + sp0[r].start + q) : 0.0f;
+    }
+  }
+  if (tid == 0) {
+    s_budget_req = 0;
+    s_bad_span = 0;
+  }
+  for (int w = tid; w < 2 * W; w += kSelThreads) masks[w] = 0u;
+  for (int b = tid; b < 2 * kSelWaves * 256; b += kSelThreads) (&hist[0][0][0])[b] = 0u;
+  if (tid < 3 * 256) (&hl[0][0])[tid] = 0u;
+  lds_barrier();  // the loads above stay in flight
+
+  // Phase 1: per-chunk rel / escalation / budget, one wavefront per chunk, summed in the
+  // contract's order (lane-strided, ascending, then the xor butterfly).
+  for (int c = wave, r = 0; c < n_chunks; c += kSelWaves, ++r) {
+    const bool pre = r < kPre;
+    const ckv_chunk_span sp = pre ? sp0[r < kPre ? r : 0] : chunks[c];
+    const bool ok = sp.start >= 0 && sp.length >= 0 && (int64_t)sp.start + sp.length <= n_tokens;
+    float sd = 0.0f, sn = 0.0f;
+    if (ok) {
+      for (int q0 = 0; q0 < sp.length; q0 += kBatch * kWave) {
+        float bd[kBatch], bn[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int q = q0 + j * kWave + lane;
+          if (pre && q0 == 0) {
+            bd[j] = r == 0 ? bd0[0][j] : bd0[kPre - 1][j];
+            bn[j] = r == 0 ? bn0[0][j] : bn0[kPre - 1][j];
+          } else {
+            bd[j] = q < sp.length ? ld_val<COH>(diff + sp.start + q) : 0.0f;
+            bn[j] = q < sp.length ? ld_val<COH>(norm + sp.start + q) : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          if (q0 + j * kWave + lane < sp.length) {
+            sd = sd + bd[j];
+            sn = sn + bn[j];
+          }
+        }
+      }
+    }
+    sd = wave_butterfly_sum(sd);
+    sn = wave_butterfly_sum(sn);
+    const float rel = sd / sn;
+    const bool esc = ok && a.has_thr && ((double)rel > a.thr);
+    if (lane == 0) {
+      a.rel_out[c] = rel;
+      a.esc_out[c] = esc ? 1 : 0;
+      if (!ok) atomicAdd(&s_bad_span, 1);
+    }
+    if (!ok) continue;
+    if (esc) {
+      set_bit_range(escw, sp.start, sp.start + sp.length, lane);
+    } else if (sp.pooled) {
+      set_bit_range(poolw, sp.start, sp.start + sp.length, lane);
+      if (lane == 0) atomicAdd(&s_budget_req, sp.budget);
+    }
+  }
+  lds_barrier();  // the rel/escalation stores above need no acknowledgement here
+
+  uint32_t key[KPT];  // order-preserving deviation keys of the owned positions
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) key[i] = dev_key(dv[i]);
+
+  // Phase 2: keep = ~cached | sink | escalated span; candidates = pooled span minus keep.
+  // The run [p0, p0 + KPT) lies in mask words p0 / 32 and p0 / 32 + 1 ((p0 % 32) + KPT <= 64):
+  // two reads per mask, bit i of the shifted window is position p0 + i.
+  uint64_t esc_bits = 0u, pool_bits = 0u;
+  if (p0 < n_tokens) {
+    const int w0 = p0 >> 5;
+    const bool two = w0 + 1 < W;
+    esc_bits = ((uint64_t)escw[w0] | (two ? (uint64_t)escw[w0 + 1] << 32 : 0ull)) >> (p0 & 31);
+    pool_bits = ((uint64_t)poolw[w0] | (two ? (uint64_t)poolw[w0 + 1] << 32 : 0ull)) >> (p0 & 31);
+  }
+  uint64_t cand = 0u, kept_static = 0u;
+  int mism = 0;  // positions where the histogram's candidate rule and the true one disagree
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int p = p0 + i;
+    if (p < n_tokens) {
+      const uint32_t f = (fl[i / 4] >> (8 * (i % 4))) & 0xffu;
+      const bool k = !(f & CKV_POS_CACHED) || (f & CKV_POS_SINK) || ((esc_bits >> i) & 1u);
+      kept_static |= (uint64_t)k << i;
+      const bool c = !k && ((pool_bits >> i) & 1u);
+      if (c) cand |= 1ull << i;
+      const bool hc = (f & CKV_POS_CACHED) && !(f & CKV_POS_SINK) && (f & CKV_POS_POOLED);
+      mism += hc != c;
+    }
+  }
+  // One scan: candidates, mismatches, and this thread's share of the top-digit histogram (its
+  // exclusive prefix = candidates in higher bins than its own).
+  const uint32_t gsum = g4.x + g4.y + g4.z + g4.w;
+  if (gmine != nullptr) st16(gmine, vec16{0u, 0u, 0u, 0u});  // leave the histogram zeroed for the next call
+  uint64_t scan_tot = 0;
+  const uint64_t scan_ex = block_scan_1b_u64((uint64_t)__popcll(cand) | ((uint64_t)mism << 21) |
+                                                 ((uint64_t)gsum << 42), slots64[0], scan_tot);
+  const int n_cand = (int)(scan_tot & kField);
+  const int budget_req = s_budget_req;
+  const int budget = max(0, min(budget_req, n_cand));
+  const bool use_top = ghist != nullptr && ((scan_tot >> 21) & kField) == 0 &&
+                       (int)((scan_tot >> 42) & kField) == n_cand;  // uniform
+
+  // Phase 3: radix select of the budget-th largest candidate key.
+  uint32_t prefix = 0u, pmask = 0u;
+  int need = budget;
+  int tie_count = 0;  // candidates with key == T (the last pass's bin of T)
+  int first_pass = 0;
+  if (budget > 0 && use_top) {
+    // the bin holding the budget-th largest key, from the counted histogram
+    uint32_t above = (uint32_t)((scan_ex >> 42) & kField);
+    const uint32_t h4[4] = {g4.w, g4.z, g4.y, g4.x};  // bins b0 + 3, b0 + 2, b0 + 1, b0 (descending)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (above < (uint32_t)need && (uint32_t)need <= above + h4[i]) {
+        s_top[0] = kTopBins - 4 * tid - 1 - i;
+        s_top[1] = need - (int)above;
+        s_top[2] = (int)h4[i];
+      }
+      above += h4[i];
+    }
+    lds_barrier();
+    prefix = (uint32_t)s_top[0] << kTopShift;
+    pmask = 0xffffffffu << kTopShift;
+    need = s_top[1];
+    tie_count = s_top[2];
+    first_pass = 1;
+  }
+  // After the top digit, few candidates share its bin: one shared histogram per pass (its own
+  // buffer, cleared up front) and one LDS barrier. Otherwise per-wavefront histograms folded
+  // after a second barrier, so hot bins do not serialise LDS atomics.
+  const bool light = use_top && tie_count <= kLightPass;
+  if (budget > 0) {
+    // passes over the bits below the known prefix: 8, 8, 8, 8 from bit 31, or, after the
+    // top-digit histogram, 8, 8 and 4 from bit 19
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      if (pass < first_pass) continue;
+      const int shift = use_top ? (pass == 1 ? 12 : pass == 2 ? 4 : 0) : 24 - 8 * pass;
+      const uint32_t dmask = (use_top && pass == 3) ? 15u : 255u;
+      uint32_t(*h)[256] = hist[pass & 1];
+      uint32_t* hmine = light ? hl[pass > 0 ? pass - 1 : 0] : h[wave];
+      // Run-length aggregate equal digits within the thread: in the high passes almost every key
+      // shares one or two digits, and unaggregated LDS atomics would serialize.
+      uint32_t run_digit = 0u, run_count = 0u;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        if (((cand >> i) & 1ull) && (key[i] & pmask) == prefix) {
+          const uint32_t d = (key[i] >> shift) & dmask;
+          if (run_count != 0u && d != run_digit) {
+            atomicAdd(&hmine[run_digit], run_count);
+            run_count = 0u;
+          }
+          run_digit = d;
+          ++run_count;
+        }
+      }
+      if (run_count != 0u) atomicAdd(&hmine[run_digit], run_count);
+      if (light) {
+        lds_barrier();
+      } else {
+        __syncthreads();
+        if (tid < 256) {  // fold the per-wavefront histograms into h[0]
+          uint32_t t = 0;
+#pragma unroll
+          for (int w = 0; w < kSelWaves; ++w) t += h[w][tid];
+          h[0][tid] = t;
+        } else {  // the other buffer was last read before this pass's barrier: clear it for pass+1
+          uint32_t* o = &hist[(pass + 1) & 1][0][0];
+          for (int b = tid - 256; b < kSelWaves * 256; b += kSelThreads - 256) o[b] = 0u;
+        }
+        __syncthreads();
+      }
+      const uint32_t* hsum = light ? hmine : h[0];
+      // every wavefront finds the digit: lane l owns digits 255-4l .. 252-4l (descending)
+      uint32_t h4[4];
+      uint32_t local_sum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h4[i] = hsum[255 - (lane * 4 + i)];
+        local_sum += h4[i];
+      }
+      const uint32_t incl = wave_incl_scan(local_sum);
+      uint32_t above = incl - local_sum;
+      int my_digit = -1;
+      uint32_t my_above = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (above < (uint32_t)need && (uint32_t)need <= above + h4[i]) {
+          my_digit = 255 - (lane * 4 + i);
+          my_above = above;
+        }
+        above += h4[i];
+      }
+      const uint64_t found = __ballot(my_digit >= 0);
+      const int src = found ? (int)__ffsll((unsigned long long)found) - 1 : 0;  // wavefront-uniform
+      const int digit = __builtin_amdgcn_readlane(my_digit, src);
+      need -= (int)__builtin_amdgcn_readlane((int)my_above, src);
+      prefix |= (uint32_t)digit << shift;
+      pmask |= dmask << shift;
+      if (pass == 3) tie_count = (int)hsum[digit];
+    }
+  }
+  const uint32_t T = prefix;
+
+  // Phase 4: take key > T and the first `need` ties at T in token order, then compact.
+  uint64_t take = 0u, tie = 0u;
+  if (budget > 0) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      if ((cand >> i) & 1ull) {
+        take |= (uint64_t)(key[i] > T) << i;
+        tie |= (uint64_t)(key[i] == T) << i;
+      }
+    }
+  }
+  if (need < tie_count) {  // uniform: only then do ties need ranking (lowest positions first)
+    int tie_total = 0;
+    int tie_rank = block_scan_1b(__popcll(tie), slots[1], tie_total);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      if ((tie >> i) & 1ull) {
+        take |= (uint64_t)(tie_rank < need) << i;
+        ++tie_rank;
+      }
+    }
+  } else {
+    take |= tie;  // every tie at T is taken
+  }
+  const uint64_t kept = kept_static | take;
+  // One scan for three counts in 21-bit fields (each total <= n_tokens < 2^21): kept positions
+  // (the rank of each), kept cached positions, kept positions absent from the active set.
+  uint64_t mine = (uint64_t)__popcll(kept);
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    if ((kept >> i) & 1ull) {
+      mine += (((fl[i / 4] >> (8 * (i % 4))) & CKV_POS_CACHED) ? 1ull : 0ull) << 21;
+      mine += (uint64_t)(lv[i] < 0) << 42;
+    }
+  }
+  uint64_t all = 0;
+  int rank = (int)(block_scan_1b_u64(mine, slots64[1], all) & kField);
+  const int n_keep = (int)(all & kField);
+  const int sel_cached = (int)((all >> 21) & kField);
+  const int uncomputed = (int)((all >> 42) & kField);
+  int kr[KPT];  // keep_rank of the owned positions
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    kr[i] = ((kept >> i) & 1ull) ? rank : -1;
+    if ((kept >> i) & 1ull) {
+      const int p = p0 + i;
+      a.keep_abs[rank] = p;
+      a.keep_local[rank] = lv[i] < 0 ? 0 : lv[i];
+      ++rank;
+    }
+  }
+  if (keep_rank != nullptr) {
+#pragma unroll
+    for (int i0 = 0; i0 < KPT; i0 += 4) {
+      if (vec_ok && p0 + i0 + 4 <= n_tokens) {
+        *(int4*)(keep_rank + p0 + i0) = make_int4(kr[i0], kr[i0 + 1], kr[i0 + 2], kr[i0 + 3]);
+      } else {
+#pragma unroll
+        for (int i = i0; i < i0 + 4 && i < KPT; ++i)
+          if (p0 + i < n_tokens) keep_rank[p0 + i] = kr[i];
+      }
+    }
+  }
+  if (tid == 0) {
+    int32_t* counts = a.counts;
+    counts[CKV_COUNT_KEEP] = n_keep;
+    counts[CKV_COUNT_SELECTED_CACHED] = sel_cached;
+    counts[CKV_COUNT_BUDGET] = budget;
+    counts[CKV_COUNT_CANDIDATES] = n_cand;
+    counts[CKV_COUNT_UNCOMPUTED] = uncomputed;
+    counts[CKV_COUNT_BUDGET_REQUESTED] = budget_req;
+    counts[6] = s_bad_span;
+    counts[7] = use_top ? 1 : 0;
+  }
+}
+
+}  // namespace ckv

@@ -14,7 +14,7 @@ the fresh-token RoPE and the attention run on the HIP kernels:
                                                        straight into the cache rows of the active
                                                        positions (layer 1: into tensors, for the
                                                        deviation; its kept rows then go through
-                                                       ckv_scatter_rows)
+                                                       ckv_scatter_kept_rows)
   base_kv (:96-103; ~13 launches per placement and   ckv_rerope_gather_layers (overlap=True: on
     layer, zero-filled cache, every layer)             a side stream): at the start, layer 1's
                                                        base cache (and layer 0's rows of exact
@@ -28,7 +28,11 @@ the fresh-token RoPE and the attention run on the HIP kernels:
                                                        that reads them
   deviation (:117-124)                               ckv_deviation (one wavefront per token)
   rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
-    one .item() per chunk)                             nothing back unless a threshold is set
+    one .item() per chunk)                             nothing back unless a threshold is set.
+                                                       fused_select=True: both in one launch,
+                                                       ckv_deviation_select
+  h, q, k, v = ...[sel]; K[:, :, active] = k (:152,  h and q index-selected; k/v compacted and
+    :155-156)                                          scattered by ckv_scatter_kept_rows
   mask + SDPA (:157, :68-72)                         ckv_attention_active: matrix-core
                                                        attention masked by the active positions
                                                        (bf16, head_dim 64/128)
@@ -113,10 +117,16 @@ def _stack_params(mods: list, name: str) -> torch.Tensor | None:
 
 
 class HipEngine(DecoderPieces):
-    def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = False):
+    def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = False, fused_select: bool = False):
         if attention not in ("fused", "reference"):
             raise ValueError("attention must be 'fused' or 'reference'")
         self.attention = attention
+        # fused_select=True runs the layer-1 deviation and the selection as one launch
+        # (ckv_deviation_select) instead of two (ckv_deviation, ckv_select); same results. Off by
+        # default: in the 8k request's step the one launch takes ~41 us against 12 + 20 us, because
+        # the selecting workgroup's registers leave the deviation phase one 1024-thread workgroup
+        # per CU.
+        self.fused_select = fused_select
         # overlap=True issues the cached-row gathers on a side stream, joined by events where a
         # layer needs its rows, instead of in order on the main stream (same launches, same rows).
         # Off by default: on MI355X the side stream did not shorten the 8k request's TTFT (42.47 vs
@@ -124,6 +134,7 @@ class HipEngine(DecoderPieces):
         self.overlap = overlap
         self._side: torch.cuda.Stream | None = None
         self._rope_tab: torch.Tensor | None = None  # (cos, sin) per position, grown on demand
+        self._ws: dict[int, torch.Tensor] = {}  # deviation_select workspaces, per stream
         # generate(): replay each decode step after the first from a HIP graph (device-side loop)
         self.decode_graphs = True
         # Set to a dict to record the layer-1 selection inputs/outputs (device tensors) of the
@@ -307,6 +318,16 @@ class HipEngine(DecoderPieces):
             else torch.empty(0, dtype=_TORCH_OF[a.dtype], device=self.device)
             for a, o in zip(parts, offs)
         ]
+
+    def _workspace(self) -> torch.Tensor:
+        """ckv_deviation_select's workspace for torch's current stream (zeroed once; every call
+        leaves it zeroed). One per stream, so prefills issued on different streams never share
+        one."""
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        ws = self._ws.get(st)
+        if ws is None:
+            ws = self._ws[st] = ops.deviation_select_workspace(self.device)
+        return ws
 
     def _table(self, n: int) -> torch.Tensor:
         """Per-position (cos, sin) table covering positions [0, n), kept across requests."""
@@ -502,8 +523,12 @@ class HipEngine(DecoderPieces):
                 v = v_in.view(1, -1, H, D).transpose(1, 2)
                 if ready.get(1) is not None:
                     torch.cuda.current_stream(dev).wait_event(ready[1])
-                diff, norm = ops.deviation(k, v, K, V, flags_d, local_d, err)
-                sel = ops.select(diff, norm, flags_d, local_d, spans_d, config.escalate_threshold)
+                if self.fused_select:
+                    diff, norm, sel = ops.deviation_select(k, v, K, V, flags_d, local_d, spans_d,
+                                                           config.escalate_threshold, self._workspace(), err)
+                else:
+                    diff, norm = ops.deviation(k, v, K, V, flags_d, local_d, err)
+                    sel = ops.select(diff, norm, flags_d, local_d, spans_d, config.escalate_threshold)
                 if config.escalate_threshold is None and not plan.has_overlap:
                     n_keep = plan.n_keep  # fixed by the layout: no device round trip
                 else:
@@ -516,9 +541,9 @@ class HipEngine(DecoderPieces):
                     self.trace.update(k=k, v=v, K=K.clone(), V=V.clone(), flags=flags_d, local=local_d, spans=spans_d,
                                       diff=diff, norm=norm, sel=sel, n_keep=n_keep)
                 rows = sel.keep_local[:n_keep]
-                h, q, k, v = h.index_select(1, rows), q.index_select(1, rows), k.index_select(2, rows), v.index_select(2, rows)
+                h, q = h.index_select(1, rows), q.index_select(1, rows)
                 active = sel.keep_abs[:n_keep]
-                ops.scatter_rows(K, V, k, v, active, err)
+                ops.scatter_kept_rows(K, V, k, v, active, rows, err)  # k/v compaction folded in
                 if n_cached_segs and n_layers > 2:
                     ready[2] = gather((2, n_layers), sel.keep_rank)
             else:

@@ -194,6 +194,17 @@ class Selection:
     counts: torch.Tensor  # int32 (COUNT_N,)
 
 
+def _new_selection(N: int, C: int, dev) -> Selection:
+    return Selection(
+        keep_abs=torch.empty(N, dtype=torch.int64, device=dev),
+        keep_local=torch.empty(N, dtype=torch.int64, device=dev),
+        keep_rank=torch.empty(N, dtype=torch.int32, device=dev),
+        rel_dev=torch.empty(C, dtype=torch.float32, device=dev),
+        escalated=torch.empty(C, dtype=torch.uint8, device=dev),
+        counts=torch.empty(_native.COUNT_N, dtype=torch.int32, device=dev),
+    )
+
+
 def select(
     diff: torch.Tensor,
     norm: torch.Tensor,
@@ -213,14 +224,7 @@ def select(
     C = spans.numel() // 4
     dev = diff.device
     if out is None:
-        out = Selection(
-            keep_abs=torch.empty(N, dtype=torch.int64, device=dev),
-            keep_local=torch.empty(N, dtype=torch.int64, device=dev),
-            keep_rank=torch.empty(N, dtype=torch.int32, device=dev),
-            rel_dev=torch.empty(C, dtype=torch.float32, device=dev),
-            escalated=torch.empty(C, dtype=torch.uint8, device=dev),
-            counts=torch.empty(_native.COUNT_N, dtype=torch.int32, device=dev),
-        )
+        out = _new_selection(N, C, dev)
     has_thr = escalate_threshold is not None
     check(
         lib().ckv_select(
@@ -231,6 +235,106 @@ def select(
         "ckv_select",
     )
     return out
+
+
+def deviation_select_workspace(device) -> torch.Tensor:
+    """A zeroed workspace for deviation_select. Every call leaves it zeroed again, so one
+    workspace serves any number of calls issued in order (one stream); concurrent calls need one
+    each."""
+    return torch.zeros(_native.DEVIATION_SELECT_WORKSPACE_BYTES // 4, dtype=torch.int32, device=device)
+
+
+def deviation_select(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    flags: torch.Tensor,
+    local: torch.Tensor,
+    spans: torch.Tensor,
+    escalate_threshold: float | None,
+    workspace: torch.Tensor,
+    err: torch.Tensor | None = None,
+    out: Selection | None = None,
+    diff_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, Selection]:
+    """deviation() then select() in one launch (torch_engine.py:117-153): returns (diff, norm,
+    selection), bit-identical to the two calls. flags must carry the planner's pooled bit for
+    the fast path (without it the result is the same, the selection slower). workspace: from
+    deviation_select_workspace(), not shared by calls that may run concurrently."""
+    _dev(k, v, K, V, flags, local, spans, workspace)
+    k, v = _rows_view(k), _rows_view(v)
+    if K.dtype != k.dtype or V.dtype != k.dtype or v.dtype != k.dtype:
+        raise TypeError("fresh and cached K/V must share a dtype")
+    _, H, N, D = K.shape
+    if not (K.is_contiguous() and V.is_contiguous() and V.shape == K.shape):
+        raise ValueError("cached K/V must be contiguous (1, H, N, D)")
+    if k.shape[1] != H or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"fresh k/v shape {tuple(k.shape)} does not match cache {tuple(K.shape)}")
+    if flags.dtype != torch.uint8 or local.dtype != torch.int32 or flags.numel() != N or local.numel() != N:
+        raise ValueError("flags must be uint8 (N,) and local int32 (N,)")
+    if not (flags.is_contiguous() and local.is_contiguous()):
+        raise ValueError("flags and local must be contiguous")
+    if N > _native.SELECT_MAX_TOKENS:
+        raise ValueError(f"selection supports at most {_native.SELECT_MAX_TOKENS} tokens, got {N}")
+    if spans.dtype != torch.int32 or (spans.numel() % 4):
+        raise ValueError("spans must be int32 (C, 4)")
+    if (workspace.numel() * workspace.element_size() < _native.DEVIATION_SELECT_WORKSPACE_BYTES
+            or not workspace.is_contiguous()):
+        raise ValueError("workspace must come from deviation_select_workspace()")
+    C = spans.numel() // 4
+    dev = K.device
+    if diff_norm is None:
+        diff_norm = (torch.empty(N, dtype=torch.float32, device=dev), torch.empty(N, dtype=torch.float32, device=dev))
+    diff, norm = diff_norm
+    if out is None:
+        out = _new_selection(N, C, dev)
+    has_thr = escalate_threshold is not None
+    check(
+        lib().ckv_deviation_select(
+            _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2), _ptr(K), _ptr(V), N * D, _ptr(flags),
+            _ptr(local), N, k.shape[2], H, D, dtype_code(K.dtype), _ptr(spans), C, int(has_thr),
+            float(escalate_threshold) if has_thr else 0.0, _ptr(diff), _ptr(norm), _ptr(out.keep_abs),
+            _ptr(out.keep_local), _ptr(out.keep_rank), _ptr(out.rel_dev), _ptr(out.escalated), _ptr(out.counts),
+            _ptr(workspace), workspace.numel() * workspace.element_size(), _ptr(err), _stream(dev),
+        ),
+        "ckv_deviation_select",
+    )
+    return diff, norm, out
+
+
+def scatter_kept_rows(
+    K: torch.Tensor,
+    V: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dst_rows: torch.Tensor,
+    src_rows: torch.Tensor,
+    err: torch.Tensor | None = None,
+) -> None:
+    """K[:, :, dst_rows] = k[:, :, src_rows]; V likewise, one launch: the compaction of the kept
+    rows and their scatter into the cache (torch_engine.py:152, :155-156). k/v: (1, H, n_src, D)
+    with contiguous rows (token-major views included); dst_rows/src_rows: int64, equal length."""
+    _dev(K, V, k, v, dst_rows, src_rows)
+    k, v = _rows_view(k), _rows_view(v)
+    _, H, N, D = K.shape
+    if not (K.is_contiguous() and V.is_contiguous() and V.shape == K.shape):
+        raise ValueError("cache K/V must be contiguous (1, H, N, D)")
+    if k.dtype != K.dtype or v.dtype != K.dtype:
+        raise TypeError("fresh rows and cache must share a dtype")
+    if k.dim() != 4 or k.shape[0] != 1 or k.shape[1] != H or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"fresh rows {tuple(k.shape)} do not match the cache {tuple(K.shape)}")
+    n = dst_rows.numel()
+    if dst_rows.dtype != torch.int64 or src_rows.dtype != torch.int64 or src_rows.numel() != n:
+        raise ValueError("dst_rows and src_rows must be int64 of one length")
+    dst_rows, src_rows = dst_rows.contiguous(), src_rows.contiguous()
+    check(
+        lib().ckv_scatter_kept_rows(
+            _ptr(K), _ptr(V), N * D, _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2),
+            _ptr(dst_rows), _ptr(src_rows), n, k.shape[2], N, H, D, dtype_code(K.dtype), _ptr(err), _stream(K.device),
+        ),
+        "ckv_scatter_kept_rows",
+    )
 
 
 def assemble_layer(

@@ -4,7 +4,7 @@ Everything here is integer bookkeeping on the host, vectorised with numpy (the r
 it with Python loops over every position: src/chunkkv/engine/base.py:63-73 and
 src/chunkkv/engine/torch_engine.py:89-94, :106, :128-142):
 
-* per-position flags cached / exact / sink and the index lists fresh_idx, layer0_idx;
+* per-position flags cached / exact / sink / pooled and the index lists fresh_idx, layer0_idx;
 * gather segments: one per run of positions owned by the same placement, the last placement
   winning where placements overlap (the reference assigns slices in placement order);
 * the layer-1 selection spans of the non-exact placements with their token budgets
@@ -22,6 +22,7 @@ import numpy as np
 POS_CACHED = 1
 POS_SINK = 2
 POS_EXACT = 4
+POS_POOLED = 8  # inside a non-exact placement with ratio > 0 (the layer-1 pool, torch_engine.py:137-139)
 
 SEG_FIELDS = 6  # dst_start, n_tokens, chunk, src_start, src_len, delta
 SPAN_FIELDS = 4  # start, length, budget, pooled
@@ -68,6 +69,7 @@ def plan_request(n_tokens: int, placements: list, n_sink: int, recompute_ratio: 
     cached = np.zeros(N, dtype=bool)
     exact = np.zeros(N, dtype=bool)
     sink = np.zeros(N, dtype=bool)
+    pooled = np.zeros(N, dtype=bool)
     owner = np.full(N, -1, dtype=np.int64)
 
     chunk_ids: dict[int, int] = {}
@@ -95,10 +97,11 @@ def plan_request(n_tokens: int, placements: list, n_sink: int, recompute_ratio: 
                 sink[s : s + min(L, n_sink)] = True
             ratio = recompute_ratio if p.ratio is None else p.ratio
             spans.append((s, L, round_budget(ratio, L) if ratio > 0 else 0, 1 if ratio > 0 else 0))
+            if ratio > 0:
+                pooled[s : s + L] = True
 
     flags = (cached.astype(np.uint8) * POS_CACHED) | (sink.astype(np.uint8) * POS_SINK) | (
-        exact.astype(np.uint8) * POS_EXACT
-    )
+        exact.astype(np.uint8) * POS_EXACT) | (pooled.astype(np.uint8) * POS_POOLED)
 
     # Runs of equal owner -> gather segments (last placement wins on overlap).
     segments = np.zeros((0, SEG_FIELDS), dtype=np.int32)

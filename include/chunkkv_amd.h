@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define CKV_ABI_VERSION 1
+#define CKV_ABI_VERSION 2
 
 typedef enum ckv_status {
   CKV_OK = 0,
@@ -53,6 +53,8 @@ typedef enum ckv_dtype {
 #define CKV_POS_CACHED 1u /* covered by a placement                                   */
 #define CKV_POS_SINK 2u   /* one of the first n_sink tokens of a non-exact placement    */
 #define CKV_POS_EXACT 4u  /* covered by an exact placement (never recomputed)          */
+#define CKV_POS_POOLED 8u /* inside a non-exact placement with ratio > 0 (the layer-1 pool,
+                           * torch_engine.py:137-139); read by ckv_deviation_select only     */
 
 /* Supported head dimensions (template instantiations). */
 #define CKV_SELECT_MAX_TOKENS 131072 /* ckv_select keeps two N-bit masks in LDS */
@@ -93,7 +95,12 @@ typedef struct ckv_chunk_span {
 #define CKV_COUNT_CANDIDATES 3      /* pooled tokens not already kept                       */
 #define CKV_COUNT_UNCOMPUTED 4      /* kept tokens absent from the previous active set      */
 #define CKV_COUNT_BUDGET_REQUESTED 5
+#define CKV_COUNT_BAD_SPANS 6       /* spans outside [0, n_tokens), skipped                  */
+#define CKV_COUNT_TOP_HISTOGRAM 7   /* 1 when ckv_deviation_select's histogram path ran      */
 #define CKV_COUNT_N 8
+
+/* Bytes of the workspace ckv_deviation_select takes (a 4096-bin histogram and a ticket). */
+#define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 16640
 
 /* ABI version compiled into the library (CKV_ABI_VERSION). */
 int32_t ckv_abi_version(void);
@@ -211,6 +218,35 @@ int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flag
                    uint8_t* escalated, int32_t* counts, void* stream);
 
 /*
+ * ckv_deviation followed by ckv_select, in one launch: the layer-1 repair decision
+ * (torch_engine.py:117-153) from the fresh and cached rows to the new active set, with outputs
+ * and results bit-identical to the two calls (same arguments, same meaning; see both above).
+ * The workgroups that compute the deviations also count every position flagged
+ * CKV_POS_CACHED | CKV_POS_POOLED and not CKV_POS_SINK into a histogram of its key's top 12 bits;
+ * the last workgroup to finish runs the selection from it. When the pooled flags disagree with
+ * the pooled spans, or a chunk escalates, the selection ignores the histogram (same result,
+ * slower); counts[CKV_COUNT_TOP_HISTOGRAM] says which path ran.
+ *   workspace        device memory of >= CKV_DEVIATION_SELECT_WORKSPACE_BYTES, 16-byte aligned,
+ *                    ZERO before its first use; every call leaves it zero again. Calls that
+ *                    share a workspace must be ordered (one stream, or events): concurrent
+ *                    calls on one workspace race.
+ * n_tokens <= CKV_SELECT_MAX_TOKENS; above 33792 the call runs the two launches instead (the
+ * workspace is then not touched).
+ * Replaces: torch_engine.py:117-153 (the deviation :117-124, rel/escalation/budget :128-142,
+ *           argsort top-k :143-146, keep.nonzero and local compaction :146-153).
+ */
+int32_t ckv_deviation_select(const void* k_fresh, int64_t kf_head_stride, int64_t kf_token_stride,
+                             const void* v_fresh, int64_t vf_head_stride, int64_t vf_token_stride,
+                             const void* k_cache, const void* v_cache, int64_t cache_head_stride,
+                             const uint8_t* pos_flags, const int32_t* local, int32_t n_tokens,
+                             int32_t n_fresh, int32_t n_heads, int32_t head_dim, int32_t dtype,
+                             const ckv_chunk_span* chunks, int32_t n_chunks, int32_t has_threshold,
+                             double escalate_threshold, float* diff, float* norm, int64_t* keep_abs,
+                             int64_t* keep_local, int32_t* keep_rank, float* rel_dev, uint8_t* escalated,
+                             int32_t* counts, void* workspace, int64_t workspace_bytes, int32_t* err,
+                             void* stream);
+
+/*
  * Assemble one layer's cache with every row written once: for each segment row at position p,
  *   local[p] >= 0  -> K/V[h, p, :] = fresh k/v[h, local[p], :]            (an active position)
  *   otherwise      -> K/V[h, p, :] = the chunk's row, keys re-rotated by delta (as the gather)
@@ -242,6 +278,21 @@ int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride,
                          const int64_t* rows, int32_t n_rows, int32_t n_tokens,
                          int32_t n_heads, int32_t head_dim, int32_t dtype, int32_t* err,
                          void* stream);
+
+/*
+ * Scatter the kept rows of the previous active set into one layer's cache, the compaction
+ * folded in:
+ *   K[h, dst_rows[j], :] = k[h, src_rows[j], :],  V[h, dst_rows[j], :] = v[h, src_rows[j], :]
+ * for j < n_rows, with src_rows[j] < n_src (a selection's keep_abs / keep_local).
+ * Replaces: the k/v compaction k[:, :, sel], v[:, :, sel] (torch_engine.py:152) and the scatter
+ * K[:, :, active] = k, V[:, :, active] = v (:155-156) that follows it.
+ */
+int32_t ckv_scatter_kept_rows(void* dst_k, void* dst_v, int64_t dst_head_stride,
+                              const void* src_k, int64_t sk_head_stride, int64_t sk_token_stride,
+                              const void* src_v, int64_t sv_head_stride, int64_t sv_token_stride,
+                              const int64_t* dst_rows, const int64_t* src_rows, int32_t n_rows,
+                              int32_t n_src, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
+                              int32_t dtype, int32_t* err, void* stream);
 
 /*
  * Fresh-token RoPE of projected q/k rows, with the v rows copied alongside:

@@ -133,6 +133,23 @@ def test_side_stream_and_one_stream_builds_identical(models, parts, ratio):
     assert torch.equal(ra.logits, rb.logits)
 
 
+@pytest.mark.parametrize("thr", [None, 0.05])
+def test_fused_select_builds_identical(models, parts, thr):
+    """The layer-1 deviation and selection as one launch (fused_select=True) or two: the same
+    caches, logits and stats, bit for bit, with and without an escalation threshold."""
+    _, gpu = models
+    a = HipEngine(gpu, StubTokenizer(), fused_select=True)
+    b = HipEngine(gpu, StubTokenizer())
+    toks2, pl = _swap_setup(a, parts)
+    cfg = BlendConfig(recompute_ratio=0.3, n_sink=4, escalate_threshold=thr)
+    ra, rb = a.prefill(toks2, pl, cfg), b.prefill(toks2, pl, cfg)
+    torch.cuda.synchronize()
+    for x, y in zip(ra.keys + ra.values, rb.keys + rb.values):
+        assert torch.equal(x, y)
+    assert torch.equal(ra.logits, rb.logits)
+    assert ra.stats == rb.stats
+
+
 def test_blend_matches_rocm_reference_ops(models, parts):
     """Same device, same model, reference SDPA call: only the KV repair differs."""
     from chunkkv_amd.baseline import torch_base_kv

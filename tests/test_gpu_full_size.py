@@ -138,3 +138,15 @@ def test_full_size_layer1_repair_matches_oracle(setup):
         Kg, Vg = O.to_numpy(res.keys[li])[0], O.to_numpy(res.values[li])[0]
         np.testing.assert_array_equal(Kg[:, dropped], Klo[:, dropped])
         np.testing.assert_array_equal(Vg[:, dropped], Vlo[:, dropped])
+
+
+def test_full_size_fused_select_identical(setup):
+    """The 8k request with the layer-1 deviation and selection in one launch: the same caches and
+    logits as the two-launch default, bit for bit."""
+    model, eng, tokens, placements = setup
+    cfg = BlendConfig(recompute_ratio=0.3, n_sink=4)
+    a = HipEngine(model, StubTokenizer(), fused_select=True).prefill(tokens, placements, cfg)
+    b = eng.prefill(tokens, placements, cfg)
+    assert torch.equal(a.logits, b.logits) and a.stats == b.stats
+    for li in (0, 1, 2, 27):
+        assert torch.equal(a.keys[li], b.keys[li]) and torch.equal(a.values[li], b.values[li])

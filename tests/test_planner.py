@@ -5,7 +5,7 @@ selection sizes the oracle computes."""
 import numpy as np
 import pytest
 
-from chunkkv_amd.planner import local_index, plan_request, round_budget, stats_dict
+from chunkkv_amd.planner import POS_POOLED, local_index, plan_request, round_budget, stats_dict
 from chunkkv_amd.types import BlendConfig, ChunkKV, Placement, plan_positions
 from oracle import engine_ref as R
 from oracle import oracle as O
@@ -52,6 +52,14 @@ def test_flags_match_reference_lists(seed, overlap):
     np.testing.assert_array_equal(plan.fresh_idx, [i for i in range(N) if not cached[i]])
     np.testing.assert_array_equal(plan.layer0_idx, [i for i in range(N) if not exact[i]])
     assert plan.has_overlap == (sum(p.chunk.keys[0].shape[2] for p in pls) != sum(cached))
+    # the pooled bit: the reference's pool mask before escalation (torch_engine.py:128-139)
+    pool = np.zeros(N, dtype=bool)
+    for p in pls:
+        ratio = 0.15 if p.ratio is None else p.ratio
+        if not p.exact and ratio > 0:
+            pool[p.start : p.start + p.chunk.keys[0].shape[2]] = True
+    np.testing.assert_array_equal((plan.flags & POS_POOLED) != 0, pool)
+    np.testing.assert_array_equal(plan.flags & 7, np.asarray(cached) * 1 + np.asarray(sink) * 2 + np.asarray(exact) * 4)
 
 
 @pytest.mark.parametrize("seed", range(10))
