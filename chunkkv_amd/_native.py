@@ -101,6 +101,11 @@ SIGNATURES = {
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f64,
          _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p],
     ),
+    "ckv_deviation_select_noalloc": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f64,
+         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    ),
 }
 
 _lib = None

@@ -247,6 +247,27 @@ int32_t ckv_deviation_select(const void* k_fresh, int64_t kf_head_stride, int64_
                              void* stream);
 
 /*
+ * ckv_deviation_select without the workspace argument, for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
+ * in the reference. The workspace is a static device array of the library,
+ * CKV_DEVIATION_SELECT_WORKSPACE_BYTES (16640 bytes) per GPU, enough for every n_tokens the call
+ * takes (n_tokens > CKV_SELECT_MAX_TOKENS returns CKV_ERR_TOO_LARGE); its device address is looked
+ * up once per GPU on the first call there. The call allocates nothing. All calls on one GPU share
+ * that array, which every call leaves zeroed: calls that overlap on one GPU (different streams
+ * without ordering) race and must not be issued. Same arguments, results and errors as
+ * ckv_deviation_select otherwise.
+ */
+int32_t ckv_deviation_select_noalloc(const void* k_fresh, int64_t kf_head_stride, int64_t kf_token_stride,
+                                     const void* v_fresh, int64_t vf_head_stride, int64_t vf_token_stride,
+                                     const void* k_cache, const void* v_cache, int64_t cache_head_stride,
+                                     const uint8_t* pos_flags, const int32_t* local, int32_t n_tokens,
+                                     int32_t n_fresh, int32_t n_heads, int32_t head_dim, int32_t dtype,
+                                     const ckv_chunk_span* chunks, int32_t n_chunks, int32_t has_threshold,
+                                     double escalate_threshold, float* diff, float* norm, int64_t* keep_abs,
+                                     int64_t* keep_local, int32_t* keep_rank, float* rel_dev, uint8_t* escalated,
+                                     int32_t* counts, int32_t* err, void* stream);
+
+/*
  * Assemble one layer's cache with every row written once: for each segment row at position p,
  *   local[p] >= 0  -> K/V[h, p, :] = fresh k/v[h, local[p], :]            (an active position)
  *   otherwise      -> K/V[h, p, :] = the chunk's row, keys re-rotated by delta (as the gather)
