@@ -463,20 +463,25 @@ class _Tok:
     eos_token_id = 151645
 
 
-def bench_ttft(n_requests: int, dev) -> dict:
-    """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests. Both run
-    the model's library GEMMs with the same committed TunableOp selection table (when present)."""
+def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20) -> dict:
+    """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests, and of
+    HipEngine with the reference's own SDPA call (attention="reference": only the KV repair on the
+    HIP kernels, attention on PyTorch-ROCm, the north star's split) on the first
+    n_reference_attention of them. All run the model's library GEMMs with the same committed
+    TunableOp selection table (when present)."""
     from chunkkv_amd.baseline import TorchOpsEngine
     from chunkkv_amd.engine import HipEngine
     from chunkkv_amd.types import BlendConfig
 
-    t = time.perf_counter()
-    model = random_qwen25_7b(dev)
-    log(f"[bench] random-init Qwen2.5-7B architecture ready in {time.perf_counter() - t:.1f}s")
+    if model is None:
+        t = time.perf_counter()
+        model = random_qwen25_7b(dev)
+        log(f"[bench] random-init Qwen2.5-7B architecture ready in {time.perf_counter() - t:.1f}s")
     tuned = use_tuned_gemms()
     log(f"[bench] library GEMMs: {'tuned table (TunableOp, lookup only)' if tuned else 'default heuristics'} "
-        "for both engines")
+        "for all engines")
     hip, ref = HipEngine(model, _Tok()), TorchOpsEngine(model, _Tok())
+    hip_ref_attn = HipEngine(model, _Tok(), attention="reference")
     gen = torch.Generator().manual_seed(7)
     vocab = model.config.vocab_size
     # Chunk pool: each chunk prefilled alone at position 0 (its own context), stored like KVStore does.
@@ -497,9 +502,10 @@ def bench_ttft(n_requests: int, dev) -> dict:
         reqs.append((tokens, placements))
     cfg = BlendConfig(recompute_ratio=RATIO, n_sink=N_SINK)
     out = {}
-    for name, eng in (("hip", hip), ("torch_ops", ref)):
+    for name, eng, n_req in (("hip", hip, len(reqs)), ("torch_ops", ref, len(reqs)),
+                              ("hip_attention_reference", hip_ref_attn, min(len(reqs), n_reference_attention + 2))):
         times, stats = [], None
-        for i, (tokens, placements) in enumerate(reqs):
+        for i, (tokens, placements) in enumerate(reqs[:n_req]):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             res = eng.prefill(tokens, placements, cfg)
@@ -510,10 +516,11 @@ def bench_ttft(n_requests: int, dev) -> dict:
             stats = res.stats
             del res
         out[name] = dict(p50=float(np.percentile(times, 50)), p99=float(np.percentile(times, 99)), stats=stats,
-                         tuned_gemms=tuned)
+                         tuned_gemms=tuned, requests=len(times))
         log(f"[bench] TTFT {name}: p50 {out[name]['p50']:.2f} ms  p99 {out[name]['p99']:.2f} ms")
-    del hip, ref, model
+    del hip, ref, hip_ref_attn
     torch.cuda.empty_cache()
+    out["model"] = model
     return out
 
 
@@ -547,7 +554,7 @@ def bench_cpu(seconds: float) -> dict:
         times.append(time.perf_counter() - t0)
     assert len(keep) == 2976
     med = float(np.median(times))
-    return dict(value=repair_bytes(2976) / med / 1e9, unit="GB/s", cores=threads, kind="port",
+    return dict(value=repair_bytes(2976) / med / 1e9, unit="GB/s", cores=threads, kind="port", cpu_model=_cpu_model(),
                 sample=f"{len(times)} requests of the same workload (one request = 28-layer base_kv + layer-1 "
                        f"deviation/selection + 28 scatters), torch {torch.__version__} CPU eager, median "
                        f"{med * 1e3:.0f} ms/request")
@@ -649,10 +656,15 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         sels = [None] * DEV_SETS
         dns = [(torch.empty(N, device=dev), torch.empty(N, device=dev)) for _ in range(DEV_SETS)]
 
-        def dev_sel(i):
+        def dev_sel(i):  # one launch: ckv_deviation_select
             st = sets[i]
             sels[i] = ops.deviation_select(st["k"], st["v"], st["K"], st["V"], flags, local, spans, None, st["ws"],
                                            out=sels[i], diff_norm=dns[i])[2]
+
+        def dev_then_sel(i):  # two launches, as HipEngine issues them by default
+            st = sets[i]
+            d_, n_ = ops.deviation(st["k"], st["v"], st["K"], st["V"], flags, local)
+            sels[i] = ops.select(d_, n_, flags, local, spans, None, sels[i])
 
         def scat(i):
             st = sets[i]
@@ -664,13 +676,17 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         # one graph = every input set once (DEV_SETS launches back to back: a replay's own launch
         # cost is spread over them; what remains per launch is the kernel's time and its gaps)
         g_dev = _graph_of(lambda: [dev_sel(i) for i in range(DEV_SETS)])
+        assert all(int(sl.counts[0].item()) == n and int(sl.counts[7].item()) == 1 for sl in sels)
+        g_two = _graph_of(lambda: [dev_then_sel(i) for i in range(DEV_SETS)])
         g_sc = _graph_of(lambda: [scat(i) for i in range(DEV_SETS)])
-        g_both = _graph_of(lambda: [(dev_sel(i), scat(i)) for i in range(DEV_SETS)])
+        g_both = _graph_of(lambda: [(dev_then_sel(i), scat(i)) for i in range(DEV_SETS)])
         t_dev = _timed(lambda i: g_dev.replay(), steps, stream) / DEV_SETS
+        t_two = _timed(lambda i: g_two.replay(), steps, stream) / DEV_SETS
         t_sc = _timed(lambda i: g_sc.replay(), steps, stream) / DEV_SETS
         t_both = _timed(lambda i: g_both.replay(), steps, stream) / DEV_SETS
-        assert all(int(sl.counts[0].item()) == n and int(sl.counts[7].item()) == 1 for sl in sels)
-        out[ratio] = dict(n_keep=n, dev_sel_ms=t_dev, scatter_ms=t_sc, both_ms=t_both, scatter_bytes=n * ROW_BYTES * 4)
+        assert all(int(sl.counts[0].item()) == n for sl in sels)
+        out[ratio] = dict(n_keep=n, dev_sel_two_launches_ms=t_two, dev_sel_one_launch_ms=t_dev, scatter_ms=t_sc,
+                          both_ms=t_both, scatter_bytes=n * ROW_BYTES * 4)
     dev_bytes = N * 4 * ROW_BYTES + N * 8
     r30 = out[0.30]
     nb = dev_bytes + r30["scatter_bytes"]
@@ -678,14 +694,16 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         "deviation + pooled top-k + scatter HBM GB/s, Qwen2.5-7B KV shape", nb / (r30["both_ms"] * 1e-3) / 1e9,
         r30["both_ms"], steps, warmup,
         {"workload": "layer-1 deviation + pooled top-k (30%) + 4 sinks x 32 chunks x 256 + scatter of the kept rows, "
-                     "4 KV heads, head_dim 128, bf16; 16 input sets rotated (cold HBM)", "bytes_per_step": nb},
-        _rooffor("deviation_select_kernel<bf16,8> (deviation + top-k, one launch)", dev_bytes, r30["dev_sel_ms"]))
+                     "4 KV heads, head_dim 128, bf16; 16 input sets rotated (cold HBM); deviation and selection as "
+                     "two launches (the engine's default); the one-launch form is in ratios", "bytes_per_step": nb},
+        _rooffor("deviation_kernel<bf16> + select_reg_kernel<8> (deviation + top-k)", dev_bytes,
+                 r30["dev_sel_two_launches_ms"]))
     line["ratios"] = {str(r): {k2: (round(v2, 5) if isinstance(v2, float) else v2) for k2, v2 in o.items()}
                       for r, o in out.items()}
     return line
 
 
-def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests: int = 6) -> dict:
+def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests: int = 6, model=None) -> dict:
     """Long-context multi-request replay at the Qwen2.5-7B shape: an HBM-resident store of 256
     chunks x 256 tokens x 2 context variants (7.0 GiB); 4 concurrent requests of 128 chunks
     sampled with replacement (Zipf s=1.1) at random order + a 64-token query (32832 tokens), 15%
@@ -729,8 +747,7 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
                          spans=torch.from_numpy(plan.spans.reshape(-1)).to(dev),
                          layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), proj=proj,
                          fresh1=(torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16(),
-                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None,
-                         ws=ops.deviation_select_workspace(dev)))
+                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None))
     assert reqs[0]["plan"].budget == 4864
     streams = [torch.cuda.Stream() for _ in range(n_streams)]
 
@@ -742,8 +759,8 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         ops.rope_qkv(None, *rq["proj"][0], rq["layer0"], 0, N_KV, HEAD_DIM, THETA, k_out=K[0], v_out=V[0],
                      rows=rq["layer0"], table=cs_tab)
         k1, v1 = rq["fresh1"]
-        _, _, rq["sel"] = ops.deviation_select(k1, v1, K[1], V[1], rq["flags"], rq["local"], rq["spans"], None, rq["ws"],
-                                               out=rq["sel"])
+        d, n = ops.deviation(k1, v1, K[1], V[1], rq["flags"], rq["local"])
+        rq["sel"] = ops.select(d, n, rq["flags"], rq["local"], rq["spans"], None, rq["sel"])
         rows = rq["sel"].keep_abs[: plan.n_keep]
         ops.scatter_kept_rows(K[1], V[1], k1, v1, rows, rq["sel"].keep_local[: plan.n_keep])
         ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(2, N_LAYERS),
@@ -790,7 +807,9 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         from chunkkv_amd.engine import HipEngine
         from chunkkv_amd.types import BlendConfig
 
-        model = random_qwen25_7b(dev)
+        own_model = model is None
+        if own_model:
+            model = random_qwen25_7b(dev)
         use_tuned_gemms()
         hip = HipEngine(model, _Tok())
         cfg = BlendConfig(recompute_ratio=0.15, n_sink=N_SINK)
@@ -811,7 +830,9 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         line["ttft_requests"] = len(times)
         line["ttft_note"] = ("HipEngine, one request at a time; the reference op sequence is not timed at 32k "
                              "(its math-path SDPA would hold ~120 GB of fp32 scores per layer)")
-        del hip, model
+        del hip
+        if own_model:
+            del model
         torch.cuda.empty_cache()
     return line
 
@@ -1046,6 +1067,31 @@ def repair_bytes_for(plan) -> int:
             + (N_LAYERS - 1) * plan.n_keep * row * 4)
 
 
+def _config_summary(line: dict) -> dict:
+    """The figures of one microbenchmark line kept in the default line's `configs`."""
+    out = {"workload": line["config"]["workload"], "bytes_per_step": line["config"].get("bytes_per_step"),
+           "ms_per_step": line["ms_per_step"], "gbs": line["value"], "pct_of_peak": line["pct_of_peak"]}
+    if line.get("roofline"):
+        rf = line["roofline"]
+        out["roofline"] = {k: rf[k] for k in ("kernel", "achieved", "peak", "frac", "bytes_per_launch", "avg_launch_us")
+                           if k in rf}
+    for k in ("ratios", "store_gib", "ms_per_step_eager", "ttft_p50_ms", "ttft_p99_ms", "ttft_requests"):
+        if k in line:
+            out[k] = line[k]
+    return out
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1053,6 +1099,9 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ttft-requests", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config-2, config-3 and config-5 sub-measurements of the default line")
+    ap.add_argument("--replay-ttft-requests", type=int, default=20)
     ap.add_argument("--workload", default="request",
                     choices=["request", "gather", "deviation", "replay", "traffic", "dropped", "attention", "extract",
                              "decode"],
@@ -1073,10 +1122,24 @@ def main() -> None:
 
     r = bench_repair(args.steps, args.warmup, dev)
     log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_two']:.3f} ms two "
-        f"streams, {r['ms_asm']:.3f} ms assemble variant, {r['ms_eager']:.3f} ms eager); dropped-row gather "
-        f"{r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
+        f"streams, {r['ms_asm']:.3f} ms assemble variant, {r['ms_fused']:.3f} ms one-launch selection, "
+        f"{r['ms_eager']:.3f} ms eager); dropped-row gather {r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
         f"assemble {r['asm_gbs']:.1f} GB/s ({r['asm_ms'] * 1e3:.2f} us)")
+    configs = {}
+    if not args.no_configs:
+        sub_steps = min(args.steps, 30)
+        configs["config2_rerope_gather"] = _config_summary(bench_gather_only(sub_steps, args.warmup, dev))
+        log(f"[bench] config 2 {configs['config2_rerope_gather']}")
+        configs["config3_deviation_topk_scatter"] = _config_summary(bench_deviation_topk(sub_steps, args.warmup, dev))
+        log(f"[bench] config 3 {configs['config3_deviation_topk_scatter']}")
     ttft = bench_ttft(args.ttft_requests, dev) if args.ttft_requests > 0 else None
+    model = ttft.pop("model") if ttft is not None else None
+    if not args.no_configs:
+        configs["config5_replay"] = _config_summary(
+            bench_replay(min(args.steps, 20), args.warmup, dev, ttft_requests=args.replay_ttft_requests, model=model))
+        log(f"[bench] config 5 {configs['config5_replay']}")
+    del model
+    torch.cuda.empty_cache()
     cpu = bench_cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None
 
     line = {
@@ -1136,6 +1199,12 @@ def main() -> None:
         line["ttft_gemm_selection"] = "committed TunableOp table" if ttft["hip"]["tuned_gemms"] else "default heuristics"
         line["ttft_p99_ms_torch_ops"] = round(ttft["torch_ops"]["p99"], 2)
         line["ttft_requests"] = args.ttft_requests
+        # KV repair on the HIP kernels, attention on PyTorch-ROCm with the reference's own SDPA call
+        line["ttft_p50_ms_attention_reference"] = round(ttft["hip_attention_reference"]["p50"], 2)
+        line["ttft_p99_ms_attention_reference"] = round(ttft["hip_attention_reference"]["p99"], 2)
+        line["ttft_requests_attention_reference"] = ttft["hip_attention_reference"]["requests"]
+    if configs:
+        line["configs"] = configs
     print(json.dumps(line), flush=True)
 
 
