@@ -101,6 +101,7 @@ SIGNATURES = {
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f64,
          _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p],
     ),
+    "ckv_token_hash_prefixes": (_i32, [_p, _i64, _p, _i32, _p, _i32]),
     "ckv_deviation_select_noalloc": (
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f64,

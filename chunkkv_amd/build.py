@@ -21,7 +21,9 @@ LIB_DIR = PKG / "_lib"
 LIB_NAME = "libchunkkv_amd.so"
 SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "deviation_select.hip",
            "scatter.hip", "attention.hip", "rope.hip", "extract.hip", "norm.hip"]
+HOST_SOURCES = ["token_hash.cpp"]
 ARCH = "gfx950"
+GXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wextra"]
 
 # -ffp-contract=off: products and sums stay separately rounded, like the reference's torch ops.
 # -packed-fp32-ops disabled: no v_pk_*_f32 code generation (kept scalar fp32).
@@ -65,9 +67,13 @@ def build(verbose: bool = False) -> Path:
         cmd = [cc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
         _run(cmd, verbose)
         objs.append(str(obj))
+    for src in HOST_SOURCES:  # host-only C++ (no device code): the system compiler
+        obj = obj_dir / (Path(src).stem + ".o")
+        _run(["g++", *GXX_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)], verbose)
+        objs.append(str(obj))
     out = lib_path()
     tmp = out.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-pthread", "-o", str(tmp)], verbose)
     os.replace(tmp, out)
     return out
 

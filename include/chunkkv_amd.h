@@ -439,6 +439,21 @@ int32_t ckv_silu_mul(void* out, int64_t out_row_stride, const void* gate, int64_
                      const void* up, int64_t up_row_stride, int64_t n_rows, int32_t width, int32_t dtype,
                      void* stream);
 
+/*
+ * Token-prefix hashes (host memory, host code): digests[32*i .. 32*i + 32) = SHA-256 of the
+ * message LE32(s) || LE32(tokens[0]) || ... || LE32(tokens[s - 1]) with s = starts[i], i.e.
+ * the reference's keys.token_hash(tokens[:s]) as raw bytes (its hexdigest is their hex).
+ *   tokens     n_tokens ids; every id of a hashed prefix must lie in [0, 2^32)
+ *              (CKV_ERR_OUT_OF_RANGE otherwise, where the reference raises OverflowError)
+ *   starts     n_starts prefix lengths in [0, n_tokens]
+ *   n_threads  host threads to use, 0 = one per available core (at most 16)
+ * Replaces: keys.token_hash (src/chunkkv/store/keys.py:15-20) as called per segment by
+ *           ReuseGate.decide (src/chunkkv/gate/gate.py:42) and ChunkReuseRuntime.prefill
+ *           (src/chunkkv/runtime.py:89).
+ */
+int32_t ckv_token_hash_prefixes(const int64_t* tokens, int64_t n_tokens, const int64_t* starts,
+                                int32_t n_starts, uint8_t* digests, int32_t n_threads);
+
 #ifdef __cplusplus
 }
 #endif
