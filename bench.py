@@ -184,8 +184,6 @@ class RepairWorkload:
         self.dn = (torch.empty(N_TOKENS, dtype=torch.float32, device=dev),
                    torch.empty(N_TOKENS, dtype=torch.float32, device=dev))
         self.side = torch.cuda.Stream(device=dev)  # default priority
-        # the engine's per-position (cos, sin) table, built once per engine (not per request)
-        self.rope_tab = ops.rope_table(N_TOKENS, HEAD_DIM, THETA, dev)
 
     def gather(self):
         from chunkkv_amd import ops
@@ -219,7 +217,7 @@ class RepairWorkload:
         pos = self.layer0 if li == 0 else self.sel.keep_abs[: self.plan.n_keep]
         k_in, v_in = self.proj[li]
         ops.rope_qkv(None, k_in, v_in, pos, 0, N_KV, HEAD_DIM, THETA, k_out=self.k_slab[li], v_out=self.v_slab[li],
-                     rows=pos, table=self.rope_tab, err=self.err)
+                     rows=pos, err=self.err)
 
     def step(self, two_streams: bool = False):
         """One request's KV repair as HipEngine issues it (32 launches, in order on one stream):
@@ -726,7 +724,6 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
     zipf = 1.0 / np.arange(1, POOL + 1) ** 1.1
     zipf /= zipf.sum()
     rng = np.random.default_rng(11)
-    cs_tab = ops.rope_table(N, HEAD_DIM, THETA, dev)
     row = N_KV * HEAD_DIM
     reqs, placements_of = [], []
     for r in range(2 * n_streams):
@@ -757,7 +754,7 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         nseg, mseg = len(plan.segments), plan.max_seg_tokens
         ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(1, 2))
         ops.rope_qkv(None, *rq["proj"][0], rq["layer0"], 0, N_KV, HEAD_DIM, THETA, k_out=K[0], v_out=V[0],
-                     rows=rq["layer0"], table=cs_tab)
+                     rows=rq["layer0"])
         k1, v1 = rq["fresh1"]
         d, n = ops.deviation(k1, v1, K[1], V[1], rq["flags"], rq["local"])
         rq["sel"] = ops.select(d, n, rq["flags"], rq["local"], rq["spans"], None, rq["sel"])
@@ -766,8 +763,7 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(2, N_LAYERS),
                           skip=rq["sel"].keep_rank)
         for li in range(2, N_LAYERS):
-            ops.rope_qkv(None, *rq["proj"][li], rows, 0, N_KV, HEAD_DIM, THETA, k_out=K[li], v_out=V[li], rows=rows,
-                         table=cs_tab)
+            ops.rope_qkv(None, *rq["proj"][li], rows, 0, N_KV, HEAD_DIM, THETA, k_out=K[li], v_out=V[li], rows=rows)
 
     def round_(i):
         base = (i % 2) * n_streams

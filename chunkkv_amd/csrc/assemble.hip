@@ -38,7 +38,7 @@ __global__ __launch_bounds__(kAsmThreads) void assemble_kernel(
     char* dst_k, char* dst_v, int64_t dst_head_stride_b, const uint64_t* __restrict__ src_tab, int n_chunks,
     int n_layers, int layer, const ckv_segment* __restrict__ segs, const char* __restrict__ kf,
     int64_t kf_hs_b, int64_t kf_ts_b, const char* __restrict__ vf, int64_t vf_hs_b, int64_t vf_ts_b,
-    int n_fresh, const int32_t* __restrict__ local, int n_heads, int n_tokens, double theta,
+    int n_fresh, const int32_t* __restrict__ local, int n_heads, int n_tokens, const InvFreq inv,
     int32_t* __restrict__ err) {
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(kAsmThreads) void assemble_kernel(
       }
     }
     if (rotate && r0 == 0) {  // uniform; the table is built once, behind the first loads
-      if (threadIdx.x < HALF) cs_tab[threadIdx.x] = rope_shift_cos_sin(threadIdx.x, D, theta, s.delta);
+      if (threadIdx.x < HALF) cs_tab[threadIdx.x] = shift_cos_sin(inv.v[threadIdx.x], s.delta);
       __syncthreads();
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
@@ -152,7 +152,7 @@ static void launch_assemble(char* dk, char* dv, int64_t hs_b, const uint64_t* ta
                             hipStream_t st) {
   hipLaunchKernelGGL((assemble_kernel<DTYPE, D>), dim3((unsigned)n_segs, (unsigned)max_tiles), dim3(kAsmThreads), 0,
                      st, dk, dv, hs_b, tab, n_chunks, n_layers, layer, segs, kf, kf_hs_b, kf_ts_b, vf, vf_hs_b,
-                     vf_ts_b, n_fresh, local, n_heads, n_tokens, theta, err);
+                     vf_ts_b, n_fresh, local, n_heads, n_tokens, host_inv_freq(D, theta), err);
 }
 
 using AssembleFn = void (*)(char*, char*, int64_t, const uint64_t*, int, int, int, const ckv_segment*, int, int,

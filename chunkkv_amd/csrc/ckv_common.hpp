@@ -8,6 +8,7 @@
 #include <type_traits>
 
 #include "chunkkv_amd.h"
+#include "cos_sin.hpp"
 
 namespace ckv {
 
@@ -160,24 +161,69 @@ __device__ __forceinline__ void flag_error(int32_t* err, uint32_t bits) {
 
 // ---- rotary frequencies -------------------------------------------------------------------
 
-// inv_freq_i = fp32(theta_f ** e_i), e_i = fp32(-(2i) / D), evaluated in fp64 and rounded
-// once to fp32: the correctly rounded value of the reference's fp32 expression
-// `base ** (-arange(0, D, 2) / D)`.
-__device__ __forceinline__ float rope_inv_freq(int i, int head_dim, double theta) {
-  const float theta_f = (float)theta;
-  const float e = (float)(-2 * i) / (float)head_dim;
-  return (float)pow((double)theta_f, (double)e);
+// inv_freq_i = fp32(theta_f ** e_i), e_i = fp32(-(2i) / D), i < D/2: the reference's fp32
+// expression `base ** (-arange(0, D, 2) / D)` (torch_engine.py:33), evaluated on the host in fp64
+// (libm pow) and rounded once, as the reference computes it once per engine. Kernels take the
+// D/2 values by value in their arguments (no table in device memory, no pow on the device).
+constexpr int kMaxHalf = 128;  // head_dim <= 256
+struct alignas(16) InvFreq {
+  float v[kMaxHalf];
+};
+
+// The last (head_dim, theta) per host thread is kept: launches of one model reuse it.
+inline const InvFreq& host_inv_freq(int head_dim, double theta) {
+  static thread_local int c_dim = 0;
+  static thread_local double c_theta = 0.0;
+  static thread_local InvFreq c_val;
+  if (head_dim != c_dim || !(theta == c_theta)) {
+    const float theta_f = (float)theta;
+    for (int i = 0; i < kMaxHalf; ++i) {
+      const float e = (float)(-2 * i) / (float)head_dim;
+      c_val.v[i] = i < head_dim / 2 ? (float)std::pow((double)theta_f, (double)e) : 0.0f;
+    }
+    c_dim = head_dim;
+    c_theta = theta;
+  }
+  return c_val;
 }
 
-// cos/sin of the shift `delta` for frequency i: the fp32 angle fl32(fl32(delta) * inv_freq_i), as
-// torch forms `delta * inv_freq`, then cos/sin of that angle evaluated in fp64 and rounded once,
-// i.e. the correctly rounded fp32 values. (x = cos, y = sin.)
-__device__ __forceinline__ float2 rope_shift_cos_sin(int i, int head_dim, double theta, int delta) {
-  const float ang = (float)delta * rope_inv_freq(i, head_dim, theta);
-  double sd, cd;
-  sincos((double)ang, &sd, &cd);
-  return make_float2((float)cd, (float)sd);
+// cos/sin of an fp32 angle, each evaluated in fp64 and rounded once to fp32 (x = cos, y = sin):
+// the short reduction + series of cos_sin.hpp for |ang| < 2^31, the library's fp64 sincos beyond.
+__device__ __forceinline__ float2 angle_cos_sin(float ang) {
+  float c, s;
+  if (!cos_sin_fast(ang, c, s)) {
+    double sd, cd;
+    sincos((double)ang, &sd, &cd);
+    c = (float)cd;
+    s = (float)sd;
+  }
+  return make_float2(c, s);
 }
+
+// N angles at once: the fast evaluations first, without branches between them, then the library
+// sincos for any angle they do not cover (one branch, taken only for |angle| >= 2^31).
+template <int N>
+__device__ __forceinline__ void angles_cos_sin(const float (&ang)[N], float (&c)[N], float (&s)[N]) {
+  bool all = true;
+#pragma unroll
+  for (int e = 0; e < N; ++e) all = cos_sin_fast(ang[e], c[e], s[e]) && all;
+  if (!all) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      if (!(std::fabs(ang[e]) < 0x1p31f)) {
+        double sd, cd;
+        sincos((double)ang[e], &sd, &cd);
+        c[e] = (float)cd;
+        s[e] = (float)sd;
+      }
+    }
+  }
+}
+
+// cos/sin of the shift `delta` at inverse frequency inv: the fp32 angle fl32(fl32(delta) * inv),
+// as torch forms `delta * inv_freq`, then cos/sin of that angle evaluated in fp64 and rounded
+// once, i.e. the correctly rounded fp32 values. (x = cos, y = sin.)
+__device__ __forceinline__ float2 shift_cos_sin(float inv, int delta) { return angle_cos_sin((float)delta * inv); }
 
 // Rotate VEC frequency pairs held as two 16-byte vectors: a = first-half elements, b = the
 // matching second-half elements. y1 = a*cos - b*sin, y2 = a*sin + b*cos with every product and

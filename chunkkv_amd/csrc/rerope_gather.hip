@@ -15,8 +15,9 @@
 // (MLX twin: src/chunkkv/scheduler/rerope.py:31-61.)
 //
 // Design (gfx950): one workgroup = one (segment, token tile, layer). cos/sin depend only on
-// (delta, frequency index), so each workgroup builds a D/2-entry table in LDS once, from theta,
-// while its first 16-byte loads are in flight. The table holds the correctly rounded fp32 cos/sin
+// (delta, frequency index), so each workgroup builds a D/2-entry table in LDS once, from the
+// inverse frequencies (computed from theta on the host, passed by value in the kernel
+// arguments), while its first 16-byte loads are in flight. The table holds the correctly rounded fp32 cos/sin
 // of the fp32 angle (evaluated in fp64, rounded once). Every thread then rotates VEC frequency
 // pairs (the 16 bytes at column c of the first half and the matching 16 bytes of the second
 // half) of several rows. Memory traffic is exactly one read and one write of every gathered
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
     int64_t dst_head_stride_b, const uint64_t* __restrict__ src_tab, int n_chunks,
     const ckv_segment* __restrict__ segs, ckv_segment one_seg, uint64_t one_src_k,
     uint64_t one_src_v, int64_t one_src_head_stride_b, int n_layers, int layer_begin, int n_heads,
-    int n_tokens, const int32_t* __restrict__ skip, double theta, int32_t* __restrict__ err) {
+    int n_tokens, const int32_t* __restrict__ skip, const InvFreq inv, int32_t* __restrict__ err) {
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
   constexpr int HALF = D / 2;
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
   const bool rotate = s.delta != 0;
   float c[VEC], sn[VEC];
   if (rotate) {
-    if (threadIdx.x < HALF) cs_tab[threadIdx.x] = rope_shift_cos_sin(threadIdx.x, D, theta, s.delta);
+    if (threadIdx.x < HALF) cs_tab[threadIdx.x] = shift_cos_sin(inv.v[threadIdx.x], s.delta);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -204,10 +205,10 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
   }
 }
 
-// Writes the D/2 inverse frequencies the kernels above inline.
-__global__ void inv_freq_kernel(float* out, int head_dim, double theta) {
+// Writes the D/2 inverse frequencies the kernels above take in their arguments.
+__global__ void inv_freq_kernel(float* out, int head_dim, const InvFreq inv) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < head_dim / 2) out[i] = rope_inv_freq(i, head_dim, theta);
+  if (i < head_dim / 2) out[i] = inv.v[i];
 }
 
 template <int DTYPE, int D>
@@ -223,7 +224,7 @@ static void launch_gather(char* dk, char* dv, int64_t ls_b, int64_t hs_b, const 
                                      : dim3(tiles, (unsigned)n_segs, (unsigned)layer_count);
     hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D, S>), grid, dim3(S::kThreads), 0, st, dk, dv, ls_b, hs_b, tab,
                        n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, layer_begin, n_heads, n_tokens, skip,
-                       theta, err);
+                       host_inv_freq(D, theta), err);
   };
   if (n_segs >= kGatherWideSegs) go(GatherWide{});
   else if (skip != nullptr) go(GatherSkip{});
@@ -252,10 +253,11 @@ static int elem_bytes(int dtype) { return dtype == CKV_DTYPE_BF16 ? 2 : 4; }
 }  // namespace ckv
 
 extern "C" int32_t ckv_inv_freq(float* out, int32_t head_dim, double theta, void* stream) {
-  if (out == nullptr || head_dim <= 0 || (head_dim & 1) || !(theta > 0.0)) return CKV_ERR_INVALID_ARGUMENT;
+  if (out == nullptr || head_dim <= 0 || (head_dim & 1) || head_dim > 2 * ckv::kMaxHalf || !(theta > 0.0))
+    return CKV_ERR_INVALID_ARGUMENT;
   const int half = head_dim / 2;
   hipLaunchKernelGGL(ckv::inv_freq_kernel, dim3((half + 63) / 64), dim3(64), 0, (hipStream_t)stream, out,
-                     (int)head_dim, theta);
+                     (int)head_dim, ckv::host_inv_freq(head_dim, theta));
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

@@ -10,11 +10,12 @@
 // rounded fp32 cos/sin of that angle (evaluated in fp64), the same rotation ckv_shift_keys
 // applies for a shift by pos[t]; products and sums are separately rounded fp32 operations.
 //
-// Design (gfx950): with a per-position cos/sin table (built once by ckv_rope_table and kept by
-// the caller) one thread handles one (token, 16-byte item), grid-stride. Without a table, one
-// workgroup per token builds its D/2 cos/sin pairs in LDS while the token's first 16-byte loads
-// are in flight; then every (head, 16-byte column) pair of q and k
-// is rotated and stored, and the v row copied, with 16-byte accesses. The ~20 elementwise torch
+// Design (gfx950): no cos/sin table by default. cos/sin come from the inverse frequencies (host,
+// from theta, passed by value in the kernel arguments) and each token's position, evaluated in
+// fp64 with the short reduction + series of cos_sin.hpp. A k/v-only launch (the cache repair)
+// runs one wavefront per token, each lane evaluating one frequency once and the lanes sharing
+// them through ds_bpermute; a launch with q shares each evaluation over 4 heads. A caller-kept
+// per-position table (ckv_rope_table) is also accepted. All accesses are 16 bytes. The ~20 elementwise torch
 // launches of the reference's RoPE (fp32 temporaries, cat, cast) and the separate scatter of k/v
 // into the cache become one pass over the projection output.
 #include <algorithm>
@@ -25,85 +26,225 @@ namespace ckv {
 
 constexpr int kRopeThreads = 256;
 
+// Without a table, k/v only (the cache-repair launch): one wavefront per token (TW tokens when
+// D/2 < 64). An item is a 16-byte column pair (col, col + D/2) of one head row, rotated for k
+// heads and copied for v heads; a token of Hkv k and Hkv v heads has 2 Hkv D/2/VEC items (64 at
+// Hkv = 4, D = 128: one per lane). Lane l evaluates frequency l of its token once, from the
+// position (loaded first: vector loads complete in order) while the lane's row data is still in
+// flight, and the lanes fetch the VEC frequencies of their column from the evaluating lanes with
+// ds_bpermute: every (token, frequency) is evaluated exactly once, with no LDS and no barrier.
+constexpr int kWaveBatch = 2;  // items per lane whose loads go out before the cos/sin are built
+
 template <int DTYPE, int D>
-__global__ __launch_bounds__(kRopeThreads) void rope_qkv_kernel(
+__global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(
     char* __restrict__ q_out, int64_t qo_hs_b, int64_t qo_ts_b, char* __restrict__ k_out, int64_t ko_hs_b,
     int64_t ko_ts_b, char* __restrict__ v_out, int64_t vo_hs_b, int64_t vo_ts_b, const int64_t* __restrict__ rows,
     int n_out, const char* __restrict__ q_in, int64_t qi_hs_b, int64_t qi_ts_b, const char* __restrict__ k_in,
     int64_t ki_hs_b, int64_t ki_ts_b, const char* __restrict__ v_in, int64_t vi_hs_b, int64_t vi_ts_b,
-    const int64_t* __restrict__ pos, const float2* __restrict__ cs_table, int64_t n_table, int Hq, int Hkv,
-    double theta, int32_t* __restrict__ err) {
+    const int64_t* __restrict__ pos, const InvFreq inv, int n, int Hq, int Hkv, int32_t* __restrict__ err) {
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
   constexpr int HALF = D / 2;
-  constexpr int TPR = HALF / VEC;              // threads per rotated row
+  constexpr int TPR = HALF / VEC;  // items per head row
   constexpr int HALF_B = HALF * E::kBytes;
-  constexpr int CPR = D * E::kBytes / 16;      // 16-byte chunks per copied row
-  static_assert(HALF % VEC == 0 && kRopeThreads >= HALF, "head_dim out of range");
+  constexpr int TW = HALF >= kWave ? 1 : kWave / HALF;   // tokens per wavefront
+  constexpr int EVL = HALF >= kWave ? HALF / kWave : 1;  // evaluations per lane
+  static_assert(kWave % TPR == 0 && (HALF % kWave == 0 || kWave % HALF == 0), "head_dim out of range");
 
-  __shared__ float2 cs_tab[HALF];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t0 = (int)((blockIdx.x * (kRopeThreads / kWave) + threadIdx.x / kWave) * TW);
+  if (t0 >= n) return;  // uniform per wavefront
+  const int ntok = min(TW, n - t0);
+  const int n_rk = Hq + Hkv;                                    // rotated heads: q, then k
+  const int per = (n_rk + (v_out != nullptr ? Hkv : 0)) * TPR;  // items per token
+  const int total = ntok * per;
 
-  const int t = blockIdx.x;
-  const int64_t p = pos[t];
-  const int64_t row = rows != nullptr ? rows[t] : t;
-  if (p < INT32_MIN || p > INT32_MAX || row < 0 || row >= n_out ||
-      (cs_table != nullptr && (p < 0 || p >= n_table))) {  // uniform per workgroup
-    if (threadIdx.x == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
-    return;
+  // 1. positions and rows of the wavefront's tokens
+  int64_t pv[TW], rv[TW];
+#pragma unroll
+  for (int tl = 0; tl < TW; ++tl) {
+    const int t = t0 + min(tl, ntok - 1);
+    pv[tl] = pos[t];
+    rv[tl] = rows != nullptr ? rows[t] : t;
   }
-  const int n_rot = (Hq + Hkv) * TPR;  // q heads then k heads
-
+  // 2. the first kWaveBatch items' data, unconditionally (a lane past the end reloads the last
+  // item), so that no branch hides a load from the wait counters
   auto src_of = [&](int it) {
-    const int h = it / TPR, col = it % TPR;
-    return h < Hq ? q_in + h * qi_hs_b + t * qi_ts_b + col * 16
-                  : k_in + (h - Hq) * ki_hs_b + t * ki_ts_b + col * 16;
+    const int tl = it / per, k = it - tl * per;
+    const int h = k / TPR, col = k % TPR;
+    const int t = t0 + tl;
+    const char* base = h < Hq    ? q_in + h * qi_hs_b + t * qi_ts_b
+                       : h < n_rk ? k_in + (h - Hq) * ki_hs_b + t * ki_ts_b
+                                  : v_in + (h - n_rk) * vi_hs_b + t * vi_ts_b;
+    return base + col * 16;
   };
-  auto dst_of = [&](int it) {
-    const int h = it / TPR, col = it % TPR;
-    return h < Hq ? q_out + h * qo_hs_b + t * qo_ts_b + col * 16
-                  : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b + col * 16;
-  };
-
-  // First item's loads go out before the cos/sin are fetched or built (one item per thread at
-  // Hq+Hkv=32, D=128). With a table the pairs come straight from it (the row of position p, in
-  // L2 for all heads of the token); without one the workgroup builds them in LDS.
-  int it = threadIdx.x;
-  vec16 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-  if (it < n_rot) {
-    const char* s = src_of(it);
-    a = ld16(s);
-    b = ld16(s + HALF_B);
+  vec16 a[kWaveBatch], b[kWaveBatch];
+#pragma unroll
+  for (int j = 0; j < kWaveBatch; ++j) {
+    const char* src = src_of(min(lane + j * kWave, total - 1));
+    a[j] = ld16(src);
+    b[j] = ld16(src + HALF_B);
   }
-  const float2* trow = cs_table != nullptr ? cs_table + p * HALF : nullptr;
-  if (trow == nullptr) {  // uniform
-    if (threadIdx.x < HALF) cs_tab[threadIdx.x] = rope_shift_cos_sin(threadIdx.x, D, theta, (int)p);
-    __syncthreads();
-  }
-
-  for (; it < n_rot; it += kRopeThreads) {
-    if (it != (int)threadIdx.x) {
-      const char* s = src_of(it);
-      a = ld16(s);
-      b = ld16(s + HALF_B);
-    }
-    const int col = it % TPR;
-    float c[VEC], sn[VEC];
+  // 3. this lane's frequencies: token etl, frequencies lane (+ 64 j)
+  const int etl = HALF >= kWave ? 0 : lane / HALF;
+  int64_t pe = pv[0];
+#pragma unroll
+  for (int tl = 1; tl < TW; ++tl) pe = etl == tl ? pv[tl] : pe;
+  const int pp = pe >= INT32_MIN && pe <= INT32_MAX ? (int)pe : 0;
+  float ang[EVL], cv[EVL], sv[EVL];
+#pragma unroll
+  for (int j = 0; j < EVL; ++j) ang[j] = (float)pp * inv.v[HALF >= kWave ? lane + j * kWave : lane % HALF];
+  angles_cos_sin<EVL>(ang, cv, sv);
+  // 4. the VEC frequencies of this lane's column (the same column for all its items), per token
+  const int col = lane % TPR;
+  float c[TW][VEC], sn[TW][VEC];
+#pragma unroll
+  for (int tl = 0; tl < TW; ++tl) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float2 cs = trow != nullptr ? trow[col * VEC + e] : cs_tab[col * VEC + e];
-      c[e] = cs.x;
-      sn[e] = cs.y;
+      const int f = col * VEC + e;
+      const int src = HALF >= kWave ? f % kWave : tl * HALF + f;
+      float cc = __shfl(cv[0], src), ss = __shfl(sv[0], src);
+#pragma unroll
+      for (int j = 1; j < EVL; ++j) {
+        const float cj = __shfl(cv[j], src), sj = __shfl(sv[j], src);
+        cc = f / kWave == j ? cj : cc;
+        ss = f / kWave == j ? sj : ss;
+      }
+      c[tl][e] = cc;
+      sn[tl][e] = ss;
     }
-    vec16 y1, y2;
-    rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
-    char* d = dst_of(it);
-    st16(d, y1);
-    st16(d + HALF_B, y2);
   }
-  if (v_out != nullptr) {
-    for (int i = threadIdx.x; i < Hkv * CPR; i += kRopeThreads) {
-      const int h = i / CPR, c = i % CPR;
-      st16(v_out + h * vo_hs_b + row * vo_ts_b + c * 16, ld16(v_in + h * vi_hs_b + t * vi_ts_b + c * 16));
+  bool ok[TW];
+#pragma unroll
+  for (int tl = 0; tl < TW; ++tl) {
+    ok[tl] = tl < ntok && pv[tl] >= INT32_MIN && pv[tl] <= INT32_MAX && rv[tl] >= 0 && rv[tl] < n_out;
+    if (tl < ntok && !ok[tl] && lane == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+  }
+  // 5. rotate k (and q), copy v, store; items past the first kWaveBatch of a lane load here
+  for (int j0 = 0; lane + j0 * kWave < total; j0 += kWaveBatch) {
+#pragma unroll
+    for (int j = 0; j < kWaveBatch; ++j) {
+      const int it = lane + (j0 + j) * kWave;
+      if (it >= total) break;
+      if (j0 > 0) {
+        const char* src = src_of(it);
+        a[j] = ld16(src);
+        b[j] = ld16(src + HALF_B);
+      }
+      const int tl = it / per, h = (it - tl * per) / TPR;
+      bool okt = ok[0];
+      int64_t row = rv[0];
+#pragma unroll
+      for (int u = 1; u < TW; ++u) {
+        okt = tl == u ? ok[u] : okt;
+        row = tl == u ? rv[u] : row;
+      }
+      if (!okt) continue;
+      const int t = t0 + tl;
+      char* d = (h < Hq    ? q_out + h * qo_hs_b + t * qo_ts_b
+                 : h < n_rk ? k_out + (h - Hq) * ko_hs_b + row * ko_ts_b
+                            : v_out + (h - n_rk) * vo_hs_b + row * vo_ts_b) +
+                col * 16;
+      vec16 y1 = a[j], y2 = b[j];
+      if (h < n_rk) {
+        float cc[VEC], ss[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          cc[e] = c[0][e];
+          ss[e] = sn[0][e];
+#pragma unroll
+          for (int u = 1; u < TW; ++u) {
+            cc[e] = tl == u ? c[u][e] : cc[e];
+            ss[e] = tl == u ? sn[u][e] : ss[e];
+          }
+        }
+        rotate_pairs<DTYPE>(a[j], b[j], cc, ss, y1, y2);
+      }
+      st16(d, y1);
+      st16(d + HALF_B, y2);
+    }
+  }
+}
+
+// Without a table, with q (32+ rotated heads share each token's cos/sin): one thread per
+// (token, 16-byte column, group of kRopeFreeHG heads), grid-stride, evaluating its VEC
+// frequencies itself (kRopeFreeHG-fold sharing), v copied in 16-byte chunks. The thread's loads go
+// out in the order their values are needed (position, row, inverse frequencies, data) and it
+// branches on none of them before its stores.
+constexpr int kRopeFreeHG = 4;
+
+template <int DTYPE, int D>
+__global__ __launch_bounds__(kRopeThreads) void rope_free_kernel(
+    char* __restrict__ q_out, int64_t qo_hs_b, int64_t qo_ts_b, char* __restrict__ k_out, int64_t ko_hs_b,
+    int64_t ko_ts_b, char* __restrict__ v_out, int64_t vo_hs_b, int64_t vo_ts_b, const int64_t* __restrict__ rows,
+    int n_out, const char* __restrict__ q_in, int64_t qi_hs_b, int64_t qi_ts_b, const char* __restrict__ k_in,
+    int64_t ki_hs_b, int64_t ki_ts_b, const char* __restrict__ v_in, int64_t vi_hs_b, int64_t vi_ts_b,
+    const int64_t* __restrict__ pos, const InvFreq inv, int n, int Hq, int Hkv, int32_t* __restrict__ err) {
+  using E = Elem<DTYPE>;
+  constexpr int VEC = E::kVec;
+  constexpr int HALF = D / 2;
+  constexpr int TPR = HALF / VEC;
+  constexpr int HALF_B = HALF * E::kBytes;
+  constexpr int CPR = D * E::kBytes / 16;
+  constexpr int HG = kRopeFreeHG;
+  typedef __attribute__((address_space(1))) const int64_t gi64;
+  const int n_heads = Hq + Hkv;
+  const unsigned n_rot = (unsigned)((n_heads + HG - 1) / HG * TPR);  // rotation items per token
+  const unsigned n_cp = v_out != nullptr ? (unsigned)(Hkv * CPR) : 0u;  // copy items per token
+  const unsigned rot_total = (unsigned)n * n_rot;
+  const unsigned total = rot_total + (unsigned)n * n_cp;  // < 2^31, checked by the host
+  for (unsigned idx = blockIdx.x * kRopeThreads + threadIdx.x; idx < total; idx += gridDim.x * kRopeThreads) {
+    const bool rot = idx < rot_total;
+    const unsigned j = rot ? idx : idx - rot_total;
+    const unsigned per = rot ? n_rot : n_cp;
+    const int t = (int)(j / per), it = (int)(j - (unsigned)t * per);
+    const int64_t p = *(gi64*)(pos + t);
+    const int64_t row = rows != nullptr ? *(gi64*)(rows + t) : t;
+    if (rot) {
+      const int h0 = (it / TPR) * HG, col = it % TPR;
+      float iv[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; e += 4) {
+        const vec16 w = *reinterpret_cast<const vec16*>(&inv.v[col * VEC + e]);
+        iv[e] = __uint_as_float(w[0]);
+        iv[e + 1] = __uint_as_float(w[1]);
+        iv[e + 2] = __uint_as_float(w[2]);
+        iv[e + 3] = __uint_as_float(w[3]);
+      }
+      vec16 a[HG], b[HG];
+#pragma unroll
+      for (int jj = 0; jj < HG; ++jj) {
+        const int h = min(h0 + jj, n_heads - 1);
+        const char* s = (h < Hq ? q_in + h * qi_hs_b + t * qi_ts_b : k_in + (h - Hq) * ki_hs_b + t * ki_ts_b) +
+                        col * 16;
+        a[jj] = ld16(s);
+        b[jj] = ld16(s + HALF_B);
+      }
+      const bool ok = p >= INT32_MIN && p <= INT32_MAX && row >= 0 && row < n_out;
+      const int pp = ok ? (int)p : 0;
+      float ang[VEC], c[VEC], sn[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ang[e] = (float)pp * iv[e];
+      angles_cos_sin<VEC>(ang, c, sn);
+#pragma unroll
+      for (int jj = 0; jj < HG; ++jj) {
+        const int h = h0 + jj;
+        vec16 y1, y2;
+        rotate_pairs<DTYPE>(a[jj], b[jj], c, sn, y1, y2);
+        if (ok && h < n_heads) {
+          char* d = (h < Hq ? q_out + h * qo_hs_b + t * qo_ts_b : k_out + (h - Hq) * ko_hs_b + row * ko_ts_b) +
+                    col * 16;
+          st16(d, y1);
+          st16(d + HALF_B, y2);
+        }
+      }
+      if (!ok && it == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+    } else {
+      const int h = it / CPR, c = it % CPR;
+      const vec16 x = ld16(v_in + h * vi_hs_b + t * vi_ts_b + c * 16);
+      const bool ok = p >= INT32_MIN && p <= INT32_MAX && row >= 0 && row < n_out;
+      if (ok) st16(v_out + h * vo_hs_b + row * vo_ts_b + c * 16, x);
     }
   }
 }
@@ -208,9 +349,22 @@ static void launch_rope(int n, hipStream_t st, char* qo, int64_t qo_hs, int64_t 
                        vi_hs, vi_ts, pos, tab, n_tab, n, Hq, Hkv, err);
     return;
   }
-  hipLaunchKernelGGL((rope_qkv_kernel<DTYPE, D>), dim3((unsigned)n), dim3(kRopeThreads), 0, st, qo, qo_hs, qo_ts, ko,
-                     ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, qi, qi_hs, qi_ts, ki, ki_hs, ki_ts, vi, vi_hs,
-                     vi_ts, pos, tab, n_tab, Hq, Hkv, theta, err);
+  const InvFreq& inv = host_inv_freq(D, theta);
+  if (Hq == 0) {
+    constexpr int TW = D / 2 >= kWave ? 1 : kWave / (D / 2);
+    const int per_wg = (kRopeThreads / kWave) * TW;
+    hipLaunchKernelGGL((rope_wave_kernel<DTYPE, D>), dim3((unsigned)((n + per_wg - 1) / per_wg)), dim3(kRopeThreads),
+                       0, st, qo, qo_hs, qo_ts, ko, ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, qi, qi_hs, qi_ts, ki,
+                       ki_hs, ki_ts, vi, vi_hs, vi_ts, pos, inv, n, Hq, Hkv, err);
+    return;
+  }
+  using E = Elem<DTYPE>;
+  const int64_t per_tok = (int64_t)(Hq + Hkv + kRopeFreeHG - 1) / kRopeFreeHG * (D / 2 / E::kVec) +
+                          (vo != nullptr ? Hkv * (D * E::kBytes / 16) : 0);
+  const int64_t blocks = std::min<int64_t>((n * per_tok + kRopeThreads - 1) / kRopeThreads, 1 << 20);
+  hipLaunchKernelGGL((rope_free_kernel<DTYPE, D>), dim3((unsigned)blocks), dim3(kRopeThreads), 0, st, qo, qo_hs, qo_ts,
+                     ko, ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, qi, qi_hs, qi_ts, ki, ki_hs, ki_ts, vi, vi_hs,
+                     vi_ts, pos, inv, n, Hq, Hkv, err);
 }
 
 typedef void (*RopeLaunch)(int, hipStream_t, char*, int64_t, int64_t, char*, int64_t, int64_t, char*, int64_t,
@@ -232,23 +386,24 @@ static RopeLaunch pick_rope(int dtype, int head_dim) {
 }
 
 // table[p][i] = (cos, sin) of the fp32 angle fl32(fl32(p) * inv_freq_i), correctly rounded.
-__global__ void rope_table_kernel(float2* __restrict__ tab, int64_t n_pos, int head_dim, double theta) {
+__global__ void rope_table_kernel(float2* __restrict__ tab, int64_t n_pos, int head_dim, const InvFreq inv) {
   const int half = head_dim / 2;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n_pos * half) tab[i] = rope_shift_cos_sin((int)(i % half), head_dim, theta, (int)(i / half));
+  if (i < n_pos * half) tab[i] = shift_cos_sin(inv.v[i % half], (int)(i / half));
 }
 
 }  // namespace ckv
 
 extern "C" int32_t ckv_rope_table(void* table, int64_t n_positions, int32_t head_dim, double theta, void* stream) {
   using namespace ckv;
-  if (table == nullptr || n_positions < 0 || head_dim <= 0 || (head_dim & 1) || head_dim > 512 || !(theta > 0.0))
+  if (table == nullptr || n_positions < 0 || head_dim <= 0 || (head_dim & 1) || head_dim > 2 * kMaxHalf ||
+      !(theta > 0.0))
     return CKV_ERR_INVALID_ARGUMENT;
   if (n_positions > 0x7fffffff) return CKV_ERR_TOO_LARGE;
   const int64_t total = n_positions * (head_dim / 2);
   if (total == 0) return CKV_OK;
   hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     (float2*)table, n_positions, (int)head_dim, theta);
+                     (float2*)table, n_positions, (int)head_dim, host_inv_freq(head_dim, theta));
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }
@@ -271,7 +426,7 @@ extern "C" int32_t ckv_rope_qkv(void* q_out, int64_t qo_head_stride, int64_t qo_
     return CKV_ERR_INVALID_ARGUMENT;
   if (rows == nullptr && n_out_rows < n_tokens) return CKV_ERR_OUT_OF_RANGE;
   if (cs_table != nullptr && (n_table < 0 || (uintptr_t)cs_table % 16)) return CKV_ERR_INVALID_ARGUMENT;
-  if (cs_table != nullptr && (int64_t)n_tokens * ((n_q_heads + n_kv_heads) * 64 + n_kv_heads * 64) >= (1ll << 31))
+  if ((int64_t)n_tokens * ((n_q_heads + n_kv_heads) * 64 + n_kv_heads * 64) >= (1ll << 31))
     return CKV_ERR_TOO_LARGE;  // the flattened (token, item) index stays below 2^31
   const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
   const int64_t strides[] = {qo_head_stride, qo_token_stride, ko_head_stride, ko_token_stride, vo_head_stride,

@@ -133,7 +133,6 @@ class HipEngine(DecoderPieces):
         # 42.38 ms p50) and it lengthens the KV-repair launches' own span (0.320 vs 0.314 ms).
         self.overlap = overlap
         self._side: torch.cuda.Stream | None = None
-        self._rope_tab: torch.Tensor | None = None  # (cos, sin) per position, grown on demand
         self._ws: dict[int, torch.Tensor] = {}  # deviation_select workspaces, per stream
         # generate(): replay each decode step after the first from a HIP graph (device-side loop)
         self.decode_graphs = True
@@ -329,14 +328,6 @@ class HipEngine(DecoderPieces):
             ws = self._ws[st] = ops.deviation_select_workspace(self.device)
         return ws
 
-    def _table(self, n: int) -> torch.Tensor:
-        """Per-position (cos, sin) table covering positions [0, n), kept across requests."""
-        if self._rope_tab is None or self._rope_tab.shape[0] < n:
-            size = max(n, 4096)
-            size = (size + 4095) // 4096 * 4096
-            self._rope_tab = ops.rope_table(size, self.head_dim, self.theta, self.device)
-        return self._rope_tab
-
     def _project(self, li: int, x: torch.Tensor):
         """q|k|v projection of layer li in one GEMM: views (1, n, H*D) of its token-major output."""
         lin = F.linear(x, self._w_qkv[li], self._b_qkv[li])
@@ -390,7 +381,6 @@ class HipEngine(DecoderPieces):
         for li in range(L):
             Ks[li, :, :, :N].copy_(result.keys[li])
             Vs[li, :, :, :N].copy_(result.values[li])
-        tab = self._table(cap)
         err = torch.zeros(1, dtype=torch.int32, device=dev)
         device_loop = self._native_attention and self.attention == "fused"
         tok = torch.tensor([[nxt]], dtype=torch.int64, device=dev)
@@ -399,21 +389,21 @@ class HipEngine(DecoderPieces):
         while len(out) < max_tokens and nxt not in self.eos:
             out.append(nxt)
             if not device_loop:
-                self._decode_step_sdpa(tok, N + len(out) - 1, Ks, Vs, tab, err)
+                self._decode_step_sdpa(tok, N + len(out) - 1, Ks, Vs, err)
             elif graph is not None:
                 graph.replay()
             else:
-                self._decode_step(tok, where, Ks, Vs, tab, err)  # also the warm-up of the capture
+                self._decode_step(tok, where, Ks, Vs, err)  # also the warm-up of the capture
                 if max_tokens - len(out) >= 2 and self.decode_graphs:
                     graph = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(graph):
-                        self._decode_step(tok, where, Ks, Vs, tab, err)
+                        self._decode_step(tok, where, Ks, Vs, err)
             nxt = int(tok.item())
         if int(err.item()) != 0:
             raise RuntimeError("a decode kernel reported an out-of-range position")
         return out
 
-    def _decode_step(self, tok, where, Ks, Vs, tab, err) -> None:
+    def _decode_step(self, tok, where, Ks, Vs, err) -> None:
         """One token (tok: (1, 1) int64 at position where: (1,) int64) through every layer; writes
         the next greedy token into tok and advances where. No host values are read."""
         H, D = self.n_kv, self.head_dim
@@ -422,13 +412,13 @@ class HipEngine(DecoderPieces):
             h, x = self._norm(li, layer, h, pending)
             q_in, k_in, v_in = self._project(li, x)
             q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=Ks[li], v_out=Vs[li],
-                                rows=where, table=tab, err=err)
+                                rows=where, err=err)
             o = ops.attention_active(q.transpose(1, 2), Ks[li], Vs[li], where, err=err)
             h, pending = self._mlp(li, layer, h, layer.self_attn.o_proj(o.view(1, 1, -1)))
         tok.copy_(self._final_logits(h, pending)[0, -1].argmax().view(1, 1))
         where.add_(1)
 
-    def _decode_step_sdpa(self, tok, pos: int, Ks, Vs, tab, err) -> None:
+    def _decode_step_sdpa(self, tok, pos: int, Ks, Vs, err) -> None:
         """_decode_step for models outside the attention kernel's range (SDPA over rows <= pos)."""
         H, D = self.n_kv, self.head_dim
         where = torch.tensor([pos], dtype=torch.int64, device=self.device)
@@ -437,7 +427,7 @@ class HipEngine(DecoderPieces):
             h, x = self._norm(li, layer, h, pending)
             q_in, k_in, v_in = self._project(li, x)
             q, _ = ops.rope_qkv(q_in, k_in, v_in, where, self.n_heads, H, D, self.theta, k_out=Ks[li], v_out=Vs[li],
-                                rows=where, table=tab, err=err)
+                                rows=where, err=err)
             o = F.scaled_dot_product_attention(q.transpose(1, 2), Ks[li][:, :, : pos + 1], Vs[li][:, :, : pos + 1],
                                                enable_gqa=True)
             h, pending = self._mlp(li, layer, h, layer.self_attn.o_proj(o.transpose(1, 2).reshape(1, 1, -1)))
@@ -496,7 +486,6 @@ class HipEngine(DecoderPieces):
         masks: dict = {}
         sel = None
         ready: dict[int, torch.cuda.Event | None] = {}  # layer -> its cached rows are in place
-        tab = self._table(N)
         gather = lambda layers, skip: self._gather(  # noqa: E731
             k_slab, v_slab, tab_d, segs_d, n_cached_segs, plan.max_seg_tokens, layers, skip, err)
         # Cached rows that do not depend on the model go out first (overlap=True: beside layer 0):
@@ -519,7 +508,7 @@ class HipEngine(DecoderPieces):
                 q_in, k_in, v_in = self._project(li, x)
             K, V = keys_out[li], values_out[li]
             if li == 1 and select_layer:
-                q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, table=tab, err=err)
+                q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, err=err)
                 v = v_in.view(1, -1, H, D).transpose(1, 2)
                 if ready.get(1) is not None:
                     torch.cuda.current_stream(dev).wait_event(ready[1])
@@ -549,7 +538,7 @@ class HipEngine(DecoderPieces):
             else:
                 # RoPE of q/k with k and v written straight into this layer's cache rows
                 q, _ = ops.rope_qkv(q_in, k_in, v_in, active, self.n_heads, H, D, self.theta, k_out=K, v_out=V,
-                                    rows=active, table=tab, err=err)
+                                    rows=active, err=err)
                 if ready.get(li) is not None:
                     torch.cuda.current_stream(dev).wait_event(ready[li])
             h, pending = self._attend_active(li, layer, h, q, K, V, active, ar, masks, err)

@@ -501,7 +501,8 @@ def rope_qkv(
     Returns (q_out, k_out): q_out (1, n, Hq, D) token-major (the layout attention_active reads)
     unless given; k_out (1, Hkv, n, D) unless given. With rows (int64 (n,)), k/v land in rows
     rows[t] of k_out/v_out, e.g. the layer's cache (1, Hkv, N, D): the fresh-row scatter fused in.
-    table: a rope_table() covering every position (same results, no per-call cos/sin evaluation).
+    table: optional rope_table() covering every position (the same results). Without one (the
+    default, and what HipEngine does) the kernel evaluates cos/sin from theta and the positions.
     """
     if table is not None:
         _dev(k_in, table)

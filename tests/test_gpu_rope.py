@@ -108,17 +108,45 @@ def test_rope_qkv_kv_only():
     np.testing.assert_array_equal(O.to_numpy(V)[0][:, pos], _heads(vn, Hkv, D))
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 def test_rope_table_matches_oracle(D):
     """ckv_rope_table equals the oracle's cos/sin (read off a rotation of unit vectors: x1 = 1,
-    x2 = 0 gives y1 = cos, y2 = sin exactly)."""
-    N = 5000
+    x2 = 0 gives y1 = cos, y2 = sin exactly): every frequency at 65,536 positions."""
+    N = 1 << 16
     tab = O.to_numpy(ops.rope_table(N, D, THETA, DEV))
     x = np.zeros((1, N, D), np.float32)
     x[..., : D // 2] = 1.0
     y = O.rope(x, np.arange(N), THETA)[0]
     np.testing.assert_array_equal(tab[..., 0].view(np.uint32), y[:, : D // 2].view(np.uint32))
     np.testing.assert_array_equal(tab[..., 1].view(np.uint32), y[:, D // 2 :].view(np.uint32))
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 28, 4), (64, 0, 2), (256, 2, 1)])
+def test_rope_rows_far_and_negative_positions(D, Hq, Hkv):
+    """The table-free path (cos/sin evaluated per token) at positions anywhere in int32, negative
+    ones included, where angles reach 2^31: q and k bit-exact against the oracle, v copied."""
+    rng = np.random.default_rng(D + 7 * Hq)
+    n = 700
+    pos = rng.integers(-(2**31), 2**31, n)
+    pos[:6] = [0, 1, -1, 2**31 - 1, -(2**31), 2**20]
+    lin = _proj(rng, n, Hq, Hkv, D, True)
+    lt = O.from_numpy(lin, DEV)
+    q_in, k_in, v_in = _split(lt, Hq, Hkv, D)
+    pt = torch.from_numpy(pos).to(DEV)
+    out = torch.zeros((1, Hkv, n, D), dtype=torch.bfloat16, device=DEV)
+    vout = torch.zeros_like(out)
+    rows = torch.arange(n, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    q, _ = ops.rope_qkv(q_in if Hq else None, k_in, v_in, pt, Hq, Hkv, D, THETA, k_out=out, v_out=vout, rows=rows,
+                        err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    qn, kn, vn = _split(lin, Hq, Hkv, D)
+    np.testing.assert_array_equal(O.to_numpy(out)[0], O.rope(_heads(kn, Hkv, D), pos, THETA))
+    np.testing.assert_array_equal(O.to_numpy(vout)[0], _heads(vn, Hkv, D))
+    if Hq:
+        want_q = O.rope(_heads(qn, Hq, D), pos, THETA)
+        np.testing.assert_array_equal(O.to_numpy(q)[0], want_q.transpose(1, 0, 2))
 
 
 def test_rope_qkv_with_table_identical_and_bounds():
