@@ -835,14 +835,16 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
 
 def traffic_probe(steps: int, warmup: int, dev) -> dict:
     """Dispatches for the HBM traffic counters (run under rocprofv3 --pmc): `steps` re-RoPE +
-    gather launches of the 8k request alternating two input sets, then `steps` elementwise kernels
-    that read and write exactly COPY_BYTES each, whose FETCH_SIZE / WRITE_SIZE calibrate the
-    counters (a plain D2D copy goes to the DMA engine and is not counted)."""
+    gather launches of the 8k request alternating two input sets, `steps` request steps (the
+    fresh-row writes, the layer-1 deviation, selection and scatter as the step issues them),
+    `steps` dropped-row gathers, then `steps` elementwise kernels that read and write exactly
+    COPY_BYTES each, whose FETCH_SIZE / WRITE_SIZE calibrate the counters (a plain D2D copy goes to
+    the DMA engine and is not counted)."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
     for i in range(steps):
         wls[i % 2].gather()
-    for w in wls:
-        w.step()  # selection output for the launches below
+    for i in range(max(steps, 2)):
+        wls[i % 2].step()  # also the selection output for the launches below
     torch.cuda.synchronize()
     for i in range(steps):
         wls[i % 2].gather_dropped()

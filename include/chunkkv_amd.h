@@ -109,9 +109,10 @@ int32_t ckv_abi_version(void);
 const char* ckv_status_string(int32_t status);
 
 /*
- * Rotary inverse frequencies, computed on the device by the same function the re-RoPE
- * kernels inline: out[i] = fp32(theta_f ** e_i) correctly rounded, with
- * theta_f = fp32(theta) and e_i = fp32(-(2i) / head_dim), i in [0, head_dim/2).
+ * Rotary inverse frequencies, the values every rotary kernel of this library takes in its
+ * arguments: out[i] = fp32(theta_f ** e_i), evaluated on the host in fp64 (libm pow) and
+ * rounded once, with theta_f = fp32(theta) and e_i = fp32(-(2i) / head_dim),
+ * i in [0, head_dim/2), head_dim <= 256. Written to out on the stream.
  * Replaces: TorchEngine.__init__ inv_freq (torch_engine.py:33); scheduler/rerope.py:31-33.
  * out: head_dim/2 floats.
  */
