@@ -181,6 +181,7 @@ class RepairWorkload:
             .to(dev) for _ in range(2)) for li in range(N_LAYERS)]
         self.sel = None
         self.ws = ops.deviation_select_workspace(dev)
+        self.ws1 = ops.layer1_repair_workspace(dev)
         self.dn = (torch.empty(N_TOKENS, dtype=torch.float32, device=dev),
                    torch.empty(N_TOKENS, dtype=torch.float32, device=dev))
         self.side = torch.cuda.Stream(device=dev)  # default priority
@@ -219,17 +220,18 @@ class RepairWorkload:
         ops.rope_qkv(None, k_in, v_in, pos, 0, N_KV, HEAD_DIM, THETA, k_out=self.k_slab[li], v_out=self.v_slab[li],
                      rows=pos, err=self.err)
 
+    layer1_mode = "one"  # as HipEngine: layer 1's whole repair in one launch (ckv_layer1_repair)
+
     def step(self, two_streams: bool = False):
-        """One request's KV repair as HipEngine issues it (32 launches, in order on one stream):
-        layer 1's base cache, layer 0's fresh rows, the layer-1 deviation, selection and scatter of
-        the kept rows, the gather of the dropped rows of layers 2-27, those layers' fresh rows.
-        two_streams=True issues the two gathers on a second stream instead, as
-        HipEngine(overlap=True) does (the base cache beside layer 0's rows, the dropped rows beside
-        the fresh rows of layers 2-27: disjoint rows)."""
+        """One request's KV repair as HipEngine issues it (29 launches, in order on one stream):
+        layer 0's fresh rows; layer 1's base cache, deviation, selection and kept rows in one launch;
+        the gather of the dropped rows of layers 2-27; those layers' fresh rows. With layer1_mode
+        "split", layer 1 is the four launches that launch replaces (base cache, deviation, selection,
+        kept-row scatter). two_streams=True issues the gathers on a second stream instead, as
+        HipEngine(overlap=True) does (beside the fresh rows they do not touch)."""
         from chunkkv_amd import ops
 
         plan = self.plan
-        K, V = self.k_slab.unbind(0), self.v_slab.unbind(0)
         main = torch.cuda.current_stream()
 
         def fork(fn):
@@ -239,43 +241,51 @@ class RepairWorkload:
             with torch.cuda.stream(self.side):
                 fn()
 
-        fork(lambda: ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(plan.segments),
-                                       plan.max_seg_tokens, THETA, self.err, layers=(1, 2)))
-        self.kv_rows(0)
-        if two_streams:
-            main.wait_stream(self.side)
-        self.layer1()
+        if self.layer1_mode == "one":
+            self.kv_rows(0)
+            self.layer1_one()
+        else:
+            fork(lambda: ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(plan.segments),
+                                           plan.max_seg_tokens, THETA, self.err, layers=(1, 2)))
+            self.kv_rows(0)
+            if two_streams:
+                main.wait_stream(self.side)
+            self.layer1()
         fork(self.gather_dropped)
         for li in range(2, N_LAYERS):
             self.kv_rows(li)
         if two_streams:
             main.wait_stream(self.side)
 
-    fused_select = False  # as HipEngine: deviation and selection as two launches by default
+    def layer1_one(self):
+        """Layer 1's whole repair in one launch: the cached rows re-rotated from the chunk store,
+        the deviation, the selection, the kept rows from the fresh rows (ckv_layer1_repair)."""
+        from chunkkv_amd import ops
+
+        k1, v1 = self.fresh[1]
+        _, _, self.sel = ops.layer1_repair(self.k_slab[1], self.v_slab[1], self.tab, N_LAYERS, 1, self.segs,
+                                           len(self.plan.segments), k1, v1, self.flags, self.local, self.spans, None,
+                                           THETA, self.ws1, self.err, self.sel, self.dn)
 
     def layer1(self):
-        """Layer 1 after its base cache: the deviation and the selection (two launches, or one
-        with fused_select), then the kept rows compacted and scattered into the cache."""
+        """Layer 1 after its base cache, as three launches: the deviation, the selection, the kept
+        rows compacted and scattered into the cache."""
         from chunkkv_amd import ops
 
         n = self.plan.n_keep
         K, V = self.k_slab[1], self.v_slab[1]
         k1, v1 = self.fresh[1]
-        if self.fused_select:
-            _, _, self.sel = ops.deviation_select(k1, v1, K, V, self.flags, self.local, self.spans, None, self.ws,
-                                                  self.err, self.sel, self.dn)
-        else:
-            diff, norm = ops.deviation(k1, v1, K, V, self.flags, self.local, self.err)
-            self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
+        diff, norm = ops.deviation(k1, v1, K, V, self.flags, self.local, self.err)
+        self.sel = ops.select(diff, norm, self.flags, self.local, self.spans, None, self.sel)
         ops.scatter_kept_rows(K, V, k1, v1, self.sel.keep_abs[:n], self.sel.keep_local[:n], self.err)
 
-    def step_fused_select(self):
-        """The step with the layer-1 deviation and selection in one launch (ckv_deviation_select)."""
-        self.fused_select = True
+    def step_split(self):
+        """The step with layer 1 as the four launches ckv_layer1_repair replaces."""
+        self.layer1_mode = "split"
         try:
             self.step()
         finally:
-            self.fused_select = False
+            self.layer1_mode = "one"
 
     def step_two_streams(self):
         """The same launches with the gathers on a second stream."""
@@ -343,9 +353,9 @@ def _graph_of(fn):
 
 
 def bench_repair(steps: int, warmup: int, dev) -> dict:
-    """Time the KV-repair step as HipEngine issues it (32 launches on one stream, captured once
-    per input set in a HIP graph and replayed; the eager time, launch-bound from Python, the
-    two-stream issue of the same launches and the assemble-per-layer variant are reported too),
+    """Time the KV-repair step as HipEngine issues it (29 launches on one stream, captured once
+    per input set in a HIP graph and replayed; the eager time, launch-bound from Python, layer 1
+    as four launches, the two-stream issue and the assemble-per-layer variant are reported too),
     and the dominant kernel (the gather of the dropped rows of layers 2..27) from a burst of
     back-to-back launches."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
@@ -353,21 +363,19 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
         wls[i % 2].step()
         wls[i % 2].step_two_streams()
         wls[i % 2].step_assemble()
-    torch.cuda.synchronize()
-    for w in wls:
-        w.step_fused_select()
+        wls[i % 2].step_split()
     torch.cuda.synchronize()
     graphs = [_graph_of(w.step) for w in wls]
     two = [_graph_of(w.step_two_streams) for w in wls]
     asm_graphs = [_graph_of(w.step_assemble) for w in wls]
-    fused = [_graph_of(w.step_fused_select) for w in wls]
+    split = [_graph_of(w.step_split) for w in wls]
     stream = torch.cuda.current_stream(dev)
-    for g in graphs + two + asm_graphs + fused:
+    for g in graphs + two + asm_graphs + split:
         g.replay()
     ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
     ms_two = _timed(lambda i: two[i % 2].replay(), steps, stream)
     ms_asm = _timed(lambda i: asm_graphs[i % 2].replay(), steps, stream)
-    ms_fused = _timed(lambda i: fused[i % 2].replay(), steps, stream)
+    ms_split = _timed(lambda i: split[i % 2].replay(), steps, stream)
     for w in wls:  # the selection state of the one-stream step again
         w.step()
     ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
@@ -381,7 +389,7 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     nbytes = repair_bytes(n_keep)
     gd_bytes = dropped_bytes(plan)
     ms_conc = _concurrent_steps(wls, steps, dev)
-    return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_fused=ms_fused, ms_eager=ms_eager, bytes=nbytes,
+    return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_split=ms_split, ms_eager=ms_eager, bytes=nbytes,
                 moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
                 asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep, ms_conc=ms_conc,
@@ -1120,7 +1128,7 @@ def main() -> None:
 
     r = bench_repair(args.steps, args.warmup, dev)
     log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_two']:.3f} ms two "
-        f"streams, {r['ms_asm']:.3f} ms assemble variant, {r['ms_fused']:.3f} ms one-launch selection, "
+        f"streams, {r['ms_asm']:.3f} ms assemble variant, {r['ms_split']:.3f} ms layer 1 as four launches, "
         f"{r['ms_eager']:.3f} ms eager); dropped-row gather {r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
         f"assemble {r['asm_gbs']:.1f} GB/s ({r['asm_ms'] * 1e3:.2f} us)")
     configs = {}
@@ -1169,7 +1177,7 @@ def main() -> None:
         "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
         "ms_per_step_two_streams": round(r["ms_two"], 4),
         "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
-        "ms_per_step_fused_select": round(r["ms_fused"], 4),
+        "ms_per_step_layer1_four_launches": round(r["ms_split"], 4),
         "concurrent_requests": {"requests": CONCURRENT, "ms_per_round": round(r["ms_conc"], 4),
                                 "gbs": round(r["conc_gbs"], 1), "pct_of_peak": round(100.0 * r["conc_gbs"] / PEAK_GBS, 2),
                                 "note": "the same request's KV repair, CONCURRENT independent requests in flight on "

@@ -36,10 +36,12 @@ COUNT_TOP_HISTOGRAM = 7
 COUNT_N = 8
 
 DEVIATION_SELECT_WORKSPACE_BYTES = 16640
+LAYER1_REPAIR_WORKSPACE_BYTES = 172288
 POS_POOLED = 8
 
 SELECT_MAX_TOKENS = 131072
 DEVICE_ERR_RANGE = 1
+DEVICE_ERR_SYNC = 2
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -102,6 +104,11 @@ SIGNATURES = {
          _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p],
     ),
     "ckv_token_hash_prefixes": (_i32, [_p, _i64, _p, _i32, _p, _i32]),
+    "ckv_layer1_repair": (
+        _i32,
+        [_p, _p, _i64, _p, _i32, _i32, _i32, _p, _i32, _p, _i64, _i64, _p, _i64, _i64, _i32, _p, _p, _i32, _i32, _i32,
+         _i32, _f64, _p, _i32, _i32, _f64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p],
+    ),
     "ckv_deviation_select_noalloc": (
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f64,

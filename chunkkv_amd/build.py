@@ -20,7 +20,7 @@ INCLUDE = ROOT / "include"
 LIB_DIR = PKG / "_lib"
 LIB_NAME = "libchunkkv_amd.so"
 SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "deviation_select.hip",
-           "scatter.hip", "attention.hip", "rope.hip", "extract.hip", "norm.hip"]
+           "scatter.hip", "layer1_repair.hip", "attention.hip", "rope.hip", "extract.hip", "norm.hip"]
 HOST_SOURCES = ["token_hash.cpp"]
 ARCH = "gfx950"
 GXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wextra"]

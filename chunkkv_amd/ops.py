@@ -303,6 +303,84 @@ def deviation_select(
     return diff, norm, out
 
 
+def layer1_repair_workspace(device) -> torch.Tensor:
+    """A zeroed workspace for layer1_repair. Each call leaves it ready for the next, so one
+    workspace serves any number of calls issued in order (one stream); concurrent calls need one
+    each."""
+    return torch.zeros(_native.LAYER1_REPAIR_WORKSPACE_BYTES // 4, dtype=torch.int32, device=device)
+
+
+def layer1_repair(
+    K: torch.Tensor,
+    V: torch.Tensor,
+    src_tab: torch.Tensor,
+    n_layers: int,
+    layer: int,
+    segments: torch.Tensor,
+    n_segs: int,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    flags: torch.Tensor,
+    local: torch.Tensor,
+    spans: torch.Tensor,
+    escalate_threshold: float | None,
+    theta: float,
+    workspace: torch.Tensor,
+    err: torch.Tensor | None = None,
+    out: Selection | None = None,
+    diff_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, Selection]:
+    """Layer 1's KV repair in one launch (torch_engine.py:96-103 for this layer, :117-156): the
+    cache K/V (1, H, N, D) gets every cached row re-rotated from the chunks (src_tab column
+    `layer`, the cached-run segments) and the fresh rows of the kept positions; returns (diff,
+    norm, selection), bit-identical to rerope_gather (this layer) + deviation + select +
+    scatter_kept_rows. k/v: the fresh rows (1, H, n, D), any row-contiguous strides. workspace:
+    from layer1_repair_workspace(), not shared by calls that may run concurrently."""
+    _dev(K, V, src_tab, segments, k, v, flags, local, spans, workspace)
+    k, v = _rows_view(k), _rows_view(v)
+    if K.dtype != k.dtype or V.dtype != k.dtype or v.dtype != k.dtype:
+        raise TypeError("fresh and cached K/V must share a dtype")
+    _, H, N, D = K.shape
+    if not (K.is_contiguous() and V.is_contiguous() and V.shape == K.shape):
+        raise ValueError("cache K/V must be contiguous (1, H, N, D)")
+    if k.dim() != 4 or k.shape[1] != H or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"fresh k/v shape {tuple(k.shape)} does not match cache {tuple(K.shape)}")
+    if flags.dtype != torch.uint8 or local.dtype != torch.int32 or flags.numel() != N or local.numel() != N:
+        raise ValueError("flags must be uint8 (N,) and local int32 (N,)")
+    if not (flags.is_contiguous() and local.is_contiguous()):
+        raise ValueError("flags and local must be contiguous")
+    if src_tab.dtype != torch.int64 or src_tab.numel() % (2 * int(n_layers)):
+        raise ValueError("src_tab must be int64 with 2 addresses per (chunk, layer)")
+    if segments.dtype != torch.int32 or segments.numel() < 6 * int(n_segs):
+        raise ValueError("segments must be int32 with 6 fields per segment")
+    if spans.dtype != torch.int32 or (spans.numel() % 4):
+        raise ValueError("spans must be int32 (C, 4)")
+    if (workspace.numel() * workspace.element_size() < _native.LAYER1_REPAIR_WORKSPACE_BYTES
+            or not workspace.is_contiguous()):
+        raise ValueError("workspace must come from layer1_repair_workspace()")
+    C = spans.numel() // 4
+    dev = K.device
+    if diff_norm is None:
+        diff_norm = (torch.empty(N, dtype=torch.float32, device=dev), torch.empty(N, dtype=torch.float32, device=dev))
+    diff, norm = diff_norm
+    if out is None:
+        out = _new_selection(N, C, dev)
+    has_thr = escalate_threshold is not None
+    n_tab = src_tab.numel() // (2 * int(n_layers))
+    check(
+        lib().ckv_layer1_repair(
+            _ptr(K), _ptr(V), N * D, _ptr(src_tab), n_tab, int(n_layers), int(layer), _ptr(segments), int(n_segs),
+            _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2), k.shape[2], _ptr(flags),
+            _ptr(local), N, H, D, dtype_code(K.dtype), float(theta), _ptr(spans), C, int(has_thr),
+            float(escalate_threshold) if has_thr else 0.0, _ptr(diff), _ptr(norm), _ptr(out.keep_abs),
+            _ptr(out.keep_local), _ptr(out.keep_rank), _ptr(out.rel_dev), _ptr(out.escalated), _ptr(out.counts),
+            _ptr(workspace), workspace.numel() * workspace.element_size(), _ptr(err), _stream(dev),
+        ),
+        "ckv_layer1_repair",
+    )
+    return diff, norm, out
+
+
 def scatter_kept_rows(
     K: torch.Tensor,
     V: torch.Tensor,

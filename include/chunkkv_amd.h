@@ -47,6 +47,8 @@ typedef enum ckv_dtype {
 
 /* Bits a kernel ORs into the optional device status word `err`. */
 #define CKV_DEVICE_ERR_RANGE 1u
+#define CKV_DEVICE_ERR_SYNC 2u /* ckv_layer1_repair: a grid-wide wait passed its bound; outputs
+                                * of that call are unspecified                                  */
 
 /* Per-position flags (one byte per token position), built by the host planner.
  * Mirrors the lists returned by plan_positions (src/chunkkv/engine/base.py:63-73). */
@@ -101,6 +103,10 @@ typedef struct ckv_chunk_span {
 
 /* Bytes of the workspace ckv_deviation_select takes (a 4096-bin histogram and a ticket). */
 #define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 16640
+
+/* Bytes of the workspace ckv_layer1_repair takes (control words, two sets of radix-round
+ * histograms and claim flags, per-tile counts, escalation flags and the threshold-bin list). */
+#define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 172288
 
 /* ABI version compiled into the library (CKV_ABI_VERSION). */
 int32_t ckv_abi_version(void);
@@ -267,6 +273,44 @@ int32_t ckv_deviation_select_noalloc(const void* k_fresh, int64_t kf_head_stride
                                      double escalate_threshold, float* diff, float* norm, int64_t* keep_abs,
                                      int64_t* keep_local, int32_t* keep_rank, float* rel_dev, uint8_t* escalated,
                                      int32_t* counts, int32_t* err, void* stream);
+
+/*
+ * Layer 1's whole KV repair in one launch: its base cache, the deviation, the selection and the
+ * scatter of the kept rows, with every output bit-identical to
+ *   ckv_rerope_gather_layers(layer, every cached row) -> ckv_deviation -> ckv_select ->
+ *   ckv_scatter_kept_rows(keep_abs, keep_local)
+ * (same arguments, same meaning; see each above). The cache rows are written once: the fresh row
+ * (k_fresh/v_fresh at local[p]) at every kept position with a fresh row, the chunk's row (keys
+ * re-rotated by delta) at every other cached position. dst_k/dst_v are the layer's (H, n_tokens, D)
+ * cache, head stride dst_head_stride; src_tab/n_tab_chunks/n_layers/layer select the chunks' rows as
+ * in ckv_assemble_layer; segs are the cached runs, sorted by dst_start and disjoint (the planner's
+ * segments, n_segs <= 3840), read for every position flagged CKV_POS_CACHED.
+ *   workspace  >= CKV_LAYER1_REPAIR_WORKSPACE_BYTES, 16-byte aligned, ZERO before its first use;
+ *              each call leaves it ready for the next. Calls that share a workspace must be
+ *              ordered (one stream, or events). Words 8 and 9, when nonzero, replace the bound
+ *              of every grid-wide wait and the wait before taking over unstarted tiles (in polls;
+ *              tests use them to drive those paths).
+ * The launch runs one 1024-thread workgroup per CU with the rows in registers across grid-wide
+ * barriers; it completes whatever other work occupies the GPU (late workgroups' tiles are taken
+ * over), and a wait past its bound flags CKV_DEVICE_ERR_SYNC in *err instead of hanging.
+ * Limits: H * D * elem <= 1024 bytes per row (CKV_ERR_TOO_LARGE beyond, e.g. for the two-launch
+ * path), head_dim <= 128 and a power of two, n_tokens <= CKV_SELECT_MAX_TOKENS, n_chunks <= 4096.
+ * counts[CKV_COUNT_TOP_HISTOGRAM] = the grid-wide radix rounds the threshold took (1-3).
+ * Replaces: base_kv for layer 1 (torch_engine.py:96-103, with shift_keys :56-59), the deviation
+ *           (:117-124), rel/escalation/budget (:125-142), the top-k (:143-147), the compaction
+ *           (:148-153) and the scatter (:155-156).
+ */
+int32_t ckv_layer1_repair(void* dst_k, void* dst_v, int64_t dst_head_stride, const uint64_t* src_tab,
+                          int32_t n_tab_chunks, int32_t n_layers, int32_t layer, const ckv_segment* segs,
+                          int32_t n_segs, const void* k_fresh, int64_t kf_head_stride,
+                          int64_t kf_token_stride, const void* v_fresh, int64_t vf_head_stride,
+                          int64_t vf_token_stride, int32_t n_fresh, const uint8_t* pos_flags,
+                          const int32_t* local, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
+                          int32_t dtype, double theta, const ckv_chunk_span* chunks, int32_t n_chunks,
+                          int32_t has_threshold, double escalate_threshold, float* diff, float* norm,
+                          int64_t* keep_abs, int64_t* keep_local, int32_t* keep_rank, float* rel_dev,
+                          uint8_t* escalated, int32_t* counts, void* workspace, int64_t workspace_bytes,
+                          int32_t* err, void* stream);
 
 /*
  * Assemble one layer's cache with every row written once: for each segment row at position p,

@@ -1,0 +1,333 @@
+"""ckv_layer1_repair (layer 1's base cache, deviation, selection and kept-row scatter in one launch,
+torch_engine.py:96-103 and :117-156) against the same work done by the four launches it replaces
+(ckv_rerope_gather_layers, ckv_deviation, ckv_select, ckv_scatter_kept_rows) and against the
+oracle, bit for bit: the layer's K/V cache, diff/norm, keep_abs, keep_local, keep_rank, rel_dev,
+escalated and the counts.
+
+Cases: the 8k request's shape (24 chunks x 320 at shuffled positions + 576 uncached, 30 %), the
+config-3 shape at 15/30/50 %, the replay's 32,832-token request (tiles beyond the grid, reloaded),
+small requests with exact and overlapping placements at head_dim 64 in bf16 and fp32, an
+escalation threshold, deviations that tie (the threshold's bin larger than the list: more radix
+rounds, then equal keys ranked by position), NaN deviations, workgroups forced to take over
+unstarted tiles, a forced wait bound (the call flags the failure and the next call is correct),
+one workspace across calls of different sizes, and replays of a captured HIP graph."""
+
+import numpy as np
+import pytest
+import torch
+
+from chunkkv_amd import _native, ops
+from chunkkv_amd.planner import local_index, plan_request
+from chunkkv_amd.types import ChunkKV, Placement
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+THETA = 1e6
+SENT = -7.0
+
+
+class Request:
+    """A blend request as the engine sees it at layer 1: chunk store (n_layers columns), plan,
+    descriptors on the device and the fresh rows (cached rows + per-chunk noise)."""
+
+    def __init__(self, seed, chunk_lens, starts, N, ratio=0.3, n_sink=4, H=4, D=128, dtype=torch.bfloat16,
+                 n_layers=2, layer=1, exact=(), pool=None, noise=None, ratios=None, zero_store=False):
+        g = torch.Generator(device=DEV).manual_seed(seed)
+        rng = np.random.default_rng(seed)
+        self.H, self.D, self.dtype, self.n_layers, self.layer, self.N = H, D, dtype, n_layers, layer, N
+        self.zero_store = zero_store
+        if pool is None:
+            pool = [self._chunk(g, rng, L) for L in chunk_lens]
+        self.pool = pool
+        self.placements = [
+            Placement(pool[c], s, exact=(i in exact), ratio=None if ratios is None else ratios[i])
+            for i, (c, s) in enumerate(starts)
+        ]
+        plan = plan_request(N, self.placements, n_sink, ratio)
+        self.plan = plan
+        tab = np.array([[[k.data_ptr(), v.data_ptr()] for k, v in zip(ch.keys, ch.values)] for ch in plan.chunks],
+                       dtype=np.uint64)
+        self.tab = torch.from_numpy(tab.reshape(-1).view(np.int64)).to(DEV)
+        self.segs = torch.from_numpy(plan.segments.reshape(-1).copy()).to(DEV)
+        self.n_segs = len(plan.segments)
+        self.flags_np = plan.flags
+        self.local_np = local_index(N, plan.layer0_idx)
+        self.flags = torch.from_numpy(self.flags_np).to(DEV)
+        self.local = torch.from_numpy(self.local_np).to(DEV)
+        self.spans = torch.from_numpy(plan.spans.reshape(-1).copy()).to(DEV)
+        self.err = torch.zeros(1, dtype=torch.int32, device=DEV)
+        # fresh rows of the active positions: the re-rotated cached row plus per-chunk noise
+        # (uncached positions: random), k contiguous, v token-major as v_proj leaves it
+        base_k, base_v = self.gather_reference()[:2]
+        n_act = len(plan.layer0_idx)
+        act = torch.from_numpy(plan.layer0_idx).to(DEV)
+        cached = torch.from_numpy(plan.cached).to(DEV)[act][None, None, :, None]
+        sig = torch.ones(N, device=DEV)
+        for p in self.placements:
+            L = int(p.chunk.keys[0].shape[2])
+            s = float(torch.exp(torch.randn((), generator=g, device=DEV) - 3.0)) if noise is None else noise
+            sig[p.start : p.start + L] = s
+        sig = sig[act][None, None, :, None]
+        rnd = lambda: torch.randn((1, H, n_act, D), generator=g, device=DEV)  # noqa: E731
+        bk, bv = base_k[:, :, act].float(), base_v[:, :, act].float()
+        self.k = torch.where(cached, bk + sig * rnd(), rnd()).to(dtype)
+        v_rows = torch.where(cached, bv + sig * rnd(), rnd()).to(dtype)
+        self.v = v_rows.transpose(1, 2).contiguous().transpose(1, 2)
+
+    def _chunk(self, g, rng, L):
+        mk = lambda: (torch.zeros((1, self.H, L, self.D), device=DEV) if self.zero_store  # noqa: E731
+                      else torch.randn((1, self.H, L, self.D), generator=g, device=DEV)).to(self.dtype)
+        keys = [mk() for _ in range(self.n_layers)]
+        values = [mk() for _ in range(self.n_layers)]
+        return ChunkKV(keys, values, int(rng.integers(0, 4096)))
+
+    def gather_reference(self):
+        """Layer `layer` of a slab filled by ckv_rerope_gather_layers (sentinel elsewhere)."""
+        K = torch.full((self.n_layers, 1, self.H, self.N, self.D), SENT, dtype=self.dtype, device=DEV)
+        V = torch.full_like(K, SENT)
+        if self.n_segs:
+            ops.rerope_gather(K, V, self.tab, self.segs, self.n_segs, self.plan.max_seg_tokens, THETA, self.err,
+                              layers=(self.layer, self.layer + 1))
+        return K[self.layer], V[self.layer], K, V
+
+    def four_launches(self, thr):
+        K, V, _, _ = self.gather_reference()
+        K, V = K.clone(), V.clone()
+        diff, norm = ops.deviation(self.k, self.v, K, V, self.flags, self.local, self.err)
+        sel = ops.select(diff, norm, self.flags, self.local, self.spans, thr)
+        n = int(sel.counts[0].item())
+        ops.scatter_kept_rows(K, V, self.k, self.v, sel.keep_abs[:n], sel.keep_local[:n], self.err)
+        return K, V, diff, norm, sel
+
+    def fused(self, thr, ws, out=None):
+        K = torch.full((1, self.H, self.N, self.D), 3.0, dtype=self.dtype, device=DEV)
+        V = torch.full_like(K, 3.0)
+        diff, norm, sel = ops.layer1_repair(K, V, self.tab, self.n_layers, self.layer, self.segs, self.n_segs,
+                                            self.k, self.v, self.flags, self.local, self.spans, thr, THETA, ws,
+                                            self.err, out)
+        return K, V, diff, norm, sel
+
+
+def _bits(t):
+    return O.to_numpy(t)
+
+
+def _same(a, b, what):
+    np.testing.assert_array_equal(_bits(a), _bits(b), err_msg=what)
+
+
+def check(req: Request, thr=None, ws=None, oracle=True):
+    """Fused vs the four launches (and the oracle when asked), bit for bit; returns the counts."""
+    ws = ops.layer1_repair_workspace(DEV) if ws is None else ws
+    Kr, Vr, dr, nr, sr = req.four_launches(thr)
+    Kf, Vf, df, nf, sf = req.fused(thr, ws)
+    torch.cuda.synchronize()
+    assert int(req.err.item()) == 0, f"device status {int(req.err.item())}"
+    N, C = req.N, len(req.plan.spans)
+    cr, cf = _bits(sr.counts), _bits(sf.counts)
+    np.testing.assert_array_equal(cf[:7], cr[:7], err_msg="counts")
+    n = int(cr[0])
+    _same(df.view(torch.int32), dr.view(torch.int32), "diff")
+    _same(nf.view(torch.int32), nr.view(torch.int32), "norm")
+    _same(sf.keep_abs[:n], sr.keep_abs[:n], "keep_abs")
+    _same(sf.keep_local[:n], sr.keep_local[:n], "keep_local")
+    _same(sf.keep_rank, sr.keep_rank, "keep_rank")
+    if C:
+        _same(sf.rel_dev[:C].view(torch.int32), sr.rel_dev[:C].view(torch.int32), "rel_dev")
+        _same(sf.escalated[:C], sr.escalated[:C], "escalated")
+    _same(Kf, Kr, "K cache")
+    _same(Vf, Vr, "V cache")
+    if oracle:
+        Ko = np.full((1, req.H, N, req.D), 0, dtype=np.uint16 if req.dtype == torch.bfloat16 else np.float32)
+        Vo = np.zeros_like(Ko)
+        ks = [[_bits(ch.keys[req.layer])[0]] for ch in req.plan.chunks]
+        vs = [[_bits(ch.values[req.layer])[0]] for ch in req.plan.chunks]
+        if req.n_segs:
+            assert O.rerope_gather(Ko, Vo, ks, vs, req.plan.segments, THETA) == 0
+        act = req.plan.layer0_idx
+        k_np = _bits(req.k)[0]
+        v_np = np.ascontiguousarray(_bits(req.v.contiguous())[0])
+        d_o, n_o = O.deviation(k_np, v_np, Ko[0], Vo[0], req.flags_np, req.local_np)
+        np.testing.assert_array_equal(_bits(df).view(np.uint32), d_o.view(np.uint32))
+        want = O.select(d_o, n_o, req.flags_np, req.local_np, req.plan.spans, thr)
+        np.testing.assert_array_equal(cf[:7], want["counts"][:7])
+        np.testing.assert_array_equal(_bits(sf.keep_abs)[:n], want["keep_abs"])
+        np.testing.assert_array_equal(_bits(sf.keep_rank), want["keep_rank"])
+        ka, kl = want["keep_abs"], want["keep_local"]
+        K1, V1 = Ko[0].copy(), Vo[0].copy()
+        K1[:, ka], V1[:, ka] = k_np[:, kl], v_np[:, kl]
+        np.testing.assert_array_equal(_bits(Kf)[0], K1)
+        np.testing.assert_array_equal(_bits(Vf)[0], V1)
+        assert len(act) == len(req.local_np[req.local_np >= 0])
+    return cf
+
+
+def _shuffled(rng, n_chunks, L, tail):
+    order = rng.permutation(n_chunks)
+    return [(int(c), int(j * L)) for j, c in enumerate(order)], n_chunks * L + tail
+
+
+def test_8k_request_shape():
+    """24 chunks x 320 at shuffled positions + 576 uncached positions, 30 % + 4 sinks: 8256
+    positions, six per wavefront (T = 6), 2976 kept rows."""
+    rng = np.random.default_rng(8)
+    starts, N = _shuffled(rng, 24, 320, 576)
+    req = Request(8, [320] * 24, starts, N)
+    counts = check(req)
+    assert counts[0] == 2976 and req.plan.n_keep == 2976
+
+
+@pytest.mark.parametrize("ratio", [0.15, 0.3, 0.5])
+def test_config3_shape(ratio):
+    """32 chunks x 256 in order (shift 0 keeps the keys bit for bit), T = 4."""
+    starts = [(c, c * 256) for c in range(32)]
+    req = Request(int(ratio * 100), [256] * 32, starts, 8192, ratio=ratio)
+    counts = check(req)
+    assert counts[0] == {0.15: 1344, 0.3: 2592, 0.5: 4224}[ratio]
+
+
+def test_replay_request_shape_tiles_beyond_the_grid():
+    """128 chunks of 256 drawn with replacement (Zipf 1.1) from 24, + 64 query positions: 32,832
+    positions, more tiles than workgroups (reloaded rows), chunks repeated at several shifts."""
+    rng = np.random.default_rng(55)
+    zipf = 1.0 / np.arange(1, 25) ** 1.1
+    ids = rng.choice(24, 128, p=zipf / zipf.sum())
+    starts = [(int(c), j * 256) for j, c in enumerate(ids)]
+    req = Request(55, [256] * 24, starts, 128 * 256 + 64, ratio=0.15)
+    counts = check(req, oracle=False)
+    assert counts[0] == req.plan.n_keep
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_small_exact_and_overlapping_head_dim_64(dtype):
+    """0.5B KV shape (2 heads x 64): an exact placement (never recomputed: cached rows only),
+    overlapping placements (the later one wins), a ratio-0 placement, uncached gaps."""
+    lens = [40, 33, 50, 29, 61]
+    starts = [(0, 5), (1, 60), (2, 80), (3, 150), (4, 190)]  # 2 overlaps 1 (80 < 93)
+    req = Request(3, lens, starts, 270, H=2, D=64, dtype=dtype, n_layers=3, layer=1, exact=(3,),
+                  ratios=[0.3, 0.5, None, 0.0, 0.25])
+    assert req.plan.has_overlap and req.plan.exact.any()
+    check(req)
+
+
+def test_escalation_threshold():
+    """Chunks whose relative deviation passes the threshold keep every position and leave the
+    pool; the threshold sits between the chunks' noise levels."""
+    rng = np.random.default_rng(7)
+    starts, N = _shuffled(rng, 12, 128, 100)
+    req = Request(7, [128] * 12, starts, N, ratio=0.3)
+    rel = O.to_numpy(req.four_launches(None)[4].rel_dev)[:12]
+    thr = float(np.median(rel))
+    counts = check(req, thr=thr)
+    esc = int((rel > thr).sum())
+    assert 0 < esc < 12 and counts[0] > req.plan.n_keep
+
+
+def test_tied_deviations_take_more_rounds_and_rank_by_position():
+    """Fresh rows equal to the cached ones: every candidate's deviation is 0, one bin of more
+    candidates than the list takes, so the 12- and 8-bit rounds run and the lowest positions win."""
+    starts = [(c, c * 256) for c in range(48)]
+    req = Request(11, [256] * 48, starts, 48 * 256 + 64, ratio=0.3, noise=0.0)
+    counts = check(req, oracle=False)
+    assert counts[_native.COUNT_TOP_HISTOGRAM] == 3
+
+
+def test_quantised_deviations_tie_inside_the_list():
+    """Three distinct deviation values (a zero store, fresh rows zero but for one element of 0.5, 1
+    or 2): the threshold's bin fits the list and the ties at the threshold go by position."""
+    starts = [(c, c * 64) for c in range(16)]
+    req = Request(12, [64] * 16, starts, 16 * 64 + 8, ratio=0.5, noise=0.0, zero_store=True)
+    k = req.k.clone()
+    cached = torch.from_numpy(req.plan.cached[req.plan.layer0_idx]).to(DEV)
+    mag = torch.tensor([0.5, 1.0, 2.0], device=DEV)[torch.arange(k.shape[2], device=DEV) % 3]
+    k[0, 0, :, 0] = torch.where(cached, mag, k[0, 0, :, 0].float()).to(k.dtype)
+    req.k = k
+    counts = check(req)
+    assert counts[_native.COUNT_TOP_HISTOGRAM] == 1
+
+
+def test_nan_deviations_rank_last():
+    starts = [(c, c * 200) for c in range(10)]
+    req = Request(13, [200] * 10, starts, 2100, ratio=0.4)
+    k = req.k.clone()
+    k[0, 1, 5:40, 3] = float("nan")
+    req.k = k
+    check(req)
+
+
+def test_forced_take_over_of_unstarted_tiles():
+    """Workgroups take over any tile still unclaimed after one poll (workspace word 9): the rows
+    of such tiles are reloaded at the end, results unchanged. Repeated on one workspace."""
+    rng = np.random.default_rng(21)
+    starts, N = _shuffled(rng, 24, 320, 576)
+    req = Request(21, [320] * 24, starts, N)
+    ws = ops.layer1_repair_workspace(DEV)
+    ws[9] = 1
+    for _ in range(3):
+        check(req, ws=ws, oracle=False)
+
+
+def test_forced_wait_bound_flags_and_the_next_call_is_correct():
+    """A wait bound of one poll (workspace word 8) makes the grid-wide waits give up: the call
+    ends, flags CKV_DEVICE_ERR_SYNC or finishes in time, and a call with the normal bound on the
+    same workspace is bit-exact again."""
+    rng = np.random.default_rng(22)
+    starts, N = _shuffled(rng, 24, 320, 576)
+    req = Request(22, [320] * 24, starts, N)
+    ws = ops.layer1_repair_workspace(DEV)
+    ws[8] = 1
+    req.fused(None, ws)
+    torch.cuda.synchronize()
+    status = int(req.err.item())
+    assert status in (0, _native.DEVICE_ERR_SYNC)
+    req.err.zero_()
+    ws[8] = 0
+    check(req, ws=ws, oracle=False)
+
+
+def test_one_workspace_across_sizes():
+    ws = ops.layer1_repair_workspace(DEV)
+    for seed, (n_ch, L, tail) in enumerate([(24, 320, 576), (3, 50, 17), (32, 256, 0), (6, 100, 300)]):
+        rng = np.random.default_rng(100 + seed)
+        starts, N = _shuffled(rng, n_ch, L, tail)
+        check(Request(100 + seed, [L] * n_ch, starts, N), ws=ws, oracle=False)
+
+
+def test_graph_replays():
+    """One captured launch replayed three times, eager work and a synchronisation between the
+    replays, each replay's outputs equal to the eager call's."""
+    rng = np.random.default_rng(30)
+    starts, N = _shuffled(rng, 24, 320, 576)
+    req = Request(30, [320] * 24, starts, N)
+    ws = ops.layer1_repair_workspace(DEV)
+    Kr, Vr, dr, nr, sr = req.fused(None, ws)
+    torch.cuda.synchronize()
+    K = torch.zeros_like(Kr)
+    V = torch.zeros_like(Vr)
+    out = ops._new_selection(N, len(req.plan.spans), DEV)
+    dn = (torch.empty_like(dr), torch.empty_like(nr))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.layer1_repair(K, V, req.tab, req.n_layers, req.layer, req.segs, req.n_segs, req.k, req.v, req.flags,
+                          req.local, req.spans, None, THETA, ws, req.err, out, dn)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.layer1_repair(K, V, req.tab, req.n_layers, req.layer, req.segs, req.n_segs, req.k, req.v, req.flags,
+                          req.local, req.spans, None, THETA, ws, req.err, out, dn)
+    for i in range(3):
+        K.fill_(float(i))
+        out.keep_rank.fill_(-5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(req.err.item()) == 0
+        _same(K, Kr, f"K, replay {i}")
+        _same(V, Vr, f"V, replay {i}")
+        _same(dn[0].view(torch.int32), dr.view(torch.int32), f"diff, replay {i}")
+        _same(out.keep_rank, sr.keep_rank, f"keep_rank, replay {i}")
+        n = int(sr.counts[0].item())
+        _same(out.keep_abs[:n], sr.keep_abs[:n], f"keep_abs, replay {i}")
+        _same(out.counts[:7], sr.counts[:7], f"counts, replay {i}")
