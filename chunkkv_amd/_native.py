@@ -36,12 +36,11 @@ COUNT_TOP_HISTOGRAM = 7
 COUNT_N = 8
 
 DEVIATION_SELECT_WORKSPACE_BYTES = 16640
-LAYER1_REPAIR_WORKSPACE_BYTES = 172288
+LAYER1_REPAIR_WORKSPACE_BYTES = 16384
 POS_POOLED = 8
 
 SELECT_MAX_TOKENS = 131072
 DEVICE_ERR_RANGE = 1
-DEVICE_ERR_SYNC = 2
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -11,7 +11,7 @@
 // Consecutive threads walk one row (D elements), then the next head, then the next active
 // token, so the destination writes of a row are one contiguous 256-byte burst (D = 128, bf16)
 // and the source reads follow the fresh tensor's own strides.
-#include "ckv_common.hpp"
+#include "launch.hpp"
 
 namespace ckv {
 
@@ -25,7 +25,8 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
     char* dst_k, char* dst_v, int64_t d_hs_b, const char* __restrict__ sk, int64_t sk_hs_b,
     int64_t sk_ts_b, const char* __restrict__ sv, int64_t sv_hs_b, int64_t sv_ts_b,
     const int64_t* __restrict__ rows, const int64_t* __restrict__ src_rows, int n_rows, int n_src, int n_tokens,
-    int n_heads, int vecs_per_row, int64_t row_b, int32_t* __restrict__ err) {
+    int n_heads, int vecs_per_row, int64_t row_b, const int32_t* __restrict__ n_rows_dev, int32_t* __restrict__ err) {
+  if (n_rows_dev != nullptr) n_rows = min(n_rows, max(0, *n_rows_dev));  // a count only the device knows
   const int64_t per_tok = (int64_t)n_heads * vecs_per_row;
   const int64_t total = (int64_t)n_rows * per_tok;
   const int64_t stride = (int64_t)gridDim.x * kScatterThreads;
@@ -64,14 +65,11 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
   }
 }
 
-}  // namespace ckv
-
-static int32_t scatter_launch(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
-                              int64_t sk_head_stride, int64_t sk_token_stride, const void* src_v,
-                              int64_t sv_head_stride, int64_t sv_token_stride, const int64_t* rows,
-                              const int64_t* src_rows, int32_t n_rows, int32_t n_src, int32_t n_tokens,
-                              int32_t n_heads, int32_t head_dim, int32_t dtype, int32_t* err, void* stream) {
-  using namespace ckv;
+int32_t scatter_launch(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k, int64_t sk_head_stride,
+                       int64_t sk_token_stride, const void* src_v, int64_t sv_head_stride, int64_t sv_token_stride,
+                       const int64_t* rows, const int64_t* src_rows, int32_t n_rows, int32_t n_src, int32_t n_tokens,
+                       int32_t n_heads, int32_t head_dim, int32_t dtype, const int32_t* n_rows_dev, int32_t* err,
+                       void* stream) {
   if (dtype != CKV_DTYPE_BF16 && dtype != CKV_DTYPE_F32) return CKV_ERR_INVALID_ARGUMENT;
   const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
   if (head_dim <= 0 || (head_dim * eb) % 16 != 0 || n_heads <= 0 || n_rows < 0 || n_tokens < 0 || n_src < 0)
@@ -89,19 +87,21 @@ static int32_t scatter_launch(void* dst_k, void* dst_v, int64_t dst_head_stride,
                      (char*)dst_k, (char*)dst_v, dst_head_stride * eb, (const char*)src_k, sk_head_stride * eb,
                      sk_token_stride * eb, (const char*)src_v, sv_head_stride * eb, sv_token_stride * eb, rows,
                      src_rows, (int)n_rows, (int)n_src, (int)n_tokens, (int)n_heads, vecs_per_row,
-                     (int64_t)head_dim * eb, err);
+                     (int64_t)head_dim * eb, n_rows_dev, err);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }
+
+}  // namespace ckv
 
 extern "C" int32_t ckv_scatter_rows(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
                                     int64_t sk_head_stride, int64_t sk_token_stride, const void* src_v,
                                     int64_t sv_head_stride, int64_t sv_token_stride, const int64_t* rows,
                                     int32_t n_rows, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
                                     int32_t dtype, int32_t* err, void* stream) {
-  return scatter_launch(dst_k, dst_v, dst_head_stride, src_k, sk_head_stride, sk_token_stride, src_v, sv_head_stride,
-                        sv_token_stride, rows, nullptr, n_rows, n_rows, n_tokens, n_heads, head_dim, dtype, err,
-                        stream);
+  return ckv::scatter_launch(dst_k, dst_v, dst_head_stride, src_k, sk_head_stride, sk_token_stride, src_v,
+                             sv_head_stride, sv_token_stride, rows, nullptr, n_rows, n_rows, n_tokens, n_heads, head_dim,
+                             dtype, nullptr, err, stream);
 }
 
 extern "C" int32_t ckv_scatter_kept_rows(void* dst_k, void* dst_v, int64_t dst_head_stride, const void* src_k,
@@ -111,7 +111,7 @@ extern "C" int32_t ckv_scatter_kept_rows(void* dst_k, void* dst_v, int64_t dst_h
                                          int32_t n_heads, int32_t head_dim, int32_t dtype, int32_t* err,
                                          void* stream) {
   if (n_rows > 0 && src_rows == nullptr) return CKV_ERR_INVALID_ARGUMENT;
-  return scatter_launch(dst_k, dst_v, dst_head_stride, src_k, sk_head_stride, sk_token_stride, src_v, sv_head_stride,
-                        sv_token_stride, dst_rows, src_rows, n_rows, n_src, n_tokens, n_heads, head_dim, dtype, err,
-                        stream);
+  return ckv::scatter_launch(dst_k, dst_v, dst_head_stride, src_k, sk_head_stride, sk_token_stride, src_v,
+                             sv_head_stride, sv_token_stride, dst_rows, src_rows, n_rows, n_src, n_tokens, n_heads,
+                             head_dim, dtype, nullptr, err, stream);
 }

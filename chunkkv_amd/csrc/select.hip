@@ -4,17 +4,18 @@
 // and the register-resident algorithm are in select_common.hpp (shared with the fused
 // ckv_deviation_select); requests above 33792 tokens use select_kernel below, which re-reads
 // keys from L2 in every pass.
-#include "select_common.hpp"
+#include "launch.hpp"
 
 namespace ckv {
 
-// Register-resident selection (select_run) for n_tokens <= KPT * 1024.
+// Register-resident selection (select_run) for n_tokens <= KPT * 1024; ghist (may be NULL) is a
+// top-12-bit candidate histogram counted by an earlier launch, left zeroed.
 template <int KPT>
-__global__ __launch_bounds__(kSelThreads) void select_reg_kernel(SelectArgs a) {
+__global__ __launch_bounds__(kSelThreads) void select_reg_kernel(SelectArgs a, uint32_t* ghist) {
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
   ckv_chunk_span sp[kSelPre<KPT>];
   load_first_spans<KPT>(a.chunks, a.n_chunks, __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), sp);
-  select_run<KPT>(a, nullptr, masks, sp);
+  select_run<KPT>(a, ghist, masks, sp);
 }
 
 // Selection for any n_tokens <= CKV_SELECT_MAX_TOKENS: keys are re-read from global memory
@@ -212,6 +213,32 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(
   }
 }
 
+int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st) {
+  const int n_tokens = args.n_tokens;
+  const int W = (n_tokens + 31) / 32;
+  const size_t lds = (size_t)(W > 0 ? W : 1) * 2 * sizeof(uint32_t);
+  const int kpt = (n_tokens + kSelThreads - 1) / kSelThreads;
+#define CKV_SEL_REG(K)                                                                            \
+  if (kpt <= K) {                                                                                 \
+    hipLaunchKernelGGL(select_reg_kernel<K>, dim3(1), dim3(kSelThreads), lds, st, args, ghist);  \
+    CKV_RETURN_IF_LAUNCH_FAILED();                                                                \
+    return CKV_OK;                                                                                \
+  }
+  CKV_SEL_REG(4)
+  CKV_SEL_REG(8)
+  CKV_SEL_REG(12)
+  CKV_SEL_REG(16)
+  CKV_SEL_REG(24)
+  CKV_SEL_REG(33)
+#undef CKV_SEL_REG
+  if (ghist != nullptr) return CKV_ERR_INVALID_ARGUMENT;  // the L2 form takes no histogram
+  hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, st, args.diff, args.norm, args.flags,
+                     args.local, n_tokens, args.chunks, args.n_chunks, args.has_thr, args.thr, args.keep_abs,
+                     args.keep_local, args.keep_rank, args.rel_out, args.esc_out, args.counts);
+  CKV_RETURN_IF_LAUNCH_FAILED();
+  return CKV_OK;
+}
+
 }  // namespace ckv
 
 extern "C" int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flags,
@@ -226,29 +253,8 @@ extern "C" int32_t ckv_select(const float* diff, const float* norm, const uint8_
   if (n_chunks > 0 && (chunks == nullptr || rel_dev == nullptr || escalated == nullptr))
     return CKV_ERR_INVALID_ARGUMENT;
   if (n_tokens > CKV_SELECT_MAX_TOKENS) return CKV_ERR_TOO_LARGE;
-  const int W = (n_tokens + 31) / 32;
-  const size_t lds = (size_t)(W > 0 ? W : 1) * 2 * sizeof(uint32_t);
-  hipStream_t st = (hipStream_t)stream;
-  const int kpt = (n_tokens + kSelThreads - 1) / kSelThreads;
   const SelectArgs args{diff,     norm,     pos_flags, local,      (int)n_tokens, chunks,   (int)n_chunks,
                         (int)(has_threshold != 0), escalate_threshold, keep_abs, keep_local, keep_rank, rel_dev,
                         escalated, counts};
-#define CKV_SEL_REG(K)                                                                          \
-  if (kpt <= K) {                                                                               \
-    hipLaunchKernelGGL(select_reg_kernel<K>, dim3(1), dim3(kSelThreads), lds, st, args);       \
-    CKV_RETURN_IF_LAUNCH_FAILED();                                                              \
-    return CKV_OK;                                                                              \
-  }
-  CKV_SEL_REG(4)
-  CKV_SEL_REG(8)
-  CKV_SEL_REG(12)
-  CKV_SEL_REG(16)
-  CKV_SEL_REG(24)
-  CKV_SEL_REG(33)
-#undef CKV_SEL_REG
-  hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, st, diff, norm, pos_flags, local, (int)n_tokens,
-                     chunks, (int)n_chunks, (int)(has_threshold != 0), escalate_threshold, keep_abs, keep_local,
-                     keep_rank, rel_dev, escalated, counts);
-  CKV_RETURN_IF_LAUNCH_FAILED();
-  return CKV_OK;
+  return select_launch(args, nullptr, (hipStream_t)stream);
 }

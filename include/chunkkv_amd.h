@@ -47,8 +47,6 @@ typedef enum ckv_dtype {
 
 /* Bits a kernel ORs into the optional device status word `err`. */
 #define CKV_DEVICE_ERR_RANGE 1u
-#define CKV_DEVICE_ERR_SYNC 2u /* ckv_layer1_repair: a grid-wide wait passed its bound; outputs
-                                * of that call are unspecified                                  */
 
 /* Per-position flags (one byte per token position), built by the host planner.
  * Mirrors the lists returned by plan_positions (src/chunkkv/engine/base.py:63-73). */
@@ -104,9 +102,8 @@ typedef struct ckv_chunk_span {
 /* Bytes of the workspace ckv_deviation_select takes (a 4096-bin histogram and a ticket). */
 #define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 16640
 
-/* Bytes of the workspace ckv_layer1_repair takes (control words, two sets of radix-round
- * histograms and claim flags, per-tile counts, escalation flags and the threshold-bin list). */
-#define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 172288
+/* Bytes of the workspace ckv_layer1_repair takes (the selection's top-12-bit histogram). */
+#define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 16384
 
 /* ABI version compiled into the library (CKV_ABI_VERSION). */
 int32_t ckv_abi_version(void);
@@ -275,27 +272,26 @@ int32_t ckv_deviation_select_noalloc(const void* k_fresh, int64_t kf_head_stride
                                      int32_t* counts, int32_t* err, void* stream);
 
 /*
- * Layer 1's whole KV repair in one launch: its base cache, the deviation, the selection and the
+ * Layer 1's whole KV repair in one call: its base cache, the deviation, the selection and the
  * scatter of the kept rows, with every output bit-identical to
  *   ckv_rerope_gather_layers(layer, every cached row) -> ckv_deviation -> ckv_select ->
  *   ckv_scatter_kept_rows(keep_abs, keep_local)
- * (same arguments, same meaning; see each above). The cache rows are written once: the fresh row
- * (k_fresh/v_fresh at local[p]) at every kept position with a fresh row, the chunk's row (keys
- * re-rotated by delta) at every other cached position. dst_k/dst_v are the layer's (H, n_tokens, D)
- * cache, head stride dst_head_stride; src_tab/n_tab_chunks/n_layers/layer select the chunks' rows as
- * in ckv_assemble_layer; segs are the cached runs, sorted by dst_start and disjoint (the planner's
- * segments, n_segs <= 3840), read for every position flagged CKV_POS_CACHED.
+ * (same arguments, same meaning; see each above). dst_k/dst_v are the layer's (H, n_tokens, D)
+ * cache, head stride dst_head_stride; src_tab/n_tab_chunks/n_layers/layer select the chunks' rows
+ * as in ckv_assemble_layer; segs are the cached runs, sorted by dst_start and disjoint (the
+ * planner's segments, n_segs <= 3840), read for every position flagged CKV_POS_CACHED.
+ * Three launches, nothing read back on the host: (1) every position's rows, the cached rows
+ * written into the cache, the deviations, and the positions flagged CKV_POS_CACHED |
+ * CKV_POS_POOLED and not CKV_POS_SINK counted by their key's top 12 bits; (2) the selection,
+ * starting from that count (as ckv_deviation_select's does, same result when the flags disagree
+ * with the spans or a chunk escalates, just slower); (3) the kept rows, their count read on the
+ * device.
  *   workspace  >= CKV_LAYER1_REPAIR_WORKSPACE_BYTES, 16-byte aligned, ZERO before its first use;
- *              each call leaves it ready for the next. Calls that share a workspace must be
- *              ordered (one stream, or events). Words 8 and 9, when nonzero, replace the bound
- *              of every grid-wide wait and the wait before taking over unstarted tiles (in polls;
- *              tests use them to drive those paths).
- * The launch runs one 1024-thread workgroup per CU with the rows in registers across grid-wide
- * barriers; it completes whatever other work occupies the GPU (late workgroups' tiles are taken
- * over), and a wait past its bound flags CKV_DEVICE_ERR_SYNC in *err instead of hanging.
- * Limits: H * D * elem <= 1024 bytes per row (CKV_ERR_TOO_LARGE beyond, e.g. for the two-launch
- * path), head_dim <= 128 and a power of two, n_tokens <= CKV_SELECT_MAX_TOKENS, n_chunks <= 4096.
- * counts[CKV_COUNT_TOP_HISTOGRAM] = the grid-wide radix rounds the threshold took (1-3).
+ *              each call leaves it zeroed. Calls that share a workspace must be ordered (one
+ *              stream, or events).
+ * Limits: H * D * elem <= 1024 bytes per row (CKV_ERR_TOO_LARGE beyond: use the four calls),
+ * head_dim <= 128 and a power of two, n_tokens <= CKV_SELECT_MAX_TOKENS (above 33792 the
+ * selection counts its own histogram).
  * Replaces: base_kv for layer 1 (torch_engine.py:96-103, with shift_keys :56-59), the deviation
  *           (:117-124), rel/escalation/budget (:125-142), the top-k (:143-147), the compaction
  *           (:148-153) and the scatter (:155-156).
