@@ -26,13 +26,16 @@ the fresh-token RoPE and the attention run on the HIP kernels:
                                                        gathered; with the side stream the main
                                                        stream waits only before the attention
                                                        that reads them
-  deviation (:117-124)                               ckv_deviation (one wavefront per token)
-  rel/escalation/budget/argsort/nonzero (:125-153;   ckv_select (one workgroup); the host reads
-    one .item() per chunk)                             nothing back unless a threshold is set.
-                                                       fused_select=True: both in one launch,
-                                                       ckv_deviation_select
-  h, q, k, v = ...[sel]; K[:, :, active] = k (:152,  h and q index-selected; k/v compacted and
-    :155-156)                                          scattered by ckv_scatter_kept_rows
+  layer 1: base_kv, deviation (:117-124),            ckv_layer1_repair, one call: the cached rows
+    rel/escalation/budget/argsort/nonzero (:125-153;   re-rotated into the cache with the
+    one .item() per chunk), K[:, :, active] = k        deviations, the selection (one workgroup),
+    (:155-156)                                         the kept rows scattered; the host reads
+                                                       nothing back unless a threshold is set.
+                                                       layer1="four_launches" / "fused_select":
+                                                       the base cache at the start, then
+                                                       ckv_deviation + ckv_select (or
+                                                       ckv_deviation_select) + ckv_scatter_kept_rows
+  h, q = ...[sel] (:152)                             index-selected by the selection's keep_local
   mask + SDPA (:157, :68-72)                         ckv_attention_active: matrix-core
                                                        attention masked by the active positions
                                                        (bf16, head_dim 64/128)
@@ -117,23 +120,27 @@ def _stack_params(mods: list, name: str) -> torch.Tensor | None:
 
 
 class HipEngine(DecoderPieces):
-    def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = False, fused_select: bool = False):
+    def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = False,
+                 layer1: str = "one_call"):
         if attention not in ("fused", "reference"):
             raise ValueError("attention must be 'fused' or 'reference'")
+        if layer1 not in ("one_call", "four_launches", "fused_select"):
+            raise ValueError("layer1 must be 'one_call', 'four_launches' or 'fused_select'")
         self.attention = attention
-        # fused_select=True runs the layer-1 deviation and the selection as one launch
-        # (ckv_deviation_select) instead of two (ckv_deviation, ckv_select); same results. Off by
-        # default: in the 8k request's step the one launch takes ~41 us against 12 + 20 us, because
-        # the selecting workgroup's registers leave the deviation phase one 1024-thread workgroup
-        # per CU.
-        self.fused_select = fused_select
+        # Layer 1's repair: "one_call" (default) is ckv_layer1_repair (the cached rows gathered with
+        # the deviations, the selection, the kept rows; 3 launches); "four_launches" gathers layer
+        # 1's base cache at the start and runs ckv_deviation, ckv_select and ckv_scatter_kept_rows;
+        # "fused_select" the same with ckv_deviation_select. Same results, bit for bit. Shapes the
+        # one call does not take (rows wider than 1 KiB, head_dim > 128, > 3840 cached runs) use
+        # the four launches.
+        self.layer1 = layer1
         # overlap=True issues the cached-row gathers on a side stream, joined by events where a
         # layer needs its rows, instead of in order on the main stream (same launches, same rows).
         # Off by default: on MI355X the side stream did not shorten the 8k request's TTFT (42.47 vs
         # 42.38 ms p50) and it lengthens the KV-repair launches' own span (0.320 vs 0.314 ms).
         self.overlap = overlap
         self._side: torch.cuda.Stream | None = None
-        self._ws: dict[int, torch.Tensor] = {}  # deviation_select workspaces, per stream
+        self._ws: dict[tuple, torch.Tensor] = {}  # layer-1 workspaces, per (kind, stream)
         # generate(): replay each decode step after the first from a HIP graph (device-side loop)
         self.decode_graphs = True
         # Set to a dict to record the layer-1 selection inputs/outputs (device tensors) of the
@@ -318,15 +325,22 @@ class HipEngine(DecoderPieces):
             for a, o in zip(parts, offs)
         ]
 
-    def _workspace(self) -> torch.Tensor:
-        """ckv_deviation_select's workspace for torch's current stream (zeroed once; every call
-        leaves it zeroed). One per stream, so prefills issued on different streams never share
-        one."""
-        st = torch.cuda.current_stream(self.device).cuda_stream
-        ws = self._ws.get(st)
+    def _workspace(self, kind: str) -> torch.Tensor:
+        """The layer-1 workspace of `kind` ("one_call" or "fused_select") for torch's current
+        stream (zeroed once; every call leaves it zeroed). One per stream, so prefills issued on
+        different streams never share one."""
+        key = (kind, torch.cuda.current_stream(self.device).cuda_stream)
+        ws = self._ws.get(key)
         if ws is None:
-            ws = self._ws[st] = ops.deviation_select_workspace(self.device)
+            make = ops.layer1_repair_workspace if kind == "one_call" else ops.deviation_select_workspace
+            ws = self._ws[key] = make(self.device)
         return ws
+
+    def _one_call_fits(self, plan: RequestPlan) -> bool:
+        """Whether ckv_layer1_repair takes this request's layer 1 (its limits)."""
+        D, row = self.head_dim, self.n_kv * self.head_dim * torch.finfo(self.kv_dtype).bits // 8
+        return (self.layer1 == "one_call" and D <= 128 and D & (D - 1) == 0 and row <= 1024
+                and len(plan.segments) <= 3840 and plan.n_tokens <= _native.SELECT_MAX_TOKENS)
 
     def _project(self, li: int, x: torch.Tensor):
         """q|k|v projection of layer li in one GEMM: views (1, n, H*D) of its token-major output."""
@@ -456,6 +470,7 @@ class HipEngine(DecoderPieces):
 
         plan: RequestPlan = plan_request(N, placements, config.n_sink, config.recompute_ratio)
         select_layer = bool(placements) and config.full_first_layer and n_layers > 1
+        one_call = select_layer and self._one_call_fits(plan)
         active_np = plan.layer0_idx if config.full_first_layer else plan.fresh_idx
         local_np = local_index(N, active_np)
         if first is not None and len(active_np) != N:
@@ -496,7 +511,8 @@ class HipEngine(DecoderPieces):
             if select_layer:
                 if plan.exact.any():
                     ready[0] = gather((0, 1), local_d)
-                ready[1] = gather((1, 2), None)
+                if not one_call:
+                    ready[1] = gather((1, 2), None)
             else:
                 ready[0] = gather((0, n_layers), local_d)
         pending = None  # the previous layer's MLP output, when its residual add is deferred
@@ -510,14 +526,26 @@ class HipEngine(DecoderPieces):
             if li == 1 and select_layer:
                 q, k = ops.rope_qkv(q_in, k_in, None, active, self.n_heads, H, D, self.theta, err=err)
                 v = v_in.view(1, -1, H, D).transpose(1, 2)
-                if ready.get(1) is not None:
-                    torch.cuda.current_stream(dev).wait_event(ready[1])
-                if self.fused_select:
-                    diff, norm, sel = ops.deviation_select(k, v, K, V, flags_d, local_d, spans_d,
-                                                           config.escalate_threshold, self._workspace(), err)
+                base = None
+                if one_call:
+                    if self.trace is not None:  # the base cache the deviations compare against
+                        base = (torch.empty_like(K), torch.empty_like(V))
+                        ops.assemble_layer(*base, tab_d, n_layers, 1, segs_d, n_cached_segs, plan.max_seg_tokens,
+                                           None, None, None, self.theta, err)
+                    diff, norm, sel = ops.layer1_repair(K, V, tab_d, n_layers, 1, segs_d, n_cached_segs, k, v, flags_d,
+                                                        local_d, spans_d, config.escalate_threshold, self.theta,
+                                                        self._workspace("one_call"), err)
                 else:
-                    diff, norm = ops.deviation(k, v, K, V, flags_d, local_d, err)
-                    sel = ops.select(diff, norm, flags_d, local_d, spans_d, config.escalate_threshold)
+                    if ready.get(1) is not None:
+                        torch.cuda.current_stream(dev).wait_event(ready[1])
+                    base = (K.clone(), V.clone()) if self.trace is not None else None
+                    if self.layer1 == "fused_select":
+                        diff, norm, sel = ops.deviation_select(k, v, K, V, flags_d, local_d, spans_d,
+                                                               config.escalate_threshold,
+                                                               self._workspace("fused_select"), err)
+                    else:
+                        diff, norm = ops.deviation(k, v, K, V, flags_d, local_d, err)
+                        sel = ops.select(diff, norm, flags_d, local_d, spans_d, config.escalate_threshold)
                 if config.escalate_threshold is None and not plan.has_overlap:
                     n_keep = plan.n_keep  # fixed by the layout: no device round trip
                 else:
@@ -527,12 +555,13 @@ class HipEngine(DecoderPieces):
                     n_keep = int(counts[_native.COUNT_KEEP])
                 n_keep_used = n_keep
                 if self.trace is not None:
-                    self.trace.update(k=k, v=v, K=K.clone(), V=V.clone(), flags=flags_d, local=local_d, spans=spans_d,
+                    self.trace.update(k=k, v=v, K=base[0], V=base[1], flags=flags_d, local=local_d, spans=spans_d,
                                       diff=diff, norm=norm, sel=sel, n_keep=n_keep)
                 rows = sel.keep_local[:n_keep]
                 h, q = h.index_select(1, rows), q.index_select(1, rows)
                 active = sel.keep_abs[:n_keep]
-                ops.scatter_kept_rows(K, V, k, v, active, rows, err)  # k/v compaction folded in
+                if not one_call:
+                    ops.scatter_kept_rows(K, V, k, v, active, rows, err)  # k/v compaction folded in
                 if n_cached_segs and n_layers > 2:
                     ready[2] = gather((2, n_layers), sel.keep_rank)
             else:

@@ -133,13 +133,17 @@ def test_side_stream_and_one_stream_builds_identical(models, parts, ratio):
     assert torch.equal(ra.logits, rb.logits)
 
 
+@pytest.mark.parametrize("mode", ["four_launches", "fused_select"])
 @pytest.mark.parametrize("thr", [None, 0.05])
-def test_fused_select_builds_identical(models, parts, thr):
-    """The layer-1 deviation and selection as one launch (fused_select=True) or two: the same
-    caches, logits and stats, bit for bit, with and without an escalation threshold."""
+def test_layer1_paths_build_identical(models, parts, thr, mode):
+    """Layer 1's repair as one call (ckv_layer1_repair, the default), as the base-cache gather plus
+    the deviation, the selection and the kept-row scatter, or with the deviation and selection in
+    one launch: the same caches, logits and stats, bit for bit, with and without an escalation
+    threshold."""
     _, gpu = models
-    a = HipEngine(gpu, StubTokenizer(), fused_select=True)
+    a = HipEngine(gpu, StubTokenizer(), layer1=mode)
     b = HipEngine(gpu, StubTokenizer())
+    assert b.layer1 == "one_call"
     toks2, pl = _swap_setup(a, parts)
     cfg = BlendConfig(recompute_ratio=0.3, n_sink=4, escalate_threshold=thr)
     ra, rb = a.prefill(toks2, pl, cfg), b.prefill(toks2, pl, cfg)

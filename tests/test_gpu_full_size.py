@@ -140,12 +140,12 @@ def test_full_size_layer1_repair_matches_oracle(setup):
         np.testing.assert_array_equal(Vg[:, dropped], Vlo[:, dropped])
 
 
-def test_full_size_fused_select_identical(setup):
-    """The 8k request with the layer-1 deviation and selection in one launch: the same caches and
-    logits as the two-launch default, bit for bit."""
+def test_full_size_layer1_four_launches_identical(setup):
+    """The 8k request with layer 1 as four launches (base cache, deviation, selection, kept-row
+    scatter): the same caches and logits as the one-call default, bit for bit."""
     model, eng, tokens, placements = setup
     cfg = BlendConfig(recompute_ratio=0.3, n_sink=4)
-    a = HipEngine(model, StubTokenizer(), fused_select=True).prefill(tokens, placements, cfg)
+    a = HipEngine(model, StubTokenizer(), layer1="four_launches").prefill(tokens, placements, cfg)
     b = eng.prefill(tokens, placements, cfg)
     assert torch.equal(a.logits, b.logits) and a.stats == b.stats
     for li in (0, 1, 2, 27):
