@@ -9,13 +9,21 @@
 namespace ckv {
 
 // Register-resident selection (select_run) for n_tokens <= KPT * 1024; ghist (may be NULL) is a
-// top-12-bit candidate histogram counted by an earlier launch, left zeroed.
-template <int KPT>
+// top-12-bit candidate histogram counted by an earlier launch, left zeroed. Without a threshold
+// (SUMS = false) workgroup 0 selects and the others compute the chunks' rel_dev, one wavefront
+// per chunk, beside it.
+template <int KPT, bool SUMS>
 __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(SelectArgs a, uint32_t* ghist) {
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
+  if (!SUMS && blockIdx.x > 0) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+    for (int c = ((int)blockIdx.x - 1) * kSelWaves + wave; c < a.n_chunks; c += ((int)gridDim.x - 1) * kSelWaves)
+      chunk_sums_wave(a, c);
+    return;
+  }
   ckv_chunk_span sp[kSelPre<KPT>];
   load_first_spans<KPT>(a.chunks, a.n_chunks, __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), sp);
-  select_run<KPT>(a, ghist, masks, sp);
+  select_run<KPT, false, SUMS>(a, ghist, masks, sp);
 }
 
 // Selection for any n_tokens <= CKV_SELECT_MAX_TOKENS: keys are re-read from global memory
@@ -218,11 +226,17 @@ int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st) {
   const int W = (n_tokens + 31) / 32;
   const size_t lds = (size_t)(W > 0 ? W : 1) * 2 * sizeof(uint32_t);
   const int kpt = (n_tokens + kSelThreads - 1) / kSelThreads;
-#define CKV_SEL_REG(K)                                                                            \
-  if (kpt <= K) {                                                                                 \
-    hipLaunchKernelGGL(select_reg_kernel<K>, dim3(1), dim3(kSelThreads), lds, st, args, ghist);  \
-    CKV_RETURN_IF_LAUNCH_FAILED();                                                                \
-    return CKV_OK;                                                                                \
+  // without a threshold the chunk sums run in workgroups of their own beside the selection
+  const unsigned sum_groups = args.has_thr ? 0u : (unsigned)((args.n_chunks + kSelWaves - 1) / kSelWaves);
+#define CKV_SEL_REG(K)                                                                                    \
+  if (kpt <= K) {                                                                                         \
+    if (args.has_thr)                                                                                     \
+      hipLaunchKernelGGL((select_reg_kernel<K, true>), dim3(1), dim3(kSelThreads), lds, st, args, ghist); \
+    else                                                                                                  \
+      hipLaunchKernelGGL((select_reg_kernel<K, false>), dim3(1 + sum_groups), dim3(kSelThreads), lds, st,  \
+                         args, ghist);                                                                    \
+    CKV_RETURN_IF_LAUNCH_FAILED();                                                                        \
+    return CKV_OK;                                                                                        \
   }
   CKV_SEL_REG(4)
   CKV_SEL_REG(8)

@@ -140,6 +140,41 @@ struct SelectArgs {
   int32_t* counts;
 };
 
+// rel_dev / escalated of chunk c (no threshold: never escalated), computed by the calling
+// wavefront in the selection's order: lane l adds positions start + l, start + l + 64, ...
+// ascending, then the xor butterfly (what select_run does with SUMS).
+__device__ __forceinline__ void chunk_sums_wave(const SelectArgs& a, int c) {
+  constexpr int kBatch = 8;
+  const int lane = (int)(threadIdx.x % kWave);
+  const ckv_chunk_span sp = a.chunks[c];
+  const bool ok = sp.start >= 0 && sp.length >= 0 && (int64_t)sp.start + sp.length <= a.n_tokens;
+  float sd = 0.0f, sn = 0.0f;
+  if (ok) {
+    for (int q0 = 0; q0 < sp.length; q0 += kBatch * kWave) {
+      float bd[kBatch], bn[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int q = q0 + j * kWave + lane;
+        bd[j] = q < sp.length ? a.diff[sp.start + q] : 0.0f;
+        bn[j] = q < sp.length ? a.norm[sp.start + q] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (q0 + j * kWave + lane < sp.length) {
+          sd = sd + bd[j];
+          sn = sn + bn[j];
+        }
+      }
+    }
+  }
+  sd = wave_butterfly_sum(sd);
+  sn = wave_butterfly_sum(sn);
+  if (lane == 0) {
+    a.rel_out[c] = sd / sn;
+    a.esc_out[c] = 0;
+  }
+}
+
 constexpr uint64_t kField = 0x1fffffull;  // 21-bit count fields of the packed workgroup scans
 constexpr int kLightPass = 1024;          // candidates in the top bin up to which passes are light
 
@@ -183,7 +218,9 @@ __device__ __forceinline__ uint32_t ld_val(const uint32_t* p) {
   return *p;
 }
 
-template <int KPT, bool COH = false>
+// SUMS = false (only without a threshold): the per-chunk sums and rel_dev/escalated are left to
+// other workgroups (chunk_sums_wave); the budget and the pool come from the spans alone.
+template <int KPT, bool COH = false, bool SUMS = true>
 __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist, uint32_t* masks,
                                            const ckv_chunk_span (&sp0)[kSelPre<KPT>]) {
   static_assert(KPT <= 33, "a run of KPT positions spans at most two mask words and one 64-bit word");
@@ -268,7 +305,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   // the first batch of this wavefront's first chunks' deviations
   float bd0[kPre][kBatch], bn0[kPre][kBatch];
 #pragma unroll
-  for (int r = 0; r < kPre; ++r) {
+  for (int r = 0; r < (SUMS ? kPre : 0); ++r) {
     const int c = wave + r * kSelWaves;
     const bool ok0 = sp0[r].start >= 0 && sp0[r].length >= 0 && (int64_t)sp0[r].start + sp0[r].length <= n_tokens;
 #pragma unroll
@@ -290,12 +327,21 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
 
   // Phase 1: per-chunk rel / escalation / budget, one wavefront per chunk, summed in the
   // contract's order (lane-strided, ascending, then the xor butterfly).
+  const ckv_chunk_span sp_first = sp0[0], sp_last = sp0[kPre - 1];
   for (int c = wave, r = 0; c < n_chunks; c += kSelWaves, ++r) {
     const bool pre = r < kPre;
-    const ckv_chunk_span sp = pre ? sp0[r < kPre ? r : 0] : chunks[c];
+    // selected by value, field by field (a select between the addresses would put the spans in
+    // scratch memory)
+    const ckv_chunk_span ld = pre ? sp_first : chunks[c];
+    const bool f = r == 0;
+    ckv_chunk_span sp;
+    sp.start = pre ? (f ? sp_first.start : sp_last.start) : ld.start;
+    sp.length = pre ? (f ? sp_first.length : sp_last.length) : ld.length;
+    sp.budget = pre ? (f ? sp_first.budget : sp_last.budget) : ld.budget;
+    sp.pooled = pre ? (f ? sp_first.pooled : sp_last.pooled) : ld.pooled;
     const bool ok = sp.start >= 0 && sp.length >= 0 && (int64_t)sp.start + sp.length <= n_tokens;
     float sd = 0.0f, sn = 0.0f;
-    if (ok) {
+    if (SUMS && ok) {
       for (int q0 = 0; q0 < sp.length; q0 += kBatch * kWave) {
         float bd[kBatch], bn[kBatch];
 #pragma unroll
@@ -318,15 +364,18 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
         }
       }
     }
-    sd = wave_butterfly_sum(sd);
-    sn = wave_butterfly_sum(sn);
-    const float rel = sd / sn;
-    const bool esc = ok && a.has_thr && ((double)rel > a.thr);
-    if (lane == 0) {
-      a.rel_out[c] = rel;
-      a.esc_out[c] = esc ? 1 : 0;
-      if (!ok) atomicAdd(&s_bad_span, 1);
+    bool esc = false;
+    if constexpr (SUMS) {
+      sd = wave_butterfly_sum(sd);
+      sn = wave_butterfly_sum(sn);
+      const float rel = sd / sn;
+      esc = ok && a.has_thr && ((double)rel > a.thr);
+      if (lane == 0) {
+        a.rel_out[c] = rel;
+        a.esc_out[c] = esc ? 1 : 0;
+      }
     }
+    if (lane == 0 && !ok) atomicAdd(&s_bad_span, 1);
     if (!ok) continue;
     if (esc) {
       set_bit_range(escw, sp.start, sp.start + sp.length, lane);
