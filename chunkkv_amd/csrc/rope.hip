@@ -167,6 +167,70 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(
   }
 }
 
+// k/v only with head_dim <= 128 and both k and v (the cache-repair launch of every layer): one
+// wavefront per token and no integer division. Item i of a token is the 16-byte column pair
+// (col, col + D/2) of head row i / TPR: k heads first (rotated), then v heads (copied). Lane f
+// evaluates frequency f of the token's position once; the lanes fetch their column's VEC
+// frequencies with ds_bpermute. One position load per token (the row index too only when the
+// caller passes rows other than the positions; NULL rows: row = token index).
+template <int DTYPE, int D>
+__global__ __launch_bounds__(kRopeThreads) void rope_kv_kernel(
+    char* __restrict__ k_out, int64_t ko_hs_b, int64_t ko_ts_b, char* __restrict__ v_out, int64_t vo_hs_b,
+    int64_t vo_ts_b, const int64_t* __restrict__ rows, int n_out, const char* __restrict__ k_in, int64_t ki_hs_b,
+    int64_t ki_ts_b, const char* __restrict__ v_in, int64_t vi_hs_b, int64_t vi_ts_b, const int64_t* __restrict__ pos,
+    const InvFreq inv, int n, int Hkv, int32_t* __restrict__ err) {
+  using E = Elem<DTYPE>;
+  constexpr int VEC = E::kVec;
+  constexpr int HALF = D / 2;
+  constexpr int TPR = HALF / VEC;  // column pairs per head row (a power of two)
+  constexpr int HALF_B = HALF * E::kBytes;
+  static_assert(HALF <= kWave && kWave % HALF == 0 && (TPR & (TPR - 1)) == 0, "head_dim out of range");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = (int)(blockIdx.x * (kRopeThreads / kWave) + threadIdx.x / kWave);
+  if (t >= n) return;  // uniform per wavefront
+  const int64_t p = pos[t];
+  const int64_t row = rows == nullptr ? t : rows == pos ? p : rows[t];
+  const bool ok = p >= INT32_MIN && p <= INT32_MAX && row >= 0 && row < n_out;
+  const int items = 2 * Hkv * TPR;
+  // the first item's data goes out before the position is needed
+  const int col = lane & (TPR - 1);
+  auto src_of = [&](int it) {
+    const int hh = it / TPR;  // TPR is a power of two: a shift
+    return hh < Hkv ? k_in + hh * ki_hs_b + t * ki_ts_b + col * 16 : v_in + (hh - Hkv) * vi_hs_b + t * vi_ts_b + col * 16;
+  };
+  const int it0 = min(lane, items - 1);
+  const char* s0 = src_of(it0);
+  vec16 a = ld16(s0), b = ld16(s0 + HALF_B);
+  const float ang = (float)(ok ? (int)p : 0) * inv.v[lane & (HALF - 1)];
+  float cv[1], sv[1];
+  const float angs[1] = {ang};
+  angles_cos_sin<1>(angs, cv, sv);
+  float c[VEC], sn[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    c[e] = __shfl(cv[0], col * VEC + e);
+    sn[e] = __shfl(sv[0], col * VEC + e);
+  }
+  if (!ok) {
+    if (lane == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+    return;
+  }
+  for (int it = lane; it < items; it += kWave) {
+    if (it != lane) {
+      const char* si = src_of(it);
+      a = ld16(si);
+      b = ld16(si + HALF_B);
+    }
+    const int hh = it / TPR;
+    char* d = hh < Hkv ? k_out + hh * ko_hs_b + row * ko_ts_b + col * 16
+                       : v_out + (hh - Hkv) * vo_hs_b + row * vo_ts_b + col * 16;
+    vec16 y1 = a, y2 = b;
+    if (hh < Hkv) rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
+    st16(d, y1);
+    st16(d + HALF_B, y2);
+  }
+}
+
 // Without a table, with q (32+ rotated heads share each token's cos/sin): one thread per
 // (token, 16-byte column, group of kRopeFreeHG heads), grid-stride, evaluating its VEC
 // frequencies itself (kRopeFreeHG-fold sharing), v copied in 16-byte chunks. The thread's loads go
@@ -350,6 +414,15 @@ static void launch_rope(int n, hipStream_t st, char* qo, int64_t qo_hs, int64_t 
     return;
   }
   const InvFreq& inv = host_inv_freq(D, theta);
+  if constexpr (D <= 2 * kWave) {
+    if (Hq == 0 && vo != nullptr) {
+      const int per_wg = kRopeThreads / kWave;
+      hipLaunchKernelGGL((rope_kv_kernel<DTYPE, D>), dim3((unsigned)((n + per_wg - 1) / per_wg)), dim3(kRopeThreads),
+                         0, st, ko, ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, ki, ki_hs,
+                         ki_ts, vi, vi_hs, vi_ts, pos, inv, n, Hkv, err);
+      return;
+    }
+  }
   if (Hq == 0) {
     constexpr int TW = D / 2 >= kWave ? 1 : kWave / (D / 2);
     const int per_wg = (kRopeThreads / kWave) * TW;
