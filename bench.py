@@ -488,6 +488,7 @@ def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20
         "for all engines")
     hip, ref = HipEngine(model, _Tok()), TorchOpsEngine(model, _Tok())
     hip_ref_attn = HipEngine(model, _Tok(), attention="reference")
+    hip_overlap = HipEngine(model, _Tok(), overlap=True)
     gen = torch.Generator().manual_seed(7)
     vocab = model.config.vocab_size
     # Chunk pool: each chunk prefilled alone at position 0 (its own context), stored like KVStore does.
@@ -509,7 +510,8 @@ def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20
     cfg = BlendConfig(recompute_ratio=RATIO, n_sink=N_SINK)
     out = {}
     for name, eng, n_req in (("hip", hip, len(reqs)), ("torch_ops", ref, len(reqs)),
-                              ("hip_attention_reference", hip_ref_attn, min(len(reqs), n_reference_attention + 2))):
+                              ("hip_attention_reference", hip_ref_attn, min(len(reqs), n_reference_attention + 2)),
+                              ("hip_overlap", hip_overlap, min(len(reqs), n_reference_attention + 2))):
         times, stats = [], None
         for i, (tokens, placements) in enumerate(reqs[:n_req]):
             torch.cuda.synchronize()
@@ -524,7 +526,7 @@ def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20
         out[name] = dict(p50=float(np.percentile(times, 50)), p99=float(np.percentile(times, 99)), stats=stats,
                          tuned_gemms=tuned, requests=len(times))
         log(f"[bench] TTFT {name}: p50 {out[name]['p50']:.2f} ms  p99 {out[name]['p99']:.2f} ms")
-    del hip, ref, hip_ref_attn
+    del hip, ref, hip_ref_attn, hip_overlap
     torch.cuda.empty_cache()
     out["model"] = model
     return out
@@ -1209,6 +1211,8 @@ def main() -> None:
         line["ttft_p50_ms_attention_reference"] = round(ttft["hip_attention_reference"]["p50"], 2)
         line["ttft_p99_ms_attention_reference"] = round(ttft["hip_attention_reference"]["p99"], 2)
         line["ttft_requests_attention_reference"] = ttft["hip_attention_reference"]["requests"]
+        # the same engine with the dropped-row gather on a side stream (HipEngine(overlap=True))
+        line["ttft_p50_ms_side_stream"] = round(ttft["hip_overlap"]["p50"], 2)
     if configs:
         line["configs"] = configs
     print(json.dumps(line), flush=True)

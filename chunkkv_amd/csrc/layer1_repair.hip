@@ -286,8 +286,8 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(L1A
     const int p = pb + t;
     if ((cls[t] & kCCached) && !(cls[t] & kCSink) && lane_on) {  // cls: p < N
       const int64_t off = hoff + (int64_t)p * rowb;
-      st16(a.dk + off, r.kc[t]);
-      st16(a.dv + off, r.vc[t]);
+      st16_stream(a.dk + off, r.kc[t]);  // non-temporal, as every cache-row writer here
+      st16_stream(a.dv + off, r.vc[t]);
     }
   }
   if (lane == 0) {

@@ -58,9 +58,9 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
   }
 #pragma unroll
   for (int u = 0; u < kScatterUnroll; ++u) {
-    if (dst_o[u] >= 0) {
-      st16(dst_k + dst_o[u], a[u]);
-      st16(dst_v + dst_o[u], b[u]);
+    if (dst_o[u] >= 0) {  // non-temporal: no dirty L2 lines left for the kernel boundary
+      st16_stream(dst_k + dst_o[u], a[u]);
+      st16_stream(dst_v + dst_o[u], b[u]);
     }
   }
 }
