@@ -35,6 +35,9 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",  # MFMA accumulators in VGPRs (no accumulator-register copies)
+    # the first 16 dwords of every kernel's arguments arrive in SGPRs at wave start instead of through
+    # a scalar load (measured ~0.2 us less per short launch in a chain of them)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]

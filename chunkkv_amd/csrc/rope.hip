@@ -171,38 +171,56 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(
 // wavefront per token and no integer division. Item i of a token is the 16-byte column pair
 // (col, col + D/2) of head row i / TPR: k heads first (rotated), then v heads (copied). Lane f
 // evaluates frequency f of the token's position once; the lanes fetch their column's VEC
-// frequencies with ds_bpermute. One position load per token (the row index too only when the
-// caller passes rows other than the positions; NULL rows: row = token index). The rows are
-// stored non-temporally: a launch leaves no dirty lines in L2 for the next kernel boundary to
-// write back (measured: ~0.9 us less per 2976-row launch in a chain of them).
-template <int DTYPE, int D>
+// frequencies with ds_bpermute. The rows are stored non-temporally: a launch leaves no dirty
+// lines in L2 for the next kernel boundary to write back (measured: ~0.9 us less per 2976-row
+// launch in a chain of them).
+// SHAPE: kKvLoop = items strided over the wavefront; kKvOne = at most one item per lane;
+// kKvFull = exactly one item per lane (2 * Hkv * TPR == 64, Hkv a compile-time constant: the
+// k/v split is lane < 32). RM: where a token's row goes: kRowToken (rows NULL: row = token),
+// kRowPos (rows are the positions: no second load), kRowIndexed (row = rows[t]). Both are
+// template parameters because the runtime forms cost ~0.3-0.4 us per 2976-row launch.
+constexpr int kKvLoop = 0, kKvOne = 1, kKvFull = 2;
+constexpr int kRowToken = 0, kRowPos = 1, kRowIndexed = 2;
+
+// The arguments come in the order a wavefront needs them: the first 64 bytes (what the token
+// count check and the first loads use) fit the 16 SGPRs the library preloads, the frequency table
+// comes last.
+template <int DTYPE, int D, int SHAPE, int RM>
 __global__ __launch_bounds__(kRopeThreads) void rope_kv_kernel(
-    char* __restrict__ k_out, int64_t ko_hs_b, int64_t ko_ts_b, char* __restrict__ v_out, int64_t vo_hs_b,
-    int64_t vo_ts_b, const int64_t* __restrict__ rows, int n_out, const char* __restrict__ k_in, int64_t ki_hs_b,
-    int64_t ki_ts_b, const char* __restrict__ v_in, int64_t vi_hs_b, int64_t vi_ts_b, const int64_t* __restrict__ pos,
-    const InvFreq inv, int n, int Hkv, int32_t* __restrict__ err) {
+    int n, int n_kv_heads, const int64_t* __restrict__ pos, const char* __restrict__ k_in,
+    const char* __restrict__ v_in, int64_t ki_hs_b, int64_t ki_ts_b, int64_t vi_hs_b, int64_t vi_ts_b,
+    char* __restrict__ k_out, char* __restrict__ v_out, int64_t ko_hs_b, int64_t ko_ts_b, int64_t vo_hs_b,
+    int64_t vo_ts_b, const int64_t* __restrict__ rows, int n_out, int32_t* __restrict__ err, const InvFreq inv) {
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
   constexpr int HALF = D / 2;
   constexpr int TPR = HALF / VEC;  // column pairs per head row (a power of two)
   constexpr int HALF_B = HALF * E::kBytes;
   static_assert(HALF <= kWave && kWave % HALF == 0 && (TPR & (TPR - 1)) == 0, "head_dim out of range");
+  const int Hkv = SHAPE == kKvFull ? kWave / 2 / TPR : n_kv_heads;
   const int lane = threadIdx.x & (kWave - 1);
   const int t = (int)(blockIdx.x * (kRopeThreads / kWave) + threadIdx.x / kWave);
   if (t >= n) return;  // uniform per wavefront
   const int64_t p = pos[t];
-  const int64_t row = rows == nullptr ? t : rows == pos ? p : rows[t];
-  const bool ok = p >= INT32_MIN && p <= INT32_MAX && row >= 0 && row < n_out;
   const int items = 2 * Hkv * TPR;
-  // the first item's data goes out before the position is needed
   const int col = lane & (TPR - 1);
-  auto src_of = [&](int it) {
-    const int hh = it / TPR;  // TPR is a power of two: a shift
-    return hh < Hkv ? k_in + hh * ki_hs_b + t * ki_ts_b + col * 16 : v_in + (hh - Hkv) * vi_hs_b + t * vi_ts_b + col * 16;
+  // item it: head row it / TPR (TPR is a power of two: a shift), k rows first. Base pointer,
+  // strides and head index are picked by value, so the k and v lanes share one address path.
+  auto src_of = [&](int hh) {
+    const bool k = hh < Hkv;
+    return (k ? k_in : v_in) + (k ? hh : hh - Hkv) * (k ? ki_hs_b : vi_hs_b) + t * (k ? ki_ts_b : vi_ts_b) + col * 16;
   };
-  const int it0 = min(lane, items - 1);
-  const char* s0 = src_of(it0);
+  // the first item's data goes out before anything waits on the position load
+  const int h0 = (SHAPE == kKvFull ? lane : min(lane, items - 1)) / TPR;
+  const char* s0 = src_of(h0);
   vec16 a = ld16(s0), b = ld16(s0 + HALF_B);
+  const int64_t row = RM == kRowToken ? (int64_t)t : RM == kRowPos ? p : rows[t];
+  const bool ok = p >= INT32_MIN && p <= INT32_MAX && row >= 0 && row < n_out;
+  auto dst_of = [&](int hh) {
+    const bool k = hh < Hkv;
+    return (k ? k_out : v_out) + (k ? hh : hh - Hkv) * (k ? ko_hs_b : vo_hs_b) + row * (k ? ko_ts_b : vo_ts_b) +
+           col * 16;
+  };
   const float ang = (float)(ok ? (int)p : 0) * inv.v[lane & (HALF - 1)];
   float cv[1], sv[1];
   const float angs[1] = {ang};
@@ -217,19 +235,28 @@ __global__ __launch_bounds__(kRopeThreads) void rope_kv_kernel(
     if (lane == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
     return;
   }
-  for (int it = lane; it < items; it += kWave) {
-    if (it != lane) {
-      const char* si = src_of(it);
-      a = ld16(si);
-      b = ld16(si + HALF_B);
-    }
-    const int hh = it / TPR;
-    char* d = hh < Hkv ? k_out + hh * ko_hs_b + row * ko_ts_b + col * 16
-                       : v_out + (hh - Hkv) * vo_hs_b + row * vo_ts_b + col * 16;
+  if constexpr (SHAPE != kKvLoop) {  // items <= one wavefront: a single pass, no loop
+    char* d = dst_of(h0);
     vec16 y1 = a, y2 = b;
-    if (hh < Hkv) rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
-    st16_stream(d, y1);
-    st16_stream(d + HALF_B, y2);
+    if (h0 < Hkv) rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
+    if (SHAPE == kKvFull || lane < items) {
+      st16_stream(d, y1);
+      st16_stream(d + HALF_B, y2);
+    }
+  } else {
+    for (int it = lane; it < items; it += kWave) {
+      const int hh = it / TPR;
+      if (it != lane) {
+        const char* si = src_of(hh);
+        a = ld16(si);
+        b = ld16(si + HALF_B);
+      }
+      char* d = dst_of(hh);
+      vec16 y1 = a, y2 = b;
+      if (hh < Hkv) rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
+      st16_stream(d, y1);
+      st16_stream(d + HALF_B, y2);
+    }
   }
 }
 
@@ -419,9 +446,21 @@ static void launch_rope(int n, hipStream_t st, char* qo, int64_t qo_hs, int64_t 
   if constexpr (D <= 2 * kWave) {
     if (Hq == 0 && vo != nullptr) {
       const int per_wg = kRopeThreads / kWave;
-      hipLaunchKernelGGL((rope_kv_kernel<DTYPE, D>), dim3((unsigned)((n + per_wg - 1) / per_wg)), dim3(kRopeThreads),
-                         0, st, ko, ko_hs, ko_ts, vo, vo_hs, vo_ts, rows, n_out, ki, ki_hs,
-                         ki_ts, vi, vi_hs, vi_ts, pos, inv, n, Hkv, err);
+      const dim3 grid((unsigned)((n + per_wg - 1) / per_wg));
+      constexpr int TPR = D / 2 / Elem<DTYPE>::kVec;
+      const int items = 2 * Hkv * TPR;
+      const int shape = items == kWave ? kKvFull : items < kWave ? kKvOne : kKvLoop;
+      const int rm = rows == nullptr ? kRowToken : rows == pos ? kRowPos : kRowIndexed;
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(kRopeThreads), 0, st, n, Hkv, pos, ki, vi, ki_hs, ki_ts, vi_hs, vi_ts, ko,
+                           vo, ko_hs, ko_ts, vo_hs, vo_ts, rows, n_out, err, inv);
+      };
+#define CKV_KV(S, R) \
+  if (shape == S && rm == R) go(rope_kv_kernel<DTYPE, D, S, R>);
+      CKV_KV(kKvFull, kRowToken) CKV_KV(kKvFull, kRowPos) CKV_KV(kKvFull, kRowIndexed)
+      CKV_KV(kKvOne, kRowToken) CKV_KV(kKvOne, kRowPos) CKV_KV(kKvOne, kRowIndexed)
+      CKV_KV(kKvLoop, kRowToken) CKV_KV(kKvLoop, kRowPos) CKV_KV(kKvLoop, kRowIndexed)
+#undef CKV_KV
       return;
     }
   }
