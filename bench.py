@@ -8,13 +8,14 @@ shuffled positions (each chunk computed at its own original offset, so every pla
 its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
 
 A step is one request's whole KV repair with every input already resident in HBM, issued as
-HipEngine issues it (32 launches in order on one stream): layer 1's base cache gathered, layer
-0's fresh rows written into its cache; the layer-1 deviation, the selection (2304 pooled + 96
-sinks + 576 uncached = 2976 kept rows) and the scatter of the kept rows; then the gather of the
-cached rows of the 5280 dropped positions of layers 2-27 in one launch, and the fresh rows of
-layers 2-27 (disjoint rows). The fresh rows are written by ckv_rope_qkv as in the engine (k
-rotated to its position, v copied, straight into the cache rows); the engine's launch also
-rotates q for the attention, which the step leaves out as the reference's KV-repair bytes do.
+HipEngine issues it (29 launches in order on one stream): layer 0's fresh rows written into its
+cache; layer 1's repair as one ckv_layer1_repair call (three launches: the cached rows
+re-rotated into the cache with the deviation, the selection of 2304 pooled + 96 sinks + 576
+uncached = 2976 kept rows, the scatter of the kept rows); then the gather of the cached rows of
+the 5280 dropped positions of layers 2-27 in one launch, and the fresh rows of layers 2-27
+(disjoint rows). The fresh rows are written by ckv_rope_qkv as in the engine (k rotated to its
+position, v copied, straight into the cache rows); the engine's launch also rotates q for the
+attention, which the step leaves out as the reference's KV-repair bytes do.
 The unit of work is one request's KV repair as the reference's op sequence moves it (re-RoPE +
 gather of every cached row of all 28 layers, the layer-0 scatter of all 8256 rows, the
 deviation, the scatters of layers 1-27):
@@ -25,8 +26,9 @@ deviation, the scatters of layers 1-27):
     total                                                                      = 1,277,624,832
 `value` = that total / measured time per step (GB/s), the step replayed from a HIP graph (the
 eager time, launch-bound from Python, is reported as ms_per_step_eager, the same launches with
-both gathers on a second stream (HipEngine(overlap=True)) as ms_per_step_two_streams, and layers
-0 and 2-27 built by one assemble launch each as
+the gathers on a second stream (HipEngine(overlap=True)) as ms_per_step_two_streams, layer 1 as
+the four launches ckv_layer1_repair replaces (base-cache gather, deviation, selection, scatter)
+as ms_per_step_layer1_four_launches, and layers 0 and 2-27 built by one assemble launch each as
 ms_per_step_assemble_variant); the fused flow itself moves 990,577,152 B per step
 (moved_bytes_per_step, moved_gbs). `roofline` is the dominant kernel (the gather of the dropped
 rows of layers 2-27, 562,298,880 B per launch) timed live with HIP events around a burst of
@@ -703,7 +705,8 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         r30["both_ms"], steps, warmup,
         {"workload": "layer-1 deviation + pooled top-k (30%) + 4 sinks x 32 chunks x 256 + scatter of the kept rows, "
                      "4 KV heads, head_dim 128, bf16; 16 input sets rotated (cold HBM); deviation and selection as "
-                     "two launches (the engine's default); the one-launch form is in ratios", "bytes_per_step": nb},
+                     "two launches (ckv_deviation + ckv_select, as HipEngine(layer1='four_launches') issues them); "
+                     "the one-launch ckv_deviation_select is in ratios", "bytes_per_step": nb},
         _rooffor("deviation_kernel<bf16> + select_reg_kernel<8> (deviation + top-k)", dev_bytes,
                  r30["dev_sel_two_launches_ms"]))
     line["ratios"] = {str(r): {k2: (round(v2, 5) if isinstance(v2, float) else v2) for k2, v2 in o.items()}
@@ -1090,14 +1093,21 @@ def _config_summary(line: dict) -> dict:
 
 
 def _cpu_model() -> str:
+    """The host CPU's model name with its family/model/stepping numbers (a virtualised host may
+    report only the brand, e.g. "AMD EPYC"; the numbers still name the generation)."""
+    info: dict[str, str] = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                if not ln.strip():
+                    break  # the first processor's block is enough
+                key, _, val = ln.partition(":")
+                info.setdefault(key.strip(), val.strip())
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    nums = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    return f"{name} ({', '.join(nums)})" if nums else name
 
 
 def main() -> None:

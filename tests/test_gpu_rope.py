@@ -170,3 +170,51 @@ def test_rope_qkv_with_table_identical_and_bounds():
     ops.rope_qkv(q_in, k_in, None, pt, Hq, Hkv, D, THETA, table=short, err=err)
     torch.cuda.synchronize()
     assert int(err.item()) == _native.DEVICE_ERR_RANGE
+
+
+# (bf16, D, Hkv) per shape of the k/v-only kernel: items per token = 2 Hkv D/2/VEC (VEC = 8 bf16,
+# 4 fp32); 64 = one item per lane with the k/v split at lane 32, < 64 one item per lane at most,
+# > 64 items strided over the wavefront.
+KV_SHAPES = {
+    "full_bf16_128": (True, 128, 4), "full_bf16_64": (True, 64, 8), "full_f32_128": (False, 128, 2),
+    "one_bf16_128": (True, 128, 2), "one_bf16_64": (True, 64, 3), "one_f32_64": (False, 64, 1),
+    "loop_bf16_128": (True, 128, 8), "loop_f32_128": (False, 128, 4),
+}
+
+
+@pytest.mark.parametrize("row_mode", ["token", "positions", "indexed"])
+@pytest.mark.parametrize("shape", list(KV_SHAPES))
+def test_rope_kv_every_row_mode_and_shape(shape, row_mode):
+    """The k/v-only launch (no q: every layer's cache write) in each shape and row mode: rows
+    NULL (row = token index), rows = the positions tensor itself, rows indexed separately from
+    the positions. k rotated bit-exactly, v copied, every other cache row untouched."""
+    bf16, D, Hkv = KV_SHAPES[shape]
+    rng = np.random.default_rng(sum(map(ord, shape + row_mode)))
+    n, N = 157, 700
+    lin = _proj(rng, n, 0, Hkv, D, bf16)
+    if row_mode == "positions":
+        pos = np.sort(rng.choice(N, n, replace=False))
+        rows = pos
+    else:
+        pos = rng.integers(0, 40000, n)
+        pos[0] = 0
+        rows = np.arange(n) if row_mode == "token" else rng.choice(N, n, replace=False)
+    lt = O.from_numpy(lin, DEV)
+    _, k_in, v_in = _split(lt, 0, Hkv, D)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    K = torch.full((1, Hkv, N, D), -3.0, dtype=dt, device=DEV)
+    V = torch.full_like(K, -3.0)
+    pt = torch.from_numpy(pos).to(DEV)
+    rt = None if row_mode == "token" else pt if row_mode == "positions" else torch.from_numpy(rows).to(DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.rope_qkv(None, k_in, v_in, pt, 0, Hkv, D, THETA, k_out=K, v_out=V, rows=rt, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    _, kn, vn = _split(lin, 0, Hkv, D)
+    fill = O.f32_to_bf16_bits(np.float32([-3.0]))[0] if bf16 else np.float32(-3.0)
+    Kw = np.full((Hkv, N, D), fill, dtype=np.uint16 if bf16 else np.float32)
+    Vw = Kw.copy()
+    Kw[:, rows] = O.rope(_heads(kn, Hkv, D), pos, THETA)
+    Vw[:, rows] = _heads(vn, Hkv, D)
+    np.testing.assert_array_equal(O.to_numpy(K)[0], Kw)
+    np.testing.assert_array_equal(O.to_numpy(V)[0], Vw)
