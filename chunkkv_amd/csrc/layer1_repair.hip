@@ -108,28 +108,59 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
   const int64_t colb = (int64_t)col * 16;
   const int N = a.n_tokens;
 
-  // 1. flags, local indices and the segment descriptors around the positions, all in flight
+  // 1. every first-level load at once, unconditionally: indices are clamped into range and the
+  // results masked where they are used. (A load behind a condition made the compiler wait for it
+  // before the next one went out: flags, local indices, segments, inverse frequencies and the
+  // chunk addresses were eight memory round trips in a row.)
+  const int half = a.head_dim >> 1;
+  const float my_inv = inv.v[lane & (half - 1)];
   uint32_t fl[T];
+  int lraw[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int pc = min(pb + t, N - 1);  // N >= 1
+    fl[t] = a.flags[pc];
+    lraw[t] = a.local[pc];
+  }
+  const int n_segs = a.n_segs;
+  const int stride = (n_segs + kWave - 1) / kWave;
+  int st1 = 0x7fffffff;
+  if (n_segs > kWave) {  // uniform: 64 samples first, then the window that holds the positions
+    const int si = lane * stride;
+    st1 = a.segs[min(si, n_segs - 1)].dst_start;
+    st1 = si < n_segs ? st1 : 0x7fffffff;
+  }
+
+  // 2. the segment records around the positions (the chain to the cached rows: record, chunk
+  // address, row) go out before the fresh rows: vector loads complete in issue order, so a
+  // record loaded after the fresh rows could not be used before they had arrived
+  int sbase = 0, scount = n_segs;
+  if (n_segs > kWave) {
+    const uint64_t m = __ballot(st1 <= pb);
+    const int bk = m ? 63 - __builtin_clzll(m) : 0;
+    sbase = bk * stride;
+    scount = min(stride + T, n_segs - sbase);
+  }
+  // unconditional (segs is readable even without segments: the host passes the workspace), so
+  // no branch merges paths with different loads in flight
+  ckv_segment sd = a.segs[sbase + max(min(lane, scount - 1), 0)];
+
+  // 3. the fresh rows: lanes past the rows and positions without a fresh row load a valid row
+  // and drop it where it is used
+  const int hc = min(h, a.n_heads - 1);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int p = pb + t;
-    fl[t] = p < N ? a.flags[p] : 0u;
-    li[t] = p < N ? a.local[p] : -1;
+    const bool okl = p < N && lraw[t] >= 0 && lraw[t] < a.n_fresh;
+    li[t] = okl ? lraw[t] : -1;
+    r.kc[t] = r.vc[t] = vec16{0u, 0u, 0u, 0u};
+    const int64_t lc = okl ? lraw[t] : 0;  // kf/vf are readable with n_fresh == 0: the workspace
+    r.kf[t] = ld16(a.kf + hc * a.kf_hs_b + lc * a.kf_ts_b + colb);
+    r.vf[t] = ld16(a.vf + hc * a.vf_hs_b + lc * a.vf_ts_b + colb);
   }
-  int sbase = 0, scount = a.n_segs;
-  if (a.n_segs > kWave) {  // 64 samples, then the window that holds every position's segment
-    const int stride = (a.n_segs + kWave - 1) / kWave;
-    const int si = lane * stride;
-    const int st = si < a.n_segs ? a.segs[si].dst_start : 0x7fffffff;
-    const uint64_t m = __ballot(st <= pb);
-    const int bk = m ? 63 - __builtin_clzll(m) : 0;
-    sbase = bk * stride;
-    scount = min(stride + T, a.n_segs - sbase);
-  }
-  ckv_segment sd{0x7fffffff, 0, -1, 0, 0, 0};
-  if (lane < scount) sd = a.segs[sbase + lane];
 
-  // 2. each position's segment (the last with dst_start <= p) and its chunk's base addresses
+  // 4. each position's segment (the last with dst_start <= p) and its chunk's base addresses
+  sd.dst_start = lane < scount ? sd.dst_start : 0x7fffffff;
   int delta[T];
   bool have[T];
   const char* kb[T];
@@ -139,6 +170,7 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int p = pb + t;
+    const uint32_t f = __builtin_amdgcn_readfirstlane(fl[t]) & (p < N ? 0xffu : 0u);  // every lane loaded the same byte
     const uint64_t m = __ballot(lane < scount && sd.dst_start <= p);
     const int L = m ? 63 - __builtin_clzll(m) : 0;
     const int dst = __builtin_amdgcn_readlane(sd.dst_start, L);
@@ -147,31 +179,34 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     const int ss = __builtin_amdgcn_readlane(sd.src_start, L);
     const int sl = __builtin_amdgcn_readlane(sd.src_len, L);
     delta[t] = __builtin_amdgcn_readlane(sd.delta, L);
-    const bool cached = p < N && (fl[t] & CKV_POS_CACHED);
+    const bool cached = p < N && (f & CKV_POS_CACHED);
     const bool found = m != 0ull && p < dst + n;
     const bool seg_ok = found && dst >= 0 && ss >= 0 && ch >= 0 && ch < a.tab_chunks && (int64_t)dst + n <= N &&
                         (int64_t)ss + n <= sl;
     bad = bad || (cached && !seg_ok);
     have[t] = cached && seg_ok;
-    kb[t] = vb[t] = nullptr;
-    soff[t] = (int64_t)h * sl * rowb + (int64_t)(ss + (p - dst)) * rowb + colb;
-    if (have[t]) {
-      const int64_t ti = ((int64_t)ch * a.n_layers + a.layer) * 2;
-      kb[t] = reinterpret_cast<const char*>(a.tab[ti]);
-      vb[t] = reinterpret_cast<const char*>(a.tab[ti + 1]);
-    }
-    bad = bad || li[t] >= a.n_fresh;
-    li[t] = li[t] >= a.n_fresh ? -1 : li[t];
+    soff[t] = (int64_t)hc * sl * rowb + (int64_t)(ss + (p - dst)) * rowb + colb;
+    // unconditional (entry 0 when there is no row to load; the host passes a readable table),
+    // so both positions' address loads are in flight together
+    const int64_t ti = have[t] ? ((int64_t)ch * a.n_layers + a.layer) * 2 : 0;
+    kb[t] = reinterpret_cast<const char*>(a.tab[ti]);
+    vb[t] = reinterpret_cast<const char*>(a.tab[ti + 1]);
+    bad = bad || (p < N && lraw[t] >= a.n_fresh);
     cls[t] = (p < N ? kCValid : 0u) | (cached ? kCCached : 0u) | (li[t] < 0 ? kCNoLocal : 0u) |
-             ((fl[t] & CKV_POS_SINK) ? kCSink : 0u) | ((fl[t] & CKV_POS_POOLED) ? kCPooled : 0u);
+             ((f & CKV_POS_SINK) ? kCSink : 0u) | ((f & CKV_POS_POOLED) ? kCPooled : 0u);
   }
   if (bad && lane == 0) flag_error(a.err, CKV_DEVICE_ERR_RANGE);
 
-  // 3. cos/sin of each position's shift while the chunk addresses arrive: lane f evaluates
-  // frequency f (mod D/2) once per distinct shift; the rotation fetches its column's VEC
-  // frequencies from the evaluating lanes
-  const int half = a.head_dim >> 1;
-  const float my_inv = inv.v[lane & (half - 1)];
+  // 5. the chunk's K/V at the segment's source row; cos/sin of each position's shift while they
+  // arrive: lane f evaluates frequency f (mod D/2) once per distinct shift, the rotation fetches
+  // its column's VEC frequencies from the evaluating lanes
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    if (have[t]) {  // uniform
+      r.kc[t] = ld16(kb[t] + soff[t]);
+      r.vc[t] = ld16(vb[t] + soff[t]);
+    }
+  }
   float cv[T], sv[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -188,21 +223,7 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     sv[t] = cs.y;
   }
 
-  // 4. the rows: fresh k/v at the local index, the chunk's K/V at the segment's source row
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    r.kf[t] = r.vf[t] = r.kc[t] = r.vc[t] = vec16{0u, 0u, 0u, 0u};
-    if (li[t] >= 0 && lane_on) {
-      r.kf[t] = ld16(a.kf + h * a.kf_hs_b + (int64_t)li[t] * a.kf_ts_b + colb);
-      r.vf[t] = ld16(a.vf + h * a.vf_hs_b + (int64_t)li[t] * a.vf_ts_b + colb);
-    }
-    if (have[t] && lane_on) {
-      r.kc[t] = ld16(kb[t] + soff[t]);
-      r.vc[t] = ld16(vb[t] + soff[t]);
-    }
-  }
-
-  // 5. re-rotate the cached keys: the partner half comes from lane l ^ (vpr / 2)
+  // 6. re-rotate the cached keys: the partner half comes from lane l ^ (vpr / 2)
   const int half_v = vpr >> 1;
   const bool first_half = col < half_v;
   const int f0 = (col & (half_v - 1)) * VEC;
@@ -230,15 +251,16 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     if (lane_on) r.kc[t] = E::pack(y);
   }
 
-  // 6. deviations in the contract's order: lane q adds its vector's elements in ascending order,
+  // 7. deviations in the contract's order: lane q adds its vector's elements in ascending order,
   // then the xor butterfly; diff = Sk + Sv, norm = Nk + Nv
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     float kx[VEC], vx[VEC], kcx[VEC], vcx[VEC];
-    E::unpack(r.kf[t], kx);
-    E::unpack(r.vf[t], vx);
-    E::unpack(r.kc[t], kcx);
-    E::unpack(r.vc[t], vcx);
+    const vec16 zero = {0u, 0u, 0u, 0u};  // lanes past the rows add nothing
+    E::unpack(lane_on ? r.kf[t] : zero, kx);
+    E::unpack(lane_on ? r.vf[t] : zero, vx);
+    E::unpack(lane_on ? r.kc[t] : zero, kcx);
+    E::unpack(lane_on ? r.vc[t] : zero, vcx);
     float sk = 0.0f, sv = 0.0f, nk = 0.0f, nw = 0.0f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -366,18 +388,21 @@ extern "C" int32_t ckv_layer1_repair(
   args.dk = (char*)dst_k;
   args.dv = (char*)dst_v;
   args.d_hs_b = dst_head_stride * eb;
-  args.tab = src_tab;
-  args.tab_chunks = n_tab_chunks;
+  args.tab = n_tab_chunks > 0 && src_tab != nullptr ? src_tab : (const uint64_t*)workspace;
+  args.tab_chunks = args.tab == src_tab ? n_tab_chunks : 0;
   args.n_layers = n_layers;
   args.layer = layer;
-  args.segs = segs;
+  // the first launch loads a segment record and the fresh rows without branching on their
+  // counts: with none, it reads the workspace (16 KB, 16-byte aligned) and drops what it read
+  args.segs = n_segs > 0 ? segs : (const ckv_segment*)workspace;
   args.n_segs = n_segs;
-  args.kf = (const char*)k_fresh;
-  args.kf_hs_b = kf_head_stride * eb;
-  args.kf_ts_b = kf_token_stride * eb;
-  args.vf = (const char*)v_fresh;
-  args.vf_hs_b = vf_head_stride * eb;
-  args.vf_ts_b = vf_token_stride * eb;
+  const bool fresh = n_fresh > 0;
+  args.kf = fresh ? (const char*)k_fresh : (const char*)workspace;
+  args.kf_hs_b = fresh ? kf_head_stride * eb : 0;
+  args.kf_ts_b = fresh ? kf_token_stride * eb : 0;
+  args.vf = fresh ? (const char*)v_fresh : (const char*)workspace;
+  args.vf_hs_b = fresh ? vf_head_stride * eb : 0;
+  args.vf_ts_b = fresh ? vf_token_stride * eb : 0;
   args.n_fresh = n_fresh;
   args.flags = pos_flags;
   args.local = local;

@@ -261,9 +261,13 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   int32_t* keep_rank = a.keep_rank;
   const bool vec_ok = KPT % 4 == 0 && (((uintptr_t)diff | (uintptr_t)local) % 16 == 0) &&
                       ((uintptr_t)flags % 4 == 0) && (keep_rank == nullptr || (uintptr_t)keep_rank % 16 == 0);
+  // One branch per wavefront, not per thread and group: with a per-thread choice the two paths
+  // write the same registers, so every vector group had to land before the next could go out
+  // (three memory round trips in a row instead of one).
+  const int wave_end = __builtin_amdgcn_readfirstlane((wave + 1) * kWave * KPT);
+  if (vec_ok && wave_end <= n_tokens) {  // uniform: the whole wavefront's runs are in range
 #pragma unroll
-  for (int i0 = 0; i0 < KPT; i0 += 4) {
-    if (vec_ok && p0 + i0 + 4 <= n_tokens) {
+    for (int i0 = 0; i0 < KPT; i0 += 4) {
       float4 d;
       if constexpr (COH) {
         d = make_float4(ld_val<true>(diff + p0 + i0), ld_val<true>(diff + p0 + i0 + 1), ld_val<true>(diff + p0 + i0 + 2),
@@ -281,14 +285,14 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
       lv[i0 + 1] = l.y;
       lv[i0 + 2] = l.z;
       lv[i0 + 3] = l.w;
-    } else {
+    }
+  } else {
 #pragma unroll
-      for (int i = i0; i < i0 + 4 && i < KPT; ++i) {
-        const int p = p0 + i;
-        dv[i] = p < n_tokens ? ld_val<COH>(diff + p) : __uint_as_float(0x7fc00000u);  // NaN: key 0
-        lv[i] = p < n_tokens ? local[p] : 0;
-        if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
-      }
+    for (int i = 0; i < KPT; ++i) {
+      const int p = p0 + i;
+      dv[i] = p < n_tokens ? ld_val<COH>(diff + p) : __uint_as_float(0x7fc00000u);  // NaN: key 0
+      lv[i] = p < n_tokens ? local[p] : 0;
+      if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
     }
   }
   // the top-digit bins this thread owns: bins b0 .. b0 + 3, b0 = kTopBins - 4 (tid + 1), so that
