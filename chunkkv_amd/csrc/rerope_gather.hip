@@ -41,7 +41,8 @@ namespace ckv {
 //    neighbouring tiles of one segment. Dense gathers (every row of a segment): 256 threads x 8
 //    tokens x 2 slots. Gathers with a skip map (a selection leaves rows out at scattered
 //    positions): 512 x 16 x 1; the 8k request's dropped rows of 26 layers (24 segments) take
-//    95 us, against 112 us with the segment-fastest grid.
+//    95 us, against 112 us with the segment-fastest grid, and 108 / 114 us with 256 threads x
+//    16 tokens x 2 slots / 32 tokens x 4 slots.
 //  - Segment-fastest grid (x = segment, y = tile), 256 x 16 x 4, for launches of 64 segments or
 //    more: the replay's 4 concurrent 32k requests (128 segments each) reach 75.0 % of HBM peak
 //    with it, 68.2 % with the tile-fastest shapes above.
@@ -90,6 +91,18 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
 
   __shared__ float2 cs_tab[HALF];
 
+  // the inverse frequency of each cos/sin lane, assembled from the argument segment's scalars
+  // (lane k of the evaluating wavefront gets inv[k]): the evaluation below then depends on no
+  // vector load, so it runs while the row loads are in flight (a vector load of its own would
+  // wait for every row load issued before it)
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int ln = (int)threadIdx.x % kWave;
+  float my_inv = 0.0f;
+#pragma unroll
+  for (int k = 0; k < HALF; ++k) {
+    if (k / kWave == wave) my_inv = ln == k % kWave ? inv.v[k] : my_inv;  // uniform test, scalar operand
+  }
+
   ckv_segment s = one_seg;
   if (segs != nullptr) {
     typedef __attribute__((address_space(1))) const int32_t gi32;
@@ -137,10 +150,26 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
   bool live[kGatherUnroll];
 
   // A row is gathered unless its token lies past the segment or skip marks it (skip[p] >= 0:
-  // an active position whose row the fresh K/V provides).
+  // an active position whose row the fresh K/V provides). The tile's skip entries come in
+  // together as scalar loads beside the chunk addresses (indices clamped into the segment) and
+  // make one mask, so no row load waits for a skip load of its own.
+  uint32_t skipped = 0u;  // bit t: token t0 + t is skipped
+  if (skip != nullptr) {  // uniform
+    const int base = s.dst_start + t0;
+    int sv[kGatherTile];
+    if (base + kGatherTile <= n_tokens) {  // adjacent entries: merged into wide scalar loads
+#pragma unroll
+      for (int t = 0; t < kGatherTile; ++t) sv[t] = skip[base + t];
+    } else {  // the request's last tile: indices clamped (entries past the tile are not used)
+#pragma unroll
+      for (int t = 0; t < kGatherTile; ++t) sv[t] = skip[min(base + t, n_tokens - 1)];
+    }
+#pragma unroll
+    for (int t = 0; t < kGatherTile; ++t) skipped |= (sv[t] >= 0 ? 1u : 0u) << t;
+  }
   auto row_ok = [&](int r) {
-    if (r >= rows || (r % kGatherTile) >= ntok) return false;
-    return skip == nullptr || skip[s.dst_start + t0 + (r % kGatherTile)] < 0;
+    const int tok = r % kGatherTile;
+    return r < rows && tok < ntok && !((skipped >> tok) & 1u);
   };
   auto src_off = [&](int r) { return (int64_t)(r / kGatherTile) * src_head_b + (int64_t)(r % kGatherTile) * ROW_B; };
   auto dst_off = [&](int r) { return (int64_t)(r / kGatherTile) * dst_head_stride_b + (int64_t)(r % kGatherTile) * ROW_B; };
@@ -168,7 +197,7 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
   const bool rotate = s.delta != 0;
   float c[VEC], sn[VEC];
   if (rotate) {
-    if (threadIdx.x < HALF) cs_tab[threadIdx.x] = shift_cos_sin(inv.v[threadIdx.x], s.delta);
+    if (threadIdx.x < HALF) cs_tab[threadIdx.x] = shift_cos_sin(my_inv, s.delta);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {

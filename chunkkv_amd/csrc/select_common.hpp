@@ -87,13 +87,15 @@ __device__ __forceinline__ void set_bit_range(uint32_t* w, int a, int b, int lan
   }
 }
 
-// Exclusive workgroup scan of one int per thread with ONE barrier: each call must get its own
-// `slots` array (kSelWaves ints) that no call in flight since the previous barrier reads.
+// Exclusive workgroup scan of one int per thread with ONE barrier, which orders LDS only (the
+// scan exchanges nothing through global memory; a full barrier would wait for this wavefront's
+// stores in flight): each call must get its own `slots` array (kSelWaves ints) that no call in
+// flight since the previous barrier reads.
 __device__ __forceinline__ int block_scan_1b(int v, int* slots, int& total) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int x = (int)wave_incl_scan((uint32_t)v);
   if (lane == kWave - 1) slots[wave] = x;
-  __syncthreads();
+  lds_barrier();
   int before = 0, all = 0;
 #pragma unroll
   for (int w = 0; w < kSelWaves; ++w) {
@@ -110,7 +112,7 @@ __device__ __forceinline__ uint64_t block_scan_1b_u64(uint64_t v, uint64_t* slot
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const uint64_t x = wave_incl_scan(v);
   if (lane == kWave - 1) slots[wave] = x;
-  __syncthreads();
+  lds_barrier();
   uint64_t before = 0, all = 0;
 #pragma unroll
   for (int w = 0; w < kSelWaves; ++w) {
@@ -177,6 +179,7 @@ __device__ __forceinline__ void chunk_sums_wave(const SelectArgs& a, int c) {
 
 constexpr uint64_t kField = 0x1fffffull;  // 21-bit count fields of the packed workgroup scans
 constexpr int kLightPass = 1024;          // candidates in the top bin up to which passes are light
+constexpr int kRankMax = 128;             // candidates in the top bin up to which they are ranked directly
 
 // The selection for n_tokens <= KPT * 1024, run by one whole 1024-thread workgroup: thread t owns
 // positions [t*KPT, (t+1)*KPT), whose keys stay in registers through every radix pass.
@@ -229,7 +232,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   __shared__ uint32_t hl[3][256];  // one shared histogram per pass after the top digit (few candidates)
   __shared__ int slots[2][kSelWaves];
   __shared__ uint64_t slots64[2][kSelWaves];
-  __shared__ int s_budget_req, s_bad_span;
+  __shared__ int s_budget_req, s_bad_span, s_rk_n;
   __shared__ int s_top[3];  // threshold top digit, ties still to take after it, its bin's count
 
   const float* __restrict__ diff = a.diff;
@@ -323,6 +326,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   if (tid == 0) {
     s_budget_req = 0;
     s_bad_span = 0;
+    s_rk_n = 0;
   }
   for (int w = tid; w < 2 * W; w += kSelThreads) masks[w] = 0u;
   for (int b = tid; b < 2 * kSelWaves * 256; b += kSelThreads) (&hist[0][0][0])[b] = 0u;
@@ -457,11 +461,61 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     tie_count = s_top[2];
     first_pass = 1;
   }
+  // With the top digit known and at most kRankMax candidates in its bin, the bin's candidates
+  // are listed in LDS and each ranked against the others by (key descending, position
+  // ascending): the first `need` are taken, ties included, in one pass and two barriers instead
+  // of three radix passes and a tie scan. The list and the taken-position bitmap use the
+  // per-wavefront histograms' storage, idle on this path (the bitmap half was cleared up front).
+  const bool ranked = budget > 0 && use_top && tie_count <= kRankMax;  // uniform
+  uint64_t take = 0u, tie = 0u;
+  if (ranked) {
+    uint2* rk = reinterpret_cast<uint2*>(&hist[0][0][0]);  // (key, position), kRankMax entries
+    uint32_t* takebits = &hist[1][0][0];                     // one bit per position, W words
+    const uint32_t bin = prefix >> kTopShift;
+    int mine_n = 0;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) mine_n += (((cand >> i) & 1ull) && (key[i] >> kTopShift) == bin) ? 1 : 0;
+    const int incl = (int)wave_incl_scan((uint32_t)mine_n);
+    int wbase = 0;
+    if (lane == kWave - 1) wbase = atomicAdd(&s_rk_n, incl);  // one LDS atomic per wavefront
+    int off = __builtin_amdgcn_readlane(wbase, kWave - 1) + incl - mine_n;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      if (((cand >> i) & 1ull) && (key[i] >> kTopShift) == bin) {
+        if (off < kRankMax) rk[off] = make_uint2(key[i], (uint32_t)(p0 + i));  // the count says so
+        ++off;
+      }
+    }
+    lds_barrier();
+    const int m = tie_count;  // the histogram's count of this bin = entries listed
+    if (tid < m) {
+      const uint2 me = rk[tid];
+      int ahead = 0;
+      for (int j = 0; j < m; ++j) {  // every lane reads the same entry: an LDS broadcast
+        const uint2 o = rk[j];
+        ahead += (o.x > me.x || (o.x == me.x && o.y < me.y)) ? 1 : 0;
+      }
+      if (ahead < need) atomicOr(&takebits[me.y >> 5], 1u << (me.y & 31));
+    }
+    lds_barrier();
+    const uint32_t above_bin = prefix | ((1u << kTopShift) - 1u);  // largest key in the bin
+    if (p0 < n_tokens) {
+      const int w0 = p0 >> 5;
+      const uint64_t tb = ((uint64_t)takebits[w0] | (w0 + 1 < W ? (uint64_t)takebits[w0 + 1] << 32 : 0ull)) >> (p0 & 31);
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        if ((cand >> i) & 1ull) {
+          const bool in_bin = (key[i] >> kTopShift) == bin;
+          take |= (uint64_t)((key[i] > above_bin) || (in_bin && ((tb >> i) & 1ull))) << i;
+        }
+      }
+    }
+  }
   // After the top digit, few candidates share its bin: one shared histogram per pass (its own
   // buffer, cleared up front) and one LDS barrier. Otherwise per-wavefront histograms folded
   // after a second barrier, so hot bins do not serialise LDS atomics.
   const bool light = use_top && tie_count <= kLightPass;
-  if (budget > 0) {
+  if (budget > 0 && !ranked) {
     // passes over the bits below the known prefix: 8, 8, 8, 8 from bit 31, or, after the
     // top-digit histogram, 8, 8 and 4 from bit 19
 #pragma unroll
@@ -490,7 +544,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
       if (light) {
         lds_barrier();
       } else {
-        __syncthreads();
+        lds_barrier();
         if (tid < 256) {  // fold the per-wavefront histograms into h[0]
           uint32_t t = 0;
 #pragma unroll
@@ -500,7 +554,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
           uint32_t* o = &hist[(pass + 1) & 1][0][0];
           for (int b = tid - 256; b < kSelWaves * 256; b += kSelThreads - 256) o[b] = 0u;
         }
-        __syncthreads();
+        lds_barrier();
       }
       const uint32_t* hsum = light ? hmine : h[0];
       // every wavefront finds the digit: lane l owns digits 255-4l .. 252-4l (descending)
@@ -535,8 +589,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   const uint32_t T = prefix;
 
   // Phase 4: take key > T and the first `need` ties at T in token order, then compact.
-  uint64_t take = 0u, tie = 0u;
-  if (budget > 0) {
+  if (budget > 0 && !ranked) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       if ((cand >> i) & 1ull) {
@@ -545,7 +598,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
       }
     }
   }
-  if (need < tie_count) {  // uniform: only then do ties need ranking (lowest positions first)
+  if (!ranked && need < tie_count) {  // uniform: only then do ties need ranking (lowest positions first)
     int tie_total = 0;
     int tie_rank = block_scan_1b(__popcll(tie), slots[1], tie_total);
 #pragma unroll
@@ -556,7 +609,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
       }
     }
   } else {
-    take |= tie;  // every tie at T is taken
+    take |= tie;  // every tie at T is taken (none when ranked)
   }
   const uint64_t kept = kept_static | take;
   // One scan for three counts in 21-bit fields (each total <= n_tokens < 2^21): kept positions
