@@ -32,7 +32,7 @@ COUNT_CANDIDATES = 3
 COUNT_UNCOMPUTED = 4
 COUNT_BUDGET_REQUESTED = 5
 COUNT_BAD_SPANS = 6
-COUNT_TOP_HISTOGRAM = 7
+COUNT_TOP_HISTOGRAM = 7  # bit 0: histogram path; bit 1: threshold bin ranked directly
 COUNT_N = 8
 
 DEVIATION_SELECT_WORKSPACE_BYTES = 16640

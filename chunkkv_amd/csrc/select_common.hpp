@@ -659,7 +659,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     counts[CKV_COUNT_UNCOMPUTED] = uncomputed;
     counts[CKV_COUNT_BUDGET_REQUESTED] = budget_req;
     counts[6] = s_bad_span;
-    counts[7] = use_top ? 1 : 0;
+    counts[7] = (use_top ? 1 : 0) | (ranked ? 2 : 0);
   }
 }
 

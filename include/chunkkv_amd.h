@@ -96,7 +96,10 @@ typedef struct ckv_chunk_span {
 #define CKV_COUNT_UNCOMPUTED 4      /* kept tokens absent from the previous active set      */
 #define CKV_COUNT_BUDGET_REQUESTED 5
 #define CKV_COUNT_BAD_SPANS 6       /* spans outside [0, n_tokens), skipped                  */
-#define CKV_COUNT_TOP_HISTOGRAM 7   /* 1 when ckv_deviation_select's histogram path ran      */
+#define CKV_COUNT_TOP_HISTOGRAM 7   /* bit 0: the selection started from a counted top-12-bit
+                                       histogram (ckv_deviation_select, ckv_layer1_repair);
+                                       bit 1: the threshold bin's candidates (at most 128)
+                                       were ranked directly instead of by radix passes      */
 #define CKV_COUNT_N 8
 
 /* Bytes of the workspace ckv_deviation_select takes (a 4096-bin histogram and a ticket). */

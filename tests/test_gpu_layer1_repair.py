@@ -7,8 +7,9 @@ escalated and the counts.
 Cases: the 8k request's shape (24 chunks x 320 at shuffled positions + 576 uncached, 30 %), the
 config-3 shape at 15/30/50 %, the replay's 32,832-token request,
 small requests with exact and overlapping placements at head_dim 64 in bf16 and fp32, an
-escalation threshold, deviations that tie (one histogram bin holding every candidate: more radix
-rounds, then equal keys ranked by position), NaN deviations, one workspace across calls of
+escalation threshold, a threshold bin ranked directly and one refined by radix passes, deviations
+that tie (one histogram bin holding every candidate: more radix rounds, then equal keys ranked by
+position), NaN deviations, one workspace across calls of
 different sizes (the histogram is left zeroed), and replays of a captured HIP graph."""
 
 import numpy as np
@@ -229,7 +230,7 @@ def test_tied_deviations_rank_by_position():
     starts = [(c, c * 256) for c in range(48)]
     req = Request(11, [256] * 48, starts, 48 * 256 + 64, ratio=0.3, noise=0.0)
     counts = check(req, oracle=False)
-    assert counts[_native.COUNT_TOP_HISTOGRAM] == 1
+    assert counts[_native.COUNT_TOP_HISTOGRAM] & 1 == 1
 
 
 def test_quantised_deviations_tie_inside_the_list():
@@ -242,6 +243,40 @@ def test_quantised_deviations_tie_inside_the_list():
     mag = torch.tensor([0.5, 1.0, 2.0], device=DEV)[torch.arange(k.shape[2], device=DEV) % 3]
     k[0, 0, :, 0] = torch.where(cached, mag, k[0, 0, :, 0].float()).to(k.dtype)
     req.k = k
+    counts = check(req)
+    assert counts[_native.COUNT_TOP_HISTOGRAM] & 1 == 1
+
+
+def _refresh_rows(req, sig):
+    """Fresh rows = the cached rows + sig[position] x N(0, 1) (uncached positions random)."""
+    g = torch.Generator(device=DEV).manual_seed(77)
+    base_k, base_v = req.gather_reference()[:2]
+    act = torch.from_numpy(req.plan.layer0_idx).to(DEV)
+    cached = torch.from_numpy(req.plan.cached).to(DEV)[act][None, None, :, None]
+    sig = sig[None, None, :, None]
+    rnd = lambda: torch.randn((1, req.H, len(act), req.D), generator=g, device=DEV)  # noqa: E731
+    req.k = torch.where(cached, base_k[:, :, act].float() + sig * rnd(), rnd()).to(req.dtype)
+    v_rows = torch.where(cached, base_v[:, :, act].float() + sig * rnd(), rnd()).to(req.dtype)
+    req.v = v_rows.transpose(1, 2).contiguous().transpose(1, 2)
+
+
+def test_threshold_bin_ranked_directly():
+    """A noise level per position spread over decades: few candidates share the threshold's
+    top-12-bit bin, so they are ranked directly (counts[7] bit 1), bit-exact with the oracle."""
+    starts = [(c, c * 256) for c in range(24)]
+    req = Request(21, [256] * 24, starts, 24 * 256 + 64, ratio=0.3)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    _refresh_rows(req, torch.exp(2.0 * torch.randn(len(req.plan.layer0_idx), generator=g, device=DEV)))
+    counts = check(req)
+    assert counts[_native.COUNT_TOP_HISTOGRAM] == 3
+
+
+def test_threshold_bin_refined_by_radix_passes():
+    """One noise level everywhere: every candidate's deviation lies within a few percent, one or
+    two bins hold them all, and the bin is refined by radix passes (counts[7] bit 1 clear)."""
+    starts = [(c, c * 256) for c in range(24)]
+    req = Request(22, [256] * 24, starts, 24 * 256 + 64, ratio=0.3)
+    _refresh_rows(req, torch.full((len(req.plan.layer0_idx),), 0.05, device=DEV))
     counts = check(req)
     assert counts[_native.COUNT_TOP_HISTOGRAM] == 1
 

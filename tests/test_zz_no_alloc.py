@@ -68,7 +68,7 @@ def test_noalloc_matches_workspace_entry_two_calls():
         torch.cuda.synchronize()
         assert int(err.item()) == 0
         n = int(s_ws.counts[0].item())
-        assert int(out.counts[_native.COUNT_TOP_HISTOGRAM].item()) == 1  # the scratch-backed path ran
+        assert int(out.counts[_native.COUNT_TOP_HISTOGRAM].item()) & 1 == 1  # the scratch-backed path ran
         assert torch.equal(diff.view(torch.int32), d_ws.view(torch.int32))
         assert torch.equal(norm.view(torch.int32), n_ws.view(torch.int32))
         assert torch.equal(out.counts, s_ws.counts)
