@@ -73,8 +73,8 @@ GATHER_BYTES = N_LAYERS * N_CHUNKS * CHUNK_LEN * ROW_BYTES * 2 * 2
 # known traffic). Counters cannot be read inside a timed run, so the measured value is recorded.
 GATHER_TRAFFIC_BYTES = 881_167_672
 # Same for one gather of the dropped rows of layers 2-27 of the 8k request (FETCH_SIZE median
-# 137,405 KiB / 0.500046 + WRITE_SIZE median 274,573 KiB; 562,298,880 algorithmic bytes).
-DROPPED_TRAFFIC_BYTES = 562_646_570
+# 137,468 KiB / 0.500023 + WRITE_SIZE median 274,565 KiB; 562,298,880 algorithmic bytes).
+DROPPED_TRAFFIC_BYTES = 562_675_830
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 
