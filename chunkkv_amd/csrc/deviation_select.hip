@@ -10,15 +10,16 @@
 // positions of a tile at a time.
 //  1. Every workgroup computes its tiles' deviations in the fixed summation order, writes
 //     diff/norm, and counts each position that is cached, pooled and not a sink (a candidate
-//     when no chunk escalates) into a 4096-bin histogram of key >> 20 in the workspace, one
+//     when no chunk escalates) into the selection's top_bin histogram (4096 bins) in the workspace, one
 //     global atomic per distinct bin of a tile.
 //  2. The writes are device-scope stores and atomics (the L2s of the XCDs are not coherent with
 //     each other) and each wavefront waits for its own to complete; then one atomic ticket per
 //     workgroup finds the last workgroup to finish. The others exit; none waits for another.
 //  3. The last workgroup acquires and runs the selection (select_run) with the histogram: the
-//     threshold's top 12 bits come from one scan over it and only 20 bits go through LDS radix
-//     passes. If the histogram does not match the candidate set (a chunk escalated, or the
-//     flags' pooled bit disagrees with the spans), the selection runs its full four passes.
+//     threshold's bin comes from one scan over it and only that bin's candidates are ranked.
+//     If the histogram does not match the candidate set (a chunk escalated, or the flags'
+//     pooled bit disagrees with the spans), or the threshold falls outside the histogram's
+//     window, the selection runs its full four passes.
 //  4. The last workgroup leaves the histogram and the ticket zeroed: the workspace needs
 //     clearing once, before its first use, and never again.
 // Up to 33792 positions (33 per thread of the selecting workgroup); larger requests run
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(kSelThreads) void deviation_select_kernel(DevArgs d
           __hip_atomic_store(diff + p, dv[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store(norm + p, nv[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           if ((fl[t] & CKV_POS_CACHED) && !(fl[t] & CKV_POS_SINK) && (fl[t] & CKV_POS_POOLED))
-            bin = dev_key(dv[t]) >> kTopShift;
+            bin = top_bin(dev_key(dv[t]));
         }
         s_bin[wave * kDsTok + t] = bin;
       }

@@ -6,7 +6,7 @@
 namespace ckv {
 
 // The selection (select.hip): the register-resident form up to 33792 positions, with ghist (may
-// be NULL) a top-12-bit candidate histogram that the launch leaves zeroed; the L2 form above
+// be NULL) a top_bin candidate histogram that the launch leaves zeroed; the L2 form above
 // (ghist must then be NULL).
 int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st);
 

@@ -3,9 +3,10 @@
 // the compaction of the new active set and the scatter of the kept rows, as three launches:
 //   1. layer1_gather_deviation_kernel: every position's rows (the chunk's row re-rotated by the
 //      placement's shift, the fresh row), the cached row written into the cache, the deviation,
-//      and the candidate count of the key's top 12 bits into a 4096-bin histogram;
-//   2. the selection (select_common.hpp) in one workgroup, its threshold's top 12 bits read off
-//      that histogram, so only the candidates of one bin go through radix passes;
+//      and the candidates counted into the selection's top-digit histogram (top_bin: 4096 bins
+//      of 1/64 octave of deviation);
+//   2. the selection (select_common.hpp) in one workgroup, its threshold's bin read off that
+//      histogram, so only the candidates of one bin are ranked;
 //   3. the kept rows scattered from the fresh rows, their count read on the device.
 // Nothing is read back on the host.
 //
@@ -284,7 +285,7 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
 // Launch 1: the positions of kL1Waves wavefronts (P consecutive ones) per workgroup. Cached rows
 // go into the cache (sinks excepted: always kept, the scatter writes them), deviations out, and
 // the positions flagged cached, pooled and not sink (the candidates when no chunk escalates)
-// counted by their key's top 12 bits, one atomic per distinct bin of the workgroup.
+// counted by their key's top_bin, one atomic per distinct bin of the workgroup.
 template <int DTYPE, int T>
 __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(L1Args a, const InvFreq inv) {
   constexpr int P = kL1Waves * T;
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(L1A
         a.norm[p] = nv[t];
       }
       const bool cand = (cls[t] & kCCached) && (cls[t] & kCPooled) && !(cls[t] & kCSink);
-      s_bin[wave * T + t] = cand ? dev_key(dv[t]) >> 20 : ~0u;
+      s_bin[wave * T + t] = cand ? top_bin(dev_key(dv[t])) : ~0u;
     }
   }
   if (a.hist == nullptr) return;  // uniform

@@ -9,7 +9,7 @@
 namespace ckv {
 
 // Register-resident selection (select_run) for n_tokens <= KPT * 1024; ghist (may be NULL) is a
-// top-12-bit candidate histogram counted by an earlier launch, left zeroed. Without a threshold
+// top_bin candidate histogram counted by an earlier launch, left zeroed. Without a threshold
 // (SUMS = false) workgroup 0 selects and the others compute the chunks' rel_dev, one wavefront
 // per chunk, beside it.
 template <int KPT, bool SUMS>

@@ -21,10 +21,10 @@
 // exact threshold key T and how many ties at T to take; then key > T plus the lowest-index ties
 // are taken and the kept positions compacted in token order. Each thread owns a contiguous run
 // of KPT <= 33 positions whose keys stay in registers for every pass. A caller that already
-// counted the candidates' top 12 key bits (ckv_deviation_select does so while it computes the
-// deviations) hands that histogram in: the threshold's top 12 bits then come from one
-// workgroup scan over it, and only the remaining 20 bits go through radix passes, over the few
-// candidates in that bin.
+// counted the candidates by top_bin (ckv_deviation_select and ckv_layer1_repair do so while they
+// compute the deviations) hands that histogram in: the threshold's bin then comes from one
+// workgroup scan over it, and only the few candidates in that bin are ranked (directly, up to
+// kRankMax of them, else by radix passes over the remaining 17 key bits).
 #pragma once
 
 #include "ckv_common.hpp"
@@ -33,9 +33,21 @@ namespace ckv {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / kWave;
-constexpr int kTopShift = 20;                    // top-digit histogram bin = key >> 20
-constexpr int kTopBins = 1 << (32 - kTopShift);  // 4096 bins
+// Top-digit histogram: kTopBins bins over a window of the keys of positive deviations. Interior
+// bin b (1 <= b <= kTopBins - 2) holds the keys [kTopLo + (b - 1) 2^kTopShift, kTopLo + b 2^kTopShift),
+// i.e. the keys whose top 32 - kTopShift bits equal those of kTopLo + (b - 1) 2^kTopShift: 1/64 of an
+// octave of deviation each (the sign, the exponent and 6 mantissa bits), 4094 of them covering
+// 2^-24 <= diff < 2^39.97. Bin 0 holds every key below the window (smaller deviations, zero, NaN)
+// and bin kTopBins - 1 every key above it; they are not key prefixes, so a threshold that falls
+// into one is found by full radix passes instead. (Deviations are sums of squares, so the window
+// spends no bins on negative values, and deviations of one chunk, which cluster within a few
+// percent of each other, spread over several bins.)
+constexpr int kTopShift = 17;
+constexpr int kTopBins = 4096;
+constexpr uint32_t kTopLo = 0x80000000u | (103u << 23);  // key of 2^-24
 static_assert(kTopBins == 4 * kSelThreads, "each thread owns four top-digit bins");
+static_assert((kTopLo & ((1u << kTopShift) - 1u)) == 0u, "interior bins are key prefixes");
+static_assert((uint64_t)kTopLo + ((uint64_t)(kTopBins - 2) << kTopShift) <= 0xffffffffull, "window inside the key range");
 
 // Order-preserving key of a deviation: larger float -> larger key; -0 == +0; NaN -> 0.
 __device__ __forceinline__ uint32_t dev_key(float f) {
@@ -44,6 +56,15 @@ __device__ __forceinline__ uint32_t dev_key(float f) {
   const uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+
+// Histogram bin of a key (monotone in the key).
+__device__ __forceinline__ uint32_t top_bin(uint32_t key) {
+  if (key < kTopLo) return 0u;
+  const uint32_t b = ((key - kTopLo) >> kTopShift) + 1u;
+  return b < (uint32_t)kTopBins - 1u ? b : (uint32_t)kTopBins - 1u;
+}
+// Smallest key of interior bin b.
+__device__ __forceinline__ uint32_t top_bin_prefix(uint32_t b) { return kTopLo + ((b - 1u) << kTopShift); }
 
 __device__ __forceinline__ bool bit_of(const uint32_t* w, int p) { return (w[p >> 5] >> (p & 31)) & 1u; }
 
@@ -183,10 +204,11 @@ constexpr int kRankMax = 128;             // candidates in the top bin up to whi
 
 // The selection for n_tokens <= KPT * 1024, run by one whole 1024-thread workgroup: thread t owns
 // positions [t*KPT, (t+1)*KPT), whose keys stay in registers through every radix pass.
-//   ghist  NULL, or the 4096-bin histogram of key >> 20 over the positions flagged cached, pooled
-//          and not sink (what the candidates are when no chunk escalates). It is used when it
-//          matches the candidate set exactly (same positions, same total), else the selection
-//          runs its full four passes. Either way it is zeroed before the function returns.
+//   ghist  NULL, or the top_bin histogram over the positions flagged cached, pooled and not sink
+//          (what the candidates are when no chunk escalates). It is used when it matches the
+//          candidate set exactly (same positions, same total) and the threshold falls into an
+//          interior bin, else the selection runs its full four passes. Either way it is zeroed
+//          before the function returns.
 //   masks  2 * ceil(n_tokens / 32) words of LDS.
 // Barrier budget: chunk phase 1; candidate scan 1; top-bin broadcast 1 (histogram path);
 // 2 per radix pass (double-buffered histograms, every wavefront derives the digit itself); tie
@@ -198,13 +220,22 @@ constexpr int kSelPre = KPT <= 16 ? 2 : 1;
 // Spans of the chunks wavefront `wave` handles first (wave + r * 16, r < kSelPre), zero past the
 // last chunk: loaded by every workgroup of ckv_deviation_select at its start, so the selecting
 // workgroup has them without a dependent round trip.
+// Span c (c uniform) through the scalar cache: the spans are constant for the launch, and a
+// scalar load leaves the wavefront's vector loads in flight (a vector load would be waited for
+// together with every one issued before it).
+__device__ __forceinline__ ckv_chunk_span span_at(const ckv_chunk_span* chunks, int c) {
+  typedef __attribute__((address_space(4))) const int32_t ci32;
+  ci32* f = (ci32*)(chunks + c);
+  return ckv_chunk_span{f[0], f[1], f[2], f[3]};
+}
+
 template <int KPT>
 __device__ __forceinline__ void load_first_spans(const ckv_chunk_span* chunks, int n_chunks, int wave,
                                                  ckv_chunk_span (&sp)[kSelPre<KPT>]) {
 #pragma unroll
   for (int r = 0; r < kSelPre<KPT>; ++r) {
     const int c = wave + r * kSelWaves;
-    sp[r] = c < n_chunks ? chunks[c] : ckv_chunk_span{0, 0, 0, 0};
+    sp[r] = c < n_chunks ? span_at(chunks, c) : ckv_chunk_span{0, 0, 0, 0};
   }
 }
 
@@ -242,7 +273,10 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   const int n_tokens = a.n_tokens;
   const ckv_chunk_span* __restrict__ chunks = a.chunks;
   const int n_chunks = a.n_chunks;
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  // uniform, so the chunk loop below loads its spans through the scalar cache: a vector load
+  // there would make the loop wait for every row load issued before it
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int W = (n_tokens + 31) >> 5;
   uint32_t* escw = masks;
   uint32_t* poolw = masks + W;
@@ -268,6 +302,22 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   // write the same registers, so every vector group had to land before the next could go out
   // (three memory round trips in a row instead of one).
   const int wave_end = __builtin_amdgcn_readfirstlane((wave + 1) * kWave * KPT);
+  // The loads go out in the order their values are needed (vector loads complete in issue order):
+  // the deviations, the top-digit histogram, the flags, and last the local indices, which only
+  // the compaction uses.
+  // The top-digit bins this thread owns: bins b0 .. b0 + 3, b0 = kTopBins - 4 (tid + 1), so that
+  // thread order is descending bin order.
+  vec16 g4 = {0u, 0u, 0u, 0u};
+  uint32_t* gmine = ghist != nullptr ? ghist + (kTopBins - 4 * (tid + 1)) : nullptr;
+  auto load_hist = [&]() {
+    if (gmine != nullptr) {
+      if constexpr (COH) {
+        g4 = vec16{ld_val<true>(gmine), ld_val<true>(gmine + 1), ld_val<true>(gmine + 2), ld_val<true>(gmine + 3)};
+      } else {
+        g4 = ld16(gmine);
+      }
+    }
+  };
   if (vec_ok && wave_end <= n_tokens) {  // uniform: the whole wavefront's runs are in range
 #pragma unroll
     for (int i0 = 0; i0 < KPT; i0 += 4) {
@@ -278,36 +328,52 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
       } else {
         d = *(const float4*)(diff + p0 + i0);
       }
-      const int4 l = *(const int4*)(local + p0 + i0);
-      fl[i0 / 4] = *(const uint32_t*)(flags + p0 + i0);  // i0 % 4 == 0: flags i0 .. i0 + 3
       dv[i0] = d.x;
       dv[i0 + 1] = d.y;
       dv[i0 + 2] = d.z;
       dv[i0 + 3] = d.w;
+    }
+    load_hist();
+#pragma unroll
+    for (int i0 = 0; i0 < KPT; i0 += 4) fl[i0 / 4] = *(const uint32_t*)(flags + p0 + i0);  // flags i0 .. i0 + 3
+#pragma unroll
+    for (int i0 = 0; i0 < KPT; i0 += 4) {
+      const int4 l = *(const int4*)(local + p0 + i0);
       lv[i0] = l.x;
       lv[i0 + 1] = l.y;
       lv[i0 + 2] = l.z;
       lv[i0 + 3] = l.w;
     }
-  } else {
+  } else if (__builtin_amdgcn_readfirstlane(wave * kWave * KPT) < n_tokens) {  // uniform
+    // The wavefront whose runs cross n_tokens: every load unconditional, its index clamped into
+    // range and the value dropped where it is used, so all of them are in flight together
+    // (loads behind per-position branches went out one round trip at a time).
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int p = p0 + i;
-      dv[i] = p < n_tokens ? ld_val<COH>(diff + p) : __uint_as_float(0x7fc00000u);  // NaN: key 0
-      lv[i] = p < n_tokens ? local[p] : 0;
-      if (p < n_tokens) fl[i / 4] |= (uint32_t)flags[p] << (8 * (i % 4));
+      const float d = ld_val<COH>(diff + min(p, n_tokens - 1));
+      dv[i] = p < n_tokens ? d : __uint_as_float(0x7fc00000u);  // NaN: key 0
     }
-  }
-  // the top-digit bins this thread owns: bins b0 .. b0 + 3, b0 = kTopBins - 4 (tid + 1), so that
-  // thread order is descending bin order
-  vec16 g4 = {0u, 0u, 0u, 0u};
-  uint32_t* gmine = ghist != nullptr ? ghist + (kTopBins - 4 * (tid + 1)) : nullptr;
-  if (gmine != nullptr) {
-    if constexpr (COH) {
-      g4 = vec16{ld_val<true>(gmine), ld_val<true>(gmine + 1), ld_val<true>(gmine + 2), ld_val<true>(gmine + 3)};
-    } else {
-      g4 = ld16(gmine);
+    load_hist();
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int p = p0 + i;
+      const uint32_t b = flags[min(p, n_tokens - 1)];
+      fl[i / 4] |= (p < n_tokens ? b : 0u) << (8 * (i % 4));
     }
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int p = p0 + i;
+      const int lr = local[min(p, n_tokens - 1)];
+      lv[i] = p < n_tokens ? lr : 0;
+    }
+  } else {  // a wavefront past the last position: nothing to load
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      dv[i] = __uint_as_float(0x7fc00000u);
+      lv[i] = 0;
+    }
+    load_hist();
   }
   // the first batch of this wavefront's first chunks' deviations
   float bd0[kPre][kBatch], bn0[kPre][kBatch];
@@ -340,7 +406,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     const bool pre = r < kPre;
     // selected by value, field by field (a select between the addresses would put the spans in
     // scratch memory)
-    const ckv_chunk_span ld = pre ? sp_first : chunks[c];
+    const ckv_chunk_span ld = pre ? sp_first : span_at(chunks, c);
     const bool f = r == 0;
     ckv_chunk_span sp;
     sp.start = pre ? (f ? sp_first.start : sp_last.start) : ld.start;
@@ -433,8 +499,8 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   const int n_cand = (int)(scan_tot & kField);
   const int budget_req = s_budget_req;
   const int budget = max(0, min(budget_req, n_cand));
-  const bool use_top = ghist != nullptr && ((scan_tot >> 21) & kField) == 0 &&
-                       (int)((scan_tot >> 42) & kField) == n_cand;  // uniform
+  bool use_top = ghist != nullptr && ((scan_tot >> 21) & kField) == 0 &&
+                 (int)((scan_tot >> 42) & kField) == n_cand;  // uniform
 
   // Phase 3: radix select of the budget-th largest candidate key.
   uint32_t prefix = 0u, pmask = 0u;
@@ -443,23 +509,29 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   int first_pass = 0;
   if (budget > 0 && use_top) {
     // the bin holding the budget-th largest key, from the counted histogram
-    uint32_t above = (uint32_t)((scan_ex >> 42) & kField);
-    const uint32_t h4[4] = {g4.w, g4.z, g4.y, g4.x};  // bins b0 + 3, b0 + 2, b0 + 1, b0 (descending)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (above < (uint32_t)need && (uint32_t)need <= above + h4[i]) {
-        s_top[0] = kTopBins - 4 * tid - 1 - i;
-        s_top[1] = need - (int)above;
-        s_top[2] = (int)h4[i];
-      }
-      above += h4[i];
+    // (one thread holds it: it walks its four bins, descending, and writes the result once)
+    const uint32_t above = (uint32_t)((scan_ex >> 42) & kField);
+    if (above < (uint32_t)need && (uint32_t)need <= above + gsum) {
+      const uint32_t a3 = above + g4.w, a2 = a3 + g4.z, a1 = a2 + g4.y;  // candidates above bins b0+2, b0+1, b0
+      const uint32_t u = (uint32_t)need;
+      const int i = u <= a3 ? 0 : u <= a2 ? 1 : u <= a1 ? 2 : 3;  // bin b0 + 3 - i
+      const uint32_t before = i == 0 ? above : i == 1 ? a3 : i == 2 ? a2 : a1;
+      const uint32_t cnt = i == 0 ? g4.w : i == 1 ? g4.z : i == 2 ? g4.y : g4.x;
+      s_top[0] = kTopBins - 4 * tid - 1 - i;
+      s_top[1] = need - (int)before;
+      s_top[2] = (int)cnt;
     }
     lds_barrier();
-    prefix = (uint32_t)s_top[0] << kTopShift;
-    pmask = 0xffffffffu << kTopShift;
-    need = s_top[1];
-    tie_count = s_top[2];
-    first_pass = 1;
+    const uint32_t tb = (uint32_t)s_top[0];
+    if (tb == 0u || tb == (uint32_t)kTopBins - 1u) {  // uniform: an edge bin is no key prefix
+      use_top = false;
+    } else {
+      prefix = top_bin_prefix(tb);
+      pmask = 0xffffffffu << kTopShift;
+      need = s_top[1];
+      tie_count = s_top[2];
+      first_pass = 1;
+    }
   }
   // With the top digit known and at most kRankMax candidates in its bin, the bin's candidates
   // are listed in LDS and each ranked against the others by (key descending, position
@@ -471,31 +543,47 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   if (ranked) {
     uint2* rk = reinterpret_cast<uint2*>(&hist[0][0][0]);  // (key, position), kRankMax entries
     uint32_t* takebits = &hist[1][0][0];                     // one bit per position, W words
-    const uint32_t bin = prefix >> kTopShift;
-    int mine_n = 0;
+    // the candidates in the threshold's (interior) bin: keys with its prefix
+    uint64_t inb = 0u;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) mine_n += (((cand >> i) & 1ull) && (key[i] >> kTopShift) == bin) ? 1 : 0;
+    for (int i = 0; i < KPT; ++i) inb |= (uint64_t)((key[i] & pmask) == prefix) << i;
+    inb &= cand;
+    const int mine_n = __popcll(inb);
     const int incl = (int)wave_incl_scan((uint32_t)mine_n);
     int wbase = 0;
     if (lane == kWave - 1) wbase = atomicAdd(&s_rk_n, incl);  // one LDS atomic per wavefront
     int off = __builtin_amdgcn_readlane(wbase, kWave - 1) + incl - mine_n;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      if (((cand >> i) & 1ull) && (key[i] >> kTopShift) == bin) {
+      if ((inb >> i) & 1ull) {
         if (off < kRankMax) rk[off] = make_uint2(key[i], (uint32_t)(p0 + i));  // the count says so
         ++off;
       }
     }
     lds_barrier();
+    // Entry e's rank (entries ahead of it) is counted by the 8 lanes 8e .. 8e + 7, each over
+    // every eighth entry (several LDS reads in flight), then summed over the 8 lanes.
+    static_assert(kRankMax * 8 <= kSelThreads, "eight threads per listed entry");
     const int m = tie_count;  // the histogram's count of this bin = entries listed
-    if (tid < m) {
-      const uint2 me = rk[tid];
+    {
+      const int e = tid >> 3, part = tid & 7;
       int ahead = 0;
-      for (int j = 0; j < m; ++j) {  // every lane reads the same entry: an LDS broadcast
-        const uint2 o = rk[j];
-        ahead += (o.x > me.x || (o.x == me.x && o.y < me.y)) ? 1 : 0;
+      uint2 me = make_uint2(0u, 0u);
+      if (e < m) {
+        me = rk[e];
+        // every eighth entry from `part`, all kRankMax / 8 of them read (inside the list's
+        // storage) and those past m dropped: no loop condition between the reads
+        uint2 o[kRankMax / 8];
+#pragma unroll
+        for (int k = 0; k < kRankMax / 8; ++k) o[k] = rk[part + 8 * k];
+#pragma unroll
+        for (int k = 0; k < kRankMax / 8; ++k)
+          ahead += (part + 8 * k < m && (o[k].x > me.x || (o[k].x == me.x && o[k].y < me.y))) ? 1 : 0;
       }
-      if (ahead < need) atomicOr(&takebits[me.y >> 5], 1u << (me.y & 31));
+      ahead += __shfl_xor(ahead, 1);
+      ahead += __shfl_xor(ahead, 2);
+      ahead += __shfl_xor(ahead, 4);
+      if (e < m && part == 0 && ahead < need) atomicOr(&takebits[me.y >> 5], 1u << (me.y & 31));
     }
     lds_barrier();
     const uint32_t above_bin = prefix | ((1u << kTopShift) - 1u);  // largest key in the bin
@@ -503,12 +591,8 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
       const int w0 = p0 >> 5;
       const uint64_t tb = ((uint64_t)takebits[w0] | (w0 + 1 < W ? (uint64_t)takebits[w0 + 1] << 32 : 0ull)) >> (p0 & 31);
 #pragma unroll
-      for (int i = 0; i < KPT; ++i) {
-        if ((cand >> i) & 1ull) {
-          const bool in_bin = (key[i] >> kTopShift) == bin;
-          take |= (uint64_t)((key[i] > above_bin) || (in_bin && ((tb >> i) & 1ull))) << i;
-        }
-      }
+      for (int i = 0; i < KPT; ++i) take |= (uint64_t)(key[i] > above_bin) << i;
+      take = (take & cand) | (inb & tb);
     }
   }
   // After the top digit, few candidates share its bin: one shared histogram per pass (its own
@@ -517,12 +601,13 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   const bool light = use_top && tie_count <= kLightPass;
   if (budget > 0 && !ranked) {
     // passes over the bits below the known prefix: 8, 8, 8, 8 from bit 31, or, after the
-    // top-digit histogram, 8, 8 and 4 from bit 19
+    // top-digit histogram, 8, 8 and 1 from bit 16
+    static_assert(kTopShift == 17, "pass layout below the top digit");
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
       if (pass < first_pass) continue;
-      const int shift = use_top ? (pass == 1 ? 12 : pass == 2 ? 4 : 0) : 24 - 8 * pass;
-      const uint32_t dmask = (use_top && pass == 3) ? 15u : 255u;
+      const int shift = use_top ? (pass == 1 ? 9 : pass == 2 ? 1 : 0) : 24 - 8 * pass;
+      const uint32_t dmask = (use_top && pass == 3) ? 1u : 255u;
       uint32_t(*h)[256] = hist[pass & 1];
       uint32_t* hmine = light ? hl[pass > 0 ? pass - 1 : 0] : h[wave];
       // Run-length aggregate equal digits within the thread: in the high passes almost every key

@@ -96,8 +96,10 @@ typedef struct ckv_chunk_span {
 #define CKV_COUNT_UNCOMPUTED 4      /* kept tokens absent from the previous active set      */
 #define CKV_COUNT_BUDGET_REQUESTED 5
 #define CKV_COUNT_BAD_SPANS 6       /* spans outside [0, n_tokens), skipped                  */
-#define CKV_COUNT_TOP_HISTOGRAM 7   /* bit 0: the selection started from a counted top-12-bit
-                                       histogram (ckv_deviation_select, ckv_layer1_repair);
+#define CKV_COUNT_TOP_HISTOGRAM 7   /* bit 0: the selection started from the counted
+                                       candidate histogram (ckv_deviation_select,
+                                       ckv_layer1_repair): 4096 bins of 1/64 octave of
+                                       deviation over 2^-24 .. 2^40, the threshold inside;
                                        bit 1: the threshold bin's candidates (at most 128)
                                        were ranked directly instead of by radix passes      */
 #define CKV_COUNT_N 8
@@ -105,7 +107,7 @@ typedef struct ckv_chunk_span {
 /* Bytes of the workspace ckv_deviation_select takes (a 4096-bin histogram and a ticket). */
 #define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 16640
 
-/* Bytes of the workspace ckv_layer1_repair takes (the selection's top-12-bit histogram). */
+/* Bytes of the workspace ckv_layer1_repair takes (the selection's candidate histogram). */
 #define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 16384
 
 /* ABI version compiled into the library (CKV_ABI_VERSION). */
@@ -229,10 +231,11 @@ int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flag
  * (torch_engine.py:117-153) from the fresh and cached rows to the new active set, with outputs
  * and results bit-identical to the two calls (same arguments, same meaning; see both above).
  * The workgroups that compute the deviations also count every position flagged
- * CKV_POS_CACHED | CKV_POS_POOLED and not CKV_POS_SINK into a histogram of its key's top 12 bits;
- * the last workgroup to finish runs the selection from it. When the pooled flags disagree with
- * the pooled spans, or a chunk escalates, the selection ignores the histogram (same result,
- * slower); counts[CKV_COUNT_TOP_HISTOGRAM] says which path ran.
+ * CKV_POS_CACHED | CKV_POS_POOLED and not CKV_POS_SINK into a histogram of its deviation (4096
+ * bins of 1/64 octave); the last workgroup to finish runs the selection from it. When the pooled
+ * flags disagree with the pooled spans, a chunk escalates, or the threshold lies outside
+ * 2^-24 .. 2^40, the selection ignores the histogram (same result, slower);
+ * counts[CKV_COUNT_TOP_HISTOGRAM] says which path ran.
  *   workspace        device memory of >= CKV_DEVIATION_SELECT_WORKSPACE_BYTES, 16-byte aligned,
  *                    ZERO before its first use; every call leaves it zero again. Calls that
  *                    share a workspace must be ordered (one stream, or events): concurrent
@@ -285,7 +288,7 @@ int32_t ckv_deviation_select_noalloc(const void* k_fresh, int64_t kf_head_stride
  * planner's segments, n_segs <= 3840), read for every position flagged CKV_POS_CACHED.
  * Three launches, nothing read back on the host: (1) every position's rows, the cached rows
  * written into the cache, the deviations, and the positions flagged CKV_POS_CACHED |
- * CKV_POS_POOLED and not CKV_POS_SINK counted by their key's top 12 bits; (2) the selection,
+ * CKV_POS_POOLED and not CKV_POS_SINK counted into the deviation histogram; (2) the selection,
  * starting from that count (as ckv_deviation_select's does, same result when the flags disagree
  * with the spans or a chunk escalates, just slower); (3) the kept rows, their count read on the
  * device.

@@ -225,12 +225,12 @@ def test_escalation_threshold():
 
 
 def test_tied_deviations_rank_by_position():
-    """Fresh rows equal to the cached ones: every candidate's deviation is 0, all of them in one
-    histogram bin; the lowest positions win."""
+    """Fresh rows equal to the cached ones: every candidate's deviation is 0, below the
+    histogram's window, so the selection runs its full radix passes; the lowest positions win."""
     starts = [(c, c * 256) for c in range(48)]
     req = Request(11, [256] * 48, starts, 48 * 256 + 64, ratio=0.3, noise=0.0)
     counts = check(req, oracle=False)
-    assert counts[_native.COUNT_TOP_HISTOGRAM] & 1 == 1
+    assert counts[_native.COUNT_TOP_HISTOGRAM] == 0
 
 
 def test_quantised_deviations_tie_inside_the_list():
@@ -262,7 +262,7 @@ def _refresh_rows(req, sig):
 
 def test_threshold_bin_ranked_directly():
     """A noise level per position spread over decades: few candidates share the threshold's
-    top-12-bit bin, so they are ranked directly (counts[7] bit 1), bit-exact with the oracle."""
+    histogram bin, so they are ranked directly (counts[7] bit 1), bit-exact with the oracle."""
     starts = [(c, c * 256) for c in range(24)]
     req = Request(21, [256] * 24, starts, 24 * 256 + 64, ratio=0.3)
     g = torch.Generator(device=DEV).manual_seed(21)
@@ -272,13 +272,34 @@ def test_threshold_bin_ranked_directly():
 
 
 def test_threshold_bin_refined_by_radix_passes():
-    """One noise level everywhere: every candidate's deviation lies within a few percent, one or
-    two bins hold them all, and the bin is refined by radix passes (counts[7] bit 1 clear)."""
+    """One noise level everywhere: every candidate's deviation lies within a few percent, a few
+    1/64-octave bins hold them all, and the threshold's bin is refined by radix passes (counts[7]
+    bit 1 clear)."""
     starts = [(c, c * 256) for c in range(24)]
     req = Request(22, [256] * 24, starts, 24 * 256 + 64, ratio=0.3)
     _refresh_rows(req, torch.full((len(req.plan.layer0_idx),), 0.05, device=DEV))
     counts = check(req)
     assert counts[_native.COUNT_TOP_HISTOGRAM] == 1
+
+
+@pytest.mark.parametrize("sig,top", [(3e5, 0), (None, 1)])
+def test_threshold_beyond_the_histogram_window(sig, top):
+    """Deviations above the histogram's window (about 2^40): with every candidate there the
+    threshold's bin is an edge bin and the selection runs its full radix passes (counts[7] 0);
+    with a few positions there and the rest spread over decades the threshold bin is interior
+    (the edge bin only counts above it). Both bit-exact with the oracle."""
+    starts = [(c, c * 256) for c in range(24)]
+    req = Request(23, [256] * 24, starts, 24 * 256 + 64, ratio=0.3)
+    n = len(req.plan.layer0_idx)
+    if sig is None:
+        g = torch.Generator(device=DEV).manual_seed(23)
+        s = torch.exp(1.5 * torch.randn(n, generator=g, device=DEV))
+        s[::97] = 3e5  # deviations ~1e14, in the top edge bin
+    else:
+        s = torch.full((n,), sig, device=DEV)
+    _refresh_rows(req, s)
+    counts = check(req)
+    assert counts[_native.COUNT_TOP_HISTOGRAM] & 1 == top
 
 
 def test_nan_deviations_rank_last():
