@@ -633,11 +633,13 @@ DEV_SETS = 16  # config-3 input sets rotated per graph replay: 16 x 50 MB > 512 
 def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
     """Deviation + pooled top-k + scatter microbenchmark: layer-1 fresh vs cached K/V for 32 chunks
     x 256 tokens (8192), 4 heads x 128, bf16; cached = fresh + sigma_c N(0,1), sigma_c ~
-    lognormal(-3, 1); pooled top-k at 15/30/50% plus 4 sinks per chunk (ckv_deviation_select, one
-    launch), then the kept rows compacted and scattered into the layer's cache
-    (ckv_scatter_kept_rows). DEV_SETS independent input sets (33.6 MB of K/V read and the kept
-    rows written per set, ~800 MB in all) are cycled through inside each graph replay, so every
-    launch reads HBM rather than the 256 MB MALL."""
+    lognormal(-3, 1); pooled top-k at 15/30/50% plus 4 sinks per chunk (ckv_deviation_select: the
+    deviation counting the candidate histogram, then the selection starting from it), then the
+    kept rows compacted and scattered into the layer's cache (ckv_scatter_kept_rows). Also timed:
+    the deviation alone (ckv_deviation, the HBM-bound launch: the roofline) and the deviation and
+    selection without the histogram (ckv_deviation + ckv_select). DEV_SETS independent input sets
+    (33.6 MB of K/V read and the kept rows written per set, ~800 MB in all) are cycled through
+    inside each graph replay, so every launch reads HBM rather than the 256 MB MALL."""
     from chunkkv_amd import ops
     from chunkkv_amd.planner import local_index, plan_request
 
@@ -666,12 +668,16 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         sels = [None] * DEV_SETS
         dns = [(torch.empty(N, device=dev), torch.empty(N, device=dev)) for _ in range(DEV_SETS)]
 
-        def dev_sel(i):  # one launch: ckv_deviation_select
+        def dev_sel(i):  # ckv_deviation_select: deviation + histogram, selection from the histogram
             st = sets[i]
             sels[i] = ops.deviation_select(st["k"], st["v"], st["K"], st["V"], flags, local, spans, None, st["ws"],
                                            out=sels[i], diff_norm=dns[i])[2]
 
-        def dev_then_sel(i):  # two launches, as HipEngine issues them by default
+        def dev_only(i):  # the deviation launch alone (ckv_deviation)
+            st = sets[i]
+            ops.deviation(st["k"], st["v"], st["K"], st["V"], flags, local)
+
+        def dev_then_sel(i):  # without the histogram: ckv_deviation + ckv_select
             st = sets[i]
             d_, n_ = ops.deviation(st["k"], st["v"], st["K"], st["V"], flags, local)
             sels[i] = ops.select(d_, n_, flags, local, spans, None, sels[i])
@@ -686,19 +692,21 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         # one graph = every input set once (DEV_SETS launches back to back: a replay's own launch
         # cost is spread over them; what remains per launch is the kernel's time and its gaps)
         g_dev = _graph_of(lambda: [dev_sel(i) for i in range(DEV_SETS)])
-        # counts[7] bit 0: the fused launch's histogram started the selection (bit 1 says whether
-        # its threshold bin was ranked directly, which depends on the ratio)
+        # counts[7] bit 0: the counted histogram started the selection (bit 1 says whether its
+        # threshold bin was ranked directly, which depends on the ratio)
         assert all(int(sl.counts[0].item()) == n and int(sl.counts[7].item()) & 1 == 1 for sl in sels)
+        g_only = _graph_of(lambda: [dev_only(i) for i in range(DEV_SETS)])
         g_two = _graph_of(lambda: [dev_then_sel(i) for i in range(DEV_SETS)])
         g_sc = _graph_of(lambda: [scat(i) for i in range(DEV_SETS)])
-        g_both = _graph_of(lambda: [(dev_then_sel(i), scat(i)) for i in range(DEV_SETS)])
+        g_both = _graph_of(lambda: [(dev_sel(i), scat(i)) for i in range(DEV_SETS)])
         t_dev = _timed(lambda i: g_dev.replay(), steps, stream) / DEV_SETS
+        t_only = _timed(lambda i: g_only.replay(), steps, stream) / DEV_SETS
         t_two = _timed(lambda i: g_two.replay(), steps, stream) / DEV_SETS
         t_sc = _timed(lambda i: g_sc.replay(), steps, stream) / DEV_SETS
         t_both = _timed(lambda i: g_both.replay(), steps, stream) / DEV_SETS
         assert all(int(sl.counts[0].item()) == n for sl in sels)
-        out[ratio] = dict(n_keep=n, dev_sel_two_launches_ms=t_two, dev_sel_one_launch_ms=t_dev, scatter_ms=t_sc,
-                          both_ms=t_both, scatter_bytes=n * ROW_BYTES * 4)
+        out[ratio] = dict(n_keep=n, dev_sel_ms=t_dev, deviation_ms=t_only, dev_sel_without_histogram_ms=t_two,
+                          scatter_ms=t_sc, both_ms=t_both, scatter_bytes=n * ROW_BYTES * 4)
     dev_bytes = N * 4 * ROW_BYTES + N * 8
     r30 = out[0.30]
     nb = dev_bytes + r30["scatter_bytes"]
@@ -706,11 +714,12 @@ def bench_deviation_topk(steps: int, warmup: int, dev) -> dict:
         "deviation + pooled top-k + scatter HBM GB/s, Qwen2.5-7B KV shape", nb / (r30["both_ms"] * 1e-3) / 1e9,
         r30["both_ms"], steps, warmup,
         {"workload": "layer-1 deviation + pooled top-k (30%) + 4 sinks x 32 chunks x 256 + scatter of the kept rows, "
-                     "4 KV heads, head_dim 128, bf16; 16 input sets rotated (cold HBM); deviation and selection as "
-                     "two launches (ckv_deviation + ckv_select, as HipEngine(layer1='four_launches') issues them); "
-                     "the one-launch ckv_deviation_select is in ratios", "bytes_per_step": nb},
-        _rooffor("deviation_kernel<bf16> + select_reg_kernel<8> (deviation + top-k)", dev_bytes,
-                 r30["dev_sel_two_launches_ms"]))
+                     "4 KV heads, head_dim 128, bf16; 16 input sets rotated (cold HBM); ckv_deviation_select (the "
+                     "deviation counting the candidate histogram, the selection starting from it: two launches) "
+                     "then ckv_scatter_kept_rows; the deviation alone and the two calls without the histogram are "
+                     "in ratios", "bytes_per_step": nb},
+        _rooffor("deviation_kernel<bf16> (the HBM-bound launch; the selection moves 74 KB)", dev_bytes,
+                 r30["deviation_ms"]))
     line["ratios"] = {str(r): {k2: (round(v2, 5) if isinstance(v2, float) else v2) for k2, v2 in o.items()}
                       for r, o in out.items()}
     return line

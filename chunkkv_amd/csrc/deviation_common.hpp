@@ -36,7 +36,12 @@ struct DevArgs {
 
 // Deviation and norm of positions p_base .. p_base + T - 1, computed by the calling wavefront.
 // Every lane returns the totals; positions outside the active set (local < 0) or past n_tokens
-// give 0. fl[t] returns the position's flag byte (0 past n_tokens).
+// give 0. fl[t] returns the position's flag byte (0 past n_tokens). Requires n_tokens >= 1.
+//
+// One memory round trip when the active set is every position (local[p] == p: the layer-1 case
+// without exact placements): the local indices, the flags, the cached rows at p and the fresh
+// rows at row p go out together (indices clamped into range, values dropped where they are
+// used), and a position whose local index turns out to be another row loads that row again.
 template <int DTYPE, int T>
 __device__ __forceinline__ void deviation_wave(const DevArgs& a, int p_base, float (&diff)[T], float (&norm)[T],
                                                uint32_t (&fl)[T]) {
@@ -46,62 +51,92 @@ __device__ __forceinline__ void deviation_wave(const DevArgs& a, int p_base, flo
   const int64_t row_b = (int64_t)a.head_dim * E::kBytes;
   const int vecs_per_row = a.head_dim / VEC;
   const int n_vecs = a.n_heads * vecs_per_row;
+  const int N = a.n_tokens;
 
-  int jj[T];
-  bool cached[T];
+  int jraw[T];
+  uint32_t fraw[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int pc = min(p_base + t, N - 1);
+    jraw[t] = a.local[pc];
+    fraw[t] = a.flags[pc];
+  }
   float sk[T], sv[T], nk[T], nv[T];
-  // every position's index and flags first (all in flight together), then the checks
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const int p = p_base + t;
-    jj[t] = p < a.n_tokens ? a.local[p] : -1;
-    fl[t] = p < a.n_tokens ? a.flags[p] : 0u;
-  }
-  bool bad = false;
+  for (int t = 0; t < T; ++t) sk[t] = sv[t] = nk[t] = nv[t] = 0.0f;
+  int jj[T];
+  bool cached[T], bad = false;
+  auto checks = [&]() {
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    cached[t] = (fl[t] & CKV_POS_CACHED) != 0;
-    bad = bad || jj[t] >= a.n_fresh;
-    jj[t] = jj[t] >= a.n_fresh ? -1 : jj[t];
-    sk[t] = sv[t] = nk[t] = nv[t] = 0.0f;
-  }
-  for (int q = lane; q < n_vecs; q += kWave) {
+    for (int t = 0; t < T; ++t) {
+      const bool valid = p_base + t < N;
+      fl[t] = valid ? fraw[t] : 0u;
+      cached[t] = (fl[t] & CKV_POS_CACHED) != 0;
+      bad = bad || (valid && jraw[t] >= a.n_fresh);
+      jj[t] = valid && jraw[t] >= 0 && jraw[t] < a.n_fresh ? jraw[t] : -1;
+    }
+  };
+  auto accumulate = [&](int t, const vec16& k16, const vec16& v16, const vec16& kc16, const vec16& vc16) {
+    float kx[VEC], vx[VEC], kcx[VEC], vcx[VEC];
+    E::unpack(k16, kx);
+    E::unpack(v16, vx);
+    E::unpack(kc16, kcx);
+    E::unpack(vc16, vcx);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float ck = cached[t] ? kcx[e] : 0.0f;  // rows outside every placement are zero
+      const float cv = cached[t] ? vcx[e] : 0.0f;
+      const float dk = E::round_trip(kx[e] - ck);
+      const float dv = E::round_trip(vx[e] - cv);
+      sk[t] = sk[t] + dk * dk;
+      sv[t] = sv[t] + dv * dv;
+      nk[t] = nk[t] + kx[e] * kx[e];
+      nv[t] = nv[t] + vx[e] * vx[e];
+    }
+  };
+
+  if (a.n_fresh <= 0) {  // uniform: no fresh rows, every position outside the active set
+    checks();
+  } else if (n_vecs <= kWave) {  // uniform: one 16-byte vector of each row per lane
+    const bool lane_on = lane < n_vecs;
+    const int q = min(lane, n_vecs - 1);
     const int h = q / vecs_per_row;
     const int64_t cb = (int64_t)(q % vecs_per_row) * 16;
     vec16 k16[T], v16[T], kc16[T], vc16[T];
+    int js[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      if (jj[t] >= 0) {
+      const int pc = min(p_base + t, N - 1);
+      js[t] = min(pc, a.n_fresh - 1);  // the fresh row when local[p] == p
+      const int64_t co = h * a.c_hs_b + (int64_t)pc * row_b + cb;
+      kc16[t] = ld16(a.kc + co);
+      vc16[t] = ld16(a.vc + co);
+      k16[t] = ld16(a.kf + h * a.kf_hs_b + js[t] * a.kf_ts_b + cb);
+      v16[t] = ld16(a.vf + h * a.vf_hs_b + js[t] * a.vf_ts_b + cb);
+    }
+    checks();
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (jj[t] >= 0 && jj[t] != js[t]) {  // uniform: another row after all
         k16[t] = ld16(a.kf + h * a.kf_hs_b + jj[t] * a.kf_ts_b + cb);
         v16[t] = ld16(a.vf + h * a.vf_hs_b + jj[t] * a.vf_ts_b + cb);
-        if (cached[t]) {
-          const int64_t co = h * a.c_hs_b + (int64_t)(p_base + t) * row_b + cb;
-          kc16[t] = ld16(a.kc + co);
-          vc16[t] = ld16(a.vc + co);
-        }
       }
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      if (jj[t] < 0) continue;
-      float kx[VEC], vx[VEC], kcx[VEC], vcx[VEC];
-      E::unpack(k16[t], kx);
-      E::unpack(v16[t], vx);
-      if (cached[t]) {
-        E::unpack(kc16[t], kcx);
-        E::unpack(vc16[t], vcx);
-      } else {
+      if (lane_on && jj[t] >= 0) accumulate(t, k16[t], v16[t], kc16[t], vc16[t]);
+    }
+  } else {  // several vectors of each row per lane: q = lane, lane + 64, ... ascending
+    checks();
+    for (int q = lane; q < n_vecs; q += kWave) {
+      const int h = q / vecs_per_row;
+      const int64_t cb = (int64_t)(q % vecs_per_row) * 16;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) kcx[e] = vcx[e] = 0.0f;
-      }
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float dk = E::round_trip(kx[e] - kcx[e]);
-        const float dv = E::round_trip(vx[e] - vcx[e]);
-        sk[t] = sk[t] + dk * dk;
-        sv[t] = sv[t] + dv * dv;
-        nk[t] = nk[t] + kx[e] * kx[e];
-        nv[t] = nv[t] + vx[e] * vx[e];
+      for (int t = 0; t < T; ++t) {
+        if (jj[t] < 0) continue;  // uniform
+        const int64_t co = h * a.c_hs_b + (int64_t)(p_base + t) * row_b + cb;
+        accumulate(t, ld16(a.kf + h * a.kf_hs_b + jj[t] * a.kf_ts_b + cb),
+                   ld16(a.vf + h * a.vf_hs_b + jj[t] * a.vf_ts_b + cb), ld16(a.kc + co), ld16(a.vc + co));
       }
     }
   }

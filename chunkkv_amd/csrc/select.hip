@@ -23,7 +23,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(SelectArgs a, u
   }
   ckv_chunk_span sp[kSelPre<KPT>];
   load_first_spans<KPT>(a.chunks, a.n_chunks, __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), sp);
-  select_run<KPT, false, SUMS>(a, ghist, masks, sp);
+  select_run<KPT, SUMS>(a, ghist, masks, sp);
 }
 
 // Selection for any n_tokens <= CKV_SELECT_MAX_TOKENS: keys are re-read from global memory

@@ -239,22 +239,9 @@ __device__ __forceinline__ void load_first_spans(const ckv_chunk_span* chunks, i
   }
 }
 
-// Loads of diff/norm/histogram words another workgroup of the same launch wrote: device-scope
-// (global_load sc1, coherent across the XCDs' L2s) when COH, plain otherwise.
-template <bool COH>
-__device__ __forceinline__ float ld_val(const float* p) {
-  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return *p;
-}
-template <bool COH>
-__device__ __forceinline__ uint32_t ld_val(const uint32_t* p) {
-  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return *p;
-}
-
 // SUMS = false (only without a threshold): the per-chunk sums and rel_dev/escalated are left to
 // other workgroups (chunk_sums_wave); the budget and the pool come from the spans alone.
-template <int KPT, bool COH = false, bool SUMS = true>
+template <int KPT, bool SUMS = true>
 __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist, uint32_t* masks,
                                            const ckv_chunk_span (&sp0)[kSelPre<KPT>]) {
   static_assert(KPT <= 33, "a run of KPT positions spans at most two mask words and one 64-bit word");
@@ -310,24 +297,12 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   vec16 g4 = {0u, 0u, 0u, 0u};
   uint32_t* gmine = ghist != nullptr ? ghist + (kTopBins - 4 * (tid + 1)) : nullptr;
   auto load_hist = [&]() {
-    if (gmine != nullptr) {
-      if constexpr (COH) {
-        g4 = vec16{ld_val<true>(gmine), ld_val<true>(gmine + 1), ld_val<true>(gmine + 2), ld_val<true>(gmine + 3)};
-      } else {
-        g4 = ld16(gmine);
-      }
-    }
+    if (gmine != nullptr) g4 = ld16(gmine);
   };
   if (vec_ok && wave_end <= n_tokens) {  // uniform: the whole wavefront's runs are in range
 #pragma unroll
     for (int i0 = 0; i0 < KPT; i0 += 4) {
-      float4 d;
-      if constexpr (COH) {
-        d = make_float4(ld_val<true>(diff + p0 + i0), ld_val<true>(diff + p0 + i0 + 1), ld_val<true>(diff + p0 + i0 + 2),
-                        ld_val<true>(diff + p0 + i0 + 3));
-      } else {
-        d = *(const float4*)(diff + p0 + i0);
-      }
+      const float4 d = *(const float4*)(diff + p0 + i0);
       dv[i0] = d.x;
       dv[i0 + 1] = d.y;
       dv[i0 + 2] = d.z;
@@ -351,7 +326,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int p = p0 + i;
-      const float d = ld_val<COH>(diff + min(p, n_tokens - 1));
+      const float d = diff[min(p, n_tokens - 1)];
       dv[i] = p < n_tokens ? d : __uint_as_float(0x7fc00000u);  // NaN: key 0
     }
     load_hist();
@@ -385,8 +360,8 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     for (int j = 0; j < kBatch; ++j) {
       const int q = j * kWave + lane;
       const bool in = c < n_chunks && ok0 && q < sp0[r].length;
-      bd0[r][j] = in ? ld_val<COH>(diff + sp0[r].start + q) : 0.0f;
-      bn0[r][j] = in ? ld_val<COH>(norm + sp0[r].start + q) : 0.0f;
+      bd0[r][j] = in ? diff[sp0[r].start + q] : 0.0f;
+      bn0[r][j] = in ? norm[sp0[r].start + q] : 0.0f;
     }
   }
   if (tid == 0) {
@@ -425,8 +400,8 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
             bd[j] = r == 0 ? bd0[0][j] : bd0[kPre - 1][j];
             bn[j] = r == 0 ? bn0[0][j] : bn0[kPre - 1][j];
           } else {
-            bd[j] = q < sp.length ? ld_val<COH>(diff + sp.start + q) : 0.0f;
-            bn[j] = q < sp.length ? ld_val<COH>(norm + sp.start + q) : 0.0f;
+            bd[j] = q < sp.length ? diff[sp.start + q] : 0.0f;
+            bn[j] = q < sp.length ? norm[sp.start + q] : 0.0f;
           }
         }
 #pragma unroll

@@ -258,10 +258,12 @@ def deviation_select(
     out: Selection | None = None,
     diff_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, Selection]:
-    """deviation() then select() in one launch (torch_engine.py:117-153): returns (diff, norm,
-    selection), bit-identical to the two calls. flags must carry the planner's pooled bit for
-    the fast path (without it the result is the same, the selection slower). workspace: from
-    deviation_select_workspace(), not shared by calls that may run concurrently."""
+    """deviation() then select() with the top-k's first digit fused into the deviation
+    (torch_engine.py:117-153): the deviation launch also counts the candidates' histogram, and the
+    selection starts from it. Returns (diff, norm, selection), bit-identical to the two calls.
+    flags must carry the planner's pooled bit for the fast path (without it the result is the
+    same, the selection slower). workspace: from deviation_select_workspace(), not shared by
+    calls that may run concurrently."""
     _dev(k, v, K, V, flags, local, spans, workspace)
     k, v = _rows_view(k), _rows_view(v)
     if K.dtype != k.dtype or V.dtype != k.dtype or v.dtype != k.dtype:
@@ -330,12 +332,12 @@ def layer1_repair(
     out: Selection | None = None,
     diff_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, Selection]:
-    """Layer 1's KV repair in one launch (torch_engine.py:96-103 for this layer, :117-156): the
-    cache K/V (1, H, N, D) gets every cached row re-rotated from the chunks (src_tab column
-    `layer`, the cached-run segments) and the fresh rows of the kept positions; returns (diff,
-    norm, selection), bit-identical to rerope_gather (this layer) + deviation + select +
-    scatter_kept_rows. k/v: the fresh rows (1, H, n, D), any row-contiguous strides. workspace:
-    from layer1_repair_workspace(), not shared by calls that may run concurrently."""
+    """Layer 1's KV repair in one call of three launches (torch_engine.py:96-103 for this layer,
+    :117-156): the cache K/V (1, H, N, D) gets every cached row re-rotated from the chunks (src_tab
+    column `layer`, the cached-run segments) and the fresh rows of the kept positions; returns
+    (diff, norm, selection), bit-identical to rerope_gather (this layer) + deviation + select +
+    scatter_kept_rows. k/v: the fresh rows (1, H, n, D), any row-contiguous strides. workspace: from
+    layer1_repair_workspace(), not shared by calls that may run concurrently."""
     _dev(K, V, src_tab, segments, k, v, flags, local, spans, workspace)
     k, v = _rows_view(k), _rows_view(v)
     if K.dtype != k.dtype or V.dtype != k.dtype or v.dtype != k.dtype:

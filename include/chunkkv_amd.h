@@ -104,7 +104,8 @@ typedef struct ckv_chunk_span {
                                        were ranked directly instead of by radix passes      */
 #define CKV_COUNT_N 8
 
-/* Bytes of the workspace ckv_deviation_select takes (a 4096-bin histogram and a ticket). */
+/* Bytes of the workspace ckv_deviation_select takes (the 16 KB candidate histogram; the 256
+   bytes after it are not used). */
 #define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 16640
 
 /* Bytes of the workspace ckv_layer1_repair takes (the selection's candidate histogram). */
@@ -227,21 +228,22 @@ int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flag
                    uint8_t* escalated, int32_t* counts, void* stream);
 
 /*
- * ckv_deviation followed by ckv_select, in one launch: the layer-1 repair decision
- * (torch_engine.py:117-153) from the fresh and cached rows to the new active set, with outputs
- * and results bit-identical to the two calls (same arguments, same meaning; see both above).
- * The workgroups that compute the deviations also count every position flagged
- * CKV_POS_CACHED | CKV_POS_POOLED and not CKV_POS_SINK into a histogram of its deviation (4096
- * bins of 1/64 octave); the last workgroup to finish runs the selection from it. When the pooled
- * flags disagree with the pooled spans, a chunk escalates, or the threshold lies outside
- * 2^-24 .. 2^40, the selection ignores the histogram (same result, slower);
- * counts[CKV_COUNT_TOP_HISTOGRAM] says which path ran.
+ * ckv_deviation followed by ckv_select with the top-k's first digit fused into the deviation:
+ * the layer-1 repair decision (torch_engine.py:117-153) from the fresh and cached rows to the new
+ * active set, with outputs and results bit-identical to the two calls (same arguments, same
+ * meaning; see both above). Two launches: the deviation kernel also counts every position
+ * flagged CKV_POS_CACHED | CKV_POS_POOLED and not CKV_POS_SINK into a histogram of its deviation
+ * (4096 bins of 1/64 octave) in the workspace; the selection starts from that histogram and
+ * ranks only the candidates of the threshold's bin. When the pooled flags disagree with the
+ * pooled spans, a chunk escalates, or the threshold lies outside 2^-24 .. 2^40, the selection
+ * ignores the histogram (same result, slower); counts[CKV_COUNT_TOP_HISTOGRAM] says which path
+ * ran.
  *   workspace        device memory of >= CKV_DEVIATION_SELECT_WORKSPACE_BYTES, 16-byte aligned,
  *                    ZERO before its first use; every call leaves it zero again. Calls that
  *                    share a workspace must be ordered (one stream, or events): concurrent
  *                    calls on one workspace race.
- * n_tokens <= CKV_SELECT_MAX_TOKENS; above 33792 the call runs the two launches instead (the
- * workspace is then not touched).
+ * n_tokens <= CKV_SELECT_MAX_TOKENS; above 33792 the deviation counts no histogram and the
+ * selection runs its L2 form (the workspace is then not touched).
  * Replaces: torch_engine.py:117-153 (the deviation :117-124, rel/escalation/budget :128-142,
  *           argsort top-k :143-146, keep.nonzero and local compaction :146-153).
  */

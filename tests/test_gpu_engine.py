@@ -137,9 +137,9 @@ def test_side_stream_and_one_stream_builds_identical(models, parts, ratio):
 @pytest.mark.parametrize("thr", [None, 0.05])
 def test_layer1_paths_build_identical(models, parts, thr, mode):
     """Layer 1's repair as one call (ckv_layer1_repair, the default), as the base-cache gather plus
-    the deviation, the selection and the kept-row scatter, or with the deviation and selection in
-    one launch: the same caches, logits and stats, bit for bit, with and without an escalation
-    threshold."""
+    the deviation, the selection and the kept-row scatter, or with the deviation and selection as
+    ckv_deviation_select: the same caches, logits and stats, bit for bit, with and without an
+    escalation threshold."""
     _, gpu = models
     a = HipEngine(gpu, StubTokenizer(), layer1=mode)
     b = HipEngine(gpu, StubTokenizer())
