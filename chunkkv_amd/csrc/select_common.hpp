@@ -229,13 +229,21 @@ __device__ __forceinline__ ckv_chunk_span span_at(const ckv_chunk_span* chunks, 
   return ckv_chunk_span{f[0], f[1], f[2], f[3]};
 }
 
+// The first spans go out as vector loads, before the selection's other loads: waiting for
+// them then waits for nothing issued later (vector loads complete in issue order), while a
+// scalar load would hold up the selection's first LDS barrier (which waits for every scalar
+// load) until the spans arrive.
 template <int KPT>
 __device__ __forceinline__ void load_first_spans(const ckv_chunk_span* chunks, int n_chunks, int wave,
                                                  ckv_chunk_span (&sp)[kSelPre<KPT>]) {
 #pragma unroll
   for (int r = 0; r < kSelPre<KPT>; ++r) {
-    const int c = wave + r * kSelWaves;
-    sp[r] = c < n_chunks ? span_at(chunks, c) : ckv_chunk_span{0, 0, 0, 0};
+    const int c = wave + r * kSelWaves;  // uniform
+    sp[r] = ckv_chunk_span{0, 0, 0, 0};
+    if (c < n_chunks) {
+      const vec16 v = ld16(chunks + c);
+      sp[r] = ckv_chunk_span{(int32_t)v.x, (int32_t)v.y, (int32_t)v.z, (int32_t)v.w};
+    }
   }
 }
 
@@ -321,27 +329,16 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     }
   } else if (__builtin_amdgcn_readfirstlane(wave * kWave * KPT) < n_tokens) {  // uniform
     // The wavefront whose runs cross n_tokens: every load unconditional, its index clamped into
-    // range and the value dropped where it is used, so all of them are in flight together
-    // (loads behind per-position branches went out one round trip at a time).
+    // range (loads behind per-position branches went out one round trip at a time). The values
+    // of positions past the end are never used: every use below is masked by the candidate or
+    // kept bits, which only positions below n_tokens get.
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int p = p0 + i;
-      const float d = diff[min(p, n_tokens - 1)];
-      dv[i] = p < n_tokens ? d : __uint_as_float(0x7fc00000u);  // NaN: key 0
-    }
+    for (int i = 0; i < KPT; ++i) dv[i] = diff[min(p0 + i, n_tokens - 1)];
     load_hist();
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int p = p0 + i;
-      const uint32_t b = flags[min(p, n_tokens - 1)];
-      fl[i / 4] |= (p < n_tokens ? b : 0u) << (8 * (i % 4));
-    }
+    for (int i = 0; i < KPT; ++i) fl[i / 4] |= (uint32_t)flags[min(p0 + i, n_tokens - 1)] << (8 * (i % 4));
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int p = p0 + i;
-      const int lr = local[min(p, n_tokens - 1)];
-      lv[i] = p < n_tokens ? lr : 0;
-    }
+    for (int i = 0; i < KPT; ++i) lv[i] = local[min(p0 + i, n_tokens - 1)];
   } else {  // a wavefront past the last position: nothing to load
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
