@@ -21,9 +21,23 @@ static_assert(kDevPerGroup <= kWave, "one lane of wavefront 0 per position of th
 
 // HIST: positions flagged cached, pooled and not sink (the candidates when no chunk escalates)
 // are counted by top_bin into hist, one atomic per distinct bin of the workgroup.
+// The pointers and sizes the first loads use lead the argument list: the library preloads the
+// first 16 argument dwords into SGPRs, but only up to the first argument passed by reference
+// (the DevArgs struct), and every other argument takes a scalar load at wave start.
 template <int DTYPE, bool HIST>
-__global__ __launch_bounds__(kDevThreads) void deviation_kernel(DevArgs a, float* __restrict__ diff,
-                                                                float* __restrict__ norm, uint32_t* __restrict__ hist) {
+__global__ __launch_bounds__(kDevThreads) void deviation_kernel(const int32_t* local, const uint8_t* flags,
+                                                                const char* kc, const char* vc, const char* kf,
+                                                                const char* vf, int n_tokens, int n_fresh, DevArgs a,
+                                                                float* __restrict__ diff, float* __restrict__ norm,
+                                                                uint32_t* __restrict__ hist) {
+  a.local = local;
+  a.flags = flags;
+  a.kc = kc;
+  a.vc = vc;
+  a.kf = kf;
+  a.vf = vf;
+  a.n_tokens = n_tokens;
+  a.n_fresh = n_fresh;
   __shared__ uint32_t s_bin[kDevPerGroup];
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
   const int lane = (int)threadIdx.x % kWave;
@@ -64,7 +78,8 @@ __global__ __launch_bounds__(kDevThreads) void deviation_kernel(DevArgs a, float
 template <int DTYPE, bool HIST>
 static void launch_deviation(const DevArgs& args, float* diff, float* norm, uint32_t* hist, hipStream_t st) {
   const unsigned blocks = (unsigned)((args.n_tokens + kDevPerGroup - 1) / kDevPerGroup);
-  hipLaunchKernelGGL((deviation_kernel<DTYPE, HIST>), dim3(blocks), dim3(kDevThreads), 0, st, args, diff, norm, hist);
+  hipLaunchKernelGGL((deviation_kernel<DTYPE, HIST>), dim3(blocks), dim3(kDevThreads), 0, st, args.local, args.flags,
+                     args.kc, args.vc, args.kf, args.vf, args.n_tokens, args.n_fresh, args, diff, norm, hist);
 }
 
 static int32_t check_deviation_args(const void* k_fresh, const void* v_fresh, const void* k_cache, const void* v_cache,

@@ -286,8 +286,21 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
 // go into the cache (sinks excepted: always kept, the scatter writes them), deviations out, and
 // the positions flagged cached, pooled and not sink (the candidates when no chunk escalates)
 // counted by their key's top_bin, one atomic per distinct bin of the workgroup.
+// The pointers and sizes the first loads use lead the argument list: the library preloads the
+// first 16 argument dwords into SGPRs, but only up to the first argument passed by reference
+// (the L1Args struct), and every other argument takes a scalar load at wave start.
 template <int DTYPE, int T>
-__global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(L1Args a, const InvFreq inv) {
+__global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
+    const uint8_t* flags, const int32_t* local, const ckv_segment* segs, const uint64_t* tab, int n_tokens, int n_segs,
+    const char* kf, const char* vf, L1Args a, const InvFreq inv) {
+  a.flags = flags;
+  a.local = local;
+  a.segs = segs;
+  a.tab = tab;
+  a.n_tokens = n_tokens;
+  a.n_segs = n_segs;
+  a.kf = kf;
+  a.vf = vf;
   constexpr int P = kL1Waves * T;
   __shared__ uint32_t s_bin[P];
   const int tid = (int)threadIdx.x, lane = tid & (kWave - 1);
@@ -420,10 +433,12 @@ extern "C" int32_t ckv_layer1_repair(
   const unsigned blocks = (unsigned)((n_tokens + P - 1) / P);
   if (dtype == CKV_DTYPE_BF16)
     hipLaunchKernelGGL((layer1_gather_deviation_kernel<CKV_DTYPE_BF16, kL1T>), dim3(blocks), dim3(kL1Threads), 0, st,
-                       args, inv);
+                       args.flags, args.local, args.segs, args.tab, args.n_tokens, args.n_segs, args.kf, args.vf, args,
+                       inv);
   else
     hipLaunchKernelGGL((layer1_gather_deviation_kernel<CKV_DTYPE_F32, kL1T>), dim3(blocks), dim3(kL1Threads), 0, st,
-                       args, inv);
+                       args.flags, args.local, args.segs, args.tab, args.n_tokens, args.n_segs, args.kf, args.vf, args,
+                       inv);
   CKV_RETURN_IF_LAUNCH_FAILED();
   int32_t rc = select_launch(sel, hist, st);
   if (rc != CKV_OK) return rc;

@@ -12,9 +12,21 @@ namespace ckv {
 // top_bin candidate histogram counted by an earlier launch, left zeroed. Without a threshold
 // (SUMS = false) workgroup 0 selects and the others compute the chunks' rel_dev, one wavefront
 // per chunk, beside it.
+// The pointers and sizes the first loads use lead the argument list: the library preloads the
+// first 16 argument dwords into SGPRs, but only up to the first argument passed by reference
+// (the SelectArgs struct), and every other argument takes a scalar load at wave start.
 template <int KPT, bool SUMS>
-__global__ __launch_bounds__(kSelThreads) void select_reg_kernel(SelectArgs a, uint32_t* ghist) {
+__global__ __launch_bounds__(kSelThreads) void select_reg_kernel(const float* diff, const uint8_t* flags,
+                                                                 const int32_t* local, uint32_t* ghist,
+                                                                 const ckv_chunk_span* chunks, int n_tokens,
+                                                                 int n_chunks, SelectArgs a) {
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
+  a.diff = diff;
+  a.flags = flags;
+  a.local = local;
+  a.chunks = chunks;
+  a.n_tokens = n_tokens;
+  a.n_chunks = n_chunks;
   if (!SUMS && blockIdx.x > 0) {
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
     for (int c = ((int)blockIdx.x - 1) * kSelWaves + wave; c < a.n_chunks; c += ((int)gridDim.x - 1) * kSelWaves)
@@ -231,10 +243,12 @@ int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st) {
 #define CKV_SEL_REG(K)                                                                                    \
   if (kpt <= K) {                                                                                         \
     if (args.has_thr)                                                                                     \
-      hipLaunchKernelGGL((select_reg_kernel<K, true>), dim3(1), dim3(kSelThreads), lds, st, args, ghist); \
+      hipLaunchKernelGGL((select_reg_kernel<K, true>), dim3(1), dim3(kSelThreads), lds, st, args.diff, args.flags, \
+                         args.local, ghist, args.chunks, args.n_tokens, args.n_chunks, args);                   \
     else                                                                                                  \
       hipLaunchKernelGGL((select_reg_kernel<K, false>), dim3(1 + sum_groups), dim3(kSelThreads), lds, st,  \
-                         args, ghist);                                                                    \
+                         args.diff, args.flags, args.local, ghist, args.chunks, args.n_tokens, args.n_chunks, \
+                         args);                                                                           \
     CKV_RETURN_IF_LAUNCH_FAILED();                                                                        \
     return CKV_OK;                                                                                        \
   }

@@ -182,15 +182,17 @@ KV_SHAPES = {
 }
 
 
+@pytest.mark.parametrize("n", [157, 6145])
 @pytest.mark.parametrize("row_mode", ["token", "positions", "indexed"])
 @pytest.mark.parametrize("shape", list(KV_SHAPES))
-def test_rope_kv_every_row_mode_and_shape(shape, row_mode):
+def test_rope_kv_every_row_mode_and_shape(shape, row_mode, n):
     """The k/v-only launch (no q: every layer's cache write) in each shape and row mode: rows
     NULL (row = token index), rows = the positions tensor itself, rows indexed separately from
-    the positions. k rotated bit-exactly, v copied, every other cache row untouched."""
+    the positions. k rotated bit-exactly, v copied, every other cache row untouched; 6145 tokens
+    are more wavefronts than the chip holds at once (layer 0 of an 8k request is 8256)."""
     bf16, D, Hkv = KV_SHAPES[shape]
-    rng = np.random.default_rng(sum(map(ord, shape + row_mode)))
-    n, N = 157, 700
+    rng = np.random.default_rng(sum(map(ord, shape + row_mode)) + n)
+    N = 700 if n < 700 else 2 * n
     lin = _proj(rng, n, 0, Hkv, D, bf16)
     if row_mode == "positions":
         pos = np.sort(rng.choice(N, n, replace=False))
