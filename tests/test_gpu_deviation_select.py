@@ -1,5 +1,5 @@
-"""ckv_deviation_select (the layer-1 deviation fused with the pooled top-k, sinks and compaction,
-torch_engine.py:117-153) and ckv_scatter_kept_rows (the k/v compaction folded into the scatter,
+"""ckv_deviation_select (the layer-1 deviation, then the pooled top-k, sinks and compaction from
+the candidate histogram the deviation counts, torch_engine.py:117-153) and ckv_scatter_kept_rows (the k/v compaction folded into the scatter,
 :152 and :155-156) against the oracle, bit for bit: diff/norm, keep_abs, keep_local, keep_rank,
 rel_dev, escalated and the counts. Cases: the config-3 and config-4 shapes, every register
 bucket of the selecting workgroup up to 33792 positions and the two-launch form above it,
