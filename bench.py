@@ -8,7 +8,7 @@ shuffled positions (each chunk computed at its own original offset, so every pla
 its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
 
 A step is one request's whole KV repair with every input already resident in HBM, issued as
-HipEngine issues it (29 launches in order on one stream): layer 0's fresh rows written into its
+HipEngine issues it (31 launches in order on one stream): layer 0's fresh rows written into its
 cache; layer 1's repair as one ckv_layer1_repair call (three launches: the cached rows
 re-rotated into the cache with the deviation, the selection of 2304 pooled + 96 sinks + 576
 uncached = 2976 kept rows, the scatter of the kept rows); then the gather of the cached rows of
@@ -222,11 +222,12 @@ class RepairWorkload:
         ops.rope_qkv(None, k_in, v_in, pos, 0, N_KV, HEAD_DIM, THETA, k_out=self.k_slab[li], v_out=self.v_slab[li],
                      rows=pos, err=self.err)
 
-    layer1_mode = "one"  # as HipEngine: layer 1's whole repair in one launch (ckv_layer1_repair)
+    layer1_mode = "one"  # as HipEngine: layer 1's whole repair in one call (ckv_layer1_repair)
 
     def step(self, two_streams: bool = False):
-        """One request's KV repair as HipEngine issues it (29 launches, in order on one stream):
-        layer 0's fresh rows; layer 1's base cache, deviation, selection and kept rows in one launch;
+        """One request's KV repair as HipEngine issues it (31 launches, in order on one stream):
+        layer 0's fresh rows; layer 1's base cache, deviation, selection and kept rows in one call of
+        three launches;
         the gather of the dropped rows of layers 2-27; those layers' fresh rows. With layer1_mode
         "split", layer 1 is the four launches that launch replaces (base cache, deviation, selection,
         kept-row scatter). two_streams=True issues the gathers on a second stream instead, as
@@ -260,8 +261,9 @@ class RepairWorkload:
             main.wait_stream(self.side)
 
     def layer1_one(self):
-        """Layer 1's whole repair in one launch: the cached rows re-rotated from the chunk store,
-        the deviation, the selection, the kept rows from the fresh rows (ckv_layer1_repair)."""
+        """Layer 1's whole repair in one call of three launches: the cached rows re-rotated from the
+        chunk store with the deviation, the selection, the kept rows from the fresh rows
+        (ckv_layer1_repair)."""
         from chunkkv_amd import ops
 
         k1, v1 = self.fresh[1]
@@ -355,7 +357,7 @@ def _graph_of(fn):
 
 
 def bench_repair(steps: int, warmup: int, dev) -> dict:
-    """Time the KV-repair step as HipEngine issues it (29 launches on one stream, captured once
+    """Time the KV-repair step as HipEngine issues it (31 launches on one stream, captured once
     per input set in a HIP graph and replayed; the eager time, launch-bound from Python, layer 1
     as four launches, the two-stream issue and the assemble-per-layer variant are reported too),
     and the dominant kernel (the gather of the dropped rows of layers 2..27) from a burst of
