@@ -442,8 +442,10 @@ extern "C" int32_t ckv_layer1_repair(
   CKV_RETURN_IF_LAUNCH_FAILED();
   int32_t rc = select_launch(sel, hist, st);
   if (rc != CKV_OK) return rc;
-  // the kept rows from the fresh rows: K[keep_abs[j]] = k[keep_local[j]], j < counts[KEEP]
-  return scatter_launch(dst_k, dst_v, dst_head_stride, k_fresh, kf_head_stride, kf_token_stride, v_fresh,
-                        vf_head_stride, vf_token_stride, keep_abs, keep_local, n_tokens, n_fresh, n_tokens, n_heads,
-                        head_dim, dtype, counts + CKV_COUNT_KEEP, err, stream);
+  // the kept rows from the fresh rows: K[keep_abs[j]] = k[keep_local[j]], j < counts[KEEP]. With
+  // no fresh rows no source row is in range (a kept row then flags the range error) and nothing
+  // is read: the workspace stands in for k/v.
+  return scatter_launch(dst_k, dst_v, dst_head_stride, fresh ? k_fresh : workspace, kf_head_stride, kf_token_stride,
+                        fresh ? v_fresh : workspace, vf_head_stride, vf_token_stride, keep_abs, keep_local, n_tokens,
+                        n_fresh, n_tokens, n_heads, head_dim, dtype, counts + CKV_COUNT_KEEP, err, stream);
 }

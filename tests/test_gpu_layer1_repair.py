@@ -6,7 +6,8 @@ escalated and the counts.
 
 Cases: the 8k request's shape (24 chunks x 320 at shuffled positions + 576 uncached, 30 %), the
 config-3 shape at 15/30/50 %, the replay's 32,832-token request,
-small requests with exact and overlapping placements at head_dim 64 in bf16 and fp32, an
+small requests with exact and overlapping placements at head_dim 64 in bf16 and fp32, requests
+with no placement, with every position exact (no fresh row), of one token and a ragged one, an
 escalation threshold, a threshold bin ranked directly and one refined by radix passes, deviations
 that tie (one histogram bin holding every candidate: more radix rounds, then equal keys ranked by
 position), NaN deviations, one workspace across calls of
@@ -209,6 +210,24 @@ def test_small_exact_and_overlapping_head_dim_64(dtype):
                   ratios=[0.3, 0.5, None, 0.0, 0.25])
     assert req.plan.has_overlap and req.plan.exact.any()
     check(req)
+
+
+@pytest.mark.parametrize("case", ["no_placements", "every_position_exact", "one_token", "ragged"])
+def test_edge_requests(case):
+    """No placement (no segment, no span: every position uncached and kept); one exact placement
+    covering the request (no fresh row, nothing kept: the scatter reads nothing); a one-token
+    request (its only position a sink); a 33-token chunk at offset 3 of 40 positions."""
+    lens, starts, N, exact, keep = {
+        "no_placements": ([], [], 7, (), 7),
+        "every_position_exact": ([50], [(0, 0)], 50, (0,), 0),
+        "one_token": ([1], [(0, 0)], 1, (), 1),
+        "ragged": ([33], [(0, 3)], 40, (), None),
+    }[case]
+    req = Request(40 + N, lens, starts, N, exact=exact)
+    counts = check(req)
+    assert counts[0] == req.plan.n_keep
+    if keep is not None:
+        assert counts[0] == keep
 
 
 def test_escalation_threshold():
