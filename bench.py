@@ -343,6 +343,21 @@ def _timed(fn, n: int, stream) -> float:
     return start.elapsed_time(end) / n
 
 
+_REQUEST_STREAMS: list = []
+
+
+def request_streams(n: int, dev) -> list:
+    """n streams for concurrent requests, created once per process, ahead of every other stream,
+    and shared by the concurrent measurements (as a server creates its request streams at start-up).
+    HIP maps each stream onto one of its hardware queues (GPU_MAX_HW_QUEUES, 4 here) when the
+    stream is created, and the mapping depends on the streams created before it: with request
+    streams created after other measurements' streams, config 5's rounds took 3.20 ms against
+    2.95 ms for the same work."""
+    while len(_REQUEST_STREAMS) < n:
+        _REQUEST_STREAMS.append(torch.cuda.Stream(device=dev))  # default priority
+    return _REQUEST_STREAMS[:n]
+
+
 def _graph_of(fn):
     """Capture fn() (already run once eagerly) into a HIP graph, warming it on a side stream."""
     side = torch.cuda.Stream()
@@ -409,7 +424,7 @@ def _concurrent_steps(wls, steps: int, dev) -> float:
     HIP graph. The single request's step is a chain of dependent launches, most of them too small
     to fill the GPU; independent requests overlap each other's latency."""
     reqs = list(wls) + [RepairWorkload(1234 + len(wls) + i, dev) for i in range(CONCURRENT - len(wls))]
-    streams = [torch.cuda.Stream(device=dev) for _ in reqs]  # default priority
+    streams = request_streams(len(reqs), dev)
 
     def round_():
         main = torch.cuda.current_stream(dev)
@@ -731,9 +746,10 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
     """Long-context multi-request replay at the Qwen2.5-7B shape: an HBM-resident store of 256
     chunks x 256 tokens x 2 context variants (7.0 GiB); 4 concurrent requests of 128 chunks
     sampled with replacement (Zipf s=1.1) at random order + a 64-token query (32832 tokens), 15%
-    recompute + 4 sinks. Each request's KV repair is the engine's launch sequence (layer 1's base
-    cache, layer 0's fresh rows, deviation, selection, scatter of the kept rows, the gather of the
-    dropped rows of layers 2-27, the fresh rows of layers 2-27) on its own HIP stream. Then TTFT
+    recompute + 4 sinks. Each request's KV repair is the engine's launch sequence (layer 0's fresh
+    rows; layer 1's repair as one ckv_layer1_repair call: base cache with the deviation, selection,
+    kept rows; the gather of the dropped rows of layers 2-27; the fresh rows of layers 2-27) on its
+    own HIP stream, with a layer-1 workspace per request. Then TTFT
     p50/p99 of HipEngine.prefill + last_logprobs on requests of the same shape (random-init
     Qwen2.5-7B architecture, bf16; the store's K/V serve as the cached chunks), one at a time."""
     from chunkkv_amd import ops
@@ -770,22 +786,23 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
                          spans=torch.from_numpy(plan.spans.reshape(-1)).to(dev),
                          layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), proj=proj,
                          fresh1=(torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16(),
-                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None))
+                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None,
+                         ws=ops.layer1_repair_workspace(dev),
+                         dn=(torch.empty(N, dtype=torch.float32, device=dev),
+                             torch.empty(N, dtype=torch.float32, device=dev))))
     assert reqs[0]["plan"].budget == 4864
-    streams = [torch.cuda.Stream() for _ in range(n_streams)]
+    streams = request_streams(n_streams, dev)
 
     def repair(rq):
         plan = rq["plan"]
         K, V = rq["K"].unbind(0), rq["V"].unbind(0)
         nseg, mseg = len(plan.segments), plan.max_seg_tokens
-        ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(1, 2))
         ops.rope_qkv(None, *rq["proj"][0], rq["layer0"], 0, N_KV, HEAD_DIM, THETA, k_out=K[0], v_out=V[0],
                      rows=rq["layer0"])
         k1, v1 = rq["fresh1"]
-        d, n = ops.deviation(k1, v1, K[1], V[1], rq["flags"], rq["local"])
-        rq["sel"] = ops.select(d, n, rq["flags"], rq["local"], rq["spans"], None, rq["sel"])
+        _, _, rq["sel"] = ops.layer1_repair(K[1], V[1], rq["tab"], N_LAYERS, 1, rq["segs"], nseg, k1, v1, rq["flags"],
+                                            rq["local"], rq["spans"], None, THETA, rq["ws"], None, rq["sel"], rq["dn"])
         rows = rq["sel"].keep_abs[: plan.n_keep]
-        ops.scatter_kept_rows(K[1], V[1], k1, v1, rows, rq["sel"].keep_local[: plan.n_keep])
         ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(2, N_LAYERS),
                           skip=rq["sel"].keep_rank)
         for li in range(2, N_LAYERS):
@@ -1144,6 +1161,7 @@ def main() -> None:
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    request_streams(CONCURRENT, dev)  # the first streams of the process
     if args.workload != "request":
         fn = {"gather": bench_gather_only, "deviation": bench_deviation_topk, "replay": bench_replay,
               "traffic": traffic_probe, "dropped": bench_dropped, "attention": bench_attention,
@@ -1163,12 +1181,12 @@ def main() -> None:
         log(f"[bench] config 2 {configs['config2_rerope_gather']}")
         configs["config3_deviation_topk_scatter"] = _config_summary(bench_deviation_topk(sub_steps, args.warmup, dev))
         log(f"[bench] config 3 {configs['config3_deviation_topk_scatter']}")
+        # before the 8k TTFT runs, like the sub-measurements above; it builds its own model
+        configs["config5_replay"] = _config_summary(
+            bench_replay(min(args.steps, 20), args.warmup, dev, ttft_requests=args.replay_ttft_requests))
+        log(f"[bench] config 5 {configs['config5_replay']}")
     ttft = bench_ttft(args.ttft_requests, dev) if args.ttft_requests > 0 else None
     model = ttft.pop("model") if ttft is not None else None
-    if not args.no_configs:
-        configs["config5_replay"] = _config_summary(
-            bench_replay(min(args.steps, 20), args.warmup, dev, ttft_requests=args.replay_ttft_requests, model=model))
-        log(f"[bench] config 5 {configs['config5_replay']}")
     del model
     torch.cuda.empty_cache()
     cpu = bench_cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None

@@ -3,11 +3,12 @@ chunks x 256 tokens x 2 context variants (7.0 GiB at the Qwen2.5-7B KV shape: 28
 heads, head_dim 128, bf16) and 4 requests of 128 chunks drawn with replacement (Zipf s=1.1) at
 shuffled positions plus a 64-token query (N = 32832), 15 % recompute + 4 sinks. Each request's
 KV repair is issued on its own HIP stream, all four in flight together, in the launch order of
-the engine (layer 1's base cache, layer 0's fresh rows, layer-1 deviation and selection, the
-scatter of the kept rows, the gather of the dropped rows of layers 2-27, the fresh rows of
-layers 2-27). Every request is then checked against the oracle, bit for bit: the base cache,
-diff/norm, the kept set, layer 1 after the scatter, the fresh rows of layers 0 and 27 (RoPE at
-their positions) and the gathered rows of layers 2 and 27.
+the engine (layer 0's fresh rows; layer 1's repair as one ckv_layer1_repair call, with a
+workspace per request: base cache with the deviation, selection, kept rows; the gather of the
+dropped rows of layers 2-27; the fresh rows of layers 2-27). The fresh layer-1 rows are built
+beforehand from a base cache of the standalone gather. Every request is then checked against the
+oracle, bit for bit: that base cache, diff/norm, the kept set, layer 1 after the repair, the
+fresh rows of layers 0 and 27 (RoPE at their positions) and the gathered rows of layers 2 and 27.
 """
 
 import numpy as np
@@ -67,24 +68,21 @@ def _fresh_layer1(g, rq):
     rq["v1"] = v1_rows.transpose(1, 2).contiguous().transpose(1, 2)  # token-major memory, as v_proj leaves it
 
 
-def _repair(rq, table):
-    """One request's KV repair after its layer-1 base cache, in the engine's launch order."""
+def _repair(rq):
+    """One request's KV repair in the engine's launch order."""
     plan = rq["plan"]
     K, V = rq["K"].unbind(0), rq["V"].unbind(0)
     nseg, mseg, err = len(plan.segments), plan.max_seg_tokens, rq["err"]
     ops.rope_qkv(None, *rq["proj"][0], rq["layer0"], 0, H, D, THETA, k_out=K[0], v_out=V[0], rows=rq["layer0"],
-                 table=table, err=err)
-    diff, norm = ops.deviation(rq["k1"], rq["v1"], K[1], V[1], rq["flags"], rq["local"], err)
-    sel = ops.select(diff, norm, rq["flags"], rq["local"], rq["spans"], None)
+                 err=err)
+    diff, norm, sel = ops.layer1_repair(K[1], V[1], rq["tab"], NL, 1, rq["segs"], nseg, rq["k1"], rq["v1"],
+                                        rq["flags"], rq["local"], rq["spans"], None, THETA, rq["ws"], err)
     rq["diff"], rq["norm"], rq["sel"] = diff, norm, sel
-    n = plan.n_keep
-    rows, src = sel.keep_abs[:n], sel.keep_local[:n]
-    ops.scatter_rows(K[1], V[1], rq["k1"].index_select(2, src), rq["v1"].index_select(2, src), rows, err)
+    rows = sel.keep_abs[: plan.n_keep]
     ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, err, layers=(2, NL),
                       skip=sel.keep_rank)
     for li in range(2, NL):
-        ops.rope_qkv(None, *rq["proj"][li], rows, 0, H, D, THETA, k_out=K[li], v_out=V[li], rows=rows, table=table,
-                     err=err)
+        ops.rope_qkv(None, *rq["proj"][li], rows, 0, H, D, THETA, k_out=K[li], v_out=V[li], rows=rows, err=err)
 
 
 def _oracle_layer(plan, li):
@@ -107,21 +105,24 @@ def test_config5_four_concurrent_requests_match_oracle():
     reqs = [_build(g, rng, store) for _ in range(N_REQ)]
     assert all(rq["plan"].budget == 4864 for rq in reqs)
     assert len({c for rq in reqs for c in map(id, rq["plan"].chunks)}) < N_REQ * PER_REQ  # chunks shared
-    table = ops.rope_table(N, D, THETA, DEV)
-    # layer 1's base caches first (the fresh layer-1 rows are built from them), then the rest of
-    # every request's repair, the four requests on four streams in flight together
+    # layer 1's base caches first (the fresh layer-1 rows are built from them; layer 1 is then
+    # reset to a sentinel, every row of which the repair must rewrite), then every request's
+    # repair, the four requests on four streams in flight together
     for rq in reqs:
         plan = rq["plan"]
         ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], len(plan.segments), plan.max_seg_tokens, THETA,
                           rq["err"], layers=(1, 2))
         rq["base_k"], rq["base_v"] = rq["K"][1].clone(), rq["V"][1].clone()
         _fresh_layer1(g, rq)
+        rq["K"][1].fill_(-7.0)
+        rq["V"][1].fill_(-7.0)
+        rq["ws"] = ops.layer1_repair_workspace(DEV)
     main = torch.cuda.current_stream()
     streams = [torch.cuda.Stream() for _ in reqs]  # default priority
     for rq, st in zip(reqs, streams):
         st.wait_stream(main)
         with torch.cuda.stream(st):
-            _repair(rq, table)
+            _repair(rq)
     for st in streams:
         main.wait_stream(st)
     torch.cuda.synchronize()
@@ -148,10 +149,11 @@ def test_config5_four_concurrent_requests_match_oracle():
         np.testing.assert_array_equal(O.to_numpy(sel.rel_dev).view(np.uint32), want["rel_dev"].view(np.uint32))
         ka = want["keep_abs"]
         dropped = plan.cached & (want["keep_rank"] < 0)
-        # layer 1 after the scatter
+        # layer 1 after the repair: the kept rows fresh, every other row the cached one
         K1, V1 = O.to_numpy(rq["K"][1])[0], O.to_numpy(rq["V"][1])[0]
         np.testing.assert_array_equal(K1[:, ka], k1[:, want["keep_local"]])
         np.testing.assert_array_equal(V1[:, ka], v1[:, want["keep_local"]])
+        assert (plan.cached | (want["keep_rank"] >= 0)).all()  # so every row is one of the two
         np.testing.assert_array_equal(K1[:, dropped], K1o[:, dropped])
         np.testing.assert_array_equal(V1[:, dropped], V1o[:, dropped])
         # fresh rows: layer 0 at every position, layer 27 at the kept positions (k rotated, v copied)
