@@ -287,7 +287,9 @@ int32_t ckv_deviation_select_noalloc(const void* k_fresh, int64_t kf_head_stride
  * (same arguments, same meaning; see each above). dst_k/dst_v are the layer's (H, n_tokens, D)
  * cache, head stride dst_head_stride; src_tab/n_tab_chunks/n_layers/layer select the chunks' rows
  * as in ckv_assemble_layer; segs are the cached runs, sorted by dst_start and disjoint (the
- * planner's segments, n_segs <= 3840), read for every position flagged CKV_POS_CACHED.
+ * planner's segments, n_segs <= 3840), read for every position flagged CKV_POS_CACHED. segs and
+ * src_tab may be NULL with n_segs == 0, k_fresh and v_fresh with n_fresh == 0 (every position
+ * exact: a kept position then flags CKV_DEVICE_ERR_RANGE, as an out-of-range local index does).
  * Three launches, nothing read back on the host: (1) every position's rows, the cached rows
  * written into the cache, the deviations, and the positions flagged CKV_POS_CACHED |
  * CKV_POS_POOLED and not CKV_POS_SINK counted into the deviation histogram; (2) the selection,
