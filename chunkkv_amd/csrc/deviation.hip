@@ -150,7 +150,7 @@ extern "C" int32_t ckv_deviation_select(
   if (n_chunks > 0 && (chunks == nullptr || rel_dev == nullptr || escalated == nullptr))
     return CKV_ERR_INVALID_ARGUMENT;
   if (n_tokens > CKV_SELECT_MAX_TOKENS) return CKV_ERR_TOO_LARGE;
-  const bool with_hist = n_tokens > 0 && n_tokens <= 33 * kSelThreads;  // the register-resident selection
+  const bool with_hist = n_tokens > 0 && n_tokens <= kSelRegMax * kSelThreads;  // the register-resident selection
   if (with_hist && (workspace == nullptr || workspace_bytes < CKV_DEVIATION_SELECT_WORKSPACE_BYTES ||
                     (uintptr_t)workspace % 16))
     return CKV_ERR_INVALID_ARGUMENT;

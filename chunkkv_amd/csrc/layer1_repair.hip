@@ -397,7 +397,7 @@ extern "C" int32_t ckv_layer1_repair(
   if (n_tokens == 0) return select_launch(sel, nullptr, st);  // nothing to repair: counts and span stats
 
   // the register-resident selection takes the histogram; above it, the L2 form counts itself
-  uint32_t* hist = n_tokens <= 33 * kSelThreads ? (uint32_t*)workspace : nullptr;
+  uint32_t* hist = n_tokens <= kSelRegMax * kSelThreads ? (uint32_t*)workspace : nullptr;
   L1Args args{};
   args.dk = (char*)dst_k;
   args.dv = (char*)dst_v;

@@ -32,6 +32,10 @@
 namespace ckv {
 
 constexpr int kSelThreads = 1024;
+#ifndef CKV_SEL_REG_MAX
+#define CKV_SEL_REG_MAX 33
+#endif
+constexpr int kSelRegMax = CKV_SEL_REG_MAX;  // positions per thread up to which the keys stay in registers
 constexpr int kSelWaves = kSelThreads / kWave;
 // Top-digit histogram: kTopBins bins over a window of the keys of positive deviations. Interior
 // bin b (1 <= b <= kTopBins - 2) holds the keys [kTopLo + (b - 1) 2^kTopShift, kTopLo + b 2^kTopShift),
@@ -247,6 +251,16 @@ __device__ __forceinline__ void load_first_spans(const ckv_chunk_span* chunks, i
   }
 }
 
+// Position p clamped into [0, n_tokens), and element idx of an array whose base address is
+// wavefront-uniform, addressed as that base plus a 32-bit offset (the base stays in scalar
+// registers; one 64-bit address per position and array put the 33-position bucket's addresses
+// into scratch memory).
+__device__ __forceinline__ uint32_t clamp_pos(int p, int n_tokens) { return (uint32_t)min(p, n_tokens - 1); }
+template <class T>
+__device__ __forceinline__ T ld_at(const T* base, uint32_t idx) {
+  return *(const T*)((const char*)base + idx * (uint32_t)sizeof(T));
+}
+
 // SUMS = false (only without a threshold): the per-chunk sums and rel_dev/escalated are left to
 // other workgroups (chunk_sums_wave); the budget and the pool come from the spans alone.
 template <int KPT, bool SUMS = true>
@@ -285,6 +299,10 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   float dv[KPT];            // the owned positions' deviations (their keys after phase 0)
   uint32_t fl[kFlagWords];  // their flag bytes, four per register
   int lv[KPT];              // their local indices (the compaction's keep_local)
+  // Above 16 positions per thread the local indices are loaded by the compaction, which alone
+  // uses them: held from the start they pushed the 24- and 33-position buckets past the 128
+  // registers a thread of a 1024-thread workgroup has, into scratch memory.
+  constexpr bool kLateLocal = KPT > 16;
 #pragma unroll
   for (int w = 0; w < kFlagWords; ++w) fl[w] = 0u;
   // A thread's run is contiguous, so lanes are KPT elements apart: with KPT % 4 == 0 and aligned
@@ -319,13 +337,38 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     load_hist();
 #pragma unroll
     for (int i0 = 0; i0 < KPT; i0 += 4) fl[i0 / 4] = *(const uint32_t*)(flags + p0 + i0);  // flags i0 .. i0 + 3
+    if constexpr (!kLateLocal) {
 #pragma unroll
-    for (int i0 = 0; i0 < KPT; i0 += 4) {
-      const int4 l = *(const int4*)(local + p0 + i0);
-      lv[i0] = l.x;
-      lv[i0 + 1] = l.y;
-      lv[i0 + 2] = l.z;
-      lv[i0 + 3] = l.w;
+      for (int i0 = 0; i0 < KPT; i0 += 4) {
+        const int4 l = *(const int4*)(local + p0 + i0);
+        lv[i0] = l.x;
+        lv[i0 + 1] = l.y;
+        lv[i0 + 2] = l.z;
+        lv[i0 + 3] = l.w;
+      }
+    }
+  } else if (wave_end + 3 <= n_tokens && (uintptr_t)flags % 4 == 0) {  // uniform
+    // Runs in range but not 16-byte loadable (KPT % 4 != 0): one address per array and thread,
+    // the positions at immediate offsets from it; the flags as the aligned 32-bit words around
+    // the run (up to 3 bytes past it, below n_tokens here), realigned by v_alignbyte (one
+    // register per four positions in flight, not one per position).
+    const float* d = diff + p0;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) dv[i] = d[i];
+    load_hist();
+    constexpr int kWin = (KPT + 2) / 4 + 1;  // words holding bytes p0 .. p0 + KPT - 1
+    const uint32_t* fw = (const uint32_t*)(flags + (p0 & ~3));
+    uint32_t win[kWin + 1];
+#pragma unroll
+    for (int w = 0; w < kWin; ++w) win[w] = fw[w];
+    win[kWin] = 0u;
+    const uint32_t sh = (uint32_t)(p0 & 3);
+#pragma unroll
+    for (int w = 0; w < kFlagWords; ++w) fl[w] = __builtin_amdgcn_alignbyte(win[w + 1], win[w], sh);
+    if constexpr (!kLateLocal) {
+      const int32_t* l = local + p0;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) lv[i] = l[i];
     }
   } else if (__builtin_amdgcn_readfirstlane(wave * kWave * KPT) < n_tokens) {  // uniform
     // The wavefront whose runs cross n_tokens: every load unconditional, its index clamped into
@@ -333,17 +376,19 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     // of positions past the end are never used: every use below is masked by the candidate or
     // kept bits, which only positions below n_tokens get.
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) dv[i] = diff[min(p0 + i, n_tokens - 1)];
+    for (int i = 0; i < KPT; ++i) dv[i] = ld_at(diff, clamp_pos(p0 + i, n_tokens));
     load_hist();
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) fl[i / 4] |= (uint32_t)flags[min(p0 + i, n_tokens - 1)] << (8 * (i % 4));
+    for (int i = 0; i < KPT; ++i) fl[i / 4] |= (uint32_t)ld_at(flags, clamp_pos(p0 + i, n_tokens)) << (8 * (i % 4));
+    if constexpr (!kLateLocal) {
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) lv[i] = local[min(p0 + i, n_tokens - 1)];
+      for (int i = 0; i < KPT; ++i) lv[i] = ld_at(local, clamp_pos(p0 + i, n_tokens));
+    }
   } else {  // a wavefront past the last position: nothing to load
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       dv[i] = __uint_as_float(0x7fc00000u);
-      lv[i] = 0;
+      if constexpr (!kLateLocal) lv[i] = 0;
     }
     load_hist();
   }
@@ -447,12 +492,14 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     pool_bits = ((uint64_t)poolw[w0] | (two ? (uint64_t)poolw[w0 + 1] << 32 : 0ull)) >> (p0 & 31);
   }
   uint64_t cand = 0u, kept_static = 0u;
+  uint64_t cached_bits = 0u;  // the compaction's count of kept cached positions (the flags die here)
   int mism = 0;  // positions where the histogram's candidate rule and the true one disagree
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     const int p = p0 + i;
     if (p < n_tokens) {
       const uint32_t f = (fl[i / 4] >> (8 * (i % 4))) & 0xffu;
+      cached_bits |= (uint64_t)((f & CKV_POS_CACHED) ? 1u : 0u) << i;
       const bool k = !(f & CKV_POS_CACHED) || (f & CKV_POS_SINK) || ((esc_bits >> i) & 1u);
       kept_static |= (uint64_t)k << i;
       const bool c = !k && ((pool_bits >> i) & 1u);
@@ -669,41 +716,62 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
     take |= tie;  // every tie at T is taken (none when ranked)
   }
   const uint64_t kept = kept_static | take;
+  if constexpr (kLateLocal) {  // the local indices, as the first loads took them
+    if (vec_ok && wave_end <= n_tokens) {  // uniform
+#pragma unroll
+      for (int i0 = 0; i0 < KPT; i0 += 4) {
+        const int4 l = *(const int4*)(local + p0 + i0);
+        lv[i0] = l.x;
+        lv[i0 + 1] = l.y;
+        lv[i0 + 2] = l.z;
+        lv[i0 + 3] = l.w;
+      }
+    } else if (wave_end <= n_tokens) {  // uniform
+      const int32_t* l = local + p0;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) lv[i] = l[i];
+    } else if (__builtin_amdgcn_readfirstlane(wave * kWave * KPT) < n_tokens) {  // uniform
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) lv[i] = ld_at(local, clamp_pos(p0 + i, n_tokens));
+    } else {
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) lv[i] = 0;
+    }
+  }
   // One scan for three counts in 21-bit fields (each total <= n_tokens < 2^21): kept positions
   // (the rank of each), kept cached positions, kept positions absent from the active set.
-  uint64_t mine = (uint64_t)__popcll(kept);
+  uint64_t mine = (uint64_t)__popcll(kept) + ((uint64_t)__popcll(kept & cached_bits) << 21);
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    if ((kept >> i) & 1ull) {
-      mine += (((fl[i / 4] >> (8 * (i % 4))) & CKV_POS_CACHED) ? 1ull : 0ull) << 21;
-      mine += (uint64_t)(lv[i] < 0) << 42;
-    }
+    if ((kept >> i) & 1ull) mine += (uint64_t)(lv[i] < 0) << 42;
   }
   uint64_t all = 0;
   int rank = (int)(block_scan_1b_u64(mine, slots64[1], all) & kField);
   const int n_keep = (int)(all & kField);
   const int sel_cached = (int)((all >> 21) & kField);
   const int uncomputed = (int)((all >> 42) & kField);
-  int kr[KPT];  // keep_rank of the owned positions
+  // four positions at a time: the kept ones' keep_abs / keep_local, then the four keep_rank entries
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    kr[i] = ((kept >> i) & 1ull) ? rank : -1;
-    if ((kept >> i) & 1ull) {
-      const int p = p0 + i;
-      a.keep_abs[rank] = p;
-      a.keep_local[rank] = lv[i] < 0 ? 0 : lv[i];
-      ++rank;
+  for (int i0 = 0; i0 < KPT; i0 += 4) {
+    int kr[4];  // keep_rank of positions i0 .. i0 + 3
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j;
+      const bool k = i < KPT && ((kept >> i) & 1ull);
+      kr[j] = k ? rank : -1;
+      if (k) {
+        a.keep_abs[rank] = p0 + i;
+        a.keep_local[rank] = lv[i] < 0 ? 0 : lv[i];
+        ++rank;
+      }
     }
-  }
-  if (keep_rank != nullptr) {
-#pragma unroll
-    for (int i0 = 0; i0 < KPT; i0 += 4) {
+    if (keep_rank != nullptr) {
       if (vec_ok && p0 + i0 + 4 <= n_tokens) {
-        *(int4*)(keep_rank + p0 + i0) = make_int4(kr[i0], kr[i0 + 1], kr[i0 + 2], kr[i0 + 3]);
+        *(int4*)(keep_rank + p0 + i0) = make_int4(kr[0], kr[1], kr[2], kr[3]);
       } else {
 #pragma unroll
-        for (int i = i0; i < i0 + 4 && i < KPT; ++i)
-          if (p0 + i < n_tokens) keep_rank[p0 + i] = kr[i];
+        for (int j = 0; j < 4; ++j)
+          if (i0 + j < KPT && p0 + i0 + j < n_tokens) keep_rank[p0 + i0 + j] = kr[j];
       }
     }
   }
