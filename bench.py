@@ -776,17 +776,30 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         tab = np.concatenate([np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(ch.keys, ch.values)],
                                        dtype=np.uint64).reshape(-1) for ch in plan.chunks])
         K = torch.empty((N_LAYERS, 1, N_KV, N, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+        V = torch.empty_like(K)
+        tab_d = torch.from_numpy(tab.view(np.int64)).to(dev)
+        segs_d = torch.from_numpy(plan.segments.reshape(-1)).to(dev)
         proj = [None if li == 1 else (torch.randn((1, N if li == 0 else plan.n_keep, row), device=dev).bfloat16(),
                                       torch.randn((1, N if li == 0 else plan.n_keep, row), device=dev).bfloat16())
                 for li in range(N_LAYERS)]
-        reqs.append(dict(plan=plan, tab=torch.from_numpy(tab.view(np.int64)).to(dev),
-                         segs=torch.from_numpy(plan.segments.reshape(-1)).to(dev), K=K, V=torch.empty_like(K),
+        # layer-1 fresh rows as the 8k request builds them: each cached position's re-rotated cached
+        # row plus noise at a per-chunk level exp(N(-3, 1)), the uncached query rows random, v
+        # token-major (uncorrelated random rows put every deviation within a few percent of the
+        # others: the selection's slowest case, measured separately)
+        ops.rerope_gather(K, V, tab_d, segs_d, len(plan.segments), plan.max_seg_tokens, THETA, layers=(1, 2))
+        sig = torch.ones(N, device=dev)
+        sig[: PER_REQ * L] = torch.exp(torch.randn(PER_REQ, generator=gen, device=dev) - 3.0).repeat_interleave(L)
+        sig = sig[None, None, :, None]
+        cached = torch.from_numpy(plan.cached).to(dev)[None, None, :, None]
+        rnd = lambda: torch.randn((1, N_KV, N, HEAD_DIM), generator=gen, device=dev)  # noqa: E731
+        k1 = torch.where(cached, K[1].float() + sig * rnd(), rnd()).bfloat16()
+        v1 = torch.where(cached, V[1].float() + sig * rnd(), rnd()).bfloat16().transpose(1, 2).contiguous()
+        reqs.append(dict(plan=plan, tab=tab_d, segs=segs_d, K=K, V=V,
                          flags=torch.from_numpy(plan.flags).to(dev),
                          local=torch.from_numpy(local_index(N, plan.layer0_idx)).to(dev),
                          spans=torch.from_numpy(plan.spans.reshape(-1)).to(dev),
                          layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), proj=proj,
-                         fresh1=(torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16(),
-                                 torch.randn((1, N_KV, N, HEAD_DIM), device=dev).bfloat16()), sel=None,
+                         fresh1=(k1, v1.transpose(1, 2)), sel=None,
                          ws=ops.layer1_repair_workspace(dev),
                          dn=(torch.empty(N, dtype=torch.float32, device=dev),
                              torch.empty(N, dtype=torch.float32, device=dev))))

@@ -256,12 +256,9 @@ int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st) {
   CKV_SEL_REG(8)
   CKV_SEL_REG(12)
   CKV_SEL_REG(16)
-#if CKV_SEL_REG_MAX >= 24
   CKV_SEL_REG(24)
-#endif
-#if CKV_SEL_REG_MAX >= 33
   CKV_SEL_REG(33)
-#endif
+  static_assert(kSelRegMax == 33, "the largest register bucket");
 #undef CKV_SEL_REG
   if (ghist != nullptr) return CKV_ERR_INVALID_ARGUMENT;  // the L2 form takes no histogram
   hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, st, args.diff, args.norm, args.flags,
