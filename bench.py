@@ -491,7 +491,7 @@ class _Tok:
 def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20) -> dict:
     """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests, and of
     HipEngine with the reference's own SDPA call (attention="reference": only the KV repair on the
-    HIP kernels, attention on PyTorch-ROCm, the north star's split) on the first
+    HIP kernels, the attention left on PyTorch-ROCm) on the first
     n_reference_attention of them. All run the model's library GEMMs with the same committed
     TunableOp selection table (when present)."""
     from chunkkv_amd.baseline import TorchOpsEngine

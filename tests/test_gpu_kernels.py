@@ -1,6 +1,6 @@
 """GPU parity of each HIP kernel against the C oracle on the same seeded inputs.
 
-Bar (from the north star): gather, scatter and the selected index set bit-exact; deviation
+Bar: gather, scatter and the selected index set bit-exact; deviation
 bit-exact under the fixed summation order; re-RoPE keys within one bf16 ulp (fp32 keys within
 a few fp32 ulps: cos/sin come from different libraries on host and device).
 """
