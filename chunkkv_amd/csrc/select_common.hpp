@@ -315,6 +315,8 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   // write the same registers, so every vector group had to land before the next could go out
   // (three memory round trips in a row instead of one).
   const int wave_end = __builtin_amdgcn_readfirstlane((wave + 1) * kWave * KPT);
+  constexpr int kWin = (KPT + 2) / 4 + 1;   // aligned flag words holding bytes p0 .. p0 + KPT - 1
+  constexpr int kFlagOver = 4 * kWin - KPT;  // their bytes past the run at most (p0 % 4 == 0)
   // The loads go out in the order their values are needed (vector loads complete in issue order):
   // the deviations, the top-digit histogram, the flags, and last the local indices, which only
   // the compaction uses.
@@ -347,16 +349,16 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
         lv[i0 + 3] = l.w;
       }
     }
-  } else if (wave_end + 3 <= n_tokens && (uintptr_t)flags % 4 == 0) {  // uniform
-    // Runs in range but not 16-byte loadable (KPT % 4 != 0): one address per array and thread,
-    // the positions at immediate offsets from it; the flags as the aligned 32-bit words around
-    // the run (up to 3 bytes past it, below n_tokens here), realigned by v_alignbyte (one
-    // register per four positions in flight, not one per position).
+  } else if (wave_end + kFlagOver <= n_tokens && (uintptr_t)flags % 4 == 0) {  // uniform
+    // Runs in range but not 16-byte loadable (KPT % 4 != 0, or arrays not aligned): one address
+    // per array and thread, the positions at immediate offsets from it; the flags as the kWin
+    // aligned 32-bit words from p0 rounded down (at most kFlagOver bytes past the run: below
+    // n_tokens here), realigned by v_alignbyte (one register per four positions in flight, not
+    // one per position).
     const float* d = diff + p0;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) dv[i] = d[i];
     load_hist();
-    constexpr int kWin = (KPT + 2) / 4 + 1;  // words holding bytes p0 .. p0 + KPT - 1
     const uint32_t* fw = (const uint32_t*)(flags + (p0 & ~3));
     uint32_t win[kWin + 1];
 #pragma unroll

@@ -438,6 +438,38 @@ def test_select_sizes(N):
     _check_select(diff, norm, flags, np.arange(N, dtype=np.int32), spans, None)
 
 
+@pytest.mark.parametrize("flags_off", [4, 1])
+@pytest.mark.parametrize("N", [1025, 8256, 16000, 20000, 33000])
+def test_select_misaligned_inputs(N, flags_off):
+    """diff, norm and local one element into their buffers (4-byte, not 16-byte aligned), flags
+    4 or 1 bytes in: the selecting threads load their runs from one address per array instead of
+    16-byte vectors, the flags as aligned words (4-byte aligned flags) or byte by byte, in every
+    register bucket from 4 to 33 positions per thread; same result as the oracle."""
+    rng = np.random.default_rng(N + flags_off)
+    L = 250
+    flags, spans = _spans(N // L, L, 0.3, 4, N)
+    diff = rng.gamma(2.0, 1.0, N).astype(np.float32)
+    norm = (diff + 1).astype(np.float32)
+    local = np.arange(N, dtype=np.int32)
+
+    def at(a, off):
+        buf = torch.zeros(len(a) + off + 16, dtype=dev(a[:1]).dtype, device=DEV)
+        buf[off : off + len(a)] = dev(a)
+        return buf[off : off + len(a)]
+
+    d, n, f, lo = at(diff, 1), at(norm, 1), at(flags, flags_off), at(local, 1)
+    assert d.data_ptr() % 16 and lo.data_ptr() % 16 and f.data_ptr() % 4 == flags_off % 4
+    got = ops.select(d, n, f, lo, dev(spans.reshape(-1)), None)
+    want = O.select(diff, norm, flags, local, spans, None)
+    counts = host(got.counts)
+    np.testing.assert_array_equal(counts[:6], want["counts"][:6])
+    k = int(counts[0])
+    np.testing.assert_array_equal(host(got.keep_abs)[:k], want["keep_abs"])
+    np.testing.assert_array_equal(host(got.keep_local)[:k], want["keep_local"])
+    np.testing.assert_array_equal(host(got.keep_rank), want["keep_rank"])
+    np.testing.assert_array_equal(host(got.rel_dev)[: len(spans)].view(np.uint32), want["rel_dev"].view(np.uint32))
+
+
 @pytest.mark.parametrize("bf16", [True, False])
 def test_scatter_bit_exact(bf16):
     rng = np.random.default_rng(7 + bf16)
