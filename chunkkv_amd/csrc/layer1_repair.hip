@@ -38,12 +38,12 @@
 
 namespace ckv {
 
-#ifndef CKV_L1_T
-#define CKV_L1_T 2
-#endif
 constexpr int kL1Threads = 256;
 constexpr int kL1Waves = kL1Threads / kWave;
-constexpr int kL1T = CKV_L1_T;  // positions per wavefront
+// Positions per wavefront. One: in the 8k request step 0.262 ms against 0.264 ms with two and
+// 0.266 ms with four (more wavefronts, each with fewer loads in flight, overlap the pass's
+// dependent load chain better).
+constexpr int kL1T = 1;
 constexpr int kL1MaxSegs = 64 * 60;  // segment search: 64 samples, then a window of stride + T
 
 // per-position class bits
