@@ -156,8 +156,8 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     li[t] = okl ? lraw[t] : -1;
     r.kc[t] = r.vc[t] = vec16{0u, 0u, 0u, 0u};
     const int64_t lc = okl ? lraw[t] : 0;  // kf/vf are readable with n_fresh == 0: the workspace
-    r.kf[t] = ld16(a.kf + hc * a.kf_hs_b + lc * a.kf_ts_b + colb);
-    r.vf[t] = ld16(a.vf + hc * a.vf_hs_b + lc * a.vf_ts_b + colb);
+    r.kf[t] = ld16_stream(a.kf + hc * a.kf_hs_b + lc * a.kf_ts_b + colb);  // read once: non-temporal
+    r.vf[t] = ld16_stream(a.vf + hc * a.vf_hs_b + lc * a.vf_ts_b + colb);
   }
 
   // 4. each position's segment (the last with dst_start <= p) and its chunk's base addresses
@@ -204,8 +204,8 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     if (have[t]) {  // uniform
-      r.kc[t] = ld16(kb[t] + soff[t]);
-      r.vc[t] = ld16(vb[t] + soff[t]);
+      r.kc[t] = ld16_stream(kb[t] + soff[t]);
+      r.vc[t] = ld16_stream(vb[t] + soff[t]);
     }
   }
   float cv[T], sv[T];

@@ -216,7 +216,8 @@ __global__ __launch_bounds__(kRopeKvThreads) void rope_kv_kernel(
   // the first item's data goes out before anything waits on the position load
   const int h0 = (SHAPE == kKvFull ? lane : min(lane, items - 1)) / TPR;
   const char* s0 = src_of(h0);
-  vec16 a = ld16(s0), b = ld16(s0 + HALF_B);
+  // non-temporal loads: each input row is read once (the request step 0.258 -> 0.244 ms)
+  vec16 a = ld16_stream(s0), b = ld16_stream(s0 + HALF_B);
   const int64_t row = RM == kRowToken ? (int64_t)t : RM == kRowPos ? p : rows[t];
   const bool ok = p >= INT32_MIN && p <= INT32_MAX && row >= 0 && row < n_out;
   auto dst_of = [&](int hh) {
@@ -251,8 +252,8 @@ __global__ __launch_bounds__(kRopeKvThreads) void rope_kv_kernel(
       const int hh = it / TPR;
       if (it != lane) {
         const char* si = src_of(hh);
-        a = ld16(si);
-        b = ld16(si + HALF_B);
+        a = ld16_stream(si);
+        b = ld16_stream(si + HALF_B);
       }
       char* d = dst_of(hh);
       vec16 y1 = a, y2 = b;

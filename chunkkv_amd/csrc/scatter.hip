@@ -46,8 +46,8 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_rows_kernel(
       const int64_t js = src_rows != nullptr ? src_rows[j] : j;
       const bool src_ok = js >= 0 && js < n_src;
       if (src_ok) {
-        a[u] = ld16(sk + h * sk_hs_b + js * sk_ts_b + cb);
-        b[u] = ld16(sv + h * sv_hs_b + js * sv_ts_b + cb);
+        a[u] = ld16_stream(sk + h * sk_hs_b + js * sk_ts_b + cb);  // read once: non-temporal
+        b[u] = ld16_stream(sv + h * sv_hs_b + js * sv_ts_b + cb);
       }
       if (src_ok && t >= 0 && t < n_tokens) {
         dst_o[u] = h * d_hs_b + t * row_b + cb;
