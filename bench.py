@@ -244,7 +244,14 @@ class RepairWorkload:
             with torch.cuda.stream(self.side):
                 fn()
 
-        if self.layer1_mode == "one":
+        if self.layer1_mode == "one" and not two_streams:
+            # as HipEngine: layer 1's repair with the dropped rows of layers 2-27 in its last launch
+            self.kv_rows(0)
+            self.layer1_gather()
+            for li in range(2, N_LAYERS):
+                self.kv_rows(li)
+            return
+        if self.layer1_mode in ("one", "separate_gather"):
             self.kv_rows(0)
             self.layer1_one()
         else:
@@ -259,6 +266,28 @@ class RepairWorkload:
             self.kv_rows(li)
         if two_streams:
             main.wait_stream(self.side)
+
+    def layer1_gather(self):
+        """Layer 1's whole repair and the gather of the dropped rows of layers 2-27 in one call of
+        three launches (ckv_layer1_repair_gather): the cached rows re-rotated with the deviation,
+        the selection, then the kept rows of layer 1 and the dropped rows of layers 2-27 in one
+        launch."""
+        from chunkkv_amd import ops
+
+        k1, v1 = self.fresh[1]
+        _, _, self.sel = ops.layer1_repair_gather(self.k_slab, self.v_slab, self.tab, 1, (2, N_LAYERS), self.segs,
+                                                  len(self.plan.segments), self.plan.max_seg_tokens, k1, v1,
+                                                  self.flags, self.local, self.spans, None, THETA, self.ws1, self.err,
+                                                  self.sel, self.dn)
+
+    def step_separate_gather(self):
+        """The step with layer 1's repair and the dropped-row gather as separate calls (the kept
+        rows' scatter its own launch)."""
+        self.layer1_mode = "separate_gather"
+        try:
+            self.step()
+        finally:
+            self.layer1_mode = "one"
 
     def layer1_one(self):
         """Layer 1's whole repair in one call of three launches: the cached rows re-rotated from the
@@ -383,18 +412,21 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
         wls[i % 2].step_two_streams()
         wls[i % 2].step_assemble()
         wls[i % 2].step_split()
+        wls[i % 2].step_separate_gather()
     torch.cuda.synchronize()
     graphs = [_graph_of(w.step) for w in wls]
     two = [_graph_of(w.step_two_streams) for w in wls]
     asm_graphs = [_graph_of(w.step_assemble) for w in wls]
     split = [_graph_of(w.step_split) for w in wls]
+    sep = [_graph_of(w.step_separate_gather) for w in wls]
     stream = torch.cuda.current_stream(dev)
-    for g in graphs + two + asm_graphs + split:
+    for g in graphs + two + asm_graphs + split + sep:
         g.replay()
     ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
     ms_two = _timed(lambda i: two[i % 2].replay(), steps, stream)
     ms_asm = _timed(lambda i: asm_graphs[i % 2].replay(), steps, stream)
     ms_split = _timed(lambda i: split[i % 2].replay(), steps, stream)
+    ms_sep = _timed(lambda i: sep[i % 2].replay(), steps, stream)
     for w in wls:  # the selection state of the one-stream step again
         w.step()
     ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
@@ -408,7 +440,8 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     nbytes = repair_bytes(n_keep)
     gd_bytes = dropped_bytes(plan)
     ms_conc = _concurrent_steps(wls, steps, dev)
-    return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_split=ms_split, ms_eager=ms_eager, bytes=nbytes,
+    return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_split=ms_split, ms_sep=ms_sep, ms_eager=ms_eager,
+                bytes=nbytes,
                 moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
                 asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep, ms_conc=ms_conc,
@@ -1234,6 +1267,7 @@ def main() -> None:
         "ms_per_step_two_streams": round(r["ms_two"], 4),
         "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
         "ms_per_step_layer1_four_launches": round(r["ms_split"], 4),
+        "ms_per_step_separate_gather": round(r["ms_sep"], 4),
         "concurrent_requests": {"requests": CONCURRENT, "ms_per_round": round(r["ms_conc"], 4),
                                 "gbs": round(r["conc_gbs"], 1), "pct_of_peak": round(100.0 * r["conc_gbs"] / PEAK_GBS, 2),
                                 "note": "the same request's KV repair, CONCURRENT independent requests in flight on "

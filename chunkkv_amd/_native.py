@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libchunkkv_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CKV_OK = 0
 CKV_ERR_INVALID_ARGUMENT = 1
@@ -36,7 +36,7 @@ COUNT_TOP_HISTOGRAM = 7  # bit 0: histogram path; bit 1: threshold bin ranked di
 COUNT_N = 8
 
 DEVIATION_SELECT_WORKSPACE_BYTES = 16640
-LAYER1_REPAIR_WORKSPACE_BYTES = 16384
+LAYER1_REPAIR_WORKSPACE_BYTES = 16640
 POS_POOLED = 8
 
 SELECT_MAX_TOKENS = 131072
@@ -107,6 +107,12 @@ SIGNATURES = {
         _i32,
         [_p, _p, _i64, _p, _i32, _i32, _i32, _p, _i32, _p, _i64, _i64, _p, _i64, _i64, _i32, _p, _p, _i32, _i32, _i32,
          _i32, _f64, _p, _i32, _i32, _f64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p],
+    ),
+    "ckv_layer1_repair_gather": (
+        _i32,
+        [_p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _p, _i64, _i64, _p, _i64, _i64, _i32,
+         _p, _p, _i32, _i32, _i32, _i32, _f64, _p, _i32, _i32, _f64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p,
+         _p],
     ),
     "ckv_deviation_select_noalloc": (
         _i32,

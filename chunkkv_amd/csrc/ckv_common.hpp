@@ -36,6 +36,20 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
   return r;
 }
 
+// Two fp32 values rounded to bf16 (round-to-nearest-even) and back to fp32, for arithmetic only:
+// one packed conversion for both. A NaN input gives a NaN (the hardware conversion maps every
+// fp32 NaN to a bf16 NaN; checked over all 2^24 NaN patterns in both slots) with an unspecified
+// payload, so callers whose results may be NaN canonicalize them (canonical_nan) before storing.
+__device__ __forceinline__ void bf16_round_pair(float a, float b, float& ra, float& rb) {
+  const f32x2_cvt v = {a, b};
+  const uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_cvt));
+  ra = __uint_as_float(r << 16);
+  rb = __uint_as_float(r & 0xffff0000u);
+}
+
+// x, or the canonical quiet NaN 0x7fc00000 if x is a NaN (any sign or payload).
+__device__ __forceinline__ float canonical_nan(float x) { return x != x ? __uint_as_float(0x7fc00000u) : x; }
+
 // fp32 -> bf16 bits, round-to-nearest-even, NaN -> 0x7fc0.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return f32x2_to_bf16x2_bits(f, 0.0f) & 0xffffu; }
 
@@ -63,6 +77,10 @@ struct Elem<CKV_DTYPE_BF16> {
   }
   // value after rounding to the element type, back in fp32
   __device__ __forceinline__ static float round_trip(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+  // two values rounded to the element type and back, for arithmetic (NaN payloads unspecified)
+  __device__ __forceinline__ static void round_trip2(float a, float b, float& ra, float& rb) {
+    bf16_round_pair(a, b, ra, rb);
+  }
 };
 
 template <>
@@ -79,6 +97,10 @@ struct Elem<CKV_DTYPE_F32> {
     return vec16{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
   }
   __device__ __forceinline__ static float round_trip(float f) { return f; }
+  __device__ __forceinline__ static void round_trip2(float a, float b, float& ra, float& rb) {
+    ra = a;
+    rb = b;
+  }
 };
 
 // ---- memory -----------------------------------------------------------------------------

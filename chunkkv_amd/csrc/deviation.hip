@@ -7,6 +7,7 @@
 // workgroup; every load of a token is issued before its arithmetic.
 #include "deviation_common.hpp"
 #include "launch.hpp"
+#include "select_slices.hpp"
 
 namespace ckv {
 
@@ -24,12 +25,14 @@ static_assert(kDevPerGroup <= kWave, "one lane of wavefront 0 per position of th
 // The pointers and sizes the first loads use lead the argument list: the library preloads the
 // first 16 argument dwords into SGPRs, but only up to the first argument passed by reference
 // (the DevArgs struct), and every other argument takes a scalar load at wave start.
+// zero_word (may be NULL) is set to 0 by the launch (a count the next launch adds to).
 template <int DTYPE, bool HIST>
 __global__ __launch_bounds__(kDevThreads) void deviation_kernel(const int32_t* local, const uint8_t* flags,
                                                                 const char* kc, const char* vc, const char* kf,
                                                                 const char* vf, int n_tokens, int n_fresh, DevArgs a,
                                                                 float* __restrict__ diff, float* __restrict__ norm,
-                                                                uint32_t* __restrict__ hist) {
+                                                                uint32_t* __restrict__ hist,
+                                                                int32_t* __restrict__ zero_word) {
   a.local = local;
   a.flags = flags;
   a.kc = kc;
@@ -44,6 +47,7 @@ __global__ __launch_bounds__(kDevThreads) void deviation_kernel(const int32_t* l
   const int p_base = ((int)blockIdx.x * kDevWaves + wave) * kDevTokens;
   float d[kDevTokens], n[kDevTokens];
   uint32_t fl[kDevTokens];
+  if (zero_word != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *zero_word = 0;
   deviation_wave<DTYPE, kDevTokens>(a, p_base, d, n, fl);
   if (lane == 0) {
 #pragma unroll
@@ -76,10 +80,12 @@ __global__ __launch_bounds__(kDevThreads) void deviation_kernel(const int32_t* l
 }
 
 template <int DTYPE, bool HIST>
-static void launch_deviation(const DevArgs& args, float* diff, float* norm, uint32_t* hist, hipStream_t st) {
+static void launch_deviation(const DevArgs& args, float* diff, float* norm, uint32_t* hist, hipStream_t st,
+                             int32_t* zero_word = nullptr) {
   const unsigned blocks = (unsigned)((args.n_tokens + kDevPerGroup - 1) / kDevPerGroup);
   hipLaunchKernelGGL((deviation_kernel<DTYPE, HIST>), dim3(blocks), dim3(kDevThreads), 0, st, args.local, args.flags,
-                     args.kc, args.vc, args.kf, args.vf, args.n_tokens, args.n_fresh, args, diff, norm, hist);
+                     args.kc, args.vc, args.kf, args.vf, args.n_tokens, args.n_fresh, args, diff, norm, hist,
+                     zero_word);
 }
 
 static int32_t check_deviation_args(const void* k_fresh, const void* v_fresh, const void* k_cache, const void* v_cache,
@@ -150,21 +156,25 @@ extern "C" int32_t ckv_deviation_select(
   if (n_chunks > 0 && (chunks == nullptr || rel_dev == nullptr || escalated == nullptr))
     return CKV_ERR_INVALID_ARGUMENT;
   if (n_tokens > CKV_SELECT_MAX_TOKENS) return CKV_ERR_TOO_LARGE;
-  const bool with_hist = n_tokens > 0 && n_tokens <= kSelRegMax * kSelThreads;  // the register-resident selection
+  // Without a threshold: the selection spread over many workgroups (select_slices.hpp); with one,
+  // the single-workgroup selection (the register-resident form takes the histogram).
+  const bool spread = has_threshold == 0 && select_slices_fits(n_tokens);
+  const bool with_hist = n_tokens > 0 && (spread || n_tokens <= kSelRegMax * kSelThreads);
   if (with_hist && (workspace == nullptr || workspace_bytes < CKV_DEVIATION_SELECT_WORKSPACE_BYTES ||
                     (uintptr_t)workspace % 16))
     return CKV_ERR_INVALID_ARGUMENT;
   hipStream_t st = (hipStream_t)stream;
   uint32_t* hist = with_hist ? (uint32_t*)workspace : nullptr;
+  int32_t* zero = spread ? counts + CKV_COUNT_UNCOMPUTED : nullptr;
   if (n_tokens > 0) {
     const DevArgs args = deviation_args(k_fresh, kf_head_stride, kf_token_stride, v_fresh, vf_head_stride,
                                         vf_token_stride, k_cache, v_cache, cache_head_stride, pos_flags, local,
                                         n_tokens, n_fresh, n_heads, head_dim, dtype, err);
     if (dtype == CKV_DTYPE_BF16) {
-      if (with_hist) launch_deviation<CKV_DTYPE_BF16, true>(args, diff, norm, hist, st);
+      if (with_hist) launch_deviation<CKV_DTYPE_BF16, true>(args, diff, norm, hist, st, zero);
       else launch_deviation<CKV_DTYPE_BF16, false>(args, diff, norm, nullptr, st);
     } else {
-      if (with_hist) launch_deviation<CKV_DTYPE_F32, true>(args, diff, norm, hist, st);
+      if (with_hist) launch_deviation<CKV_DTYPE_F32, true>(args, diff, norm, hist, st, zero);
       else launch_deviation<CKV_DTYPE_F32, false>(args, diff, norm, nullptr, st);
     }
     CKV_RETURN_IF_LAUNCH_FAILED();
@@ -172,5 +182,6 @@ extern "C" int32_t ckv_deviation_select(
   const SelectArgs sel{diff,     norm,     pos_flags, local,      (int)n_tokens, chunks,   (int)n_chunks,
                        (int)(has_threshold != 0), escalate_threshold, keep_abs, keep_local, keep_rank, rel_dev,
                        escalated, counts};
+  if (spread) return select_slices_launch(sel, hist, nullptr, err, st);
   return select_launch(sel, hist, st);
 }

@@ -82,14 +82,20 @@ __device__ __forceinline__ void deviation_wave(const DevArgs& a, int p_base, flo
     E::unpack(v16, vx);
     E::unpack(kc16, kcx);
     E::unpack(vc16, vcx);
+    // the differences rounded to the element type two at a time (NaN payloads unspecified: a NaN
+    // total is canonicalized below)
+    float dk[VEC], dv[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; e += 2) {
+      const float ck0 = cached[t] ? kcx[e] : 0.0f, ck1 = cached[t] ? kcx[e + 1] : 0.0f;  // rows outside
+      const float cv0 = cached[t] ? vcx[e] : 0.0f, cv1 = cached[t] ? vcx[e + 1] : 0.0f;  // every placement: 0
+      E::round_trip2(kx[e] - ck0, kx[e + 1] - ck1, dk[e], dk[e + 1]);
+      E::round_trip2(vx[e] - cv0, vx[e + 1] - cv1, dv[e], dv[e + 1]);
+    }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float ck = cached[t] ? kcx[e] : 0.0f;  // rows outside every placement are zero
-      const float cv = cached[t] ? vcx[e] : 0.0f;
-      const float dk = E::round_trip(kx[e] - ck);
-      const float dv = E::round_trip(vx[e] - cv);
-      sk[t] = sk[t] + dk * dk;
-      sv[t] = sv[t] + dv * dv;
+      sk[t] = sk[t] + dk[e] * dk[e];
+      sv[t] = sv[t] + dv[e] * dv[e];
       nk[t] = nk[t] + kx[e] * kx[e];
       nv[t] = nv[t] + vx[e] * vx[e];
     }
@@ -148,8 +154,8 @@ __device__ __forceinline__ void deviation_wave(const DevArgs& a, int p_base, flo
     const float y = wave_butterfly_sum(sv[t]);
     const float z = wave_butterfly_sum(nk[t]);
     const float w = wave_butterfly_sum(nv[t]);
-    diff[t] = jj[t] < 0 ? 0.0f : x + y;
-    norm[t] = jj[t] < 0 ? 0.0f : z + w;
+    diff[t] = jj[t] < 0 ? 0.0f : canonical_nan(x + y);
+    norm[t] = jj[t] < 0 ? 0.0f : canonical_nan(z + w);
   }
 }
 

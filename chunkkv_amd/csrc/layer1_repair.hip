@@ -35,6 +35,8 @@
 
 #include "ckv_common.hpp"
 #include "launch.hpp"
+#include "scatter_common.hpp"
+#include "select_slices.hpp"
 
 namespace ckv {
 
@@ -43,7 +45,10 @@ constexpr int kL1Waves = kL1Threads / kWave;
 // Positions per wavefront. One: in the 8k request step 0.262 ms against 0.264 ms with two and
 // 0.266 ms with four (more wavefronts, each with fewer loads in flight, overlap the pass's
 // dependent load chain better).
-constexpr int kL1T = 1;
+#ifndef CKV_L1_T
+#define CKV_L1_T 1
+#endif
+constexpr int kL1T = CKV_L1_T;
 constexpr int kL1MaxSegs = 64 * 60;  // segment search: 64 samples, then a window of stride + T
 
 // per-position class bits
@@ -69,6 +74,7 @@ struct L1Args {
   float* diff;
   float* norm;
   uint32_t* hist;  // NULL: no histogram (the selection runs its full passes)
+  int32_t* zero_word;  // NULL, or a word the launch sets to 0 (a count the next launch adds to)
   int32_t* err;
 };
 
@@ -96,7 +102,8 @@ struct WaveRows {
 // Loads the rows of positions pb .. pb + T - 1 (this wavefront's), re-rotates the cached keys and
 // computes the deviations. cls gets kCValid / kCCached / kCNoLocal; diff and norm are 0 at
 // positions without a fresh row.
-template <int DTYPE, int T>
+// FULL: every lane holds a vector of every row (n_heads x 16-byte vectors per row == 64).
+template <int DTYPE, int T, bool FULL>
 __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, int pb, WaveRows<DTYPE, T>& r,
                                           uint32_t (&cls)[T], float (&dv)[T], float (&nv)[T], int (&li)[T]) {
   using E = Elem<DTYPE>;
@@ -104,7 +111,7 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
   const int lane = (int)(threadIdx.x & (kWave - 1));
   const int vpr = 1 << a.vpr_log2;
   const int64_t rowb = (int64_t)vpr * 16;
-  const bool lane_on = lane < (a.n_heads << a.vpr_log2);
+  const bool lane_on = FULL || lane < (a.n_heads << a.vpr_log2);
   const int h = lane >> a.vpr_log2, col = lane & (vpr - 1);
   const int64_t colb = (int64_t)col * 16;
   const int N = a.n_tokens;
@@ -148,7 +155,7 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
 
   // 3. the fresh rows: lanes past the rows and positions without a fresh row load a valid row
   // and drop it where it is used
-  const int hc = min(h, a.n_heads - 1);
+  const int hc = FULL ? h : min(h, a.n_heads - 1);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int p = pb + t;
@@ -224,9 +231,13 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     sv[t] = cs.y;
   }
 
-  // 6. re-rotate the cached keys: the partner half comes from lane l ^ (vpr / 2)
+  // 6. re-rotate the cached keys: the partner half comes from lane l ^ (vpr / 2). With u the
+  // lane's own elements and w its partner's (same frequencies, other half), both halves are
+  // y = fl(u c) + fl(w s'), s' = -s in the first half: the first half's x1 c - x2 s and the second
+  // half's x1 s + x2 c with the same roundings (negation is exact, addition commutes), with no
+  // per-lane branch; every cos/sin is fetched before the products use them.
   const int half_v = vpr >> 1;
-  const bool first_half = col < half_v;
+  const uint32_t sgn = col < half_v ? 0x80000000u : 0u;
   const int f0 = (col & (half_v - 1)) * VEC;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -237,23 +248,27 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     other.y = __shfl_xor(mine.y, half_v);
     other.z = __shfl_xor(mine.z, half_v);
     other.w = __shfl_xor(mine.w, half_v);
-    float x1[VEC], x2[VEC], y[VEC];
-    E::unpack(first_half ? mine : other, x1);
-    E::unpack(first_half ? other : mine, x2);
+    float c[VEC], s[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float c = __shfl(cv[t], f0 + e), s = __shfl(sv[t], f0 + e);
-      const float p1 = x1[e] * c;
-      const float p2 = x2[e] * s;
-      const float p3 = x1[e] * s;
-      const float p4 = x2[e] * c;
-      y[e] = first_half ? p1 - p2 : p3 + p4;
+      c[e] = __shfl(cv[t], f0 + e);
+      s[e] = __uint_as_float(__float_as_uint(__shfl(sv[t], f0 + e)) ^ sgn);
+    }
+    float u[VEC], w[VEC], y[VEC];
+    E::unpack(mine, u);
+    E::unpack(other, w);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float p1 = u[e] * c[e];
+      const float p2 = w[e] * s[e];
+      y[e] = p1 + p2;
     }
     if (lane_on) r.kc[t] = E::pack(y);
   }
 
   // 7. deviations in the contract's order: lane q adds its vector's elements in ascending order,
-  // then the xor butterfly; diff = Sk + Sv, norm = Nk + Nv
+  // then the xor butterfly; diff = Sk + Sv, norm = Nk + Nv. The differences are rounded to the
+  // element type two at a time (NaN payloads unspecified), so a NaN result is canonicalized.
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     float kx[VEC], vx[VEC], kcx[VEC], vcx[VEC];
@@ -262,13 +277,17 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     E::unpack(lane_on ? r.vf[t] : zero, vx);
     E::unpack(lane_on ? r.kc[t] : zero, kcx);
     E::unpack(lane_on ? r.vc[t] : zero, vcx);
+    float dk[VEC], dw[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; e += 2) {
+      E::round_trip2(kx[e] - kcx[e], kx[e + 1] - kcx[e + 1], dk[e], dk[e + 1]);
+      E::round_trip2(vx[e] - vcx[e], vx[e + 1] - vcx[e + 1], dw[e], dw[e + 1]);
+    }
     float sk = 0.0f, sv = 0.0f, nk = 0.0f, nw = 0.0f;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float dk = E::round_trip(kx[e] - kcx[e]);
-      const float dw = E::round_trip(vx[e] - vcx[e]);
-      sk = sk + dk * dk;
-      sv = sv + dw * dw;
+      sk = sk + dk[e] * dk[e];
+      sv = sv + dw[e] * dw[e];
       nk = nk + kx[e] * kx[e];
       nw = nw + vx[e] * vx[e];
     }
@@ -276,8 +295,8 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
     const float y = wave_butterfly_sum(sv);
     const float z = wave_butterfly_sum(nk);
     const float w = wave_butterfly_sum(nw);
-    dv[t] = li[t] < 0 ? 0.0f : x + y;
-    nv[t] = li[t] < 0 ? 0.0f : z + w;
+    dv[t] = li[t] < 0 ? 0.0f : canonical_nan(x + y);
+    nv[t] = li[t] < 0 ? 0.0f : canonical_nan(z + w);
   }
 }
 
@@ -289,7 +308,7 @@ __device__ __forceinline__ void wave_rows(const L1Args& a, const InvFreq& inv, i
 // The pointers and sizes the first loads use lead the argument list: the library preloads the
 // first 16 argument dwords into SGPRs, but only up to the first argument passed by reference
 // (the L1Args struct), and every other argument takes a scalar load at wave start.
-template <int DTYPE, int T>
+template <int DTYPE, int T, bool FULL>
 __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
     const uint8_t* flags, const int32_t* local, const ckv_segment* segs, const uint64_t* tab, int n_tokens, int n_segs,
     const char* kf, const char* vf, L1Args a, const InvFreq inv) {
@@ -311,11 +330,11 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
   uint32_t cls[T];
   float dv[T], nv[T];
   int li[T];
-  wave_rows<DTYPE, T>(a, inv, pb, r, cls, dv, nv, li);
+  wave_rows<DTYPE, T, FULL>(a, inv, pb, r, cls, dv, nv, li);
 
   const int vpr = 1 << a.vpr_log2;
   const int64_t rowb = (int64_t)vpr * 16;
-  const bool lane_on = lane < (a.n_heads << a.vpr_log2);
+  const bool lane_on = FULL || lane < (a.n_heads << a.vpr_log2);
   const int64_t hoff = (int64_t)(lane >> a.vpr_log2) * a.d_hs_b + (int64_t)(lane & (vpr - 1)) * 16;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
@@ -338,6 +357,7 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
       s_bin[wave * T + t] = cand ? top_bin(dev_key(dv[t])) : ~0u;
     }
   }
+  if (a.zero_word != nullptr && blockIdx.x == 0 && tid == 0) *a.zero_word = 0;
   if (a.hist == nullptr) return;  // uniform
   __syncthreads();
   if (wave == 0) {
@@ -356,7 +376,21 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
 
 }  // namespace ckv
 
-extern "C" int32_t ckv_layer1_repair(
+namespace ckv {
+
+#ifndef CKV_L1_GATHER_SPREAD_MIN
+#define CKV_L1_GATHER_SPREAD_MIN 0
+#endif
+// The dropped-row gather that ckv_layer1_repair_gather carries in its last launch: the K/V slabs
+// (layer l's cache at l * layer_stride elements), the layers and the segments' longest run.
+struct GatherTail {
+  void* k_slab;
+  void* v_slab;
+  int64_t layer_stride;
+  int32_t begin, end, max_seg_tokens;
+};
+
+static int32_t layer1_repair_impl(
     void* dst_k, void* dst_v, int64_t dst_head_stride, const uint64_t* src_tab, int32_t n_tab_chunks,
     int32_t n_layers, int32_t layer, const ckv_segment* segs, int32_t n_segs, const void* k_fresh,
     int64_t kf_head_stride, int64_t kf_token_stride, const void* v_fresh, int64_t vf_head_stride,
@@ -364,8 +398,7 @@ extern "C" int32_t ckv_layer1_repair(
     int32_t n_heads, int32_t head_dim, int32_t dtype, double theta, const ckv_chunk_span* chunks, int32_t n_chunks,
     int32_t has_threshold, double escalate_threshold, float* diff, float* norm, int64_t* keep_abs,
     int64_t* keep_local, int32_t* keep_rank, float* rel_dev, uint8_t* escalated, int32_t* counts, void* workspace,
-    int64_t workspace_bytes, int32_t* err, void* stream) {
-  using namespace ckv;
+    int64_t workspace_bytes, int32_t* err, void* stream, const GatherTail* tail) {
   if (dtype != CKV_DTYPE_BF16 && dtype != CKV_DTYPE_F32) return CKV_ERR_INVALID_ARGUMENT;
   const int eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
   if (n_heads <= 0 || head_dim <= 0 || n_tokens < 0 || n_fresh < 0 || n_segs < 0 || n_chunks < 0 ||
@@ -394,10 +427,19 @@ extern "C" int32_t ckv_layer1_repair(
   hipStream_t st = (hipStream_t)stream;
   const SelectArgs sel{diff, norm, pos_flags, local, (int)n_tokens, chunks, (int)n_chunks, (int)(has_threshold != 0),
                        escalate_threshold, keep_abs, keep_local, keep_rank, rel_dev, escalated, counts};
+  if (tail != nullptr && (keep_rank == nullptr || tail->begin < 0 || tail->end < tail->begin || tail->end > n_layers ||
+                          tail->max_seg_tokens < 0 || (tail->begin < tail->end && (layer >= tail->begin &&
+                                                                                  layer < tail->end))))
+    return CKV_ERR_INVALID_ARGUMENT;
   if (n_tokens == 0) return select_launch(sel, nullptr, st);  // nothing to repair: counts and span stats
 
-  // the register-resident selection takes the histogram; above it, the L2 form counts itself
-  uint32_t* hist = n_tokens <= kSelRegMax * kSelThreads ? (uint32_t*)workspace : nullptr;
+  // Without a threshold the selection and the kept rows' scatter are one launch of many
+  // workgroups (select_slices.hpp) started from the histogram; with one, the single-workgroup
+  // selection (the register-resident form takes the histogram; above it, the L2 form counts
+  // itself) and the scatter.
+  const bool spread = has_threshold == 0 && select_slices_fits(n_tokens) &&
+                      (tail == nullptr || n_tokens >= CKV_L1_GATHER_SPREAD_MIN);
+  uint32_t* hist = spread || n_tokens <= kSelRegMax * kSelThreads ? (uint32_t*)workspace : nullptr;
   L1Args args{};
   args.dk = (char*)dst_k;
   args.dv = (char*)dst_v;
@@ -427,19 +469,48 @@ extern "C" int32_t ckv_layer1_repair(
   args.diff = diff;
   args.norm = norm;
   args.hist = hist;
+  args.zero_word = spread ? counts + CKV_COUNT_UNCOMPUTED : nullptr;
   args.err = err;
   const InvFreq& inv = host_inv_freq(head_dim, theta);
   constexpr int P = kL1Waves * kL1T;
   const unsigned blocks = (unsigned)((n_tokens + P - 1) / P);
-  if (dtype == CKV_DTYPE_BF16)
-    hipLaunchKernelGGL((layer1_gather_deviation_kernel<CKV_DTYPE_BF16, kL1T>), dim3(blocks), dim3(kL1Threads), 0, st,
-                       args.flags, args.local, args.segs, args.tab, args.n_tokens, args.n_segs, args.kf, args.vf, args,
-                       inv);
-  else
-    hipLaunchKernelGGL((layer1_gather_deviation_kernel<CKV_DTYPE_F32, kL1T>), dim3(blocks), dim3(kL1Threads), 0, st,
-                       args.flags, args.local, args.segs, args.tab, args.n_tokens, args.n_segs, args.kf, args.vf, args,
-                       inv);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kL1Threads), 0, st, args.flags, args.local, args.segs, args.tab,
+                       args.n_tokens, args.n_segs, args.kf, args.vf, args, inv);
+  };
+  const bool full = (int64_t)n_heads * vpr == kWave;  // every lane holds a vector of every row
+  if (dtype == CKV_DTYPE_BF16) {
+    if (full) go(layer1_gather_deviation_kernel<CKV_DTYPE_BF16, kL1T, true>);
+    else go(layer1_gather_deviation_kernel<CKV_DTYPE_BF16, kL1T, false>);
+  } else {
+    if (full) go(layer1_gather_deviation_kernel<CKV_DTYPE_F32, kL1T, true>);
+    else go(layer1_gather_deviation_kernel<CKV_DTYPE_F32, kL1T, false>);
+  }
   CKV_RETURN_IF_LAUNCH_FAILED();
+  if (tail != nullptr) {
+    // the selection, then one launch: the kept rows of this layer beside the gather of the
+    // dropped rows of layers [begin, end) (keep_rank >= 0 marks the kept positions)
+    const int32_t rc = spread ? select_slices_launch(sel, hist, nullptr, err, st) : select_launch(sel, hist, st);
+    if (rc != CKV_OK) return rc;
+    const RowScatter kept{(char*)dst_k,   (char*)dst_v,   dst_head_stride * eb,      args.kf,
+                          args.kf_hs_b,   args.kf_ts_b,   args.vf,                   args.vf_hs_b,
+                          args.vf_ts_b,   keep_abs,       keep_local,                counts + CKV_COUNT_KEEP,
+                          (int)n_tokens,  (int)n_fresh,   (int)n_tokens,             (int)n_heads,
+                          vpr,            (int64_t)rowb};
+    return gather_layers_launch(tail->k_slab, tail->v_slab, tail->layer_stride, dst_head_stride,
+                                n_segs > 0 ? src_tab : (const uint64_t*)workspace, n_tab_chunks, n_layers, tail->begin,
+                                tail->end, n_segs > 0 ? segs : (const ckv_segment*)workspace, n_segs,
+                                tail->max_seg_tokens, keep_rank, n_heads, n_tokens, head_dim, dtype, theta, err,
+                                stream, &kept);
+  }
+  if (spread) {
+    // with no fresh rows no source row is in range (a kept row then flags the range error)
+    const SliceRows rows{(char*)dst_k,          (char*)dst_v,        dst_head_stride * eb,
+                         (const char*)args.kf, args.kf_hs_b,        args.kf_ts_b,
+                         (const char*)args.vf, args.vf_hs_b,        args.vf_ts_b,
+                         (int)n_fresh,         (int)n_heads,        vpr};
+    return select_slices_launch(sel, hist, &rows, err, st);
+  }
   int32_t rc = select_launch(sel, hist, st);
   if (rc != CKV_OK) return rc;
   // the kept rows from the fresh rows: K[keep_abs[j]] = k[keep_local[j]], j < counts[KEEP]. With
@@ -448,4 +519,48 @@ extern "C" int32_t ckv_layer1_repair(
   return scatter_launch(dst_k, dst_v, dst_head_stride, fresh ? k_fresh : workspace, kf_head_stride, kf_token_stride,
                         fresh ? v_fresh : workspace, vf_head_stride, vf_token_stride, keep_abs, keep_local, n_tokens,
                         n_fresh, n_tokens, n_heads, head_dim, dtype, counts + CKV_COUNT_KEEP, err, stream);
+}
+
+}  // namespace ckv
+
+extern "C" int32_t ckv_layer1_repair(
+    void* dst_k, void* dst_v, int64_t dst_head_stride, const uint64_t* src_tab, int32_t n_tab_chunks,
+    int32_t n_layers, int32_t layer, const ckv_segment* segs, int32_t n_segs, const void* k_fresh,
+    int64_t kf_head_stride, int64_t kf_token_stride, const void* v_fresh, int64_t vf_head_stride,
+    int64_t vf_token_stride, int32_t n_fresh, const uint8_t* pos_flags, const int32_t* local, int32_t n_tokens,
+    int32_t n_heads, int32_t head_dim, int32_t dtype, double theta, const ckv_chunk_span* chunks, int32_t n_chunks,
+    int32_t has_threshold, double escalate_threshold, float* diff, float* norm, int64_t* keep_abs,
+    int64_t* keep_local, int32_t* keep_rank, float* rel_dev, uint8_t* escalated, int32_t* counts, void* workspace,
+    int64_t workspace_bytes, int32_t* err, void* stream) {
+  return ckv::layer1_repair_impl(dst_k, dst_v, dst_head_stride, src_tab, n_tab_chunks, n_layers, layer, segs, n_segs,
+                                 k_fresh, kf_head_stride, kf_token_stride, v_fresh, vf_head_stride, vf_token_stride,
+                                 n_fresh, pos_flags, local, n_tokens, n_heads, head_dim, dtype, theta, chunks, n_chunks,
+                                 has_threshold, escalate_threshold, diff, norm, keep_abs, keep_local, keep_rank,
+                                 rel_dev, escalated, counts, workspace, workspace_bytes, err, stream, nullptr);
+}
+
+extern "C" int32_t ckv_layer1_repair_gather(
+    void* k_slab, void* v_slab, int64_t layer_stride, int64_t head_stride, const uint64_t* src_tab,
+    int32_t n_tab_chunks, int32_t n_layers, int32_t layer, int32_t gather_begin, int32_t gather_end,
+    const ckv_segment* segs, int32_t n_segs, int32_t max_seg_tokens, const void* k_fresh, int64_t kf_head_stride,
+    int64_t kf_token_stride, const void* v_fresh, int64_t vf_head_stride, int64_t vf_token_stride, int32_t n_fresh,
+    const uint8_t* pos_flags, const int32_t* local, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
+    int32_t dtype, double theta, const ckv_chunk_span* chunks, int32_t n_chunks, int32_t has_threshold,
+    double escalate_threshold, float* diff, float* norm, int64_t* keep_abs, int64_t* keep_local, int32_t* keep_rank,
+    float* rel_dev, uint8_t* escalated, int32_t* counts, void* workspace, int64_t workspace_bytes, int32_t* err,
+    void* stream) {
+  using namespace ckv;
+  if (k_slab == nullptr || v_slab == nullptr || n_layers <= 0 || layer < 0 || layer >= n_layers || head_dim <= 0 ||
+      n_heads <= 0 || (dtype != CKV_DTYPE_BF16 && dtype != CKV_DTYPE_F32))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (layer_stride < head_stride * n_heads) return CKV_ERR_OUT_OF_RANGE;
+  const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
+  const GatherTail tail{k_slab, v_slab, layer_stride, gather_begin, gather_end, max_seg_tokens};
+  char* dk = (char*)k_slab + (int64_t)layer * layer_stride * eb;
+  char* dv = (char*)v_slab + (int64_t)layer * layer_stride * eb;
+  return layer1_repair_impl(dk, dv, head_stride, src_tab, n_tab_chunks, n_layers, layer, segs, n_segs, k_fresh,
+                            kf_head_stride, kf_token_stride, v_fresh, vf_head_stride, vf_token_stride, n_fresh,
+                            pos_flags, local, n_tokens, n_heads, head_dim, dtype, theta, chunks, n_chunks, has_threshold,
+                            escalate_threshold, diff, norm, keep_abs, keep_local, keep_rank, rel_dev, escalated,
+                            counts, workspace, workspace_bytes, err, stream, &tail);
 }

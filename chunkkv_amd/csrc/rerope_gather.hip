@@ -24,7 +24,11 @@
 // byte. Products and sums are separately rounded fp32 operations (built with -ffp-contract=off),
 // like the reference's separate torch kernels, so every output is reproducible bit-for-bit on
 // any IEEE host from the same table.
+#include <algorithm>
+
 #include "ckv_common.hpp"
+#include "launch.hpp"
+#include "scatter_common.hpp"
 
 namespace ckv {
 
@@ -69,14 +73,32 @@ __device__ __forceinline__ void gather_st(void* p, const vec16& v) {
   else st16(p, v);
 }
 
-// Grid: (tile, segment) in the order of S (x fastest), z = layer.
-template <int DTYPE, int D, class S>
+// Grid: (tile, segment) in the order of S (x fastest), z = layer. With ROWS, the first scat_z
+// z-slices scatter rows (another layer's kept rows, rs) instead, items grid-stride over them:
+// dispatched first, they run beside the gather's first tiles.
+template <int DTYPE, int D, class S, bool ROWS>
 __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
     char* __restrict__ dst_k, char* __restrict__ dst_v, int64_t dst_layer_stride_b,
     int64_t dst_head_stride_b, const uint64_t* __restrict__ src_tab, int n_chunks,
     const ckv_segment* __restrict__ segs, ckv_segment one_seg, uint64_t one_src_k,
     uint64_t one_src_v, int64_t one_src_head_stride_b, int n_layers, int layer_begin, int n_heads,
-    int n_tokens, const int32_t* __restrict__ skip, const InvFreq inv, int32_t* __restrict__ err) {
+    int n_tokens, const int32_t* __restrict__ skip, const InvFreq inv, int32_t* __restrict__ err,
+    const RowScatter rs, int scat_z) {
+  int zl = (int)blockIdx.z;
+  if constexpr (ROWS) {
+    if (zl < scat_z) {  // uniform: a scatter block
+      const int64_t per_z = (int64_t)gridDim.x * gridDim.y;
+      const int64_t stride = (int64_t)scat_z * per_z * S::kThreads;
+      int n_rows = rs.n_rows;
+      if (rs.n_rows_dev != nullptr) n_rows = min(n_rows, max(0, *rs.n_rows_dev));
+      const int64_t total = (int64_t)n_rows * rs.n_heads * rs.vecs_per_row;
+      for (int64_t g = (((int64_t)zl * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * S::kThreads + threadIdx.x;
+           g < total; g += stride)
+        scatter_items<1>(rs, g, 0, err);
+      return;
+    }
+    zl -= scat_z;
+  }
   using E = Elem<DTYPE>;
   constexpr int VEC = E::kVec;
   constexpr int HALF = D / 2;
@@ -109,7 +131,7 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
     gi32* f = (gi32*)(segs + (S::kSegFastest ? blockIdx.x : blockIdx.y));
     s = ckv_segment{f[0], f[1], f[2], f[3], f[4], f[5]};
   }
-  const int layer = layer_begin + (int)blockIdx.z;
+  const int layer = layer_begin + zl;
   const int t0 = (int)(S::kSegFastest ? blockIdx.y : blockIdx.x) * kGatherTile;
   if (t0 >= s.n_tokens) return;  // uniform: tile past this segment's end
   if (s.dst_start < 0 || s.src_start < 0 || s.chunk < 0 || s.chunk >= n_chunks ||
@@ -245,15 +267,27 @@ static void launch_gather(char* dk, char* dv, int64_t ls_b, int64_t hs_b, const 
                           int n_chunks, const ckv_segment* segs, ckv_segment one, uint64_t one_k, uint64_t one_v,
                           int64_t one_hs_b, int n_segs, int max_seg_tokens, int n_layers, int layer_begin,
                           int layer_count, int n_heads, int n_tokens, const int32_t* skip, double theta,
-                          int32_t* err, hipStream_t st) {
+                          int32_t* err, hipStream_t st, const RowScatter* rs) {
   auto go = [&](auto shape) {
     using S = decltype(shape);
     const unsigned tiles = (unsigned)((max_seg_tokens + S::kTile - 1) / S::kTile);
-    const dim3 grid = S::kSegFastest ? dim3((unsigned)n_segs, tiles, (unsigned)layer_count)
-                                     : dim3(tiles, (unsigned)n_segs, (unsigned)layer_count);
-    hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D, S>), grid, dim3(S::kThreads), 0, st, dk, dv, ls_b, hs_b, tab,
-                       n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, layer_begin, n_heads, n_tokens, skip,
-                       host_inv_freq(D, theta), err);
+    // scatter z-slices: about two items per thread for the most rows the scatter can have
+    int scat_z = 0;
+    if (rs != nullptr) {
+      const int64_t per_z = (int64_t)tiles * n_segs * S::kThreads;
+      const int64_t items = (int64_t)rs->n_rows * rs->n_heads * rs->vecs_per_row;
+      scat_z = (int)std::min<int64_t>(std::max<int64_t>(1, (items + 2 * per_z - 1) / (2 * per_z)), 1024);
+    }
+    const unsigned zs = (unsigned)(layer_count + scat_z);
+    const dim3 grid = S::kSegFastest ? dim3((unsigned)n_segs, tiles, zs) : dim3(tiles, (unsigned)n_segs, zs);
+    if (rs != nullptr)
+      hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D, S, true>), grid, dim3(S::kThreads), 0, st, dk, dv, ls_b, hs_b,
+                         tab, n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, layer_begin, n_heads, n_tokens,
+                         skip, host_inv_freq(D, theta), err, *rs, scat_z);
+    else
+      hipLaunchKernelGGL((rerope_gather_kernel<DTYPE, D, S, false>), grid, dim3(S::kThreads), 0, st, dk, dv, ls_b,
+                         hs_b, tab, n_chunks, segs, one, one_k, one_v, one_hs_b, n_layers, layer_begin, n_heads,
+                         n_tokens, skip, host_inv_freq(D, theta), err, RowScatter{}, 0);
   };
   if (n_segs >= kGatherWideSegs) go(GatherWide{});
   else if (skip != nullptr) go(GatherSkip{});
@@ -262,7 +296,7 @@ static void launch_gather(char* dk, char* dv, int64_t ls_b, int64_t hs_b, const 
 
 using GatherFn = void (*)(char*, char*, int64_t, int64_t, const uint64_t*, int, const ckv_segment*,
                           ckv_segment, uint64_t, uint64_t, int64_t, int, int, int, int, int, int, int,
-                          const int32_t*, double, int32_t*, hipStream_t);
+                          const int32_t*, double, int32_t*, hipStream_t, const RowScatter*);
 
 static GatherFn pick_gather(int dtype, int head_dim) {
 #define CKV_CASE(DT, HD) \
@@ -291,14 +325,13 @@ extern "C" int32_t ckv_inv_freq(float* out, int32_t head_dim, double theta, void
   return CKV_OK;
 }
 
-extern "C" int32_t ckv_rerope_gather_layers(void* dst_k, void* dst_v, int64_t dst_layer_stride,
-                                            int64_t dst_head_stride, const uint64_t* src_tab,
-                                            int32_t n_chunks, int32_t n_layers, int32_t layer_begin,
-                                            int32_t layer_end, const ckv_segment* segs, int32_t n_segs,
-                                            int32_t max_seg_tokens, const int32_t* skip, int32_t n_heads,
-                                            int32_t n_tokens, int32_t head_dim, int32_t dtype, double theta,
-                                            int32_t* err, void* stream) {
-  using namespace ckv;
+namespace ckv {
+
+int32_t gather_layers_launch(void* dst_k, void* dst_v, int64_t dst_layer_stride, int64_t dst_head_stride,
+                             const uint64_t* src_tab, int32_t n_chunks, int32_t n_layers, int32_t layer_begin,
+                             int32_t layer_end, const ckv_segment* segs, int32_t n_segs, int32_t max_seg_tokens,
+                             const int32_t* skip, int32_t n_heads, int32_t n_tokens, int32_t head_dim, int32_t dtype,
+                             double theta, int32_t* err, void* stream, const RowScatter* rows) {
   GatherFn fn = pick_gather(dtype, head_dim);
   if (fn == nullptr || dst_k == nullptr || dst_v == nullptr || src_tab == nullptr || segs == nullptr)
     return CKV_ERR_INVALID_ARGUMENT;
@@ -307,15 +340,35 @@ extern "C" int32_t ckv_rerope_gather_layers(void* dst_k, void* dst_v, int64_t ds
     return CKV_ERR_INVALID_ARGUMENT;
   if (dst_head_stride < (int64_t)n_tokens * head_dim || dst_layer_stride < dst_head_stride * n_heads)
     return CKV_ERR_OUT_OF_RANGE;
-  if (n_segs == 0 || max_seg_tokens == 0 || layer_end == layer_begin) return CKV_OK;
+  if (n_segs == 0 || max_seg_tokens == 0 || layer_end == layer_begin) {
+    if (rows == nullptr || rows->n_rows == 0) return CKV_OK;
+    // nothing to gather: the rows alone, one tile of one segment per z-slice
+    max_seg_tokens = 1;
+    n_segs = 1;
+    layer_end = layer_begin;
+  }
   // grid y (tiles of the segment-fastest shape, segments below kGatherWideSegs) and z (layers)
-  if ((max_seg_tokens + 15) / 16 > 65535 || layer_end - layer_begin > 65535) return CKV_ERR_TOO_LARGE;
+  if ((max_seg_tokens + 15) / 16 > 65535 || layer_end - layer_begin > 64000) return CKV_ERR_TOO_LARGE;
   const int64_t eb = elem_bytes(dtype);
   fn((char*)dst_k, (char*)dst_v, dst_layer_stride * eb, dst_head_stride * eb, src_tab, n_chunks, segs, ckv_segment{},
      0, 0, 0, n_segs, max_seg_tokens, n_layers, layer_begin, layer_end - layer_begin, n_heads, n_tokens, skip, theta, err,
-     (hipStream_t)stream);
+     (hipStream_t)stream, rows);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
+}
+
+}  // namespace ckv
+
+extern "C" int32_t ckv_rerope_gather_layers(void* dst_k, void* dst_v, int64_t dst_layer_stride,
+                                            int64_t dst_head_stride, const uint64_t* src_tab,
+                                            int32_t n_chunks, int32_t n_layers, int32_t layer_begin,
+                                            int32_t layer_end, const ckv_segment* segs, int32_t n_segs,
+                                            int32_t max_seg_tokens, const int32_t* skip, int32_t n_heads,
+                                            int32_t n_tokens, int32_t head_dim, int32_t dtype, double theta,
+                                            int32_t* err, void* stream) {
+  return ckv::gather_layers_launch(dst_k, dst_v, dst_layer_stride, dst_head_stride, src_tab, n_chunks, n_layers,
+                                   layer_begin, layer_end, segs, n_segs, max_seg_tokens, skip, n_heads, n_tokens,
+                                   head_dim, dtype, theta, err, stream, nullptr);
 }
 
 extern "C" int32_t ckv_rerope_gather(void* dst_k, void* dst_v, int64_t dst_layer_stride,
@@ -343,7 +396,7 @@ extern "C" int32_t ckv_shift_keys(void* dst, int64_t dst_head_stride, const void
   const int64_t eb = elem_bytes(dtype);
   ckv_segment one{0, n_rows, 0, 0, n_rows, delta};
   fn((char*)dst, nullptr, 0, dst_head_stride * eb, nullptr, 1, nullptr, one, (uint64_t)(uintptr_t)src, 0,
-     src_head_stride * eb, 1, n_rows, 1, 0, 1, n_heads, n_rows, nullptr, theta, nullptr, (hipStream_t)stream);
+     src_head_stride * eb, 1, n_rows, 1, 0, 1, n_heads, n_rows, nullptr, theta, nullptr, (hipStream_t)stream, nullptr);
   CKV_RETURN_IF_LAUNCH_FAILED();
   return CKV_OK;
 }

@@ -185,10 +185,16 @@ __global__ __launch_bounds__(kRopeThreads) void rope_wave_kernel(
 constexpr int kKvLoop = 0, kKvOne = 1, kKvFull = 2;
 constexpr int kRowToken = 0, kRowPos = 1, kRowIndexed = 2;
 
+#ifndef CKV_KV_TPW
+#define CKV_KV_TPW 1
+#endif
+constexpr int kKvTpw = CKV_KV_TPW;  // tokens per wavefront of the k/v write
+
 // The arguments come in the order a wavefront needs them: the first 64 bytes (what the token
 // count check and the first loads use) fit the 16 SGPRs the library preloads, the frequency table
-// comes last.
-template <int DTYPE, int D, int SHAPE, int RM>
+// comes last. TPW tokens per wavefront (TPW > 1 only with SHAPE != kKvLoop): every token's loads
+// go out first, then the positions, then each lane evaluates its frequency for every token.
+template <int DTYPE, int D, int SHAPE, int RM, int TPW>
 __global__ __launch_bounds__(kRopeKvThreads) void rope_kv_kernel(
     int n, int n_kv_heads, const int64_t* __restrict__ pos, const char* __restrict__ k_in,
     const char* __restrict__ v_in, int64_t ki_hs_b, int64_t ki_ts_b, int64_t vi_hs_b, int64_t vi_ts_b,
@@ -200,66 +206,87 @@ __global__ __launch_bounds__(kRopeKvThreads) void rope_kv_kernel(
   constexpr int TPR = HALF / VEC;  // column pairs per head row (a power of two)
   constexpr int HALF_B = HALF * E::kBytes;
   static_assert(HALF <= kWave && kWave % HALF == 0 && (TPR & (TPR - 1)) == 0, "head_dim out of range");
+  static_assert(TPW == 1 || SHAPE != kKvLoop, "several tokens per wavefront need one item per lane at most");
   const int Hkv = SHAPE == kKvFull ? kWave / 2 / TPR : n_kv_heads;
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = (int)(blockIdx.x * (kRopeKvThreads / kWave) + threadIdx.x / kWave);
-  if (t >= n) return;  // uniform per wavefront
-  const int64_t p = pos[t];
+  const int t0 = (int)(blockIdx.x * (kRopeKvThreads / kWave) + threadIdx.x / kWave) * TPW;
+  if (t0 >= n) return;  // uniform per wavefront
   const int items = 2 * Hkv * TPR;
   const int col = lane & (TPR - 1);
   // item it: head row it / TPR (TPR is a power of two: a shift), k rows first. Base pointer,
   // strides and head index are picked by value, so the k and v lanes share one address path.
-  auto src_of = [&](int hh) {
+  auto src_of = [&](int hh, int t) {
     const bool k = hh < Hkv;
     return (k ? k_in : v_in) + (k ? hh : hh - Hkv) * (k ? ki_hs_b : vi_hs_b) + t * (k ? ki_ts_b : vi_ts_b) + col * 16;
   };
+  // the tokens past n (the last wavefront) load token n - 1 again and store nothing
+  int tt[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) tt[j] = min(t0 + j, n - 1);
   // the first item's data goes out before anything waits on the position load
   const int h0 = (SHAPE == kKvFull ? lane : min(lane, items - 1)) / TPR;
-  const char* s0 = src_of(h0);
-  // non-temporal loads: each input row is read once (the request step 0.258 -> 0.244 ms)
-  vec16 a = ld16_stream(s0), b = ld16_stream(s0 + HALF_B);
-  const int64_t row = RM == kRowToken ? (int64_t)t : RM == kRowPos ? p : rows[t];
-  const bool ok = p >= INT32_MIN && p <= INT32_MAX && row >= 0 && row < n_out;
-  auto dst_of = [&](int hh) {
+  vec16 a[TPW], b[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const char* s0 = src_of(h0, tt[j]);
+    // non-temporal loads: each input row is read once (the request step 0.258 -> 0.244 ms)
+    a[j] = ld16_stream(s0);
+    b[j] = ld16_stream(s0 + HALF_B);
+  }
+  int64_t p[TPW], row[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) p[j] = pos[tt[j]];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) row[j] = RM == kRowToken ? (int64_t)tt[j] : RM == kRowPos ? p[j] : rows[tt[j]];
+  bool ok[TPW];
+  float angs[TPW], cv[TPW], sv[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    ok[j] = p[j] >= INT32_MIN && p[j] <= INT32_MAX && row[j] >= 0 && row[j] < n_out;
+    angs[j] = (float)(ok[j] ? (int)p[j] : 0) * inv.v[lane & (HALF - 1)];
+  }
+  angles_cos_sin<TPW>(angs, cv, sv);
+  auto dst_of = [&](int hh, int64_t r) {
     const bool k = hh < Hkv;
-    return (k ? k_out : v_out) + (k ? hh : hh - Hkv) * (k ? ko_hs_b : vo_hs_b) + row * (k ? ko_ts_b : vo_ts_b) +
+    return (k ? k_out : v_out) + (k ? hh : hh - Hkv) * (k ? ko_hs_b : vo_hs_b) + r * (k ? ko_ts_b : vo_ts_b) +
            col * 16;
   };
-  const float ang = (float)(ok ? (int)p : 0) * inv.v[lane & (HALF - 1)];
-  float cv[1], sv[1];
-  const float angs[1] = {ang};
-  angles_cos_sin<1>(angs, cv, sv);
-  float c[VEC], sn[VEC];
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    c[e] = __shfl(cv[0], col * VEC + e);
-    sn[e] = __shfl(sv[0], col * VEC + e);
-  }
-  if (!ok) {
-    if (lane == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
-    return;
-  }
-  if constexpr (SHAPE != kKvLoop) {  // items <= one wavefront: a single pass, no loop
-    char* d = dst_of(h0);
-    vec16 y1 = a, y2 = b;
-    if (h0 < Hkv) rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
-    if (SHAPE == kKvFull || lane < items) {
-      st16_stream(d, y1);
-      st16_stream(d + HALF_B, y2);
+  for (int j = 0; j < TPW; ++j) {
+    if (j > 0 && t0 + j >= n) break;  // uniform
+    float c[VEC], sn[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      c[e] = __shfl(cv[j], col * VEC + e);
+      sn[e] = __shfl(sv[j], col * VEC + e);
     }
-  } else {
-    for (int it = lane; it < items; it += kWave) {
-      const int hh = it / TPR;
-      if (it != lane) {
-        const char* si = src_of(hh);
-        a = ld16_stream(si);
-        b = ld16_stream(si + HALF_B);
+    if (!ok[j]) {  // uniform
+      if (lane == 0) flag_error(err, CKV_DEVICE_ERR_RANGE);
+      continue;
+    }
+    if constexpr (SHAPE != kKvLoop) {  // items <= one wavefront: a single pass, no loop
+      char* d = dst_of(h0, row[j]);
+      vec16 y1 = a[j], y2 = b[j];
+      if (h0 < Hkv) rotate_pairs<DTYPE>(a[j], b[j], c, sn, y1, y2);
+      if (SHAPE == kKvFull || lane < items) {
+        st16_stream(d, y1);
+        st16_stream(d + HALF_B, y2);
       }
-      char* d = dst_of(hh);
-      vec16 y1 = a, y2 = b;
-      if (hh < Hkv) rotate_pairs<DTYPE>(a, b, c, sn, y1, y2);
-      st16_stream(d, y1);
-      st16_stream(d + HALF_B, y2);
+    } else {
+      vec16 aa = a[0], bb = b[0];
+      for (int it = lane; it < items; it += kWave) {
+        const int hh = it / TPR;
+        if (it != lane) {
+          const char* si = src_of(hh, tt[0]);
+          aa = ld16_stream(si);
+          bb = ld16_stream(si + HALF_B);
+        }
+        char* d = dst_of(hh, row[0]);
+        vec16 y1 = aa, y2 = bb;
+        if (hh < Hkv) rotate_pairs<DTYPE>(aa, bb, c, sn, y1, y2);
+        st16_stream(d, y1);
+        st16_stream(d + HALF_B, y2);
+      }
     }
   }
 }
@@ -449,18 +476,18 @@ static void launch_rope(int n, hipStream_t st, char* qo, int64_t qo_hs, int64_t 
   const InvFreq& inv = host_inv_freq(D, theta);
   if constexpr (D <= 2 * kWave) {
     if (Hq == 0 && vo != nullptr) {
-      const int per_wg = kRopeKvThreads / kWave;
-      const dim3 grid((unsigned)((n + per_wg - 1) / per_wg));
       constexpr int TPR = D / 2 / Elem<DTYPE>::kVec;
       const int items = 2 * Hkv * TPR;
       const int shape = items == kWave ? kKvFull : items < kWave ? kKvOne : kKvLoop;
+      const int per_wg = kRopeKvThreads / kWave * (shape == kKvLoop ? 1 : kKvTpw);
+      const dim3 grid((unsigned)((n + per_wg - 1) / per_wg));
       const int rm = rows == nullptr ? kRowToken : rows == pos ? kRowPos : kRowIndexed;
       auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(kRopeKvThreads), 0, st, n, Hkv, pos, ki, vi, ki_hs, ki_ts, vi_hs, vi_ts, ko,
                            vo, ko_hs, ko_ts, vo_hs, vo_ts, rows, n_out, err, inv);
       };
 #define CKV_KV(S, R) \
-  if (shape == S && rm == R) go(rope_kv_kernel<DTYPE, D, S, R>);
+  if (shape == S && rm == R) go(rope_kv_kernel<DTYPE, D, S, R, S == kKvLoop ? 1 : kKvTpw>);
       CKV_KV(kKvFull, kRowToken) CKV_KV(kKvFull, kRowPos) CKV_KV(kKvFull, kRowIndexed)
       CKV_KV(kKvOne, kRowToken) CKV_KV(kKvOne, kRowPos) CKV_KV(kKvOne, kRowIndexed)
       CKV_KV(kKvLoop, kRowToken) CKV_KV(kKvLoop, kRowPos) CKV_KV(kKvLoop, kRowIndexed)

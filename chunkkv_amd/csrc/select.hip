@@ -5,6 +5,7 @@
 // ckv_deviation_select); requests above 33792 tokens use select_kernel below, which re-reads
 // keys from L2 in every pass.
 #include "launch.hpp"
+#include "select_slices.hpp"
 
 namespace ckv {
 
@@ -233,6 +234,48 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(
   }
 }
 
+// The spread selection: 1024-thread workgroups of G groups of 4 positions per thread (the
+// smallest G from 1, 2, 3, 4, 6, 9 that covers n_tokens), slices of S positions (a power of two
+// from 32 to 256, so a slice's groups are S/4 lanes of one wavefront), the smallest S for which
+// the selecting and the chunk-sum workgroups fit one workgroup per CU.
+bool select_slices_fits(int n_tokens) { return n_tokens >= 1 && n_tokens <= kSlicesMaxTokens; }
+
+int32_t select_slices_launch(const SelectArgs& args, uint32_t* ghist, const SliceRows* rows, int32_t* err,
+                             hipStream_t st) {
+  const int N = args.n_tokens;
+  if (!select_slices_fits(N) || args.has_thr) return CKV_ERR_INVALID_ARGUMENT;
+  if (rows != nullptr && (2 * rows->n_heads * rows->vpr > kSlThreads || (rows->vpr & (rows->vpr - 1)) != 0))
+    return CKV_ERR_INVALID_ARGUMENT;
+  const int G = (N + 4 * kSlThreads - 1) / (4 * kSlThreads);
+  const int Gb = G <= 4 ? G : G <= 6 ? 6 : 9;  // the instantiated group counts
+  const size_t lds = (size_t)2 * (kSlThreads / 8) * Gb * sizeof(uint32_t);  // pool and taken bitmaps
+  const int sum_groups = (args.n_chunks + kSlWaves - 1) / kSlWaves;
+  int S = 32;
+  while ((N + S - 1) / S + sum_groups > 256 && S < 256) S *= 2;
+  const int n_slices = (N + S - 1) / S;
+  const dim3 grid((unsigned)(n_slices + sum_groups));
+  SliceRows rw = rows != nullptr ? *rows : SliceRows{};
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(kSlThreads), lds, st, args.diff, args.flags, ghist, args.local, N,
+                       args.n_chunks, args.chunks, S, n_slices, args, rw, err);
+  };
+#define CKV_SL(G)                                                   \
+  if (N <= kSlThreads * 4 * G) {                                    \
+    if (rows != nullptr) go(select_slices_kernel<G, true>);         \
+    else go(select_slices_kernel<G, false>);                        \
+    CKV_RETURN_IF_LAUNCH_FAILED();                                  \
+    return CKV_OK;                                                  \
+  }
+  CKV_SL(1)
+  CKV_SL(2)
+  CKV_SL(3)
+  CKV_SL(4)
+  CKV_SL(6)
+  CKV_SL(9)
+#undef CKV_SL
+  return CKV_ERR_INVALID_ARGUMENT;
+}
+
 int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st) {
   const int n_tokens = args.n_tokens;
   const int W = (n_tokens + 31) / 32;
@@ -256,9 +299,7 @@ int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st) {
   CKV_SEL_REG(8)
   CKV_SEL_REG(12)
   CKV_SEL_REG(16)
-  CKV_SEL_REG(24)
-  CKV_SEL_REG(33)
-  static_assert(kSelRegMax == 33, "the largest register bucket");
+  static_assert(kSelRegMax == 16, "the largest register bucket");
 #undef CKV_SEL_REG
   if (ghist != nullptr) return CKV_ERR_INVALID_ARGUMENT;  // the L2 form takes no histogram
   hipLaunchKernelGGL(select_kernel, dim3(1), dim3(kSelThreads), lds, st, args.diff, args.norm, args.flags,

@@ -33,7 +33,7 @@ namespace ckv {
 
 constexpr int kSelThreads = 1024;
 #ifndef CKV_SEL_REG_MAX
-#define CKV_SEL_REG_MAX 33
+#define CKV_SEL_REG_MAX 16
 #endif
 constexpr int kSelRegMax = CKV_SEL_REG_MAX;  // positions per thread up to which the keys stay in registers
 constexpr int kSelWaves = kSelThreads / kWave;

@@ -485,6 +485,8 @@ class HipEngine(DecoderPieces):
              tokens_np if first is None else tokens_np[:0]]
         )
         n_cached_segs = len(plan.segments)
+        # layer 1 as one call on the main stream carries the gather of layers 2..'s dropped rows
+        merged_gather = one_call and not self.overlap and n_cached_segs > 0 and n_layers > 2
 
         # Every row of every layer is written below: active rows by ckv_rope_qkv (layer 1: by
         # ckv_scatter_rows), the other cached rows by the gathers.
@@ -532,9 +534,15 @@ class HipEngine(DecoderPieces):
                         base = (torch.empty_like(K), torch.empty_like(V))
                         ops.assemble_layer(*base, tab_d, n_layers, 1, segs_d, n_cached_segs, plan.max_seg_tokens,
                                            None, None, None, self.theta, err)
-                    diff, norm, sel = ops.layer1_repair(K, V, tab_d, n_layers, 1, segs_d, n_cached_segs, k, v, flags_d,
-                                                        local_d, spans_d, config.escalate_threshold, self.theta,
-                                                        self._workspace("one_call"), err)
+                    if merged_gather:  # the kept rows' scatter and layers 2..'s dropped rows in one launch
+                        diff, norm, sel = ops.layer1_repair_gather(
+                            k_slab, v_slab, tab_d, 1, (2, n_layers), segs_d, n_cached_segs, plan.max_seg_tokens, k, v,
+                            flags_d, local_d, spans_d, config.escalate_threshold, self.theta,
+                            self._workspace("one_call"), err)
+                    else:
+                        diff, norm, sel = ops.layer1_repair(K, V, tab_d, n_layers, 1, segs_d, n_cached_segs, k, v,
+                                                            flags_d, local_d, spans_d, config.escalate_threshold,
+                                                            self.theta, self._workspace("one_call"), err)
                 else:
                     if ready.get(1) is not None:
                         torch.cuda.current_stream(dev).wait_event(ready[1])
@@ -562,7 +570,7 @@ class HipEngine(DecoderPieces):
                 active = sel.keep_abs[:n_keep]
                 if not one_call:
                     ops.scatter_kept_rows(K, V, k, v, active, rows, err)  # k/v compaction folded in
-                if n_cached_segs and n_layers > 2:
+                if n_cached_segs and n_layers > 2 and not merged_gather:
                     ready[2] = gather((2, n_layers), sel.keep_rank)
             else:
                 # RoPE of q/k with k and v written straight into this layer's cache rows

@@ -338,6 +338,27 @@ def layer1_repair(
     (diff, norm, selection), bit-identical to rerope_gather (this layer) + deviation + select +
     scatter_kept_rows. k/v: the fresh rows (1, H, n, D), any row-contiguous strides. workspace: from
     layer1_repair_workspace(), not shared by calls that may run concurrently."""
+    k, v, diff, norm, out, C, n_tab = _layer1_args(K, V, src_tab, n_layers, segments, n_segs, k, v, flags, local, spans,
+                                                   workspace, out, diff_norm)
+    _, H, N, D = K.shape
+    has_thr = escalate_threshold is not None
+    check(
+        lib().ckv_layer1_repair(
+            _ptr(K), _ptr(V), N * D, _ptr(src_tab), n_tab, int(n_layers), int(layer), _ptr(segments), int(n_segs),
+            _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2), k.shape[2], _ptr(flags),
+            _ptr(local), N, H, D, dtype_code(K.dtype), float(theta), _ptr(spans), C, int(has_thr),
+            float(escalate_threshold) if has_thr else 0.0, _ptr(diff), _ptr(norm), _ptr(out.keep_abs),
+            _ptr(out.keep_local), _ptr(out.keep_rank), _ptr(out.rel_dev), _ptr(out.escalated), _ptr(out.counts),
+            _ptr(workspace), workspace.numel() * workspace.element_size(), _ptr(err), _stream(K.device),
+        ),
+        "ckv_layer1_repair",
+    )
+    return diff, norm, out
+
+
+def _layer1_args(K, V, src_tab, n_layers, segments, n_segs, k, v, flags, local, spans, workspace, out, diff_norm):
+    """Checks shared by layer1_repair and layer1_repair_gather (K/V: one layer's (1, H, N, D)
+    cache); allocates the outputs not given."""
     _dev(K, V, src_tab, segments, k, v, flags, local, spans, workspace)
     k, v = _rows_view(k), _rows_view(v)
     if K.dtype != k.dtype or V.dtype != k.dtype or v.dtype != k.dtype:
@@ -367,18 +388,53 @@ def layer1_repair(
     diff, norm = diff_norm
     if out is None:
         out = _new_selection(N, C, dev)
+    return k, v, diff, norm, out, C, src_tab.numel() // (2 * int(n_layers))
+
+
+def layer1_repair_gather(
+    k_slab: torch.Tensor,
+    v_slab: torch.Tensor,
+    src_tab: torch.Tensor,
+    layer: int,
+    layers: tuple[int, int],
+    segments: torch.Tensor,
+    n_segs: int,
+    max_seg_tokens: int,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    flags: torch.Tensor,
+    local: torch.Tensor,
+    spans: torch.Tensor,
+    escalate_threshold: float | None,
+    theta: float,
+    workspace: torch.Tensor,
+    err: torch.Tensor | None = None,
+    out: Selection | None = None,
+    diff_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, Selection]:
+    """layer1_repair of layer `layer` of the (L, 1, H, N, D) slabs followed by the gather of the
+    dropped rows of layers [layers) (rerope_gather(layers=layers, skip=keep_rank)), with the kept
+    rows' scatter and that gather in one launch: the same outputs, one launch fewer."""
+    if k_slab.dim() != 5 or v_slab.shape != k_slab.shape or not (k_slab.is_contiguous() and v_slab.is_contiguous()):
+        raise ValueError("k_slab/v_slab must be contiguous (L, 1, H, N, D)")
+    L, _, H, N, D = k_slab.shape
+    b, e = int(layers[0]), int(layers[1])
+    if not (0 <= b <= e <= L) or b <= int(layer) < e:
+        raise ValueError(f"gather layers {layers} must lie in [0, {L}) and exclude layer {layer}")
+    K, V = k_slab[int(layer)], v_slab[int(layer)]
+    k, v, diff, norm, out, C, n_tab = _layer1_args(K, V, src_tab, L, segments, n_segs, k, v, flags, local, spans,
+                                                   workspace, out, diff_norm)
     has_thr = escalate_threshold is not None
-    n_tab = src_tab.numel() // (2 * int(n_layers))
     check(
-        lib().ckv_layer1_repair(
-            _ptr(K), _ptr(V), N * D, _ptr(src_tab), n_tab, int(n_layers), int(layer), _ptr(segments), int(n_segs),
-            _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2), k.shape[2], _ptr(flags),
-            _ptr(local), N, H, D, dtype_code(K.dtype), float(theta), _ptr(spans), C, int(has_thr),
-            float(escalate_threshold) if has_thr else 0.0, _ptr(diff), _ptr(norm), _ptr(out.keep_abs),
+        lib().ckv_layer1_repair_gather(
+            _ptr(k_slab), _ptr(v_slab), H * N * D, N * D, _ptr(src_tab), n_tab, L, int(layer), b, e, _ptr(segments),
+            int(n_segs), int(max_seg_tokens), _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2),
+            k.shape[2], _ptr(flags), _ptr(local), N, H, D, dtype_code(K.dtype), float(theta), _ptr(spans), C,
+            int(has_thr), float(escalate_threshold) if has_thr else 0.0, _ptr(diff), _ptr(norm), _ptr(out.keep_abs),
             _ptr(out.keep_local), _ptr(out.keep_rank), _ptr(out.rel_dev), _ptr(out.escalated), _ptr(out.counts),
-            _ptr(workspace), workspace.numel() * workspace.element_size(), _ptr(err), _stream(dev),
+            _ptr(workspace), workspace.numel() * workspace.element_size(), _ptr(err), _stream(K.device),
         ),
-        "ckv_layer1_repair",
+        "ckv_layer1_repair_gather",
     )
     return diff, norm, out
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define CKV_ABI_VERSION 2
+#define CKV_ABI_VERSION 3
 
 typedef enum ckv_status {
   CKV_OK = 0,
@@ -104,12 +104,12 @@ typedef struct ckv_chunk_span {
                                        were ranked directly instead of by radix passes      */
 #define CKV_COUNT_N 8
 
-/* Bytes of the workspace ckv_deviation_select takes (the 16 KB candidate histogram; the 256
-   bytes after it are not used). */
+/* Bytes of the workspace ckv_deviation_select takes: the 16 KB candidate histogram, then the
+   word that counts the selection's workgroups done reading it (the rest is not used). */
 #define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 16640
 
-/* Bytes of the workspace ckv_layer1_repair takes (the selection's candidate histogram). */
-#define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 16384
+/* Bytes of the workspace ckv_layer1_repair takes (the same layout). */
+#define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 16640
 
 /* ABI version compiled into the library (CKV_ABI_VERSION). */
 int32_t ckv_abi_version(void);
@@ -234,16 +234,19 @@ int32_t ckv_select(const float* diff, const float* norm, const uint8_t* pos_flag
  * meaning; see both above). Two launches: the deviation kernel also counts every position
  * flagged CKV_POS_CACHED | CKV_POS_POOLED and not CKV_POS_SINK into a histogram of its deviation
  * (4096 bins of 1/64 octave) in the workspace; the selection starts from that histogram and
- * ranks only the candidates of the threshold's bin. When the pooled flags disagree with the
- * pooled spans, a chunk escalates, or the threshold lies outside 2^-24 .. 2^40, the selection
- * ignores the histogram (same result, slower); counts[CKV_COUNT_TOP_HISTOGRAM] says which path
- * ran.
+ * ranks only the candidates of the threshold's bin. Without an escalation threshold and up to
+ * 36864 positions the selection is spread over many workgroups, each finding the threshold
+ * itself and compacting one slice of positions; with a threshold it runs in one workgroup. When
+ * the pooled flags disagree with the pooled spans, a chunk escalates, or the threshold lies
+ * outside 2^-24 .. 2^40, the selection ignores the histogram (same result, slower);
+ * counts[CKV_COUNT_TOP_HISTOGRAM] says which path ran.
  *   workspace        device memory of >= CKV_DEVIATION_SELECT_WORKSPACE_BYTES, 16-byte aligned,
  *                    ZERO before its first use; every call leaves it zero again. Calls that
  *                    share a workspace must be ordered (one stream, or events): concurrent
  *                    calls on one workspace race.
- * n_tokens <= CKV_SELECT_MAX_TOKENS; above 33792 the deviation counts no histogram and the
- * selection runs its L2 form (the workspace is then not touched).
+ * n_tokens <= CKV_SELECT_MAX_TOKENS; the workspace is not touched above 36864 positions, nor
+ * above 16384 with a threshold (the deviation then counts no histogram and the selection runs
+ * its L2 form).
  * Replaces: torch_engine.py:117-153 (the deviation :117-124, rel/escalation/budget :128-142,
  *           argsort top-k :143-146, keep.nonzero and local compaction :146-153).
  */
@@ -290,18 +293,20 @@ int32_t ckv_deviation_select_noalloc(const void* k_fresh, int64_t kf_head_stride
  * planner's segments, n_segs <= 3840), read for every position flagged CKV_POS_CACHED. segs and
  * src_tab may be NULL with n_segs == 0, k_fresh and v_fresh with n_fresh == 0 (every position
  * exact: a kept position then flags CKV_DEVICE_ERR_RANGE, as an out-of-range local index does).
- * Three launches, nothing read back on the host: (1) every position's rows, the cached rows
- * written into the cache, the deviations, and the positions flagged CKV_POS_CACHED |
- * CKV_POS_POOLED and not CKV_POS_SINK counted into the deviation histogram; (2) the selection,
- * starting from that count (as ckv_deviation_select's does, same result when the flags disagree
- * with the spans or a chunk escalates, just slower); (3) the kept rows, their count read on the
- * device.
+ * Nothing is read back on the host. Launch (1): every position's rows, the cached rows written
+ * into the cache, the deviations, and the positions flagged CKV_POS_CACHED | CKV_POS_POOLED and
+ * not CKV_POS_SINK counted into the deviation histogram. Without an escalation threshold and up
+ * to 36864 positions, launch (2) is the selection and the kept rows' scatter in one launch of
+ * many workgroups, each finding the threshold from that count and compacting and scattering one
+ * slice of positions. Otherwise (2) is the selection in one workgroup (as ckv_deviation_select's)
+ * and (3) the kept rows, their count read on the device. Both give the same result when the
+ * flags disagree with the spans or a chunk escalates, just slower.
  *   workspace  >= CKV_LAYER1_REPAIR_WORKSPACE_BYTES, 16-byte aligned, ZERO before its first use;
  *              each call leaves it zeroed. Calls that share a workspace must be ordered (one
  *              stream, or events).
  * Limits: H * D * elem <= 1024 bytes per row (CKV_ERR_TOO_LARGE beyond: use the four calls),
- * head_dim <= 128 and a power of two, n_tokens <= CKV_SELECT_MAX_TOKENS (above 33792 the
- * selection counts its own histogram).
+ * head_dim <= 128 and a power of two, n_tokens <= CKV_SELECT_MAX_TOKENS (above 36864, or above
+ * 16384 with a threshold, the selection counts its own histogram).
  * Replaces: base_kv for layer 1 (torch_engine.py:96-103, with shift_keys :56-59), the deviation
  *           (:117-124), rel/escalation/budget (:125-142), the top-k (:143-147), the compaction
  *           (:148-153) and the scatter (:155-156).
@@ -317,6 +322,31 @@ int32_t ckv_layer1_repair(void* dst_k, void* dst_v, int64_t dst_head_stride, con
                           int64_t* keep_abs, int64_t* keep_local, int32_t* keep_rank, float* rel_dev,
                           uint8_t* escalated, int32_t* counts, void* workspace, int64_t workspace_bytes,
                           int32_t* err, void* stream);
+
+/*
+ * ckv_layer1_repair of layer `layer` followed by ckv_rerope_gather_layers of the dropped rows of
+ * layers [gather_begin, gather_end) (skip map keep_rank), with the kept rows' scatter and that
+ * gather in one launch: every output bit-identical to the two calls, one dependent launch fewer.
+ * k_slab/v_slab hold every layer's (H, n_tokens, D) cache, layer l at l * layer_stride elements,
+ * head stride head_stride; max_seg_tokens is the longest segment (as for the gather). The other
+ * arguments are ckv_layer1_repair's. keep_rank must not be NULL, and `layer` must lie outside
+ * [gather_begin, gather_end).
+ * Replaces: base_kv for layer 1 and the layer-1 repair (torch_engine.py:96-103, :117-156), and
+ *           base_kv of the later layers for the rows their fresh rows do not overwrite
+ *           (:96-103 with the overwrite of :155-156 left out).
+ */
+int32_t ckv_layer1_repair_gather(void* k_slab, void* v_slab, int64_t layer_stride, int64_t head_stride,
+                                 const uint64_t* src_tab, int32_t n_tab_chunks, int32_t n_layers, int32_t layer,
+                                 int32_t gather_begin, int32_t gather_end, const ckv_segment* segs, int32_t n_segs,
+                                 int32_t max_seg_tokens, const void* k_fresh, int64_t kf_head_stride,
+                                 int64_t kf_token_stride, const void* v_fresh, int64_t vf_head_stride,
+                                 int64_t vf_token_stride, int32_t n_fresh, const uint8_t* pos_flags,
+                                 const int32_t* local, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
+                                 int32_t dtype, double theta, const ckv_chunk_span* chunks, int32_t n_chunks,
+                                 int32_t has_threshold, double escalate_threshold, float* diff, float* norm,
+                                 int64_t* keep_abs, int64_t* keep_local, int32_t* keep_rank, float* rel_dev,
+                                 uint8_t* escalated, int32_t* counts, void* workspace, int64_t workspace_bytes,
+                                 int32_t* err, void* stream);
 
 /*
  * Assemble one layer's cache with every row written once: for each segment row at position p,

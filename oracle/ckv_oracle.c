@@ -215,6 +215,16 @@ static float butterfly64(float* lanes) {
 
 /* ---- a5: deviation ---------------------------------------------------------------------------- */
 
+/* A NaN deviation or norm is reported as the canonical quiet NaN 0x7fc00000: IEEE 754 and torch
+ * leave the payload of a NaN result open, and the ranking treats every NaN alike. */
+static float canonical_nan(float x) {
+  if (x == x) return x;
+  const uint32_t u = 0x7fc00000u;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
 int ckvo_deviation(const void* kf, int64_t kf_hs, int64_t kf_ts, const void* vf, int64_t vf_hs, int64_t vf_ts,
                    const void* kc, const void* vc, int64_t c_hs, const uint8_t* flags, const int32_t* local,
                    int n_tokens, int n_fresh, int n_heads, int D, int dt, float* diff, float* norm) {
@@ -248,8 +258,8 @@ int ckvo_deviation(const void* kf, int64_t kf_hs, int64_t kf_ts, const void* vf,
       }
     }
     const float a = butterfly64(sk), b = butterfly64(sv), c = butterfly64(nk), d = butterfly64(nv);
-    diff[p] = a + b;
-    norm[p] = c + d;
+    diff[p] = canonical_nan(a + b);
+    norm[p] = canonical_nan(c + d);
   }
   return bad;
 }

@@ -1,8 +1,8 @@
 """ckv_deviation_select (the layer-1 deviation, then the pooled top-k, sinks and compaction from
 the candidate histogram the deviation counts, torch_engine.py:117-153) and ckv_scatter_kept_rows (the k/v compaction folded into the scatter,
 :152 and :155-156) against the oracle, bit for bit: diff/norm, keep_abs, keep_local, keep_rank,
-rel_dev, escalated and the counts. Cases: the config-3 and config-4 shapes, every register
-bucket of the selecting workgroup up to 33792 positions and the two-launch form above it,
+rel_dev, escalated and the counts. Cases: the config-3 and config-4 shapes, every shape of the
+selection spread over many workgroups up to 36864 positions and the single-workgroup forms,
 escalation and flags without the pooled bit (the histogram is then not used: same result),
 exact placements, heavy ties and NaN deviations, the workspace left zeroed across calls of
 different sizes, and replays of a captured HIP graph."""
@@ -59,8 +59,16 @@ def _chunk_sigma(rng, N, chunks):
     return sig
 
 
-def _run_and_check(k, v, K, V, flags, local, active, spans, thr, ws=None, expect_top=None):
-    """Fused call on the device vs the oracle's deviation + selection."""
+def _at(a, off):
+    """a on the device, off elements into a larger buffer (alignment of that offset)."""
+    buf = torch.zeros(len(a) + off + 16, dtype=torch.from_numpy(a[:1]).dtype, device=DEV)
+    buf[off : off + len(a)] = torch.from_numpy(a).to(DEV)
+    return buf[off : off + len(a)]
+
+
+def _run_and_check(k, v, K, V, flags, local, active, spans, thr, ws=None, expect_top=None, offsets=(0, 0)):
+    """Fused call on the device vs the oracle's deviation + selection. offsets: flags and local
+    that many elements into their buffers."""
     kf, vf = k[:, active], v[:, active]
     kt = O.from_numpy(kf, DEV)[None]
     # fresh v as the engine has it: a token-major buffer viewed (1, H, n, D)
@@ -68,7 +76,7 @@ def _run_and_check(k, v, K, V, flags, local, active, spans, thr, ws=None, expect
     ws = ops.deviation_select_workspace(DEV) if ws is None else ws
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
     Kt, Vt = O.from_numpy(K, DEV)[None], O.from_numpy(V, DEV)[None]
-    diff, norm, sel = ops.deviation_select(kt, vt, Kt, Vt, O.from_numpy(flags, DEV), O.from_numpy(local, DEV),
+    diff, norm, sel = ops.deviation_select(kt, vt, Kt, Vt, _at(flags, offsets[0]), _at(local, offsets[1]),
                                            O.from_numpy(spans.reshape(-1), DEV), thr, ws, err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
@@ -126,16 +134,17 @@ def test_config4_shape_and_kept_row_scatter():
     np.testing.assert_array_equal(O.to_numpy(Vt)[0], Vw)
 
 
-@pytest.mark.parametrize("N", [1, 16, 17, 77, 1024, 1025, 4099, 12288, 24577, 32832, 33792, 33793])
+@pytest.mark.parametrize("N", [1, 16, 17, 77, 1024, 1025, 2048, 2049, 4099, 9216, 9217, 12288, 18432, 18433, 24577,
+                               32832, 33792, 36864, 36865])
 def test_sizes(N):
-    """Every register bucket (4, 8, 12, 16, 24, 33 positions per thread) and the two-launch form
-    above 33792 positions."""
+    """Every shape of the spread selection (256 threads x 2, 4, 9 groups of four positions, 512 x 9,
+    18), the boundaries between them, and the single-workgroup L2 form above 36864 positions."""
     rng = np.random.default_rng(N)
     L = max(1, min(256, N // 3))
     chunks = [(c * L, L) for c in range(max(1, (N - 5) // L))] if N > 5 else [(0, N)]
     flags, spans, local, active = _layout(N, chunks, 2, 0.3)
     k, v, K, V = _rows(rng, N, _chunk_sigma(rng, N, chunks))
-    _run_and_check(k, v, K, V, flags, local, active, spans, None, expect_top=N <= 33792)
+    _run_and_check(k, v, K, V, flags, local, active, spans, None, expect_top=N <= 36864)
 
 
 @pytest.mark.parametrize("thr_mode", ["none_escalate", "some_escalate"])
@@ -167,6 +176,20 @@ def test_flags_without_pooled_bit_and_exact_placements():
     no_pool = flags & ~np.uint8(POOLED)
     want2, _ = _run_and_check(k, v, K, V, no_pool, local, active, spans, None, expect_top=False)
     np.testing.assert_array_equal(want["keep_abs"], want2["keep_abs"])
+
+
+@pytest.mark.parametrize("offsets", [(1, 1), (4, 1), (2, 3)])
+@pytest.mark.parametrize("N", [4099, 8256, 9217, 32832])
+def test_misaligned_flags_and_local(N, offsets):
+    """Flags and local indices not 16-byte aligned (1, 2 or 4 bytes / 1 or 3 elements into their
+    buffers): the spread selection loads them element by element instead of as words and
+    vectors; same result as the oracle."""
+    rng = np.random.default_rng(N + 7 * offsets[0])
+    L = 256
+    chunks = [(c * L, L) for c in range(N // L - 1)]
+    flags, spans, local, active = _layout(N, chunks, 4, 0.3)
+    k, v, K, V = _rows(rng, N, _chunk_sigma(rng, N, chunks))
+    _run_and_check(k, v, K, V, flags, local, active, spans, None, expect_top=True, offsets=offsets)
 
 
 def test_ties_and_nan_deviations():

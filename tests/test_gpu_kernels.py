@@ -427,7 +427,7 @@ def test_select_nan_candidates_rank_after_finite(N_chunks):
     assert [p for p in nan_pos.tolist() if p in kept] == nan_pos[: budget - n_finite].tolist()
 
 
-@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 1023, 1024, 1025, 8256, 33792, 33793, 131072])
+@pytest.mark.parametrize("N", [1, 31, 32, 33, 64, 1023, 1024, 1025, 8256, 16384, 16385, 33792, 131072])
 def test_select_sizes(N):
     rng = np.random.default_rng(N)
     L = max(1, N // 3)
@@ -444,7 +444,8 @@ def test_select_misaligned_inputs(N, flags_off):
     """diff, norm and local one element into their buffers (4-byte, not 16-byte aligned), flags
     4 or 1 bytes in: the selecting threads load their runs from one address per array instead of
     16-byte vectors, the flags as aligned words (4-byte aligned flags) or byte by byte, in every
-    register bucket from 4 to 33 positions per thread; same result as the oracle."""
+    register bucket from 4 to 16 positions per thread and the L2 form above 16384 positions; same
+    result as the oracle."""
     rng = np.random.default_rng(N + flags_off)
     L = 250
     flags, spans = _spans(N // L, L, 0.3, 4, N)

@@ -378,3 +378,105 @@ def test_graph_replays():
         n = int(sr.counts[0].item())
         _same(out.keep_abs[:n], sr.keep_abs[:n], f"keep_abs, replay {i}")
         _same(out.counts[:7], sr.counts[:7], f"counts, replay {i}")
+
+
+def _merged_vs_separate(req, thr=None, ws=None, layers=None):
+    """ckv_layer1_repair_gather (layer `req.layer` repaired, the kept rows' scatter and the gather
+    of the dropped rows of `layers` in one launch) against layer1_repair + rerope_gather(layers,
+    skip=keep_rank): every layer of both slabs, the diff/norm and the selection, bit for bit."""
+    L = req.n_layers
+    layers = (req.layer + 1, L) if layers is None else layers
+    ws = ops.layer1_repair_workspace(DEV) if ws is None else ws
+    shape = (L, 1, req.H, req.N, req.D)
+    Ks, Vs = torch.full(shape, SENT, dtype=req.dtype, device=DEV), torch.full(shape, -SENT, dtype=req.dtype, device=DEV)
+    Km, Vm = Ks.clone(), Vs.clone()
+    ds, ns, ss = ops.layer1_repair(Ks[req.layer], Vs[req.layer], req.tab, L, req.layer, req.segs, req.n_segs, req.k,
+                                   req.v, req.flags, req.local, req.spans, thr, THETA, ws, req.err)
+    if req.n_segs:
+        ops.rerope_gather(Ks, Vs, req.tab, req.segs, req.n_segs, req.plan.max_seg_tokens, THETA, req.err,
+                          layers=layers, skip=ss.keep_rank)
+    dm, nm, sm = ops.layer1_repair_gather(Km, Vm, req.tab, req.layer, layers, req.segs, req.n_segs,
+                                          req.plan.max_seg_tokens, req.k, req.v, req.flags, req.local, req.spans, thr,
+                                          THETA, ws, req.err)
+    torch.cuda.synchronize()
+    assert int(req.err.item()) == 0, f"device status {int(req.err.item())}"
+    assert not ws.any()
+    n = int(ss.counts[0].item())
+    _same(sm.counts[:7], ss.counts[:7], "counts")
+    _same(dm.view(torch.int32), ds.view(torch.int32), "diff")
+    _same(nm.view(torch.int32), ns.view(torch.int32), "norm")
+    _same(sm.keep_abs[:n], ss.keep_abs[:n], "keep_abs")
+    _same(sm.keep_local[:n], ss.keep_local[:n], "keep_local")
+    _same(sm.keep_rank, ss.keep_rank, "keep_rank")
+    for li in range(L):
+        _same(Km[li], Ks[li], f"K layer {li}")
+        _same(Vm[li], Vs[li], f"V layer {li}")
+    return Km, Vm, sm
+
+
+def test_merged_gather_8k_request_shape():
+    """The 8k request's shape with 5 layers: layer 1 repaired, the dropped rows of layers 2-4
+    gathered in the scatter's launch; layer 0 left as it was. The gathered layers also match the
+    oracle: every cached row re-rotated except the kept ones, which keep the slab's fill."""
+    rng = np.random.default_rng(81)
+    starts, N = _shuffled(rng, 24, 320, 576)
+    req = Request(81, [320] * 24, starts, N, n_layers=5)
+    Km, Vm, sm = _merged_vs_separate(req)
+    assert int(sm.counts[0].item()) == 2976
+    kept = _bits(sm.keep_rank) >= 0
+    ks = [[_bits(ch.keys[li])[0] for li in range(5)] for ch in req.plan.chunks]
+    vs = [[_bits(ch.values[li])[0] for li in range(5)] for ch in req.plan.chunks]
+    for li in (2, 4):
+        Ko = np.full((req.H, N, req.D), 0, dtype=np.uint16)
+        Vo = np.zeros_like(Ko)
+        assert O.rerope_gather(Ko[None], Vo[None], [[c[li]] for c in ks], [[c[li]] for c in vs], req.plan.segments,
+                               THETA) == 0
+        gathered = req.plan.cached & ~kept
+        np.testing.assert_array_equal(_bits(Km[li])[0][:, gathered], Ko[:, gathered], err_msg=f"K layer {li}")
+        np.testing.assert_array_equal(_bits(Vm[li])[0][:, gathered], Vo[:, gathered], err_msg=f"V layer {li}")
+        sent = _bits(torch.tensor(SENT, dtype=req.dtype))
+        assert (_bits(Km[li])[0][:, ~gathered] == sent).all()
+
+
+@pytest.mark.parametrize("ratio", [0.15, 0.5])
+def test_merged_gather_config3_shape(ratio):
+    starts = [(c, c * 256) for c in range(32)]
+    req = Request(90 + int(ratio * 100), [256] * 32, starts, 8192, ratio=ratio, n_layers=4)
+    _merged_vs_separate(req)
+
+
+def test_merged_gather_replay_request_shape():
+    """The replay's 32,832-position request (128 chunks of 256 drawn from 24, + 64 query
+    positions), 3 layers, chunks repeated at several shifts."""
+    rng = np.random.default_rng(56)
+    zipf = 1.0 / np.arange(1, 25) ** 1.1
+    ids = rng.choice(24, 128, p=zipf / zipf.sum())
+    starts = [(int(c), j * 256) for j, c in enumerate(ids)]
+    req = Request(56, [256] * 24, starts, 128 * 256 + 64, ratio=0.15, n_layers=3)
+    _merged_vs_separate(req)
+
+
+@pytest.mark.parametrize("case", ["threshold", "small_f32", "no_placements", "every_position_exact", "empty_layers"])
+def test_merged_gather_edges(case):
+    """An escalation threshold (the single-workgroup selection), fp32 at head_dim 64 with an
+    exact and overlapping placements, no placement (nothing to gather: the launch scatters only),
+    every position exact (nothing kept: the launch gathers only), and an empty layer range."""
+    if case == "threshold":
+        rng = np.random.default_rng(9)
+        starts, N = _shuffled(rng, 12, 128, 100)
+        req = Request(9, [128] * 12, starts, N, ratio=0.3, n_layers=4)
+        rel = O.to_numpy(req.four_launches(None)[4].rel_dev)[:12]
+        _merged_vs_separate(req, thr=float(np.median(rel)))
+        return
+    if case == "small_f32":
+        req = Request(4, [40, 33, 50, 29, 61], [(0, 5), (1, 60), (2, 80), (3, 150), (4, 190)], 270, H=2, D=64,
+                      dtype=torch.float32, n_layers=4, exact=(3,), ratios=[0.3, 0.5, None, 0.0, 0.25])
+    elif case == "no_placements":
+        req = Request(5, [], [], 7, n_layers=3)
+    elif case == "every_position_exact":
+        req = Request(6, [50], [(0, 0)], 50, exact=(0,), n_layers=3)
+    else:
+        req = Request(7, [64] * 4, [(c, c * 64) for c in range(4)], 260, n_layers=2)
+        _merged_vs_separate(req, layers=(2, 2))
+        return
+    _merged_vs_separate(req)
