@@ -8,14 +8,16 @@ shuffled positions (each chunk computed at its own original offset, so every pla
 its keys), then a 512-token uncached tail and a 64-token query; 30% recompute, 4 sinks per chunk.
 
 A step is one request's whole KV repair with every input already resident in HBM, issued as
-HipEngine issues it (31 launches in order on one stream): layer 0's fresh rows written into its
-cache; layer 1's repair as one ckv_layer1_repair call (three launches: the cached rows
-re-rotated into the cache with the deviation, the selection of 2304 pooled + 96 sinks + 576
-uncached = 2976 kept rows, the scatter of the kept rows); then the gather of the cached rows of
-the 5280 dropped positions of layers 2-27 in one launch, and the fresh rows of layers 2-27
-(disjoint rows). The fresh rows are written by ckv_rope_qkv as in the engine (k rotated to its
-position, v copied, straight into the cache rows); the engine's launch also rotates q for the
-attention, which the step leaves out as the reference's KV-repair bytes do.
+HipEngine issues it (30 launches in order on one stream): layer 0's fresh rows written into its
+cache; layer 1's repair with the base cache of layers 2-27 as one ckv_layer1_repair_gather call
+of three launches (the cached rows of layer 1 re-rotated into its cache with the deviation; the
+selection of 2304 pooled + 96 sinks + 576 uncached = 2976 kept rows, with layers 2-3 gathered
+whole by the CUs the single-workgroup selection leaves idle; the scatter of layer 1's kept rows
+with the gather of the cached rows of the 5280 dropped positions of layers 4-27); then the
+fresh rows of layers 2-27 (they overwrite the kept rows of layers 2-3). The fresh rows are
+written by ckv_rope_qkv as in the engine (k rotated to its position, v copied, straight into
+the cache rows); the engine's launch also rotates q for the attention, which the step leaves
+out as the reference's KV-repair bytes do.
 The unit of work is one request's KV repair as the reference's op sequence moves it (re-RoPE +
 gather of every cached row of all 28 layers, the layer-0 scatter of all 8256 rows, the
 deviation, the scatters of layers 1-27):
@@ -25,13 +27,14 @@ deviation, the scatters of layers 1-27):
     scatter L1-27   27 x 2976 x 4096 B                                         =   329,121,792
     total                                                                      = 1,277,624,832
 `value` = that total / measured time per step (GB/s), the step replayed from a HIP graph (the
-eager time, launch-bound from Python, is reported as ms_per_step_eager, the same launches with
-the gathers on a second stream (HipEngine(overlap=True)) as ms_per_step_two_streams, layer 1 as
-the four launches ckv_layer1_repair replaces (base-cache gather, deviation, selection, scatter)
-as ms_per_step_layer1_four_launches, and layers 0 and 2-27 built by one assemble launch each as
-ms_per_step_assemble_variant); the fused flow itself moves 990,577,152 B per step
-(moved_bytes_per_step, moved_gbs). `roofline` is the dominant kernel (the gather of the dropped
-rows of layers 2-27, 562,298,880 B per launch) timed live with HIP events around a burst of
+eager time, launch-bound from Python, is reported as ms_per_step_eager; layer 1 as ckv_layer1_repair
+and the dropped rows of layers 2-27 as a separate gather launch as ms_per_step_separate_gather;
+the same launches with the gathers on a second stream (HipEngine(overlap=True)) as
+ms_per_step_two_streams; layer 1 as the four launches ckv_layer1_repair replaces (base-cache
+gather, deviation, selection, scatter) as ms_per_step_layer1_four_launches; layers 0 and 2-27
+built by one assemble launch each as ms_per_step_assemble_variant); the fused flow itself moves
+moved_bytes_per_step (moved_gbs). `roofline` is the dominant kernel (the gather of the dropped
+rows of layers 2-27 as one launch, 562,298,880 B) timed live with HIP events around a burst of
 back-to-back launches on the launch stream. Inputs rotate between two independent copies so
 consecutive steps do not hit in the 256 MB MALL.
 
@@ -225,13 +228,14 @@ class RepairWorkload:
     layer1_mode = "one"  # as HipEngine: layer 1's whole repair in one call (ckv_layer1_repair)
 
     def step(self, two_streams: bool = False):
-        """One request's KV repair as HipEngine issues it (31 launches, in order on one stream):
-        layer 0's fresh rows; layer 1's base cache, deviation, selection and kept rows in one call of
-        three launches;
-        the gather of the dropped rows of layers 2-27; those layers' fresh rows. With layer1_mode
-        "split", layer 1 is the four launches that launch replaces (base cache, deviation, selection,
-        kept-row scatter). two_streams=True issues the gathers on a second stream instead, as
-        HipEngine(overlap=True) does (beside the fresh rows they do not touch)."""
+        """One request's KV repair as HipEngine issues it (30 launches, in order on one stream):
+        layer 0's fresh rows; layer 1's base cache, deviation, selection and kept rows with the base
+        cache of layers 2-27 in one call of three launches (ckv_layer1_repair_gather); the fresh rows
+        of layers 2-27. With layer1_mode "separate_gather", layer 1 is ckv_layer1_repair and the
+        dropped rows of layers 2-27 a gather launch of their own; with "split", layer 1 is the four
+        launches ckv_layer1_repair replaces (base cache, deviation, selection, kept-row scatter).
+        two_streams=True issues the gathers on a second stream instead, as HipEngine(overlap=True)
+        does (beside the fresh rows they do not touch)."""
         from chunkkv_amd import ops
 
         plan = self.plan
@@ -401,7 +405,7 @@ def _graph_of(fn):
 
 
 def bench_repair(steps: int, warmup: int, dev) -> dict:
-    """Time the KV-repair step as HipEngine issues it (31 launches on one stream, captured once
+    """Time the KV-repair step as HipEngine issues it (30 launches on one stream, captured once
     per input set in a HIP graph and replayed; the eager time, launch-bound from Python, layer 1
     as four launches, the two-stream issue and the assemble-per-layer variant are reported too),
     and the dominant kernel (the gather of the dropped rows of layers 2..27) from a burst of
@@ -488,13 +492,25 @@ def dropped_bytes(plan) -> int:
     return (N_LAYERS - 2) * n_dropped * ROW_BYTES * 4
 
 
+def whole_layers(plan) -> int:
+    """Layers of 2..27 that ckv_layer1_repair_gather gathers whole beside its selection (kept
+    cached rows included, overwritten by the fresh rows after)."""
+    from chunkkv_amd import ops
+
+    return ops.layer1_repair_gather_whole_layers(plan.n_tokens, len(plan.spans), None, len(plan.segments),
+                                                 plan.max_seg_tokens, (2, N_LAYERS), N_KV, HEAD_DIM, torch.bfloat16)
+
+
 def moved_bytes(plan) -> int:
     """Algorithmic bytes of the step as HipEngine runs it: each assembled layer reads and writes
-    every row once; layer 1 reads and writes its cached rows (base cache), then the deviation
-    and the scatter of the kept rows."""
+    every row once, and the layers gathered whole beside the selection their kept cached rows
+    once more; layer 1 reads and writes its cached rows (base cache), then the deviation and
+    the scatter of the kept rows."""
     row = ROW_BYTES * 4  # K and V, read + write
     n_cached = int(plan.cached.sum())
-    return ((N_LAYERS - 1) * plan.n_tokens * row + n_cached * row + DEVIATION_BYTES + plan.n_keep * row)
+    kept_cached = plan.n_keep - (plan.n_tokens - n_cached)
+    return ((N_LAYERS - 1) * plan.n_tokens * row + n_cached * row + DEVIATION_BYTES + plan.n_keep * row
+            + whole_layers(plan) * kept_cached * row)
 
 
 ASSEMBLE_BYTES = N_TOKENS * ROW_BYTES * 4  # one assembled layer: 8256 rows of K and V, read + write

@@ -114,6 +114,7 @@ SIGNATURES = {
          _p, _p, _i32, _i32, _i32, _i32, _f64, _p, _i32, _i32, _f64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p,
          _p],
     ),
+    "ckv_layer1_repair_gather_whole_layers": (_i32, [_i32] * 9),
     "ckv_deviation_select_noalloc": (
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i32, _i32, _f64,

@@ -19,7 +19,7 @@ CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 LIB_DIR = PKG / "_lib"
 LIB_NAME = "libchunkkv_amd.so"
-SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "deviation_select.hip",
+SOURCES = ["abi.hip", "rerope_gather.hip", "assemble.hip", "deviation.hip", "select.hip", "select_gather.hip", "deviation_select.hip",
            "scatter.hip", "layer1_repair.hip", "attention.hip", "rope.hip", "extract.hip", "norm.hip"]
 HOST_SOURCES = ["token_hash.cpp"]
 ARCH = "gfx950"

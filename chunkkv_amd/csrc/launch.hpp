@@ -20,6 +20,29 @@ bool select_slices_fits(int n_tokens);
 int32_t select_slices_launch(const SelectArgs& args, uint32_t* ghist, const SliceRows* rows, int32_t* err,
                              hipStream_t st);
 
+// The selection's launch with dense gather workgroups beside it (select_gather.hip): the
+// register-resident selection without a threshold, plus every cached row (skip map ignored) of
+// layers [g.layer_begin, g.layer_begin + *n_pre) of the slabs g.dk/g.dv, *n_pre chosen here
+// (0..max_layers: what fits the CUs the selection leaves free and its time). Any other request
+// (a threshold, more than 16384 positions, head_dim not 64/128, no segment) gets select_launch
+// and *n_pre = 0. The caller fills g but for tiles, n_items, sum_groups and inv.
+struct PreGather {
+  char* dk;
+  char* dv;
+  int64_t ls_b;  // layer stride of the slabs, bytes
+  int64_t hs_b;  // head stride, bytes
+  const uint64_t* tab;
+  const ckv_segment* segs;
+  int n_tab_chunks, n_segs, tiles, n_items, n_layers, layer_begin, n_heads, n_tokens, sum_groups;
+  int32_t* err;
+  InvFreq inv;
+};
+int32_t pregather_layers(int32_t n_tokens, int32_t n_chunks, int32_t has_threshold, int32_t n_segs,
+                         int32_t max_seg_tokens, int32_t max_layers, int32_t n_heads, int32_t head_dim, int32_t dtype);
+int32_t select_gather_launch(const SelectArgs& args, uint32_t* ghist, PreGather g, int32_t max_layers,
+                             int32_t max_seg_tokens, int32_t head_dim, int32_t dtype, double theta, int32_t* n_pre,
+                             hipStream_t st);
+
 // ckv_rerope_gather_layers (rerope_gather.hip), with rows (may be NULL) a scatter of another
 // layer's rows carried in the same launch (its blocks dispatched first).
 struct RowScatter;

@@ -378,9 +378,6 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
 
 namespace ckv {
 
-#ifndef CKV_L1_GATHER_SPREAD_MIN
-#define CKV_L1_GATHER_SPREAD_MIN 0
-#endif
 // The dropped-row gather that ckv_layer1_repair_gather carries in its last launch: the K/V slabs
 // (layer l's cache at l * layer_stride elements), the layers and the segments' longest run.
 struct GatherTail {
@@ -436,9 +433,12 @@ static int32_t layer1_repair_impl(
   // Without a threshold the selection and the kept rows' scatter are one launch of many
   // workgroups (select_slices.hpp) started from the histogram; with one, the single-workgroup
   // selection (the register-resident form takes the histogram; above it, the L2 form counts
-  // itself) and the scatter.
-  const bool spread = has_threshold == 0 && select_slices_fits(n_tokens) &&
-                      (tail == nullptr || n_tokens >= CKV_L1_GATHER_SPREAD_MIN);
+  // itself) and the scatter. With a dropped-row gather to carry (tail) and no threshold, up to
+  // 16384 positions: the single-workgroup selection with whole layers of the gather beside it
+  // (select_gather.hip), then the kept rows with the rest of the gather.
+  const bool pre = tail != nullptr && has_threshold == 0 && n_tokens <= kSelRegMax * kSelThreads && n_segs > 0 &&
+                   tail->begin < tail->end;
+  const bool spread = !pre && has_threshold == 0 && select_slices_fits(n_tokens);
   uint32_t* hist = spread || n_tokens <= kSelRegMax * kSelThreads ? (uint32_t*)workspace : nullptr;
   L1Args args{};
   args.dk = (char*)dst_k;
@@ -488,9 +488,30 @@ static int32_t layer1_repair_impl(
   }
   CKV_RETURN_IF_LAUNCH_FAILED();
   if (tail != nullptr) {
-    // the selection, then one launch: the kept rows of this layer beside the gather of the
-    // dropped rows of layers [begin, end) (keep_rank >= 0 marks the kept positions)
-    const int32_t rc = spread ? select_slices_launch(sel, hist, nullptr, err, st) : select_launch(sel, hist, st);
+    // the selection (with the first n_pre layers of [begin, end) gathered whole beside it), then
+    // one launch: the kept rows of this layer beside the gather of the dropped rows of the other
+    // layers (keep_rank >= 0 marks the kept positions)
+    int32_t n_pre = 0, rc;
+    if (pre) {
+      PreGather g{};
+      g.dk = (char*)tail->k_slab;
+      g.dv = (char*)tail->v_slab;
+      g.ls_b = tail->layer_stride * eb;
+      g.hs_b = dst_head_stride * eb;
+      g.tab = src_tab;
+      g.segs = segs;
+      g.n_tab_chunks = n_tab_chunks;
+      g.n_segs = n_segs;
+      g.n_layers = n_layers;
+      g.layer_begin = tail->begin;
+      g.n_heads = n_heads;
+      g.n_tokens = n_tokens;
+      g.err = err;
+      rc = select_gather_launch(sel, hist, g, tail->end - tail->begin, tail->max_seg_tokens, head_dim, dtype, theta,
+                                &n_pre, st);
+    } else {
+      rc = spread ? select_slices_launch(sel, hist, nullptr, err, st) : select_launch(sel, hist, st);
+    }
     if (rc != CKV_OK) return rc;
     const RowScatter kept{(char*)dst_k,   (char*)dst_v,   dst_head_stride * eb,      args.kf,
                           args.kf_hs_b,   args.kf_ts_b,   args.vf,                   args.vf_hs_b,
@@ -498,8 +519,8 @@ static int32_t layer1_repair_impl(
                           (int)n_tokens,  (int)n_fresh,   (int)n_tokens,             (int)n_heads,
                           vpr,            (int64_t)rowb};
     return gather_layers_launch(tail->k_slab, tail->v_slab, tail->layer_stride, dst_head_stride,
-                                n_segs > 0 ? src_tab : (const uint64_t*)workspace, n_tab_chunks, n_layers, tail->begin,
-                                tail->end, n_segs > 0 ? segs : (const ckv_segment*)workspace, n_segs,
+                                n_segs > 0 ? src_tab : (const uint64_t*)workspace, n_tab_chunks, n_layers,
+                                tail->begin + n_pre, tail->end, n_segs > 0 ? segs : (const ckv_segment*)workspace, n_segs,
                                 tail->max_seg_tokens, keep_rank, n_heads, n_tokens, head_dim, dtype, theta, err,
                                 stream, &kept);
   }

@@ -412,9 +412,12 @@ def layer1_repair_gather(
     out: Selection | None = None,
     diff_norm: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, Selection]:
-    """layer1_repair of layer `layer` of the (L, 1, H, N, D) slabs followed by the gather of the
-    dropped rows of layers [layers) (rerope_gather(layers=layers, skip=keep_rank)), with the kept
-    rows' scatter and that gather in one launch: the same outputs, one launch fewer."""
+    """layer1_repair of layer `layer` of the (L, 1, H, N, D) slabs followed by the base cache of
+    layers [layers): the rows of dropped positions as rerope_gather(layers=layers,
+    skip=keep_rank) writes them; the rows of kept cached positions re-rotated in the first
+    layer1_repair_gather_whole_layers(...) layers of the range (gathered whole beside the
+    selection) and untouched in the others. The caller overwrites the kept rows of every gathered
+    layer with that layer's fresh rows, which makes both forms the same cache. Three launches."""
     if k_slab.dim() != 5 or v_slab.shape != k_slab.shape or not (k_slab.is_contiguous() and v_slab.is_contiguous()):
         raise ValueError("k_slab/v_slab must be contiguous (L, 1, H, N, D)")
     L, _, H, N, D = k_slab.shape
@@ -437,6 +440,16 @@ def layer1_repair_gather(
         "ckv_layer1_repair_gather",
     )
     return diff, norm, out
+
+
+def layer1_repair_gather_whole_layers(n_tokens: int, n_chunks: int, escalate_threshold: float | None, n_segs: int,
+                                      max_seg_tokens: int, layers: tuple[int, int], n_heads: int, head_dim: int,
+                                      dtype: torch.dtype) -> int:
+    """How many leading layers of `layers` layer1_repair_gather writes whole (kept rows included)
+    beside its selection for a request of this shape on the current device."""
+    return int(lib().ckv_layer1_repair_gather_whole_layers(
+        int(n_tokens), int(n_chunks), int(escalate_threshold is not None), int(n_segs), int(max_seg_tokens),
+        int(layers[1]) - int(layers[0]), int(n_heads), int(head_dim), dtype_code(dtype)))
 
 
 def scatter_kept_rows(

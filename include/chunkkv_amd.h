@@ -324,16 +324,24 @@ int32_t ckv_layer1_repair(void* dst_k, void* dst_v, int64_t dst_head_stride, con
                           int32_t* err, void* stream);
 
 /*
- * ckv_layer1_repair of layer `layer` followed by ckv_rerope_gather_layers of the dropped rows of
- * layers [gather_begin, gather_end) (skip map keep_rank), with the kept rows' scatter and that
- * gather in one launch: every output bit-identical to the two calls, one dependent launch fewer.
+ * ckv_layer1_repair of layer `layer` followed by the base cache of layers [gather_begin,
+ * gather_end): layer `layer` and the selection bit-identical to ckv_layer1_repair; in the gathered
+ * layers every row of a position the selection dropped bit-identical to ckv_rerope_gather_layers
+ * (the re-rotated cached row), rows of uncached positions untouched. Rows of kept cached
+ * positions: in the first W layers of the range (W = ckv_layer1_repair_gather_whole_layers of the
+ * same arguments), the re-rotated cached row (whole layers, as base_kv writes them); in the other
+ * layers untouched (ckv_rerope_gather_layers' skip map keep_rank). The caller writes the fresh
+ * rows of the kept positions into every gathered layer afterwards (as the engine does when it
+ * computes that layer), which makes both forms the same cache.
+ * Launches: the layer-1 pass; the selection, with the W whole layers gathered by workgroups
+ * beside it (the CUs the single-workgroup selection leaves idle); the kept rows' scatter with the
+ * gather of the dropped rows of the other layers.
  * k_slab/v_slab hold every layer's (H, n_tokens, D) cache, layer l at l * layer_stride elements,
  * head stride head_stride; max_seg_tokens is the longest segment (as for the gather). The other
  * arguments are ckv_layer1_repair's. keep_rank must not be NULL, and `layer` must lie outside
  * [gather_begin, gather_end).
  * Replaces: base_kv for layer 1 and the layer-1 repair (torch_engine.py:96-103, :117-156), and
- *           base_kv of the later layers for the rows their fresh rows do not overwrite
- *           (:96-103 with the overwrite of :155-156 left out).
+ *           base_kv of the later layers (:96-103) up to the overwrite of the kept rows (:155-156).
  */
 int32_t ckv_layer1_repair_gather(void* k_slab, void* v_slab, int64_t layer_stride, int64_t head_stride,
                                  const uint64_t* src_tab, int32_t n_tab_chunks, int32_t n_layers, int32_t layer,
@@ -347,6 +355,19 @@ int32_t ckv_layer1_repair_gather(void* k_slab, void* v_slab, int64_t layer_strid
                                  int64_t* keep_abs, int64_t* keep_local, int32_t* keep_rank, float* rel_dev,
                                  uint8_t* escalated, int32_t* counts, void* workspace, int64_t workspace_bytes,
                                  int32_t* err, void* stream);
+
+/*
+ * W of ckv_layer1_repair_gather: how many leading layers of the gathered range that call writes
+ * whole (kept rows included) beside its selection, for the same n_tokens, n_chunks,
+ * has_threshold, n_segs, max_seg_tokens, gather_end - gather_begin, n_heads, head_dim and dtype
+ * on the current device. 0 with a threshold, above 16384 positions, head_dim other than 64 or
+ * 128, or no segment; otherwise as many whole layers as about 8 KiB of HBM traffic per position
+ * covers (what the CUs the selection leaves free move in its time). Host only (reads the
+ * device's CU count). No counterpart in the reference.
+ */
+int32_t ckv_layer1_repair_gather_whole_layers(int32_t n_tokens, int32_t n_chunks, int32_t has_threshold,
+                                              int32_t n_segs, int32_t max_seg_tokens, int32_t gather_layers,
+                                              int32_t n_heads, int32_t head_dim, int32_t dtype);
 
 /*
  * Assemble one layer's cache with every row written once: for each segment row at position p,

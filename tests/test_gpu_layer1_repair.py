@@ -11,7 +11,12 @@ with no placement, with every position exact (no fresh row), of one token and a 
 escalation threshold, a threshold bin ranked directly and one refined by radix passes, deviations
 that tie (one histogram bin holding every candidate: more radix rounds, then equal keys ranked by
 position), NaN deviations, one workspace across calls of
-different sizes (the histogram is left zeroed), and replays of a captured HIP graph."""
+different sizes (the histogram is left zeroed), and replays of a captured HIP graph.
+
+ckv_layer1_repair_gather (the same repair, whole layers of the later layers' base cache gathered
+beside the selection, the dropped rows of the others with the kept rows' scatter) against
+layer1_repair + rerope_gather (with and without the skip map) at the 8k, config-3 and replay
+shapes, the edge requests and graph replays; the gathered layers also against the oracle."""
 
 import numpy as np
 import pytest
@@ -381,9 +386,11 @@ def test_graph_replays():
 
 
 def _merged_vs_separate(req, thr=None, ws=None, layers=None):
-    """ckv_layer1_repair_gather (layer `req.layer` repaired, the kept rows' scatter and the gather
-    of the dropped rows of `layers` in one launch) against layer1_repair + rerope_gather(layers,
-    skip=keep_rank): every layer of both slabs, the diff/norm and the selection, bit for bit."""
+    """ckv_layer1_repair_gather (layer `req.layer` repaired; the first layers of `layers` gathered
+    whole beside the selection, the kept rows' scatter and the gather of the dropped rows of the
+    others in one launch) against layer1_repair + rerope_gather(layers, skip=keep_rank), and
+    rerope_gather(layers) for the layers gathered whole: every layer of both slabs, the diff/norm
+    and the selection, bit for bit. Returns (K, V, selection, number of layers gathered whole)."""
     L = req.n_layers
     layers = (req.layer + 1, L) if layers is None else layers
     ws = ops.layer1_repair_workspace(DEV) if ws is None else ws
@@ -408,10 +415,20 @@ def _merged_vs_separate(req, thr=None, ws=None, layers=None):
     _same(sm.keep_abs[:n], ss.keep_abs[:n], "keep_abs")
     _same(sm.keep_local[:n], ss.keep_local[:n], "keep_local")
     _same(sm.keep_rank, ss.keep_rank, "keep_rank")
+    Kd, Vd = torch.full(shape, SENT, dtype=req.dtype, device=DEV), torch.full(shape, -SENT, dtype=req.dtype, device=DEV)
+    if req.n_segs:
+        ops.rerope_gather(Kd, Vd, req.tab, req.segs, req.n_segs, req.plan.max_seg_tokens, THETA, req.err,
+                          layers=layers)
+    torch.cuda.synchronize()
+    # the leading layers of the range gathered whole, as the library reports them
+    n_pre = ops.layer1_repair_gather_whole_layers(req.N, len(req.plan.spans), thr, req.n_segs, req.plan.max_seg_tokens,
+                                                  layers, req.H, req.D, req.dtype)
+    assert 0 <= n_pre <= layers[1] - layers[0]
     for li in range(L):
-        _same(Km[li], Ks[li], f"K layer {li}")
-        _same(Vm[li], Vs[li], f"V layer {li}")
-    return Km, Vm, sm
+        whole = layers[0] <= li < layers[0] + n_pre
+        _same(Km[li], Kd[li] if whole else Ks[li], f"K layer {li}")
+        _same(Vm[li], Vd[li] if whole else Vs[li], f"V layer {li}")
+    return Km, Vm, sm, n_pre
 
 
 def test_merged_gather_8k_request_shape():
@@ -421,8 +438,9 @@ def test_merged_gather_8k_request_shape():
     rng = np.random.default_rng(81)
     starts, N = _shuffled(rng, 24, 320, 576)
     req = Request(81, [320] * 24, starts, N, n_layers=5)
-    Km, Vm, sm = _merged_vs_separate(req)
+    Km, Vm, sm, n_pre = _merged_vs_separate(req)
     assert int(sm.counts[0].item()) == 2976
+    assert n_pre == 2  # ~8 KiB of traffic a position: two whole layers of 31.5 MB
     kept = _bits(sm.keep_rank) >= 0
     ks = [[_bits(ch.keys[li])[0] for li in range(5)] for ch in req.plan.chunks]
     vs = [[_bits(ch.values[li])[0] for li in range(5)] for ch in req.plan.chunks]
@@ -431,7 +449,7 @@ def test_merged_gather_8k_request_shape():
         Vo = np.zeros_like(Ko)
         assert O.rerope_gather(Ko[None], Vo[None], [[c[li]] for c in ks], [[c[li]] for c in vs], req.plan.segments,
                                THETA) == 0
-        gathered = req.plan.cached & ~kept
+        gathered = req.plan.cached & (~kept | (li < 2 + n_pre))
         np.testing.assert_array_equal(_bits(Km[li])[0][:, gathered], Ko[:, gathered], err_msg=f"K layer {li}")
         np.testing.assert_array_equal(_bits(Vm[li])[0][:, gathered], Vo[:, gathered], err_msg=f"V layer {li}")
         sent = _bits(torch.tensor(SENT, dtype=req.dtype))
@@ -442,7 +460,7 @@ def test_merged_gather_8k_request_shape():
 def test_merged_gather_config3_shape(ratio):
     starts = [(c, c * 256) for c in range(32)]
     req = Request(90 + int(ratio * 100), [256] * 32, starts, 8192, ratio=ratio, n_layers=4)
-    _merged_vs_separate(req)
+    assert _merged_vs_separate(req)[3] == 2  # both layers of the range: ~8 KiB a position
 
 
 def test_merged_gather_replay_request_shape():
@@ -453,7 +471,7 @@ def test_merged_gather_replay_request_shape():
     ids = rng.choice(24, 128, p=zipf / zipf.sum())
     starts = [(int(c), j * 256) for j, c in enumerate(ids)]
     req = Request(56, [256] * 24, starts, 128 * 256 + 64, ratio=0.15, n_layers=3)
-    _merged_vs_separate(req)
+    assert _merged_vs_separate(req)[3] == 0  # above 16384 positions: the spread selection
 
 
 @pytest.mark.parametrize("case", ["threshold", "small_f32", "no_placements", "every_position_exact", "empty_layers"])
@@ -480,3 +498,46 @@ def test_merged_gather_edges(case):
         _merged_vs_separate(req, layers=(2, 2))
         return
     _merged_vs_separate(req)
+
+
+def test_merged_gather_graph_replays():
+    """ckv_layer1_repair_gather captured once (the whole-layer gather beside the selection
+    included) and replayed three times, the slabs refilled between replays: every replay equals
+    the eager call, every layer."""
+    rng = np.random.default_rng(31)
+    starts, N = _shuffled(rng, 24, 320, 576)
+    req = Request(31, [320] * 24, starts, N, n_layers=5)
+    ws = ops.layer1_repair_workspace(DEV)
+    shape = (5, 1, req.H, N, req.D)
+    Ke, Ve = torch.full(shape, SENT, dtype=req.dtype, device=DEV), torch.full(shape, -SENT, dtype=req.dtype, device=DEV)
+    de, ne, se = ops.layer1_repair_gather(Ke, Ve, req.tab, 1, (2, 5), req.segs, req.n_segs, req.plan.max_seg_tokens,
+                                          req.k, req.v, req.flags, req.local, req.spans, None, THETA, ws, req.err)
+    torch.cuda.synchronize()
+    K, V = torch.empty_like(Ke), torch.empty_like(Ve)
+    out = ops._new_selection(N, len(req.plan.spans), DEV)
+    dn = (torch.empty_like(de), torch.empty_like(ne))
+    call = lambda: ops.layer1_repair_gather(K, V, req.tab, 1, (2, 5), req.segs, req.n_segs,  # noqa: E731
+                                            req.plan.max_seg_tokens, req.k, req.v, req.flags, req.local, req.spans,
+                                            None, THETA, ws, req.err, out, dn)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for i in range(3):
+        K.fill_(SENT)
+        V.fill_(-SENT)
+        out.keep_rank.fill_(-5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(req.err.item()) == 0
+        for li in range(5):
+            _same(K[li], Ke[li], f"K layer {li}, replay {i}")
+            _same(V[li], Ve[li], f"V layer {li}, replay {i}")
+        _same(out.keep_rank, se.keep_rank, f"keep_rank, replay {i}")
+        _same(dn[0].view(torch.int32), de.view(torch.int32), f"diff, replay {i}")
+    assert not ws.any()
