@@ -538,11 +538,12 @@ class _Tok:
 
 
 def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20) -> dict:
-    """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests, and of
-    HipEngine with the reference's own SDPA call (attention="reference": only the KV repair on the
-    HIP kernels, the attention left on PyTorch-ROCm) on the first
-    n_reference_attention of them. All run the model's library GEMMs with the same committed
-    TunableOp selection table (when present)."""
+    """TTFT p50 of HipEngine vs the reference op sequence on the same seeded requests; of HipEngine
+    with torch's fused SDPA kernels and torch's norm/MLP (attention="sdpa": the KV repair alone on
+    the HIP kernels) on all of them; and of HipEngine with the reference's own SDPA call
+    (attention="reference", its fp32 math path) on the first n_reference_attention of them. All
+    run the model's library GEMMs with the same committed TunableOp selection table (when
+    present)."""
     from chunkkv_amd.baseline import TorchOpsEngine
     from chunkkv_amd.engine import HipEngine
     from chunkkv_amd.types import BlendConfig
@@ -556,6 +557,7 @@ def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20
         "for all engines")
     hip, ref = HipEngine(model, _Tok()), TorchOpsEngine(model, _Tok())
     hip_ref_attn = HipEngine(model, _Tok(), attention="reference")
+    hip_sdpa = HipEngine(model, _Tok(), attention="sdpa")
     hip_overlap = HipEngine(model, _Tok(), overlap=True)
     gen = torch.Generator().manual_seed(7)
     vocab = model.config.vocab_size
@@ -579,6 +581,7 @@ def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20
     out = {}
     for name, eng, n_req in (("hip", hip, len(reqs)), ("torch_ops", ref, len(reqs)),
                               ("hip_attention_reference", hip_ref_attn, min(len(reqs), n_reference_attention + 2)),
+                              ("hip_torch_attention", hip_sdpa, len(reqs)),
                               ("hip_overlap", hip_overlap, min(len(reqs), n_reference_attention + 2))):
         times, stats = [], None
         for i, (tokens, placements) in enumerate(reqs[:n_req]):
@@ -594,7 +597,7 @@ def bench_ttft(n_requests: int, dev, model=None, n_reference_attention: int = 20
         out[name] = dict(p50=float(np.percentile(times, 50)), p99=float(np.percentile(times, 99)), stats=stats,
                          tuned_gemms=tuned, requests=len(times))
         log(f"[bench] TTFT {name}: p50 {out[name]['p50']:.2f} ms  p99 {out[name]['p99']:.2f} ms")
-    del hip, ref, hip_ref_attn, hip_overlap
+    del hip, ref, hip_ref_attn, hip_sdpa, hip_overlap
     torch.cuda.empty_cache()
     out["model"] = model
     return out
@@ -796,11 +799,14 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
     chunks x 256 tokens x 2 context variants (7.0 GiB); 4 concurrent requests of 128 chunks
     sampled with replacement (Zipf s=1.1) at random order + a 64-token query (32832 tokens), 15%
     recompute + 4 sinks. Each request's KV repair is the engine's launch sequence (layer 0's fresh
-    rows; layer 1's repair as one ckv_layer1_repair call: base cache with the deviation, selection,
-    kept rows; the gather of the dropped rows of layers 2-27; the fresh rows of layers 2-27) on its
-    own HIP stream, with a layer-1 workspace per request. Then TTFT
-    p50/p99 of HipEngine.prefill + last_logprobs on requests of the same shape (random-init
-    Qwen2.5-7B architecture, bf16; the store's K/V serve as the cached chunks), one at a time."""
+    rows; layer 1's repair with the base cache of layers 2-27 as one ckv_layer1_repair_gather call:
+    base cache with the deviation, the selection, the kept rows with the gather of the dropped rows
+    of layers 2-27; the fresh rows of layers 2-27) on its own HIP stream, with a layer-1 workspace
+    and an error flag per request (asserted zero). The rounds are timed with layer-1 rows that
+    follow the cached ones (per-chunk noise) and again with uncorrelated random rows (the
+    selection's hardest input). Then TTFT p50/p99 of HipEngine.prefill + last_logprobs on requests
+    of the same shape (random-init Qwen2.5-7B architecture, bf16; the store's K/V serve as the
+    cached chunks), one at a time and with 4 requests in flight."""
     from chunkkv_amd import ops
     from chunkkv_amd.planner import local_index, plan_request
 
@@ -849,6 +855,7 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
                          spans=torch.from_numpy(plan.spans.reshape(-1)).to(dev),
                          layer0=torch.from_numpy(plan.layer0_idx.astype(np.int64)).to(dev), proj=proj,
                          fresh1=(k1, v1.transpose(1, 2)), sel=None,
+                         err=torch.zeros(1, dtype=torch.int32, device=dev),
                          ws=ops.layer1_repair_workspace(dev),
                          dn=(torch.empty(N, dtype=torch.float32, device=dev),
                              torch.empty(N, dtype=torch.float32, device=dev))))
@@ -856,19 +863,21 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
     streams = request_streams(n_streams, dev)
 
     def repair(rq):
-        plan = rq["plan"]
+        """The request's KV repair as HipEngine issues it: layer 0's fresh rows; layer 1's repair
+        with the base cache of layers 2-27 (ckv_layer1_repair_gather); layers 2-27's fresh rows."""
+        plan, err = rq["plan"], rq["err"]
         K, V = rq["K"].unbind(0), rq["V"].unbind(0)
         nseg, mseg = len(plan.segments), plan.max_seg_tokens
         ops.rope_qkv(None, *rq["proj"][0], rq["layer0"], 0, N_KV, HEAD_DIM, THETA, k_out=K[0], v_out=V[0],
-                     rows=rq["layer0"])
+                     rows=rq["layer0"], err=err)
         k1, v1 = rq["fresh1"]
-        _, _, rq["sel"] = ops.layer1_repair(K[1], V[1], rq["tab"], N_LAYERS, 1, rq["segs"], nseg, k1, v1, rq["flags"],
-                                            rq["local"], rq["spans"], None, THETA, rq["ws"], None, rq["sel"], rq["dn"])
+        _, _, rq["sel"] = ops.layer1_repair_gather(rq["K"], rq["V"], rq["tab"], 1, (2, N_LAYERS), rq["segs"], nseg,
+                                                   mseg, k1, v1, rq["flags"], rq["local"], rq["spans"], None, THETA,
+                                                   rq["ws"], err, rq["sel"], rq["dn"])
         rows = rq["sel"].keep_abs[: plan.n_keep]
-        ops.rerope_gather(rq["K"], rq["V"], rq["tab"], rq["segs"], nseg, mseg, THETA, layers=(2, N_LAYERS),
-                          skip=rq["sel"].keep_rank)
         for li in range(2, N_LAYERS):
-            ops.rope_qkv(None, *rq["proj"][li], rows, 0, N_KV, HEAD_DIM, THETA, k_out=K[li], v_out=V[li], rows=rows)
+            ops.rope_qkv(None, *rq["proj"][li], rows, 0, N_KV, HEAD_DIM, THETA, k_out=K[li], v_out=V[li], rows=rows,
+                         err=err)
 
     def round_(i):
         base = (i % 2) * n_streams
@@ -891,6 +900,21 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
     per_req = sum(repair_bytes_for(rq["plan"]) for rq in reqs[:n_streams]) / n_streams
     nbytes = per_req * n_streams
     assert all(int(rq["sel"].counts[0].item()) == rq["plan"].n_keep for rq in reqs)
+    assert all(int(rq["err"].item()) == 0 for rq in reqs)
+    # The same rounds with uncorrelated layer-1 rows (every fresh row random): every candidate's
+    # deviation lies within a few percent of the others, the selection's hardest input.
+    for rq in reqs:
+        k1 = torch.randn((1, N_KV, N, HEAD_DIM), generator=gen, device=dev).bfloat16()
+        v1 = torch.randn((1, N_KV, N, HEAD_DIM), generator=gen, device=dev).bfloat16().transpose(1, 2).contiguous()
+        rq["fresh1"] = (k1, v1.transpose(1, 2))
+    for i in range(2):
+        round_(i)
+    graphs_u = [_graph_of(lambda i=i: round_(i)) for i in range(2)]
+    for g in graphs_u:
+        g.replay()
+    ms_uncorr = _timed(lambda i: graphs_u[i % 2].replay(), steps, torch.cuda.current_stream(dev))
+    assert all(int(rq["sel"].counts[0].item()) == rq["plan"].n_keep for rq in reqs)
+    assert all(int(rq["err"].item()) == 0 for rq in reqs)
     line = _workload_line(
         "aggregate KV-repair HBM GB/s, 4 concurrent 32k-token requests, Qwen2.5-7B KV shape", nbytes / (ms * 1e-3) / 1e9,
         ms, steps, warmup,
@@ -900,9 +924,11 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         None)
     line["store_gib"] = round(len(store) * N_LAYERS * 2 * N_KV * L * HEAD_DIM * 2 / 2**30, 2)
     line["ms_per_step_eager"] = round(ms_eager, 4)
+    line["ms_per_step_uncorrelated"] = round(ms_uncorr, 4)
+    line["uncorrelated_over_correlated"] = round(ms_uncorr / ms, 4)
     for rq in reqs:  # free the repair buffers before the model comes in
         rq.clear()
-    del reqs, graphs
+    del reqs, graphs, graphs_u
     torch.cuda.empty_cache()
     if ttft_requests > 0:
         from chunkkv_amd.engine import HipEngine
@@ -929,13 +955,73 @@ def bench_replay(steps: int, warmup: int, dev, n_streams: int = 4, ttft_requests
         line["ttft_p50_ms"] = round(float(np.percentile(times, 50)), 2)
         line["ttft_p99_ms"] = round(float(np.percentile(times, 99)), 2)
         line["ttft_requests"] = len(times)
-        line["ttft_note"] = ("HipEngine, one request at a time; the reference op sequence is not timed at 32k "
-                             "(its math-path SDPA would hold ~120 GB of fp32 scores per layer)")
+        conc = _concurrent_ttft(model, cfg, placements_of, n_streams, max(ttft_requests, 20), N, vocab, dev)
+        line["ttft_p50_ms_concurrent"] = round(float(np.percentile(conc, 50)), 2)
+        line["ttft_p99_ms_concurrent"] = round(float(np.percentile(conc, 99)), 2)
+        line["ttft_requests_concurrent"] = len(conc)
+        line["ttft_note"] = ("HipEngine; ttft_p50_ms / ttft_p99_ms one request at a time, *_concurrent with "
+                             f"{n_streams} requests in flight (one host thread, HipEngine and HIP stream per "
+                             "request, each request's prefill + last_logprobs timed from the round's start); "
+                             "the reference op sequence is not timed at 32k (its math-path SDPA would hold "
+                             "~120 GB of fp32 scores per layer)")
         del hip
         if own_model:
             del model
         torch.cuda.empty_cache()
     return line
+
+
+def _concurrent_ttft(model, cfg, placements_of, n_streams: int, rounds: int, N: int, vocab: int, dev) -> list:
+    """TTFT (ms) of `rounds` rounds of n_streams concurrent HipEngine prefills + last_logprobs, one
+    host thread, engine (weights shared) and request stream per request; a round's requests start
+    together (a barrier) and each is timed from the round's start to its own logprobs. One warm-up
+    round first."""
+    import threading
+
+    from chunkkv_amd.engine import HipEngine
+
+    streams = request_streams(n_streams, dev)
+    engines = [HipEngine(model, _Tok()) for _ in range(n_streams)]
+    times: list[float] = []
+    errors: list[BaseException] = []
+    for rnd in range(rounds + 1):
+        toks = [torch.randint(0, vocab, (N,), generator=torch.Generator().manual_seed(1000 + rnd * n_streams + j)).tolist()
+                for j in range(n_streams)]
+        start = threading.Barrier(n_streams + 1)
+        t0 = [0.0]
+        out = [0.0] * n_streams
+
+        def run(j):
+            try:
+                torch.cuda.set_device(dev)
+                with torch.cuda.stream(streams[j]):
+                    start.wait()
+                    res = engines[j].prefill(toks[j], placements_of[(rnd * n_streams + j) % len(placements_of)], cfg)
+                    engines[j].last_logprobs(res)
+                    out[j] = (time.perf_counter() - t0[0]) * 1e3
+                    del res
+            except BaseException as e:  # reported below, after every thread ended
+                errors.append(e)
+                start.abort()
+
+        threads = [threading.Thread(target=run, args=(j,)) for j in range(n_streams)]
+        for th in threads:
+            th.start()
+        torch.cuda.synchronize()
+        t0[0] = time.perf_counter()
+        try:
+            start.wait()
+        except threading.BrokenBarrierError:
+            pass
+        for th in threads:
+            th.join()
+        if errors:
+            raise errors[0]
+        if rnd:
+            times += out
+    del engines
+    torch.cuda.synchronize()
+    return times
 
 
 def traffic_probe(steps: int, warmup: int, dev) -> dict:
@@ -1178,7 +1264,9 @@ def _config_summary(line: dict) -> dict:
         rf = line["roofline"]
         out["roofline"] = {k: rf[k] for k in ("kernel", "achieved", "peak", "frac", "bytes_per_launch", "avg_launch_us")
                            if k in rf}
-    for k in ("ratios", "store_gib", "ms_per_step_eager", "ttft_p50_ms", "ttft_p99_ms", "ttft_requests"):
+    for k in ("ratios", "store_gib", "ms_per_step_eager", "ms_per_step_uncorrelated", "uncorrelated_over_correlated",
+              "ttft_p50_ms", "ttft_p99_ms", "ttft_requests", "ttft_p50_ms_concurrent", "ttft_p99_ms_concurrent",
+              "ttft_requests_concurrent", "ttft_note"):
         if k in line:
             out[k] = line[k]
     return out
@@ -1315,6 +1403,9 @@ def main() -> None:
         line["ttft_p50_ms_attention_reference"] = round(ttft["hip_attention_reference"]["p50"], 2)
         line["ttft_p99_ms_attention_reference"] = round(ttft["hip_attention_reference"]["p99"], 2)
         line["ttft_requests_attention_reference"] = ttft["hip_attention_reference"]["requests"]
+        # KV repair on the HIP kernels, attention on torch's fused SDPA kernels, norm/MLP on torch
+        line["ttft_p50_ms_torch_attention"] = round(ttft["hip_torch_attention"]["p50"], 2)
+        line["ttft_p99_ms_torch_attention"] = round(ttft["hip_torch_attention"]["p99"], 2)
         # the same engine with the dropped-row gather on a side stream (HipEngine(overlap=True))
         line["ttft_p50_ms_side_stream"] = round(ttft["hip_overlap"]["p50"], 2)
     if configs:

@@ -48,7 +48,12 @@ run every layer on the HIP kernel ckv_attention_active, which reads the position
 mask tensor, no KV-head expansion). Other models use SDPA with ``is_causal=True`` when every
 position is active (the mask is then the plain causal mask) and otherwise expand the KV heads and
 pass the boolean mask (built once per active set) without enable_gqa.
-``attention="reference"`` reproduces the reference's SDPA call exactly.
+``attention="sdpa"`` runs the prefill's attention on torch's fused SDPA kernels (flash or
+memory-efficient, selected explicitly so that the math path never runs: K/V heads repeated per
+query group, ``is_causal=True`` or the boolean positions mask) and the norms and MLP on torch,
+with every KV-repair kernel as in the default: it isolates what the KV repair alone gains
+(decode keeps ckv_attention_active). ``attention="reference"`` reproduces the reference's SDPA
+call exactly.
 
 Contracts where the reference leaves the result open: the selection breaks deviation ties by
 the lower token index (torch's argsort is unstable), deviation sums use a fixed order, and
@@ -63,6 +68,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from chunkkv_amd import _native, ops
 from chunkkv_amd.model import DecoderPieces
@@ -122,10 +128,15 @@ def _stack_params(mods: list, name: str) -> torch.Tensor | None:
 class HipEngine(DecoderPieces):
     def __init__(self, model, tokenizer, attention: str = "fused", overlap: bool = False,
                  layer1: str = "one_call"):
-        if attention not in ("fused", "reference"):
-            raise ValueError("attention must be 'fused' or 'reference'")
+        if attention not in ("fused", "sdpa", "reference"):
+            raise ValueError("attention must be 'fused', 'sdpa' or 'reference'")
         if layer1 not in ("one_call", "four_launches", "fused_select"):
             raise ValueError("layer1 must be 'one_call', 'four_launches' or 'fused_select'")
+        # attention: "fused" (default) = ckv_attention_active and the fused norm/MLP kernels;
+        # "sdpa" = torch's fused SDPA kernels (flash / memory-efficient, never the math path) for
+        # the active rows and torch's RMSNorm and MLP, every KV-repair kernel unchanged (isolates
+        # what the KV repair alone gains); "reference" = the reference op sequence's attention
+        # (torch_engine.py's masked SDPA) and torch's norm/MLP.
         self.attention = attention
         # Layer 1's repair: "one_call" (default) is ckv_layer1_repair (the cached rows gathered with
         # the deviations, the selection, the kept rows; 3 launches); "four_launches" gathers layer
@@ -248,17 +259,30 @@ class HipEngine(DecoderPieces):
         if self.attention == "reference":
             return self._attend(layer, h, q, K, V, active[:, None] >= ar[None, :]), None
         attn = layer.self_attn
-        if self._native_attention:
+        if self._native_attention and self.attention == "fused":
             # positions-only mask on the matrix-core kernel; output already token-major
             o = ops.attention_active(q, K, V, active, err=err)
             return self._mlp(li, layer, h, attn.o_proj(o.view(h.shape[0], h.shape[1], -1)))
-        if n_act == N:  # active == arange(N): the mask is exactly the causal mask
+        group = self.n_heads // self.n_kv
+        if self.attention == "sdpa":
+            # torch's fused kernels only: K/V repeated per query group (their GQA form), the
+            # causal flag for a full prefill, the positions mask otherwise
+            if group > 1:
+                K, V = K.repeat_interleave(group, dim=1), V.repeat_interleave(group, dim=1)
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                if n_act == N:
+                    o = F.scaled_dot_product_attention(q, K, V, is_causal=True)
+                else:
+                    if key not in masks:
+                        masks.clear()
+                        masks[key] = active[:, None] >= ar[None, :]
+                    o = F.scaled_dot_product_attention(q, K, V, attn_mask=masks[key])
+        elif n_act == N:  # active == arange(N): the mask is exactly the causal mask
             o = F.scaled_dot_product_attention(q, K, V, is_causal=True, enable_gqa=True)
         else:
             if key not in masks:
                 masks.clear()
                 masks[key] = active[:, None] >= ar[None, :]
-            group = self.n_heads // self.n_kv
             if group > 1:
                 K, V = K.repeat_interleave(group, dim=1), V.repeat_interleave(group, dim=1)
             o = F.scaled_dot_product_attention(q, K, V, attn_mask=masks[key])
@@ -396,7 +420,7 @@ class HipEngine(DecoderPieces):
             Ks[li, :, :, :N].copy_(result.keys[li])
             Vs[li, :, :, :N].copy_(result.values[li])
         err = torch.zeros(1, dtype=torch.int32, device=dev)
-        device_loop = self._native_attention and self.attention == "fused"
+        device_loop = self._native_attention and self.attention in ("fused", "sdpa")
         tok = torch.tensor([[nxt]], dtype=torch.int64, device=dev)
         where = torch.tensor([N], dtype=torch.int64, device=dev)
         graph = None

@@ -150,3 +150,19 @@ def test_full_size_layer1_four_launches_identical(setup):
     assert torch.equal(a.logits, b.logits) and a.stats == b.stats
     for li in (0, 1, 2, 27):
         assert torch.equal(a.keys[li], b.keys[li]) and torch.equal(a.values[li], b.values[li])
+
+
+def test_full_size_sdpa_mode_matches_reference_ops(setup):
+    """HipEngine(attention="sdpa"): every KV-repair kernel, torch's fused SDPA kernels for the
+    attention and torch's norm/MLP, against the reference op sequence at the 8k request: the same
+    stats, next-token distributions within the KL bound."""
+    model, _, tokens, placements = setup
+    cfg = BlendConfig(recompute_ratio=0.3, n_sink=4)
+    a = HipEngine(model, StubTokenizer(), attention="sdpa").prefill(tokens, placements, cfg)
+    b = TorchOpsEngine(model, StubTokenizer()).prefill(tokens, placements, cfg)
+    for k in ("cached_tokens", "recomputed_cached_tokens", "prefill_token_equiv"):
+        assert a.stats[k] == b.stats[k], k
+    assert a.stats["recomputed_cached_tokens"] == 2304 + 96
+    kl = _kl(b.logits, a.logits)
+    print(f"KL(reference ops || HipEngine sdpa) at the last position: {kl:.3e}")
+    assert kl < 1e-2

@@ -257,17 +257,41 @@ def test_rerope_gather_many_segments(bf16, D):
         assert (Ks[l][:, kept] == sent).all() and (Vs[l][:, kept] == sent).all()
 
 
+def _rope_rows(x, pos, theta):
+    """x (..., n, D) fp32 rotated at positions pos (n,) (rotate-half, torch_engine.py:46-54): angles
+    in fp64, the rotation in fp32."""
+    D = x.shape[-1]
+    inv = theta ** (-torch.arange(0, D, 2, dtype=torch.float64, device=x.device) / D)
+    ang = pos.to(torch.float64)[:, None] * inv[None, :]
+    c, s = ang.cos().float(), ang.sin().float()
+    x1, x2 = x[..., : D // 2], x[..., D // 2 :]
+    return torch.cat((x1 * c - x2 * s, x1 * s + x2 * c), -1)
+
+
 def test_rerope_gather_config2_full_size():
-    """Re-RoPE + gather at the Qwen2.5-7B KV shape: 28 layers, 4 heads, D=128, bf16,
-    16 chunks x 256 tokens moved by delta ~ U[-4096, 4096] into a 4096-token cache."""
+    """Re-RoPE + gather at the Qwen2.5-7B KV shape (the re-RoPE microbenchmark's workload): 28
+    layers, 4 heads, D=128, bf16, theta 1e6; 16 chunks x 256 tokens whose keys are N(0,1) vectors
+    x rotated at their original positions p_c + t, moved by delta_c ~ U[-4096, 4096] to slot
+    dst_c of a 4096-token cache (p_c = dst_c - delta_c, negative for some chunks: RoPE is defined
+    there too). Bit-exact against the oracle; and the gathered keys equal x rotated at the new
+    positions dst_c + t (the shift property of torch_engine.py:56-59, the reference's
+    tests/test_rerope.py::test_shift_moves_keys_to_new_offset) within the rounding of the two
+    steps: each element off by at most 2^-7 r, r the radius of its (x_i, x_i+D/2) pair (the rotations
+    preserve it; the cached keys' bf16 rounding and the result's each add 2^-9 r, the fp32 shift
+    angle at |delta| <= 4096 at most 2.5e-4 r)."""
     rng = np.random.default_rng(2)
     n_layers, H, D, L, C = 28, 4, 128, 256, 16
     N = L * C
-    dst_slots = rng.permutation(C)
+    dst = rng.permutation(C) * L
     deltas = rng.integers(-4096, 4097, C)
-    Kc = torch.randn((C, n_layers, 1, H, L, D), device=DEV).to(torch.bfloat16)
-    Vc = torch.randn((C, n_layers, 1, H, L, D), device=DEV).to(torch.bfloat16)
-    segs = np.array([[dst_slots[c] * L, L, c, 0, L, deltas[c]] for c in range(C)], dtype=np.int32)
+    g = torch.Generator(device=DEV).manual_seed(2)
+    t = torch.arange(L, device=DEV)
+    X = torch.randn((C, n_layers, 1, H, L, D), generator=g, device=DEV)
+    Kc = torch.empty((C, n_layers, 1, H, L, D), dtype=torch.bfloat16, device=DEV)
+    for c in range(C):
+        Kc[c] = _rope_rows(X[c], int(dst[c] - deltas[c]) + t, THETA).to(torch.bfloat16)
+    Vc = torch.randn((C, n_layers, 1, H, L, D), generator=g, device=DEV).to(torch.bfloat16)
+    segs = np.array([[dst[c], L, c, 0, L, deltas[c]] for c in range(C)], dtype=np.int32)
     tab = np.zeros((C, n_layers, 2), dtype=np.uint64)
     for c in range(C):
         for l in range(n_layers):
@@ -280,6 +304,14 @@ def test_rerope_gather_config2_full_size():
                       C, L, THETA, err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
+    # the shift property, every layer and chunk
+    for c in range(C):
+        want = _rope_rows(X[c], int(dst[c]) + t, THETA)  # (n_layers, 1, H, L, D)
+        r = torch.sqrt(X[c][..., : D // 2] ** 2 + X[c][..., D // 2 :] ** 2)
+        got = K[:, :, :, dst[c] : dst[c] + L].float()
+        bad = (got - want).abs() > 2.0 ** -7 * torch.cat((r, r), -1) + 1e-6
+        assert not bad.any(), f"chunk {c} (delta {deltas[c]}): {int(bad.sum())} keys off"
+    del X
     Kc_h, Vc_h = host(Kc), host(Vc)
     Ko = np.empty((n_layers, H, N, D), dtype=np.uint16)
     Vo = np.empty_like(Ko)
