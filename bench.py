@@ -1368,6 +1368,7 @@ def main() -> None:
         },
         "pct_of_peak": round(100.0 * r["gbs"] / PEAK_GBS, 2),
         "moved_gbs": round(r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9, 2),
+        "pct_of_peak_moved": round(100.0 * r["moved"] / (r["ms_per_step"] * 1e-3) / 1e9 / PEAK_GBS, 2),
         "ms_per_step_two_streams": round(r["ms_two"], 4),
         "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
         "ms_per_step_layer1_four_launches": round(r["ms_split"], 4),

@@ -55,6 +55,14 @@ with every KV-repair kernel as in the default: it isolates what the KV repair al
 (decode keeps ckv_attention_active). ``attention="reference"`` reproduces the reference's SDPA
 call exactly.
 
+Side effect on the caller's model: the constructor stacks each layer's q/k/v weights (and, with
+the fused MLP, gate/up) into one tensor per layer and re-points the model's q_proj/k_proj/v_proj
+(gate_proj/up_proj) Parameters at row views of it, so the weights are held once and the model
+keeps working. Moving or converting the model afterwards (model.to(...), .half()) or assigning
+new Parameters to those modules leaves the engine's stacks on the old weights: build the engine
+after the model is in its final place and dtype, and build a new one after changing it. A second
+engine over the same model views the existing stacks instead of copying them.
+
 Contracts where the reference leaves the result open: the selection breaks deviation ties by
 the lower token index (torch's argsort is unstable), deviation sums use a fixed order, and
 inv_freq is the correctly rounded fp32 value of the reference's expression (torch's fp32 pow
