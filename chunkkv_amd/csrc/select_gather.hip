@@ -6,10 +6,16 @@
 // selection's rank map, but a layer gathered in full (every cached row, as the reference's
 // base_kv writes it, torch_engine.py:96-103) does not: its kept rows are overwritten by the fresh
 // rows when that layer is computed (:155-156). This launch therefore gathers the first layers of
-// the range in full, one (segment, 64-token tile, layer) per 1024-thread workgroup, in the CUs
-// the selection leaves free; the gather launch after it takes the remaining layers with the rank
-// map. Workgroup 0 selects, workgroups 1..sum_groups compute the chunks' relative deviations (as
-// in select.hip), the rest gather.
+// the range in full in the CUs the selection leaves free (one 1024-thread workgroup per CU), and
+// the gather launch after it takes the remaining layers with the rank map. Workgroup 0 selects,
+// workgroups 1..sum_groups compute the chunks' relative deviations (as in select.hip), the rest
+// gather.
+//
+// The gather's work items are one pass of the workgroup each (RPP rows: every head of RPP / H
+// consecutive tokens of one segment and layer), tile fastest, strided over the gather
+// workgroups; each workgroup keeps two items in flight: the next item's loads (and its cos/sin
+// table) go out before the current item's rotation and stores, so reads and writes overlap. The
+// per-item work and rounding are rerope_gather's (gather_common.hpp).
 #include <atomic>
 
 #include "gather_common.hpp"
@@ -17,10 +23,115 @@
 
 namespace ckv {
 
-#ifndef CKV_PREGATHER_TILE
-#define CKV_PREGATHER_TILE 64
-#endif
-constexpr int kPreTile = CKV_PREGATHER_TILE, kPreUnroll = 2;  // tokens per gather workgroup, row slots per thread
+// rows per item (one per thread group of D/2 / VEC threads): kSelThreads / that
+template <int DTYPE, int D>
+constexpr int pre_rows() {
+  return kSelThreads / (D / 2 / Elem<DTYPE>::kVec);
+}
+
+template <int DTYPE, int D>
+__device__ __forceinline__ void pregather_items(const PreGather& g, int it, int stride) {
+  using E = Elem<DTYPE>;
+  constexpr int VEC = E::kVec;
+  constexpr int HALF = D / 2;
+  constexpr int TPR = HALF / VEC;
+  constexpr int RPP = pre_rows<DTYPE, D>();
+  constexpr int64_t ROW_B = (int64_t)D * E::kBytes;
+  constexpr int HALF_B = HALF * E::kBytes;
+  static_assert(kSelThreads % TPR == 0 && kSelThreads >= HALF, "rows must tile the workgroup");
+  __shared__ float2 cs_tab[2][HALF];  // the cos/sin tables of the two items in flight
+
+  // each cos/sin lane's inverse frequency from the argument scalars (no vector load)
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int ln = (int)threadIdx.x % kWave;
+  float my_inv = 0.0f;
+#pragma unroll
+  for (int k = 0; k < HALF; ++k) {
+    if (k / kWave == wave) my_inv = ln == k % kWave ? g.inv.v[k] : my_inv;  // uniform test, scalar operand
+  }
+  const int col = (int)threadIdx.x % TPR;
+  const int r = (int)threadIdx.x / TPR;  // row of the item: head r / tpi, token r % tpi
+  const int tpi = RPP / g.n_heads;       // tokens per item (the host checks n_heads divides RPP)
+  const int head = r / tpi, tok = r % tpi;
+  const int64_t col_b = (int64_t)col * 16;
+
+  struct Slot {
+    vec16 k1, k2, v1, v2;
+    char* dk;
+    char* dv;
+    bool live, rot;
+  };
+  // item -> (tile, segment, layer): its loads and its cos/sin table
+  auto prepare = [&](int item, Slot& sl, float2* tab) {
+    sl.live = false;
+    sl.rot = false;
+    if (item >= g.n_items) return;  // uniform
+    const int tile = item % g.tiles, rest = item / g.tiles;
+    const int layer = g.layer_begin + rest / g.n_segs;
+    typedef __attribute__((address_space(1))) const int32_t gi32;
+    gi32* f = (gi32*)(g.segs + rest % g.n_segs);
+    const ckv_segment s{f[0], f[1], f[2], f[3], f[4], f[5]};
+    const int t0 = tile * tpi;
+    if (t0 >= s.n_tokens) return;  // uniform: past this segment's end
+    if (s.dst_start < 0 || s.src_start < 0 || s.chunk < 0 || s.chunk >= g.n_tab_chunks ||
+        (int64_t)s.dst_start + s.n_tokens > g.n_tokens || (int64_t)s.src_start + s.n_tokens > s.src_len) {
+      if (threadIdx.x == 0) flag_error(g.err, CKV_DEVICE_ERR_RANGE);
+      return;
+    }
+    const int64_t ti = ((int64_t)s.chunk * g.n_layers + layer) * 2;
+    const char* src_k = reinterpret_cast<const char*>(g.tab[ti]);
+    const char* src_v = reinterpret_cast<const char*>(g.tab[ti + 1]);
+    sl.rot = s.delta != 0;
+    if (sl.rot && (int)threadIdx.x < HALF) tab[threadIdx.x] = shift_cos_sin(my_inv, s.delta);
+    if (tok < s.n_tokens - t0) {
+      const int64_t so = (int64_t)head * s.src_len * ROW_B + (int64_t)(s.src_start + t0 + tok) * ROW_B + col_b;
+      const int64_t d = (int64_t)layer * g.ls_b + (int64_t)head * g.hs_b + (int64_t)(s.dst_start + t0 + tok) * ROW_B + col_b;
+      sl.k1 = gather_ld(src_k + so);
+      sl.k2 = gather_ld(src_k + so + HALF_B);
+      sl.v1 = gather_ld(src_v + so);
+      sl.v2 = gather_ld(src_v + so + HALF_B);
+      sl.dk = g.dk + d;
+      sl.dv = g.dv + d;
+      sl.live = true;
+    }
+  };
+  auto finish = [&](const Slot& sl, const float2* tab) {
+    if (!sl.live) return;
+    if (sl.rot) {
+      float c[VEC], sn[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float2 t = tab[col * VEC + e];
+        c[e] = t.x;
+        sn[e] = t.y;
+      }
+      vec16 y1, y2;
+      rotate_pairs<DTYPE>(sl.k1, sl.k2, c, sn, y1, y2);
+      gather_st(sl.dk, y1);
+      gather_st(sl.dk + HALF_B, y2);
+    } else {
+      gather_st(sl.dk, sl.k1);
+      gather_st(sl.dk + HALF_B, sl.k2);
+    }
+    gather_st(sl.dv, sl.v1);
+    gather_st(sl.dv + HALF_B, sl.v2);
+  };
+
+  Slot a, b;
+  int cur = 0;
+  prepare(it, a, cs_tab[0]);
+  for (;;) {
+    const int nxt = it + stride;
+    prepare(nxt, b, cs_tab[cur ^ 1]);  // the next item's loads go out before this item's stores
+    __syncthreads();                   // this item's table written
+    finish(a, cs_tab[cur]);
+    if (nxt >= g.n_items) break;  // uniform
+    __syncthreads();              // this item's table read: the next prepare may rewrite it
+    a = b;
+    cur ^= 1;
+    it = nxt;
+  }
+}
 #ifndef CKV_PREGATHER_BYTES_PER_POS
 #define CKV_PREGATHER_BYTES_PER_POS 8192
 #endif
@@ -33,16 +144,7 @@ __global__ __launch_bounds__(kSelThreads) void select_gather_kernel(const float*
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
   const int sel_blocks = 1 + g.sum_groups;
   if ((int)blockIdx.x >= sel_blocks) {  // uniform: a gather workgroup
-    // items (tile, segment, layer), tile fastest, strided over the gather workgroups: the
-    // workgroups in flight together stream neighbouring tiles
-    const int n_blocks = (int)gridDim.x - sel_blocks;
-    for (int it = (int)blockIdx.x - sel_blocks; it < g.n_items; it += n_blocks) {
-      const int rest = it / g.tiles;
-      gather_tile<DTYPE, D, kSelThreads, kPreTile, kPreUnroll, false>(
-          g.dk, g.dv, g.ls_b, g.hs_b, g.tab, g.n_tab_chunks, g.segs, rest % g.n_segs, ckv_segment{}, 0, 0, 0,
-          g.n_layers, g.layer_begin + rest / g.n_segs, it % g.tiles, g.n_heads, g.n_tokens, nullptr, g.inv, g.err);
-      __syncthreads();  // the next item rewrites the cos/sin table
-    }
+    pregather_items<DTYPE, D>(g, (int)blockIdx.x - sel_blocks, (int)gridDim.x - sel_blocks);
     return;
   }
   a.diff = diff;
@@ -60,6 +162,11 @@ __global__ __launch_bounds__(kSelThreads) void select_gather_kernel(const float*
   ckv_chunk_span sp[kSelPre<KPT>];
   load_first_spans<KPT>(a.chunks, a.n_chunks, wave, sp);
   select_run<KPT, false>(a, ghist, masks, sp);
+}
+
+static int pre_rows_of(int dtype, int head_dim) {
+  if (dtype == CKV_DTYPE_BF16) return head_dim == 64 ? pre_rows<CKV_DTYPE_BF16, 64>() : pre_rows<CKV_DTYPE_BF16, 128>();
+  return head_dim == 64 ? pre_rows<CKV_DTYPE_F32, 64>() : pre_rows<CKV_DTYPE_F32, 128>();
 }
 
 static int cu_count() {
@@ -81,12 +188,15 @@ int32_t pregather_layers(int32_t n_tokens, int32_t n_chunks, int32_t has_thresho
   if (has_threshold != 0 || n_tokens <= 0 || kpt > kSelRegMax || !shape_ok || max_layers <= 0 || max_seg_tokens <= 0 ||
       n_segs <= 0 || n_heads <= 0 || n_chunks < 0)
     return 0;
+  const int rows = pre_rows_of(dtype, head_dim);
+  if (rows % n_heads != 0) return 0;  // an item is every head of rows / n_heads tokens
+  const int tpi = rows / n_heads;
   // whole layers of about CKV_PREGATHER_BYTES_PER_POS bytes per position in all (the HBM traffic
   // that fits the selection's time), on the CUs the selection leaves free
   const int64_t sum_groups = ((int64_t)n_chunks + kSelWaves - 1) / kSelWaves;
-  const int64_t per_layer_tiles = ((int64_t)max_seg_tokens + kPreTile - 1) / kPreTile * n_segs;
+  const int64_t per_layer_tiles = ((int64_t)max_seg_tokens + tpi - 1) / tpi * n_segs;
   const int64_t eb = dtype == CKV_DTYPE_BF16 ? 2 : 4;
-  const int64_t per_layer_bytes = per_layer_tiles * kPreTile * n_heads * head_dim * eb * 4;
+  const int64_t per_layer_bytes = per_layer_tiles * tpi * n_heads * head_dim * eb * 4;
   if (cu_count() - 1 - sum_groups <= 0 || per_layer_tiles > (1 << 24)) return 0;
   const int64_t k = std::min<int64_t>(max_layers, (int64_t)n_tokens * CKV_PREGATHER_BYTES_PER_POS / per_layer_bytes);
   return (int32_t)std::max<int64_t>(k, 0);
@@ -104,7 +214,8 @@ int32_t select_gather_launch(const SelectArgs& args, uint32_t* ghist, PreGather 
   const int W = (n_tokens + 31) / 32;
   const size_t lds = (size_t)W * 2 * sizeof(uint32_t);
   g.sum_groups = (args.n_chunks + kSelWaves - 1) / kSelWaves;
-  g.tiles = (max_seg_tokens + kPreTile - 1) / kPreTile;
+  const int tpi = pre_rows_of(dtype, head_dim) / g.n_heads;
+  g.tiles = (max_seg_tokens + tpi - 1) / tpi;
   g.n_items = k * g.tiles * g.n_segs;
   // one 1024-thread workgroup per CU the selection leaves free (no more than there are items)
   const int blocks = std::min<int>(g.n_items, cu_count() - 1 - g.sum_groups);
