@@ -1316,7 +1316,11 @@ def main() -> None:
         fn = {"gather": bench_gather_only, "deviation": bench_deviation_topk, "replay": bench_replay,
               "traffic": traffic_probe, "dropped": bench_dropped, "attention": bench_attention,
               "extract": bench_extract, "decode": bench_decode}[args.workload]
-        print(json.dumps(fn(args.steps, args.warmup, dev)), flush=True)
+        if args.workload == "replay":
+            print(json.dumps(bench_replay(args.steps, args.warmup, dev, ttft_requests=args.replay_ttft_requests)),
+                  flush=True)
+        else:
+            print(json.dumps(fn(args.steps, args.warmup, dev)), flush=True)
         return
 
     r = bench_repair(args.steps, args.warmup, dev)
