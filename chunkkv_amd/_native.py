@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libchunkkv_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 CKV_OK = 0
 CKV_ERR_INVALID_ARGUMENT = 1
@@ -35,8 +35,8 @@ COUNT_BAD_SPANS = 6
 COUNT_TOP_HISTOGRAM = 7  # bit 0: histogram path; bit 1: threshold bin ranked directly
 COUNT_N = 8
 
-DEVIATION_SELECT_WORKSPACE_BYTES = 16640
-LAYER1_REPAIR_WORKSPACE_BYTES = 16640
+DEVIATION_SELECT_WORKSPACE_BYTES = 65792
+LAYER1_REPAIR_WORKSPACE_BYTES = 65792
 POS_POOLED = 8
 
 SELECT_MAX_TOKENS = 131072

@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kDevThreads) void deviation_kernel(const int32_t* l
         cnt += bj == bin ? 1u : 0u;
         first = first && !(j < lane && bj == bin);
       }
-      if (bin != ~0u && first) atomicAdd(hist + bin, cnt);
+      if (bin != ~0u && first) atomicAdd(hist_copy(hist, hist_copies(a.n_tokens)) + bin, cnt);
     }
   }
 }

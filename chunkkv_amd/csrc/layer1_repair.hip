@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
       cnt += bj == bin ? 1u : 0u;
       first = first && !(j < lane && bj == bin);
     }
-    if (bin != ~0u && first) atomicAdd(a.hist + bin, cnt);
+    if (bin != ~0u && first) atomicAdd(hist_copy(a.hist, hist_copies(a.n_tokens)) + bin, cnt);
   }
 }
 

@@ -232,7 +232,10 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
   uint32_t fw[G];
 #pragma unroll
   for (int i = 0; i < G; ++i) load_group(i, dv[i], fw[i]);
-  const vec16 g4 = ghist != nullptr ? ld16(ghist + (kTopBins - BPT * (tid + 1))) : vec16{0u, 0u, 0u, 0u};
+  // G > 4 groups per thread <=> more than 16384 positions: the counting launch spread the
+  // histogram over kHistCopies copies (hist_copies)
+  constexpr int HC = G > 4 ? kHistCopies : 1;
+  const vec16 g4 = ghist != nullptr ? hist_load4<HC>(ghist + (kTopBins - BPT * (tid + 1))) : vec16{0u, 0u, 0u, 0u};
   ckv_chunk_span sp = {0, 0, 0, 0};
   if (tid < n_chunks) {
     const vec16 v = ld16(chunks + tid);
@@ -323,7 +326,7 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
   const uint64_t scan_ex =
       sl_scan_u64((uint64_t)n_cand | ((uint64_t)mism << 21) | ((uint64_t)gsum << 42), slots64[0], scan_tot);
   if (ghist != nullptr && tid == 0)  // every thread's histogram load landed before the scan's barrier
-    s_last = atomicAdd(ghist + kTopBins, 1u) == (uint32_t)(n_slices - 1) ? 1 : 0;
+    s_last = atomicAdd(ghist + kHistWords, 1u) == (uint32_t)(n_slices - 1) ? 1 : 0;
   const int cand_total = (int)(scan_tot & kField);
   const int budget_req = s_budget_req;
   const int budget = max(0, min(budget_req, cand_total));
@@ -544,8 +547,8 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
     counts[CKV_COUNT_TOP_HISTOGRAM] = (use_top ? 1 : 0) | (ranked ? 2 : 0);
   }
   if (ghist != nullptr && s_last) {  // uniform: the last ticket; every workgroup has read the histogram
-    st16(ghist + (kTopBins - BPT * (tid + 1)), vec16{0u, 0u, 0u, 0u});
-    if (tid == 0) ghist[kTopBins] = 0u;
+    hist_zero4<HC>(ghist + (kTopBins - BPT * (tid + 1)));
+    if (tid == 0) ghist[kHistWords] = 0u;
   }
 
   // ---- phase 5: the slice (its owners are S/4 consecutive lanes of one wavefront)

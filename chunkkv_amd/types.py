@@ -41,7 +41,7 @@ class Placement:
 class BlendConfig:
     """Blend-prefill knobs (base.py:36-43)."""
 
-    recompute_ratio: float = 0.15  # fraction of cached tokens recomputed at layers >= 1
+    recompute_ratio: float = 0.15  # share of each placement's cached tokens that layers >= 1 recompute
     n_sink: int = 2  # first tokens of each non-exact chunk, always recomputed
     full_first_layer: bool = True  # False = naive reuse (no repair)
     escalate_threshold: float | None = None  # whole-chunk recompute above this layer-1 deviation
@@ -56,7 +56,7 @@ class PrefillResult:
     keys: list[Any]
     values: list[Any]
     stats: dict = field(default_factory=dict)
-    copy: Callable[[Any], Any] = lambda a: a  # backend copy, so stored chunks don't pin request buffers
+    copy: Callable[[Any], Any] = lambda a: a  # how a stored chunk copies its slices out of the request's buffers
     # Batched extraction hook (spans -> one (2, L, 1, H, len, D) buffer per span); set by HipEngine
     # to its one-launch kernel. None: the per-layer `copy` path of the reference.
     extract: Callable[[list], list] | None = None

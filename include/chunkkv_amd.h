@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define CKV_ABI_VERSION 3
+#define CKV_ABI_VERSION 4
 
 typedef enum ckv_status {
   CKV_OK = 0,
@@ -104,12 +104,14 @@ typedef struct ckv_chunk_span {
                                        were ranked directly instead of by radix passes      */
 #define CKV_COUNT_N 8
 
-/* Bytes of the workspace ckv_deviation_select takes: the 16 KB candidate histogram, then the
-   word that counts the selection's workgroups done reading it (the rest is not used). */
-#define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 16640
+/* Bytes of the workspace ckv_deviation_select takes: the 16 KB candidate histogram, as four
+   copies above 16384 positions (the counting launch's workgroups spread their atomics over
+   them), then the word that counts the selection's workgroups done reading them (the rest is not
+   used). */
+#define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 65792
 
-/* Bytes of the workspace ckv_layer1_repair takes (the same layout). */
-#define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 16640
+/* Bytes of the workspace ckv_layer1_repair and ckv_layer1_repair_gather take (the same layout). */
+#define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 65792
 
 /* ABI version compiled into the library (CKV_ABI_VERSION). */
 int32_t ckv_abi_version(void);
@@ -265,7 +267,7 @@ int32_t ckv_deviation_select(const void* k_fresh, int64_t kf_head_stride, int64_
  * ckv_deviation_select without the workspace argument, for callers that cannot allocate (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart
  * in the reference. The workspace is a static device array of the library,
- * CKV_DEVIATION_SELECT_WORKSPACE_BYTES (16640 bytes) per GPU, enough for every n_tokens the call
+ * CKV_DEVIATION_SELECT_WORKSPACE_BYTES (65,792 bytes) per GPU, enough for every n_tokens the call
  * takes (n_tokens > CKV_SELECT_MAX_TOKENS returns CKV_ERR_TOO_LARGE); its device address is looked
  * up once per GPU on the first call there. The call allocates nothing. All calls on one GPU share
  * that array, which every call leaves zeroed: calls that overlap on one GPU (different streams
