@@ -1246,6 +1246,74 @@ def bench_dropped(steps: int, warmup: int, dev) -> dict:
                            "traffic": DROPPED_TRAFFIC_BYTES, "bytes_per_launch": nb, "avg_launch_us": round(ms * 1e3, 2)})
 
 
+def bench_layer1_32k(steps: int, warmup: int, dev) -> dict:
+    """Layer 1's repair of one 32,832-token request alone, as the engine issues it
+    (ckv_layer1_repair_gather: the layer-1 pass counting the candidate histogram, the selection
+    spread over 129 slice workgroups, the kept rows with the dropped rows of two later layers):
+    128 chunks x 256 tokens drawn from a pool of 64 (4 layers held) + a 64-token query, 15 %
+    recompute + 4 sinks; layer-1 rows that follow the cached ones (per-chunk noise exp(N(-3, 1)))
+    and uncorrelated random rows (every deviation within a few percent of the others), each set
+    timed from HIP-graph replays of `steps` back-to-back calls. Run under rocprofv3 for the
+    per-kernel times (the selection is `select_slices_kernel<9, false, false>`)."""
+    from chunkkv_amd import ops
+    from chunkkv_amd.planner import local_index, plan_request
+
+    L, POOL, PER_REQ, Q, NL = 256, 64, 128, 64, 4
+    N = PER_REQ * L + Q
+    gen = torch.Generator(device=dev).manual_seed(3)
+    store = [Chunk(torch.randn((NL, 1, N_KV, L, HEAD_DIM), generator=gen, device=dev).bfloat16(),
+                   torch.randn((NL, 1, N_KV, L, HEAD_DIM), generator=gen, device=dev).bfloat16(), 1000 + 7 * i)
+             for i in range(POOL)]
+    rng = np.random.default_rng(3)
+    pl = [Place(store[i], j * L) for j, i in enumerate(rng.choice(POOL, PER_REQ))]
+    plan = plan_request(N, pl, N_SINK, 0.15)
+    tab = np.concatenate([np.array([[k.data_ptr(), v.data_ptr()] for k, v in zip(c.keys, c.values)],
+                                   dtype=np.uint64).reshape(-1) for c in plan.chunks])
+    tab = torch.from_numpy(tab.view(np.int64)).to(dev)
+    segs = torch.from_numpy(plan.segments.reshape(-1)).to(dev)
+    flags = torch.from_numpy(plan.flags).to(dev)
+    local = torch.from_numpy(local_index(N, plan.layer0_idx)).to(dev)
+    spans = torch.from_numpy(plan.spans.reshape(-1)).to(dev)
+    K = torch.empty((NL, 1, N_KV, N, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+    V = torch.empty_like(K)
+    ops.rerope_gather(K, V, tab, segs, len(plan.segments), plan.max_seg_tokens, THETA, layers=(1, 2))
+    sig = torch.exp(torch.randn(PER_REQ, generator=gen, device=dev) - 3.0).repeat_interleave(L)
+    sig = torch.cat([sig, torch.ones(Q, device=dev)])[None, None, :, None]
+    cached = torch.from_numpy(plan.cached).to(dev)[None, None, :, None]
+    rnd = lambda: torch.randn((1, N_KV, N, HEAD_DIM), generator=gen, device=dev)  # noqa: E731
+    rows = {
+        "correlated": (torch.where(cached, K[1].float() + sig * rnd(), rnd()).bfloat16(),
+                       torch.where(cached, V[1].float() + sig * rnd(), rnd()).bfloat16()),
+        "uncorrelated": (rnd().bfloat16(), rnd().bfloat16()),
+    }
+    ws = ops.layer1_repair_workspace(dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    sel = ops._new_selection(N, len(plan.spans), dev)
+    dn = (torch.empty(N, device=dev), torch.empty(N, device=dev))
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    for name, (k1, v1) in rows.items():
+        def call():
+            ops.layer1_repair_gather(K, V, tab, 1, (2, NL), segs, len(plan.segments), plan.max_seg_tokens, k1, v1,
+                                     flags, local, spans, None, THETA, ws, err, sel, dn)
+        for _ in range(max(warmup, 2)):
+            call()
+        torch.cuda.synchronize()
+        g = _graph_of(call)
+        g.replay()
+        out[name] = _timed(lambda i: g.replay(), steps, stream)
+        assert int(err.item()) == 0 and int(sel.counts[0].item()) == plan.n_keep
+    ms = out["correlated"]
+    line = _workload_line("layer-1 repair of one 32,832-token request, us per call", ms * 1e3, ms, steps, warmup,
+                          {"workload": "one 32,832-token request (128 chunks x 256 + 64 query, 15 % + 4 sinks), "
+                                       "Qwen2.5-7B KV shape, ckv_layer1_repair_gather with two later layers"}, None)
+    line["higher_is_better"] = False
+    line["unit"] = "us"
+    line.pop("pct_of_peak")
+    line["us_per_call_uncorrelated"] = round(out["uncorrelated"] * 1e3, 2)
+    return line
+
+
 def repair_bytes_for(plan) -> int:
     """Algorithmic repair bytes of a request plan (gather of every cached row, deviation over the
     layer-0 active set, scatters of layer 0 and layers 1..L-1)."""
@@ -1302,7 +1370,7 @@ def main() -> None:
     ap.add_argument("--replay-ttft-requests", type=int, default=20)
     ap.add_argument("--workload", default="request",
                     choices=["request", "gather", "deviation", "replay", "traffic", "dropped", "attention", "extract",
-                             "decode"],
+                             "decode", "layer1_32k"],
                     help="request: the 8k Qwen2.5-7B blend-prefill KV repair (default); gather / deviation / replay: "
                          "the re-RoPE+gather, deviation+top-k+scatter and 4x32k replay microbenchmarks")
     args = ap.parse_args()
@@ -1315,7 +1383,7 @@ def main() -> None:
     if args.workload != "request":
         fn = {"gather": bench_gather_only, "deviation": bench_deviation_topk, "replay": bench_replay,
               "traffic": traffic_probe, "dropped": bench_dropped, "attention": bench_attention,
-              "extract": bench_extract, "decode": bench_decode}[args.workload]
+              "extract": bench_extract, "decode": bench_decode, "layer1_32k": bench_layer1_32k}[args.workload]
         if args.workload == "replay":
             print(json.dumps(bench_replay(args.steps, args.warmup, dev, ttft_requests=args.replay_ttft_requests)),
                   flush=True)
