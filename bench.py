@@ -33,9 +33,12 @@ the same launches with the gathers on a second stream (HipEngine(overlap=True)) 
 ms_per_step_two_streams; layer 1 as the four launches ckv_layer1_repair replaces (base-cache
 gather, deviation, selection, scatter) as ms_per_step_layer1_four_launches; layers 0 and 2-27
 built by one assemble launch each as ms_per_step_assemble_variant); the fused flow itself moves
-moved_bytes_per_step (moved_gbs). `roofline` is the dominant kernel (the gather of the dropped
-rows of layers 2-27 as one launch, 562,298,880 B) timed live with HIP events around a burst of
-back-to-back launches on the launch stream. Inputs rotate between two independent copies so
+moved_bytes_per_step (moved_gbs). `roofline` is the step's dominant kernel, its last KV-repair
+launch of layer 1 (layer 1's kept rows beside the dropped rows of layers 4-27, 531,234,816 B),
+called alone through ckv_rerope_gather_layers_kept with the step's inputs and launch shape and
+timed live with HIP events around a burst of back-to-back launches on the launch stream; the
+gather of the dropped rows of layers 2-27 as one launch (the separate-gather step's) is reported
+beside it. Inputs rotate between two independent copies so
 consecutive steps do not hit in the 256 MB MALL.
 
 Besides the bandwidth line, the run measures blend-prefill TTFT p50 (prefill + last_logprobs,
@@ -78,6 +81,9 @@ GATHER_TRAFFIC_BYTES = 881_167_672
 # Same for one gather of the dropped rows of layers 2-27 of the 8k request (FETCH_SIZE median
 # 137,468 KiB / 0.500023 + WRITE_SIZE median 274,565 KiB; 562,298,880 algorithmic bytes).
 DROPPED_TRAFFIC_BYTES = 562_675_830
+# rocprofv3 FETCH_SIZE / 0.500023 + WRITE_SIZE of the step's kept rows + dropped rows of layers
+# 4-27 launch (266,088,701 B read, 259,395.5 KiB written)
+MERGED_TRAFFIC_BYTES = 266_088_701 + 265_620_992
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 
@@ -212,6 +218,18 @@ class RepairWorkload:
 
         ops.rerope_gather(self.k_slab, self.v_slab, self.tab, self.segs, len(self.plan.segments),
                           self.plan.max_seg_tokens, THETA, self.err, layers=(2, N_LAYERS), skip=self.sel.keep_rank)
+
+    def gather_kept(self):
+        """The step's last KV-repair launch called alone (ckv_rerope_gather_layers_kept, as
+        ckv_layer1_repair_gather issues it: the selection's device count, N its bound): layer 1's
+        kept rows beside the dropped rows of the layers after those gathered whole."""
+        from chunkkv_amd import ops
+
+        k1, v1 = self.fresh[1]
+        ops.rerope_gather_layers_kept(self.k_slab, self.v_slab, self.tab, self.segs, len(self.plan.segments),
+                                      self.plan.max_seg_tokens, THETA, (2 + whole_layers(self.plan), N_LAYERS),
+                                      self.sel.keep_rank, 1, k1, v1, self.sel.keep_abs, self.sel.keep_local, N_TOKENS,
+                                      self.sel.counts[:1], self.err)
 
     def kv_rows(self, li: int):
         """Layer li's fresh rows into its cache as the engine writes them: the k/v part of
@@ -408,8 +426,9 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     """Time the KV-repair step as HipEngine issues it (30 launches on one stream, captured once
     per input set in a HIP graph and replayed; the eager time, launch-bound from Python, layer 1
     as four launches, the two-stream issue and the assemble-per-layer variant are reported too),
-    and the dominant kernel (the gather of the dropped rows of layers 2..27) from a burst of
-    back-to-back launches."""
+    and the dominant kernel (the step's last launch: layer 1's kept rows with the dropped rows of
+    layers 4-27) and the separate-gather step's gather of the dropped rows of layers 2-27, each
+    from a burst of back-to-back launches."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
     for i in range(max(warmup, 2)):
         wls[i % 2].step()
@@ -435,6 +454,9 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
         w.step()
     ms_eager = _timed(lambda i: wls[i % 2].step(), steps, stream)
     gd_ms = _timed(lambda i: wls[i % 2].gather_dropped(), steps, stream)
+    for w in wls:  # the selection state of the one-stream step again
+        w.step()
+    gk_ms = _timed(lambda i: wls[i % 2].gather_kept(), steps, stream)
     n_asm = N_LAYERS - 2
     asm_ms = _timed(lambda i: wls[(i // n_asm) % 2].assemble(2 + i % n_asm), steps * n_asm, stream)
     assert all(int(w.err.item()) == 0 for w in wls)
@@ -443,11 +465,13 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     assert int(wls[0].sel.counts[0].item()) == n_keep
     nbytes = repair_bytes(n_keep)
     gd_bytes = dropped_bytes(plan)
+    gk_bytes = merged_bytes(plan)
     ms_conc = _concurrent_steps(wls, steps, dev)
     return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_split=ms_split, ms_sep=ms_sep, ms_eager=ms_eager,
                 bytes=nbytes,
                 moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
+                gk_ms=gk_ms, gk_bytes=gk_bytes, gk_gbs=gk_bytes / (gk_ms * 1e-3) / 1e9,
                 asm_ms=asm_ms, asm_gbs=ASSEMBLE_BYTES / (asm_ms * 1e-3) / 1e9, n_keep=n_keep, ms_conc=ms_conc,
                 conc_gbs=CONCURRENT * nbytes / (ms_conc * 1e-3) / 1e9)
 
@@ -490,6 +514,15 @@ def dropped_bytes(plan) -> int:
     n_uncached = plan.n_tokens - int(plan.cached.sum())
     n_dropped = int(plan.cached.sum()) - (plan.n_keep - n_uncached)
     return (N_LAYERS - 2) * n_dropped * ROW_BYTES * 4
+
+
+def merged_bytes(plan) -> int:
+    """Algorithmic bytes of the step's last KV-repair launch: layer 1's kept rows (fresh rows read,
+    cache rows written) and the dropped cached rows of the layers after those gathered whole, K
+    and V, read + write."""
+    n_uncached = plan.n_tokens - int(plan.cached.sum())
+    n_dropped = int(plan.cached.sum()) - (plan.n_keep - n_uncached)
+    return (N_LAYERS - 2 - whole_layers(plan)) * n_dropped * ROW_BYTES * 4 + plan.n_keep * ROW_BYTES * 4
 
 
 def whole_layers(plan) -> int:
@@ -1394,7 +1427,8 @@ def main() -> None:
     r = bench_repair(args.steps, args.warmup, dev)
     log(f"[bench] KV repair {r['gbs']:.1f} GB/s ({r['ms_per_step']:.3f} ms/step graph, {r['ms_two']:.3f} ms two "
         f"streams, {r['ms_asm']:.3f} ms assemble variant, {r['ms_split']:.3f} ms layer 1 as four launches, "
-        f"{r['ms_eager']:.3f} ms eager); dropped-row gather {r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
+        f"{r['ms_eager']:.3f} ms eager); last launch {r['gk_gbs']:.1f} GB/s ({r['gk_ms'] * 1e3:.1f} us); "
+        f"dropped-row gather {r['gd_gbs']:.1f} GB/s ({r['gd_ms'] * 1e3:.1f} us); "
         f"assemble {r['asm_gbs']:.1f} GB/s ({r['asm_ms'] * 1e3:.2f} us)")
     configs = {}
     if not args.no_configs:
@@ -1450,15 +1484,23 @@ def main() -> None:
                                 "note": "the same request's KV repair, CONCURRENT independent requests in flight on "
                                         "their own streams (one HIP graph per round); value is the single-request step"},
         "roofline": {
-            "kernel": "rerope_gather_kernel<bf16,128> (layers 2-27, dropped rows)",
+            "kernel": "rerope_gather_kernel<bf16,128,GatherSkip,kept rows> (the step's last launch: layer 1's kept "
+                      "rows + dropped rows of layers 4-27)",
             "bound": "hbm",
-            "achieved": round(r["gd_gbs"], 1),
+            "achieved": round(r["gk_gbs"], 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(r["gd_gbs"] / PEAK_GBS, 4),
-            "traffic": DROPPED_TRAFFIC_BYTES,
-            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, profiles/traffic_gather_dropped_rows_qwen25_7b_8k.md",
-            "bytes_per_launch": r["gd_bytes"],
+            "frac": round(r["gk_gbs"] / PEAK_GBS, 4),
+            "traffic": MERGED_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, "
+                              "profiles/traffic_request_step_kernels_qwen25_7b_8k.md",
+            "bytes_per_launch": r["gk_bytes"],
+            "avg_launch_us": round(r["gk_ms"] * 1e3, 2),
+        },
+        "dropped_row_gather_layers_2_27": {
+            "kernel": "rerope_gather_kernel<bf16,128,GatherSkip> (the separate-gather step's launch)",
+            "achieved": round(r["gd_gbs"], 1), "frac": round(r["gd_gbs"] / PEAK_GBS, 4),
+            "traffic": DROPPED_TRAFFIC_BYTES, "bytes_per_launch": r["gd_bytes"],
             "avg_launch_us": round(r["gd_ms"] * 1e3, 2),
         },
         "assemble_kernel": {"bytes_per_launch": ASSEMBLE_BYTES, "avg_launch_us": round(r["asm_ms"] * 1e3, 2),

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libchunkkv_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 CKV_OK = 0
 CKV_ERR_INVALID_ARGUMENT = 1
@@ -60,6 +60,11 @@ SIGNATURES = {
     "ckv_rerope_gather_layers": (
         _i32,
         [_p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p, _i32, _i32, _p, _i32, _i32, _i32, _i32, _f64, _p, _p],
+    ),
+    "ckv_rerope_gather_layers_kept": (
+        _i32,
+        [_p, _p, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p, _i32, _i32, _p, _i32, _p, _i64, _i64, _p, _i64, _i64, _p,
+         _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p],
     ),
     "ckv_shift_keys": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f64, _p]),
     "ckv_deviation": (

@@ -190,6 +190,54 @@ extern "C" int32_t ckv_rerope_gather_layers(void* dst_k, void* dst_v, int64_t ds
                                    head_dim, dtype, theta, err, stream, nullptr);
 }
 
+// The gather of ckv_rerope_gather_layers with another layer's kept rows scattered in the same
+// launch (the z-slices in front of the gather's, as ckv_layer1_repair_gather issues it).
+extern "C" int32_t ckv_rerope_gather_layers_kept(
+    void* dst_k, void* dst_v, int64_t dst_layer_stride, int64_t dst_head_stride, const uint64_t* src_tab,
+    int32_t n_chunks, int32_t n_layers, int32_t layer_begin, int32_t layer_end, const ckv_segment* segs,
+    int32_t n_segs, int32_t max_seg_tokens, const int32_t* skip, int32_t kept_layer, const void* k_fresh,
+    int64_t kf_head_stride, int64_t kf_token_stride, const void* v_fresh, int64_t vf_head_stride,
+    int64_t vf_token_stride, const int64_t* keep_abs, const int64_t* keep_local, int32_t n_keep,
+    const int32_t* n_keep_dev, int32_t n_fresh, int32_t n_heads, int32_t n_tokens, int32_t head_dim, int32_t dtype,
+    double theta, int32_t* err, void* stream) {
+  using namespace ckv;
+  if (dst_k == nullptr || dst_v == nullptr || n_layers <= 0 || kept_layer < 0 || kept_layer >= n_layers ||
+      (kept_layer >= layer_begin && kept_layer < layer_end) || n_keep < 0 || n_fresh < 0 || n_heads <= 0 ||
+      head_dim <= 0)
+    return CKV_ERR_INVALID_ARGUMENT;
+  // with no fresh rows no source row is in range: nothing is read from k/v (they may be NULL)
+  if (n_keep > 0 && (keep_abs == nullptr || keep_local == nullptr ||
+                     (n_fresh > 0 && (k_fresh == nullptr || v_fresh == nullptr))))
+    return CKV_ERR_INVALID_ARGUMENT;
+  if (n_segs == 0 || max_seg_tokens == 0 || layer_end == layer_begin) {
+    // nothing to gather: the table and descriptors are never read (they may be NULL)
+    if (src_tab == nullptr) src_tab = (const uint64_t*)dst_k;
+    if (segs == nullptr) segs = (const ckv_segment*)dst_k;
+  }
+  const int64_t eb = elem_bytes(dtype);
+  const RowScatter kept{(char*)dst_k + kept_layer * dst_layer_stride * eb,
+                        (char*)dst_v + kept_layer * dst_layer_stride * eb,
+                        dst_head_stride * eb,
+                        (const char*)k_fresh,
+                        kf_head_stride * eb,
+                        kf_token_stride * eb,
+                        (const char*)v_fresh,
+                        vf_head_stride * eb,
+                        vf_token_stride * eb,
+                        keep_abs,
+                        keep_local,
+                        n_keep_dev,
+                        (int)n_keep,
+                        (int)n_fresh,
+                        (int)n_tokens,
+                        (int)n_heads,
+                        (int)(head_dim * eb / 16),
+                        (int64_t)head_dim * eb};
+  return gather_layers_launch(dst_k, dst_v, dst_layer_stride, dst_head_stride, src_tab, n_chunks, n_layers,
+                              layer_begin, layer_end, segs, n_segs, max_seg_tokens, skip, n_heads, n_tokens, head_dim,
+                              dtype, theta, err, stream, &kept);
+}
+
 extern "C" int32_t ckv_rerope_gather(void* dst_k, void* dst_v, int64_t dst_layer_stride,
                                      int64_t dst_head_stride, const uint64_t* src_tab,
                                      int32_t n_chunks, const ckv_segment* segs, int32_t n_segs,

@@ -148,6 +148,64 @@ def rerope_gather(
     )
 
 
+def rerope_gather_layers_kept(
+    k_slab: torch.Tensor,
+    v_slab: torch.Tensor,
+    src_tab: torch.Tensor,
+    segments: torch.Tensor,
+    n_segs: int,
+    max_seg_tokens: int,
+    theta: float,
+    layers: tuple[int, int],
+    skip: torch.Tensor | None,
+    kept_layer: int,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    keep_abs: torch.Tensor,
+    keep_local: torch.Tensor,
+    n_keep: int,
+    n_keep_dev: torch.Tensor | None = None,
+    err: torch.Tensor | None = None,
+) -> None:
+    """rerope_gather(layers=..., skip=...) and scatter_kept_rows into layer `kept_layer` of the
+    same slab in ONE launch: K[kept_layer, 0, :, keep_abs[j]] = k[0, :, keep_local[j]] (V likewise)
+    for j < n_keep, or j < min(n_keep, n_keep_dev[0]) with a device count (e.g. a selection's
+    counts; n_keep is then the upper bound). torch_engine.py:96-103 for the gathered layers,
+    :152 and :155-156 for the kept layer, which must lie outside `layers`."""
+    _dev(k_slab, v_slab, src_tab, segments, k, v, keep_abs, keep_local)
+    if not (k_slab.is_contiguous() and v_slab.is_contiguous() and k_slab.shape == v_slab.shape):
+        raise ValueError("K/V slabs must be contiguous and of equal shape")
+    n_layers, _, H, N, D = k_slab.shape
+    k, v = _rows_view(k), _rows_view(v)
+    if k.dtype != k_slab.dtype or v.dtype != k_slab.dtype or v_slab.dtype != k_slab.dtype:
+        raise TypeError("fresh rows and slabs must share a dtype")
+    if k.dim() != 4 or k.shape[0] != 1 or k.shape[1] != H or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"fresh rows {tuple(k.shape)} do not match the slab {tuple(k_slab.shape)}")
+    if src_tab.dtype != torch.int64 or src_tab.numel() % (2 * n_layers):
+        raise ValueError("src_tab must be int64 with 2 addresses per (chunk, layer)")
+    if segments.dtype != torch.int32 or segments.numel() < 6 * int(n_segs):
+        raise ValueError("segments must be int32 with 6 fields per segment")
+    if keep_abs.dtype != torch.int64 or keep_local.dtype != torch.int64 or not (
+            keep_abs.is_contiguous() and keep_local.is_contiguous()):
+        raise ValueError("keep_abs / keep_local must be contiguous int64")
+    if min(keep_abs.numel(), keep_local.numel()) < int(n_keep):
+        raise ValueError("keep_abs / keep_local hold fewer than n_keep rows")
+    if skip is not None and (skip.dtype != torch.int32 or skip.numel() != N or not skip.is_contiguous()):
+        raise ValueError("skip must be int32 (N,) contiguous")
+    if n_keep_dev is not None and (n_keep_dev.dtype != torch.int32 or n_keep_dev.device != k_slab.device):
+        raise ValueError("n_keep_dev must be an int32 tensor on the slab's device")
+    check(
+        lib().ckv_rerope_gather_layers_kept(
+            _ptr(k_slab), _ptr(v_slab), H * N * D, N * D, _ptr(src_tab), src_tab.numel() // (2 * n_layers), n_layers,
+            int(layers[0]), int(layers[1]), _ptr(segments), int(n_segs), int(max_seg_tokens), _ptr(skip),
+            int(kept_layer), _ptr(k), k.stride(1), k.stride(2), _ptr(v), v.stride(1), v.stride(2), _ptr(keep_abs),
+            _ptr(keep_local), int(n_keep), _ptr(n_keep_dev), k.shape[2], H, N, D, dtype_code(k_slab.dtype),
+            float(theta), _ptr(err), _stream(k_slab.device),
+        ),
+        "ckv_rerope_gather_layers_kept",
+    )
+
+
 def deviation(
     k: torch.Tensor,
     v: torch.Tensor,

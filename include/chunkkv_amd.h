@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define CKV_ABI_VERSION 4
+#define CKV_ABI_VERSION 5
 
 typedef enum ckv_status {
   CKV_OK = 0,
@@ -390,6 +390,34 @@ int32_t ckv_assemble_layer(void* dst_k, void* dst_v, int64_t dst_head_stride, co
                            int64_t vf_head_stride, int64_t vf_token_stride, int32_t n_fresh,
                            const int32_t* local, int32_t n_tokens, int32_t n_heads, int32_t head_dim,
                            int32_t dtype, double theta, int32_t* err, void* stream);
+
+/*
+ * ckv_rerope_gather_layers and ckv_scatter_kept_rows in ONE launch: the gather of layers
+ * [layer_begin, layer_end) (rows with skip[p] >= 0 left alone) and, in the same launch, the
+ * kept rows of layer kept_layer of the same slab:
+ *   K[kept_layer, h, keep_abs[j], :] = k[h, keep_local[j], :],  V likewise,
+ * for j < n_keep, or j < min(n_keep, *n_keep_dev) when n_keep_dev is not NULL (a count only the
+ * device knows, e.g. counts + CKV_COUNT_KEEP of a selection; n_keep is then its upper bound and
+ * sizes the launch). k/v: n_fresh rows, strides in elements (row contiguous, 16-byte aligned;
+ * NULL with n_fresh = 0, when every kept row is out of range).
+ * kept_layer must lie outside [layer_begin, layer_end) (CKV_ERR_INVALID_ARGUMENT otherwise), so
+ * no row is written twice. A kept row whose source or destination is out of range is skipped and
+ * flagged in err. With nothing to gather (n_segs, max_seg_tokens or the layer range empty)
+ * src_tab and segs are not read and may be NULL. This is the last launch of
+ * ckv_layer1_repair_gather, callable alone (e.g. after ckv_deviation_select).
+ * Replaces: base_kv (torch_engine.py:96-103) for layers >= 2 and, for the kept layer, the
+ * compaction and scatter of torch_engine.py:152, :155-156.
+ */
+int32_t ckv_rerope_gather_layers_kept(void* dst_k, void* dst_v, int64_t dst_layer_stride,
+                                      int64_t dst_head_stride, const uint64_t* src_tab, int32_t n_chunks,
+                                      int32_t n_layers, int32_t layer_begin, int32_t layer_end,
+                                      const ckv_segment* segs, int32_t n_segs, int32_t max_seg_tokens,
+                                      const int32_t* skip, int32_t kept_layer, const void* k_fresh,
+                                      int64_t kf_head_stride, int64_t kf_token_stride, const void* v_fresh,
+                                      int64_t vf_head_stride, int64_t vf_token_stride, const int64_t* keep_abs,
+                                      const int64_t* keep_local, int32_t n_keep, const int32_t* n_keep_dev,
+                                      int32_t n_fresh, int32_t n_heads, int32_t n_tokens, int32_t head_dim,
+                                      int32_t dtype, double theta, int32_t* err, void* stream);
 
 /*
  * Scatter freshly computed K/V rows into one layer's cache:

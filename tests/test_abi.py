@@ -58,6 +58,16 @@ def test_host_side_argument_validation_never_launches():
         == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_rerope_gather_layers(1, 1, 1000, 640, 1, 1, 3, 2, 2, 1, 1, 1, None, 1, 10, 64, 1, 1e6, None, None) \
         == _native.CKV_OK
+    # gather + kept rows: the kept layer inside the gathered range or past n_layers, kept rows with
+    # no keep lists, a bad dtype -> invalid; nothing gathered and no kept row -> nothing to do
+    kept = lambda *a: lib.ckv_rerope_gather_layers_kept(*a)  # noqa: E731
+    kb = [1, 1, 1000, 100, 1, 1, 3, 1, 3, 1, 1, 1, None, 0, 1, 100, 64, 1, 100, 64, 1, 1, 4, None, 10, 1, 10, 64, 1,
+          1e6, None, None]
+    assert kept(*kb[:13], 2, *kb[14:]) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert kept(*kb[:13], 3, *kb[14:]) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert kept(*kb[:20], None, *kb[21:]) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert kept(*kb[:28], 7, *kb[29:]) == _native.CKV_ERR_INVALID_ARGUMENT
+    assert kept(*kb[:2], 1000, 640, *kb[4:7], 2, 2, *kb[9:22], 0, *kb[23:]) == _native.CKV_OK
     assert lib.ckv_inv_freq(None, 128, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_inv_freq(1, 127, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT
     assert lib.ckv_shift_keys(1, 10, 1, 10, 1, 1, 100, 1, 3, 1e6, None) == _native.CKV_ERR_INVALID_ARGUMENT

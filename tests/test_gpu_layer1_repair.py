@@ -541,3 +541,115 @@ def test_merged_gather_graph_replays():
         _same(out.keep_rank, se.keep_rank, f"keep_rank, replay {i}")
         _same(dn[0].view(torch.int32), de.view(torch.int32), f"diff, replay {i}")
     assert not ws.any()
+
+
+def _kept_vs_separate(req, layers, kept_layer=1, device_count=True):
+    """ckv_rerope_gather_layers_kept after a selection against rerope_gather(layers,
+    skip=keep_rank) then scatter_kept_rows into layer `kept_layer`: every layer of the slabs bit
+    for bit. With device_count the kept-row count is the selection's device count and n_keep its
+    upper bound N (the launch shape ckv_layer1_repair_gather uses); otherwise the host count."""
+    L = req.n_layers
+    ws = ops.layer1_repair_workspace(DEV)
+    scratch = torch.empty((1, req.H, req.N, req.D), dtype=req.dtype, device=DEV)
+    _, _, sel = ops.layer1_repair(scratch, torch.empty_like(scratch), req.tab, L, req.layer, req.segs, req.n_segs,
+                                  req.k, req.v, req.flags, req.local, req.spans, None, THETA, ws, req.err)
+    torch.cuda.synchronize()
+    n = int(sel.counts[0].item())
+    shape = (L, 1, req.H, req.N, req.D)
+    Ks, Vs = torch.full(shape, SENT, dtype=req.dtype, device=DEV), torch.full(shape, -SENT, dtype=req.dtype, device=DEV)
+    Km, Vm = Ks.clone(), Vs.clone()
+    if req.n_segs:
+        ops.rerope_gather(Ks, Vs, req.tab, req.segs, req.n_segs, req.plan.max_seg_tokens, THETA, req.err,
+                          layers=layers, skip=sel.keep_rank)
+    ops.scatter_kept_rows(Ks[kept_layer], Vs[kept_layer], req.k, req.v, sel.keep_abs[:n], sel.keep_local[:n], req.err)
+    # with no segment the table and descriptors are empty (NULL): the launch scatters only
+    ops.rerope_gather_layers_kept(Km, Vm, req.tab, req.segs, req.n_segs, req.plan.max_seg_tokens, THETA, layers, sel.keep_rank,
+                                  kept_layer, req.k, req.v, sel.keep_abs, sel.keep_local, req.N if device_count else n,
+                                  sel.counts[:1] if device_count else None, req.err)
+    torch.cuda.synchronize()
+    assert int(req.err.item()) == 0, f"device status {int(req.err.item())}"
+    for li in range(L):
+        _same(Km[li], Ks[li], f"K layer {li}")
+        _same(Vm[li], Vs[li], f"V layer {li}")
+    return Km, Vm, sel
+
+
+@pytest.mark.parametrize("device_count", [True, False])
+def test_gather_layers_kept_8k_request_shape(device_count):
+    """The request step's last KV-repair launch called alone: the 8k request's kept rows of
+    layer 1 beside the dropped rows of layers 2-5; the kept layer's rows also match the
+    oracle's selection applied to the fresh rows."""
+    rng = np.random.default_rng(83)
+    starts, N = _shuffled(rng, 24, 320, 576)
+    req = Request(83, [320] * 24, starts, N, n_layers=6)
+    Km, _, sel = _kept_vs_separate(req, (2, 6), device_count=device_count)
+    n = int(sel.counts[0].item())
+    assert n == 2976
+    ka, kl = _bits(sel.keep_abs)[:n], _bits(sel.keep_local)[:n]
+    np.testing.assert_array_equal(_bits(Km[1])[0][:, ka], _bits(req.k)[0][:, kl])
+    sent = _bits(torch.tensor(SENT, dtype=req.dtype))
+    rest = np.ones(N, dtype=bool)
+    rest[ka] = False
+    assert (_bits(Km[1])[0][:, rest] == sent).all()
+
+
+@pytest.mark.parametrize("case", ["kept_layer_first", "small_f32", "no_placements", "every_position_exact",
+                                  "empty_layers", "replay_shape"])
+def test_gather_layers_kept_edges(case):
+    """The kept layer before the gathered range, fp32 at head_dim 64 with exact and overlapping
+    placements, no placement (the launch scatters only), nothing kept (the launch gathers only),
+    an empty layer range, and the replay's 32,832-position request (128 segments: the
+    segment-fastest gather shape)."""
+    if case == "kept_layer_first":
+        rng = np.random.default_rng(12)
+        starts, N = _shuffled(rng, 12, 128, 100)
+        req = Request(12, [128] * 12, starts, N, n_layers=4, layer=0)
+        _kept_vs_separate(req, (1, 4), kept_layer=0)
+        return
+    if case == "small_f32":
+        req = Request(14, [40, 33, 50, 29, 61], [(0, 5), (1, 60), (2, 80), (3, 150), (4, 190)], 270, H=2, D=64,
+                      dtype=torch.float32, n_layers=4, exact=(3,), ratios=[0.3, 0.5, None, 0.0, 0.25])
+    elif case == "no_placements":
+        req = Request(15, [], [], 7, n_layers=3)
+    elif case == "every_position_exact":
+        req = Request(16, [50], [(0, 0)], 50, exact=(0,), n_layers=3)
+    elif case == "empty_layers":
+        req = Request(17, [64] * 4, [(c, c * 64) for c in range(4)], 260, n_layers=3)
+        _kept_vs_separate(req, (2, 2))
+        return
+    else:
+        rng = np.random.default_rng(57)
+        zipf = 1.0 / np.arange(1, 25) ** 1.1
+        ids = rng.choice(24, 128, p=zipf / zipf.sum())
+        req = Request(57, [256] * 24, [(int(c), j * 256) for j, c in enumerate(ids)], 128 * 256 + 64, ratio=0.15,
+                      n_layers=3)
+    _kept_vs_separate(req, (2, req.n_layers))
+
+
+def test_gather_layers_kept_flags_an_out_of_range_source_row():
+    """A kept row whose source row is past the fresh rows is skipped and flagged; every other row
+    of the launch is written as the separate launches write it."""
+    rng = np.random.default_rng(18)
+    starts, N = _shuffled(rng, 8, 128, 60)
+    req = Request(18, [128] * 8, starts, N, n_layers=3)
+    ws = ops.layer1_repair_workspace(DEV)
+    scratch = torch.empty((1, req.H, N, req.D), dtype=req.dtype, device=DEV)
+    _, _, sel = ops.layer1_repair(scratch, torch.empty_like(scratch), req.tab, 3, 1, req.segs, req.n_segs, req.k,
+                                  req.v, req.flags, req.local, req.spans, None, THETA, ws, req.err)
+    torch.cuda.synchronize()
+    n = int(sel.counts[0].item())
+    assert n > 2
+    bad = sel.keep_local.clone()
+    bad[1] = req.k.shape[2]  # one past the last fresh row
+    shape = (3, 1, req.H, N, req.D)
+    K, V = torch.full(shape, SENT, dtype=req.dtype, device=DEV), torch.full(shape, -SENT, dtype=req.dtype, device=DEV)
+    ops.rerope_gather_layers_kept(K, V, req.tab, req.segs, req.n_segs, req.plan.max_seg_tokens, THETA, (2, 3),
+                                  sel.keep_rank, 1, req.k, req.v, sel.keep_abs, bad, n, None, req.err)
+    torch.cuda.synchronize()
+    assert int(req.err.item()) == _native.DEVICE_ERR_RANGE
+    req.err.zero_()
+    ka, kl = _bits(sel.keep_abs)[:n], _bits(sel.keep_local)[:n]
+    good = np.arange(n) != 1
+    np.testing.assert_array_equal(_bits(K[1])[0][:, ka[good]], _bits(req.k)[0][:, kl[good]])
+    sent = _bits(torch.tensor(SENT, dtype=req.dtype))
+    assert (_bits(K[1])[0][:, ka[1]] == sent).all()
