@@ -22,7 +22,7 @@ def _has_gpu() -> bool:
 
 
 def pytest_collection_modifyitems(config, items):
-    # GPU tests skip only where there is no device at all; on a GPU box a missing library fails.
+    # GPU tests skip only where there is no device at all; with a device a missing library fails.
     if _has_gpu():
         return
     skip = pytest.mark.skip(reason="no HIP device")
