@@ -14,8 +14,10 @@
 // The gather's work items are one pass of the workgroup each (RPP rows: every head of RPP / H
 // consecutive tokens of one segment and layer), tile fastest, strided over the gather
 // workgroups; each workgroup keeps two items in flight: the next item's loads (and its cos/sin
-// table) go out before the current item's rotation and stores, so reads and writes overlap. The
-// per-item work and rounding are rerope_gather's (gather_common.hpp).
+// table) go out before the current item's rotation and stores, so reads and writes overlap
+// (measured against the previous form, whose next-item loads waited on a vector descriptor load
+// and on register moves: the three launches of ckv_layer1_repair_gather 0.7-0.9 us shorter at
+// 8k positions). The per-item work and rounding are rerope_gather's (gather_common.hpp).
 #include <atomic>
 
 #include "gather_common.hpp"
@@ -36,9 +38,12 @@ __device__ __forceinline__ void pregather_items(const PreGather& g, int it, int 
   constexpr int HALF = D / 2;
   constexpr int TPR = HALF / VEC;
   constexpr int RPP = pre_rows<DTYPE, D>();
-  constexpr int64_t ROW_B = (int64_t)D * E::kBytes;
+  constexpr int RPW = kWave / TPR;  // rows per wavefront
+  constexpr int ROW_B = D * E::kBytes;
   constexpr int HALF_B = HALF * E::kBytes;
-  static_assert(kSelThreads % TPR == 0 && kSelThreads >= HALF, "rows must tile the workgroup");
+  static_assert(kSelThreads % TPR == 0 && kSelThreads >= HALF && kWave % TPR == 0, "rows must tile the workgroup");
+  typedef __attribute__((address_space(4))) const int32_t ci32;
+  typedef __attribute__((address_space(4))) const uint64_t cu64;
   __shared__ float2 cs_tab[2][HALF];  // the cos/sin tables of the two items in flight
 
   // each cos/sin lane's inverse frequency from the argument scalars (no vector load)
@@ -49,55 +54,80 @@ __device__ __forceinline__ void pregather_items(const PreGather& g, int it, int 
   for (int k = 0; k < HALF; ++k) {
     if (k / kWave == wave) my_inv = ln == k % kWave ? g.inv.v[k] : my_inv;  // uniform test, scalar operand
   }
+  // row r = threadIdx.x / TPR of an item: head r / tpi, token r % tpi. The host checks that
+  // n_heads divides kSelWaves, so tpi is a multiple of RPW and a wavefront's rows are
+  // consecutive tokens of one head.
   const int col = (int)threadIdx.x % TPR;
-  const int r = (int)threadIdx.x / TPR;  // row of the item: head r / tpi, token r % tpi
-  const int tpi = RPP / g.n_heads;       // tokens per item (the host checks n_heads divides RPP)
-  const int head = r / tpi, tok = r % tpi;
-  const int64_t col_b = (int64_t)col * 16;
+  const int tpi = RPP / g.n_heads;  // tokens per item
+  const int head = __builtin_amdgcn_readfirstlane((wave * RPW) / tpi);
+  const int wtok = __builtin_amdgcn_readfirstlane((wave * RPW) % tpi);  // the wavefront's first token
+  const int wrow = ln / TPR;                                            // this lane's row in the wavefront
+  const int tok = wtok + wrow;
 
+  // Rows move through buffer loads and stores: a slot's source and destination are a
+  // per-wavefront base (scalar) plus a small per-lane offset, and a lane with no row (past the
+  // segment, no item) takes an offset past the buffer's range, which the hardware drops (loads
+  // return 0, no memory access). The loads are then unconditional: no branch joins the
+  // registers of the item in flight, which would make the compiler wait for its loads there.
+  // Descriptors and chunk addresses come through the constant address space as scalar loads
+  // (nothing in the launch writes them), so waiting for them never waits for row loads.
+  constexpr unsigned kRange = (unsigned)(RPW * ROW_B);  // bytes a wavefront's rows span
+  constexpr unsigned kDead = 0x40000000u;               // an offset past every range
+  constexpr int kNt = 2;                                // non-temporal (read / written once)
+  // base is the same in every lane; read it from the first one so the descriptor is built in
+  // scalar registers (through uint32_t: an int would sign-extend the low word into the high one)
+  auto rsrc = [](const void* base) {
+    const uint64_t v = (uint64_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, (int)kRange, 0x00020000);
+  };
   struct Slot {
     vec16 k1, k2, v1, v2;
-    char* dk;
+    char* dk;  // the wavefront's destination rows (K, V)
     char* dv;
-    bool live, rot;
+    unsigned off;  // this lane's offset in them (kDead: no row)
+    bool rot;
   };
   // item -> (tile, segment, layer): its loads and its cos/sin table
   auto prepare = [&](int item, Slot& sl, float2* tab) {
-    sl.live = false;
-    sl.rot = false;
-    if (item >= g.n_items) return;  // uniform
-    const int tile = item % g.tiles, rest = item / g.tiles;
+    const bool in = item < g.n_items;  // uniform
+    const int itc = in ? item : 0;
+    const int tile = itc % g.tiles, rest = itc / g.tiles;
     const int layer = g.layer_begin + rest / g.n_segs;
-    typedef __attribute__((address_space(1))) const int32_t gi32;
-    gi32* f = (gi32*)(g.segs + rest % g.n_segs);
+    ci32* f = (ci32*)(g.segs + rest % g.n_segs);
     const ckv_segment s{f[0], f[1], f[2], f[3], f[4], f[5]};
     const int t0 = tile * tpi;
-    if (t0 >= s.n_tokens) return;  // uniform: past this segment's end
-    if (s.dst_start < 0 || s.src_start < 0 || s.chunk < 0 || s.chunk >= g.n_tab_chunks ||
-        (int64_t)s.dst_start + s.n_tokens > g.n_tokens || (int64_t)s.src_start + s.n_tokens > s.src_len) {
+    bool ok = in && t0 < s.n_tokens;  // uniform: an item inside its segment
+    if (ok && (s.dst_start < 0 || s.src_start < 0 || s.chunk < 0 || s.chunk >= g.n_tab_chunks ||
+               (int64_t)s.dst_start + s.n_tokens > g.n_tokens || (int64_t)s.src_start + s.n_tokens > s.src_len)) {
       if (threadIdx.x == 0) flag_error(g.err, CKV_DEVICE_ERR_RANGE);
-      return;
+      ok = false;
     }
-    const int64_t ti = ((int64_t)s.chunk * g.n_layers + layer) * 2;
-    const char* src_k = reinterpret_cast<const char*>(g.tab[ti]);
-    const char* src_v = reinterpret_cast<const char*>(g.tab[ti + 1]);
-    sl.rot = s.delta != 0;
+    const char* src_k = g.dk;  // any address: a lane with no row touches no memory
+    const char* src_v = g.dk;
+    if (ok) {  // uniform
+      const int64_t ti = ((int64_t)s.chunk * g.n_layers + layer) * 2;
+      const int64_t so = ((int64_t)head * s.src_len + s.src_start + t0 + wtok) * ROW_B;
+      src_k = reinterpret_cast<const char*>(((cu64*)g.tab)[ti]) + so;
+      src_v = reinterpret_cast<const char*>(((cu64*)g.tab)[ti + 1]) + so;
+    }
+    const int64_t d = (int64_t)layer * g.ls_b + (int64_t)head * g.hs_b + (int64_t)(s.dst_start + t0 + wtok) * ROW_B;
+    sl.dk = g.dk + (ok ? d : 0);
+    sl.dv = g.dv + (ok ? d : 0);
+    sl.rot = ok && s.delta != 0;
     if (sl.rot && (int)threadIdx.x < HALF) tab[threadIdx.x] = shift_cos_sin(my_inv, s.delta);
-    if (tok < s.n_tokens - t0) {
-      const int64_t so = (int64_t)head * s.src_len * ROW_B + (int64_t)(s.src_start + t0 + tok) * ROW_B + col_b;
-      const int64_t d = (int64_t)layer * g.ls_b + (int64_t)head * g.hs_b + (int64_t)(s.dst_start + t0 + tok) * ROW_B + col_b;
-      sl.k1 = gather_ld(src_k + so);
-      sl.k2 = gather_ld(src_k + so + HALF_B);
-      sl.v1 = gather_ld(src_v + so);
-      sl.v2 = gather_ld(src_v + so + HALF_B);
-      sl.dk = g.dk + d;
-      sl.dv = g.dv + d;
-      sl.live = true;
-    }
+    const bool live = ok && tok < s.n_tokens - t0;
+    sl.off = live ? (unsigned)(wrow * ROW_B + col * 16) : kDead;
+    const auto rk = rsrc(src_k), rv = rsrc(src_v);
+    sl.k1 = __builtin_amdgcn_raw_buffer_load_b128(rk, sl.off, 0, kNt);
+    sl.k2 = __builtin_amdgcn_raw_buffer_load_b128(rk, sl.off + HALF_B, 0, kNt);
+    sl.v1 = __builtin_amdgcn_raw_buffer_load_b128(rv, sl.off, 0, kNt);
+    sl.v2 = __builtin_amdgcn_raw_buffer_load_b128(rv, sl.off + HALF_B, 0, kNt);
   };
   auto finish = [&](const Slot& sl, const float2* tab) {
-    if (!sl.live) return;
-    if (sl.rot) {
+    vec16 y1 = sl.k1, y2 = sl.k2;
+    if (sl.rot) {  // uniform
       float c[VEC], sn[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
@@ -105,31 +135,33 @@ __device__ __forceinline__ void pregather_items(const PreGather& g, int it, int 
         c[e] = t.x;
         sn[e] = t.y;
       }
-      vec16 y1, y2;
       rotate_pairs<DTYPE>(sl.k1, sl.k2, c, sn, y1, y2);
-      gather_st(sl.dk, y1);
-      gather_st(sl.dk + HALF_B, y2);
-    } else {
-      gather_st(sl.dk, sl.k1);
-      gather_st(sl.dk + HALF_B, sl.k2);
     }
-    gather_st(sl.dv, sl.v1);
-    gather_st(sl.dv + HALF_B, sl.v2);
+    const auto rk = rsrc(sl.dk), rv = rsrc(sl.dv);
+    __builtin_amdgcn_raw_buffer_store_b128(y1, rk, sl.off, 0, kNt);
+    __builtin_amdgcn_raw_buffer_store_b128(y2, rk, sl.off + HALF_B, 0, kNt);
+    __builtin_amdgcn_raw_buffer_store_b128(sl.v1, rv, sl.off, 0, kNt);
+    __builtin_amdgcn_raw_buffer_store_b128(sl.v2, rv, sl.off + HALF_B, 0, kNt);
   };
 
+  // Slots a and b alternate (the loop body twice, no copy between them: a copy of a slot whose
+  // loads are in flight would wait for them). The barriers order LDS only (the cos/sin tables),
+  // so the next item's row loads stay in flight across them.
   Slot a, b;
-  int cur = 0;
   prepare(it, a, cs_tab[0]);
   for (;;) {
-    const int nxt = it + stride;
-    prepare(nxt, b, cs_tab[cur ^ 1]);  // the next item's loads go out before this item's stores
-    __syncthreads();                   // this item's table written
-    finish(a, cs_tab[cur]);
-    if (nxt >= g.n_items) break;  // uniform
-    __syncthreads();              // this item's table read: the next prepare may rewrite it
-    a = b;
-    cur ^= 1;
-    it = nxt;
+    it += stride;
+    prepare(it, b, cs_tab[1]);  // the next item's loads go out before this item's stores
+    lds_barrier();              // this item's table written
+    finish(a, cs_tab[0]);
+    if (it >= g.n_items) break;  // uniform
+    lds_barrier();               // this item's table read: the next prepare may rewrite it
+    it += stride;
+    prepare(it, a, cs_tab[0]);
+    lds_barrier();
+    finish(b, cs_tab[1]);
+    if (it >= g.n_items) break;
+    lds_barrier();
   }
 }
 #ifndef CKV_PREGATHER_BYTES_PER_POS
@@ -189,7 +221,8 @@ int32_t pregather_layers(int32_t n_tokens, int32_t n_chunks, int32_t has_thresho
       n_segs <= 0 || n_heads <= 0 || n_chunks < 0)
     return 0;
   const int rows = pre_rows_of(dtype, head_dim);
-  if (rows % n_heads != 0) return 0;  // an item is every head of rows / n_heads tokens
+  // an item is every head of rows / n_heads tokens, a wavefront's rows one head's
+  if (rows % n_heads != 0 || kSelWaves % n_heads != 0) return 0;
   const int tpi = rows / n_heads;
   // whole layers of about CKV_PREGATHER_BYTES_PER_POS bytes per position in all (the HBM traffic
   // that fits the selection's time), on the CUs the selection leaves free
