@@ -16,7 +16,12 @@ different sizes (the histogram is left zeroed), and replays of a captured HIP gr
 ckv_layer1_repair_gather (the same repair, whole layers of the later layers' base cache gathered
 beside the selection, the dropped rows of the others with the kept rows' scatter) against
 layer1_repair + rerope_gather (with and without the skip map) at the 8k, config-3 and replay
-shapes, the edge requests and graph replays; the gathered layers also against the oracle."""
+shapes, the edge requests, every element type / head size / head count the whole-layer gather is
+built for, and graph replays; the gathered layers also against the oracle.
+
+ckv_rerope_gather_layers_kept (that call's last launch alone) against rerope_gather(skip) then
+scatter_kept_rows, with the kept-row count from the device or the host, at the 8k and replay
+shapes and the edge requests, and with an out-of-range source row (skipped and flagged)."""
 
 import numpy as np
 import pytest
@@ -498,6 +503,26 @@ def test_merged_gather_edges(case):
         _merged_vs_separate(req, layers=(2, 2))
         return
     _merged_vs_separate(req)
+
+
+@pytest.mark.parametrize("dtype,D,H,whole", [(torch.bfloat16, 64, 4, True), (torch.bfloat16, 64, 8, True),
+                                              (torch.bfloat16, 128, 1, True), (torch.bfloat16, 128, 2, True),
+                                              (torch.float32, 128, 2, True), (torch.float32, 64, 4, True),
+                                              (torch.bfloat16, 64, 3, False)])
+def test_merged_gather_whole_layers_every_shape(dtype, D, H, whole):
+    """The whole layers beside the selection at every element type and head size it is built
+    for, head counts from 1 to 8 within the call's 1024-byte rows (a wavefront's rows are one
+    head's: with a head count that does not divide 16 no layer is gathered whole); ragged chunk
+    lengths leave partial items at the segments' ends."""
+    rng = np.random.default_rng(D + H)
+    lens = [int(x) for x in rng.integers(40, 300, 14)]
+    starts, pos = [], 0
+    for c in rng.permutation(14):
+        starts.append((int(c), pos))
+        pos += lens[c]
+    req = Request(D + H, lens, starts, pos + 37, H=H, D=D, dtype=dtype, n_layers=5)
+    n_pre = _merged_vs_separate(req)[3]
+    assert (n_pre > 0) == whole, n_pre
 
 
 def test_merged_gather_graph_replays():
