@@ -82,8 +82,8 @@ GATHER_TRAFFIC_BYTES = 881_167_672
 # 137,468 KiB / 0.500023 + WRITE_SIZE median 274,565 KiB; 562,298,880 algorithmic bytes).
 DROPPED_TRAFFIC_BYTES = 562_675_830
 # rocprofv3 FETCH_SIZE / 0.500023 + WRITE_SIZE of the step's kept rows + dropped rows of layers
-# 4-27 launch (266,088,701 B read, 259,395.5 KiB written)
-MERGED_TRAFFIC_BYTES = 266_088_701 + 265_620_992
+# 4-27 launch (266,094,844 B read, 259,394.9 KiB written)
+MERGED_TRAFFIC_BYTES = 266_094_844 + 265_620_378
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 
@@ -1061,7 +1061,8 @@ def traffic_probe(steps: int, warmup: int, dev) -> dict:
     """Dispatches for the HBM traffic counters (run under rocprofv3 --pmc): `steps` re-RoPE +
     gather launches of the 8k request alternating two input sets, `steps` request steps (the
     fresh-row writes, the layer-1 deviation, selection and scatter as the step issues them),
-    `steps` dropped-row gathers, then `steps` elementwise kernels that read and write exactly
+    `steps` dropped-row gathers, `steps` of the step's last launch called alone (the roofline
+    kernel), then `steps` elementwise kernels that read and write exactly
     COPY_BYTES each, whose FETCH_SIZE / WRITE_SIZE calibrate the counters (a plain D2D copy goes to
     the DMA engine and is not counted)."""
     wls = [RepairWorkload(1234 + i, dev) for i in range(2)]
@@ -1072,6 +1073,8 @@ def traffic_probe(steps: int, warmup: int, dev) -> dict:
     torch.cuda.synchronize()
     for i in range(steps):
         wls[i % 2].gather_dropped()
+    for i in range(steps):
+        wls[i % 2].gather_kept()
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = [torch.empty_like(src) for _ in range(2)]
     for i in range(steps):  # one elementwise kernel: reads and writes exactly COPY_BYTES
