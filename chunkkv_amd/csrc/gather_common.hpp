@@ -42,7 +42,9 @@ __device__ __forceinline__ void gather_st(void* p, const vec16& v) {
   else st16(p, v);
 }
 
-template <int DTYPE, int D, int THREADS, int TILE, int UNROLL, bool SKIP>
+
+// NT_K: the key rows' stores non-temporal (else regular); the value rows' are gather_st's.
+template <int DTYPE, int D, int THREADS, int TILE, int UNROLL, bool SKIP, bool NT_K = true>
 __device__ __forceinline__ void gather_tile(
     char* __restrict__ dst_k, char* __restrict__ dst_v, int64_t dst_layer_stride_b, int64_t dst_head_stride_b,
     const uint64_t* __restrict__ src_tab, int n_chunks, const ckv_segment* __restrict__ segs, int seg_index,
@@ -185,14 +187,16 @@ __device__ __forceinline__ void gather_tile(
       const int r = r0 + u * RPP + rl;
       if (live[u]) {
         const int64_t o = dst_off(r);
-        if (rotate) {
-          vec16 y1, y2;
-          rotate_pairs<DTYPE>(kx1[u], kx2[u], c, sn, y1, y2);
+        // one store per half whichever the shift (stores in both arms of a branch get merged by
+        // the compiler, which then drops a non-temporal hint the arms share)
+        vec16 y1 = kx1[u], y2 = kx2[u];
+        if (rotate) rotate_pairs<DTYPE>(kx1[u], kx2[u], c, sn, y1, y2);
+        if constexpr (NT_K) {
           gather_st(dk0 + o, y1);
           gather_st(dk0 + o + HALF_B, y2);
         } else {
-          gather_st(dk0 + o, kx1[u]);
-          gather_st(dk0 + o + HALF_B, kx2[u]);
+          st16(dk0 + o, y1);
+          st16(dk0 + o + HALF_B, y2);
         }
         if (with_v) {
           gather_st(dv0 + o, vx1[u]);

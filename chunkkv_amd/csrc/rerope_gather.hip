@@ -29,17 +29,23 @@ namespace ckv {
 //  - Segment-fastest grid (x = segment, y = tile), 256 x 16 x 4, for launches of 64 segments or
 //    more: the replay's 4 concurrent 32k requests (128 segments each) reach 75.0 % of HBM peak
 //    with it, 68.2 % with the tile-fastest shapes above.
+// Stores: rows are loaded non-temporally and value rows stored non-temporally by every shape; the
+// key rows of the skip shape go out as regular stores, those of the others non-temporally
+// (measured, same box: the 8k request's dropped rows of layers 4-27 with layer 1's kept rows
+// 90.3 us against 98.5 us with non-temporal key stores; config 2's dense gather 78.0 against
+// 80.4 us and config 5's rounds 2.908 against 2.984 ms the other way round; both hints regular:
+// 112.0 us / 83.9 us / 3.000 ms).
 struct GatherDense {
   static constexpr int kThreads = 256, kTile = 8, kUnroll = 2;
-  static constexpr bool kSegFastest = false;
+  static constexpr bool kSegFastest = false, kNtK = true;
 };
 struct GatherSkip {
   static constexpr int kThreads = 512, kTile = 16, kUnroll = 1;
-  static constexpr bool kSegFastest = false;
+  static constexpr bool kSegFastest = false, kNtK = false;
 };
 struct GatherWide {
   static constexpr int kThreads = 256, kTile = 16, kUnroll = 4;
-  static constexpr bool kSegFastest = true;
+  static constexpr bool kSegFastest = true, kNtK = true;
 };
 constexpr int kGatherWideSegs = 64;  // segment count from which GatherWide is used
 
@@ -69,7 +75,7 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
     }
     zl -= scat_z;
   }
-  gather_tile<DTYPE, D, S::kThreads, S::kTile, S::kUnroll, true>(
+  gather_tile<DTYPE, D, S::kThreads, S::kTile, S::kUnroll, true, S::kNtK>(
       dst_k, dst_v, dst_layer_stride_b, dst_head_stride_b, src_tab, n_chunks, segs,
       (int)(S::kSegFastest ? blockIdx.x : blockIdx.y), one_seg, one_src_k, one_src_v, one_src_head_stride_b, n_layers,
       layer_begin + zl, (int)(S::kSegFastest ? blockIdx.y : blockIdx.x), n_heads, n_tokens, skip, inv, err);
