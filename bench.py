@@ -27,8 +27,10 @@ deviation, the scatters of layers 1-27):
     scatter L1-27   27 x 2976 x 4096 B                                         =   329,121,792
     total                                                                      = 1,277,624,832
 `value` = that total / measured time per step (GB/s), the step replayed from a HIP graph (the
-eager time, launch-bound from Python, is reported as ms_per_step_eager; layer 1 as ckv_layer1_repair
-and the dropped rows of layers 2-27 as a separate gather launch as ms_per_step_separate_gather;
+eager time, launch-bound from Python, is reported as ms_per_step_eager; with random layer-1
+rows (every deviation within a few percent of the others) as ms_per_step_uncorrelated; layer 1
+as ckv_layer1_repair and the dropped rows of layers 2-27 as a separate gather launch as
+ms_per_step_separate_gather;
 the same launches with the gathers on a second stream (HipEngine(overlap=True)) as
 ms_per_step_two_streams; layer 1 as the four launches ckv_layer1_repair replaces (base-cache
 gather, deviation, selection, scatter) as ms_per_step_layer1_four_launches; layers 0 and 2-27
@@ -459,6 +461,7 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     gk_ms = _timed(lambda i: wls[i % 2].gather_kept(), steps, stream)
     n_asm = N_LAYERS - 2
     asm_ms = _timed(lambda i: wls[(i // n_asm) % 2].assemble(2 + i % n_asm), steps * n_asm, stream)
+    ms_unc = _uncorrelated_steps(wls, steps, stream, dev)
     assert all(int(w.err.item()) == 0 for w in wls)
     plan = wls[0].plan
     n_keep = plan.n_keep
@@ -468,6 +471,7 @@ def bench_repair(steps: int, warmup: int, dev) -> dict:
     gk_bytes = merged_bytes(plan)
     ms_conc = _concurrent_steps(wls, steps, dev)
     return dict(ms_per_step=ms, ms_two=ms_two, ms_asm=ms_asm, ms_split=ms_split, ms_sep=ms_sep, ms_eager=ms_eager,
+                ms_unc=ms_unc,
                 bytes=nbytes,
                 moved=moved_bytes(plan),
                 gbs=nbytes / (ms * 1e-3) / 1e9, gd_ms=gd_ms, gd_bytes=gd_bytes, gd_gbs=gd_bytes / (gd_ms * 1e-3) / 1e9,
@@ -503,6 +507,31 @@ def _concurrent_steps(wls, steps: int, dev) -> float:
     ms = _timed(lambda i: g.replay(), steps, torch.cuda.current_stream(dev))
     assert all(int(w.err.item()) == 0 for w in reqs)
     for w in wls:  # leave the step's selection state as it was
+        w.step()
+    torch.cuda.synchronize()
+    return ms
+
+
+def _uncorrelated_steps(wls, steps: int, stream, dev) -> float:
+    """ms per step with layer-1 fresh rows that do not follow the cached ones (random rows: every
+    deviation within a few percent of the others, so most candidates share a few bins of the
+    selection's histogram, its worst case); the workloads' own rows are put back after."""
+    gen = torch.Generator(device=dev).manual_seed(99)
+    saved = [w.fresh[1] for w in wls]
+    for w in wls:
+        k1 = w.fresh[1][0]
+        ku = torch.randn(k1.shape, generator=gen, device=dev).to(k1.dtype)
+        vu = torch.randn(k1.shape, generator=gen, device=dev).to(k1.dtype).transpose(1, 2).contiguous().transpose(1, 2)
+        w.fresh[1] = (ku, vu)
+        w.step()
+    torch.cuda.synchronize()
+    graphs = [_graph_of(w.step) for w in wls]
+    for g in graphs:
+        g.replay()
+    ms = _timed(lambda i: graphs[i % 2].replay(), steps, stream)
+    assert all(int(w.err.item()) == 0 and int(w.sel.counts[0].item()) == w.plan.n_keep for w in wls)
+    for w, f in zip(wls, saved):
+        w.fresh[1] = f
         w.step()
     torch.cuda.synchronize()
     return ms
@@ -1482,6 +1511,7 @@ def main() -> None:
         "ms_per_step_assemble_variant": round(r["ms_asm"], 4),
         "ms_per_step_layer1_four_launches": round(r["ms_split"], 4),
         "ms_per_step_separate_gather": round(r["ms_sep"], 4),
+        "ms_per_step_uncorrelated": round(r["ms_unc"], 4),
         "concurrent_requests": {"requests": CONCURRENT, "ms_per_round": round(r["ms_conc"], 4),
                                 "gbs": round(r["conc_gbs"], 1), "pct_of_peak": round(100.0 * r["conc_gbs"] / PEAK_GBS, 2),
                                 "note": "the same request's KV repair, CONCURRENT independent requests in flight on "

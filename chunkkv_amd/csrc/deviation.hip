@@ -181,7 +181,7 @@ extern "C" int32_t ckv_deviation_select(
   }
   const SelectArgs sel{diff,     norm,     pos_flags, local,      (int)n_tokens, chunks,   (int)n_chunks,
                        (int)(has_threshold != 0), escalate_threshold, keep_abs, keep_local, keep_rank, rel_dev,
-                       escalated, counts};
+                       escalated, counts, hist_copies((int)n_tokens)};
   if (spread) return select_slices_launch(sel, hist, nullptr, err, st);
   return select_launch(sel, hist, st);
 }

@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kL1Threads) void layer1_gather_deviation_kernel(
       cnt += bj == bin ? 1u : 0u;
       first = first && !(j < lane && bj == bin);
     }
-    if (bin != ~0u && first) atomicAdd(hist_copy(a.hist, hist_copies(a.n_tokens)) + bin, cnt);
+    if (bin != ~0u && first) atomicAdd(hist_copy(a.hist, hist_copies_l1(a.n_tokens)) + bin, cnt);
   }
 }
 
@@ -422,8 +422,10 @@ static int32_t layer1_repair_impl(
   if (dst_head_stride < (int64_t)n_tokens * head_dim) return CKV_ERR_OUT_OF_RANGE;
   if (n_tokens > CKV_SELECT_MAX_TOKENS || n_segs > kL1MaxSegs) return CKV_ERR_TOO_LARGE;
   hipStream_t st = (hipStream_t)stream;
-  const SelectArgs sel{diff, norm, pos_flags, local, (int)n_tokens, chunks, (int)n_chunks, (int)(has_threshold != 0),
-                       escalate_threshold, keep_abs, keep_local, keep_rank, rel_dev, escalated, counts};
+  const SelectArgs sel{diff,          norm,     pos_flags,  local,      (int)n_tokens,
+                       chunks,        (int)n_chunks,        (int)(has_threshold != 0),
+                       escalate_threshold, keep_abs, keep_local, keep_rank, rel_dev,
+                       escalated,     counts,   hist_copies_l1((int)n_tokens)};
   if (tail != nullptr && (keep_rank == nullptr || tail->begin < 0 || tail->end < tail->begin || tail->end > n_layers ||
                           tail->max_seg_tokens < 0 || (tail->begin < tail->end && (layer >= tail->begin &&
                                                                                   layer < tail->end))))

@@ -53,24 +53,26 @@ static_assert(kTopBins == 4 * kSelThreads, "each thread owns four top-digit bins
 static_assert((kTopLo & ((1u << kTopShift) - 1u)) == 0u, "interior bins are key prefixes");
 static_assert((uint64_t)kTopLo + ((uint64_t)(kTopBins - 2) << kTopShift) <= 0xffffffffull, "window inside the key range");
 
-// Above 16384 positions the histogram is held as kHistCopies copies of kTopBins words (the
-// workspace's first kHistWords words; the spread selection's ticket word follows them):
-// workgroup w of the counting launch adds into copy w % kHistCopies, so its atomics land on four
-// addresses per bin instead of one, and a reader sums the copies of its bins. With uncorrelated
-// fresh rows most candidates share a handful of bins and atomics on one address serialise: a
-// 32,832-position layer-1 pass took 96 us with one copy, 55 us with two, 35 us (as with
-// correlated rows) with four or eight; reading four copies costs that size's selection 0.8 us,
-// eight 1.8 us. Up to 16384 positions (the single-workgroup selection; a quarter of the counting
-// workgroups) there is one copy: reading more would cost those selections more than the atomics
-// they spread.
+// The histogram can be held as kHistCopies copies of kTopBins words (the workspace's first
+// kHistWords words; the spread selection's ticket word follows them): workgroup w of the counting
+// launch adds into copy w % kHistCopies, so its atomics land on four addresses per bin instead of
+// one, and a reader sums the copies of its bins. With uncorrelated fresh rows most candidates
+// share a handful of bins and atomics on one address serialise: a 32,832-position layer-1 pass
+// took 96 us with one copy, 55 us with two, 35 us (as with correlated rows) with four or eight,
+// and the 8k request's layer-1 repair 129.5 us with one copy against 115.4 us with four (114.2 us
+// with correlated rows either way). Reading four copies costs a selection up to ~0.8 us where it
+// is on the critical path. So the layer-1 pass (four positions a workgroup, the engine's path)
+// counts into four copies above 2048 positions (hist_copies_l1); the deviation launch of
+// ckv_deviation_select (eight positions a workgroup) above 16384 (hist_copies): its 8192-position
+// selection would pay 0.7 us for the copies (config 3: 25.2 against 26.0 us). The selection
+// reads as many copies as SelectArgs::hist_copies says.
 constexpr int kHistCopies = 4;
 constexpr int kHistWords = kHistCopies * kTopBins;
 static_assert(kHistWords * 4 + 4 <= CKV_DEVIATION_SELECT_WORKSPACE_BYTES &&
                   CKV_DEVIATION_SELECT_WORKSPACE_BYTES == CKV_LAYER1_REPAIR_WORKSPACE_BYTES,
               "the histogram copies and the ticket fit the workspaces");
-__host__ __device__ constexpr int hist_copies(int n_tokens) {
-  return n_tokens > kSelRegMax * kSelThreads ? kHistCopies : 1;
-}
+__host__ __device__ constexpr int hist_copies(int n_tokens) { return n_tokens > 16384 ? kHistCopies : 1; }
+__host__ __device__ constexpr int hist_copies_l1(int n_tokens) { return n_tokens > 2048 ? kHistCopies : 1; }
 
 // This workgroup's copy of a histogram held as `copies` copies.
 __device__ __forceinline__ uint32_t* hist_copy(uint32_t* h, int copies) {
@@ -89,6 +91,14 @@ template <int C>
 __device__ __forceinline__ void hist_zero4(uint32_t* p) {
 #pragma unroll
   for (int c = 0; c < C; ++c) st16(p + c * kTopBins, vec16{0u, 0u, 0u, 0u});
+}
+// The same for `copies` copies (1 or kHistCopies, uniform): each form's loads go out together.
+__device__ __forceinline__ vec16 hist_load4_n(const uint32_t* p, int copies) {
+  return copies > 1 ? hist_load4<kHistCopies>(p) : hist_load4<1>(p);
+}
+__device__ __forceinline__ void hist_zero4_n(uint32_t* p, int copies) {
+  if (copies > 1) hist_zero4<kHistCopies>(p);
+  else hist_zero4<1>(p);
 }
 
 // Order-preserving key of a deviation: larger float -> larger key; -0 == +0; NaN -> 0.
@@ -203,6 +213,7 @@ struct SelectArgs {
   float* rel_out;
   uint8_t* esc_out;
   int32_t* counts;
+  int hist_copies;  // copies of the candidate histogram the counting launch used (0 or 1: one)
 };
 
 // rel_dev / escalated of chunk c (no threshold: never escalated), computed by the calling
@@ -363,7 +374,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   vec16 g4 = {0u, 0u, 0u, 0u};
   uint32_t* gmine = ghist != nullptr ? ghist + (kTopBins - 4 * (tid + 1)) : nullptr;
   auto load_hist = [&]() {
-    if (gmine != nullptr) g4 = hist_load4<1>(gmine);  // up to 16384 positions: one copy
+    if (gmine != nullptr) g4 = hist_load4_n(gmine, a.hist_copies);
   };
   if (vec_ok && wave_end <= n_tokens) {  // uniform: the whole wavefront's runs are in range
 #pragma unroll
@@ -551,7 +562,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   // One scan: candidates, mismatches, and this thread's share of the top-digit histogram (its
   // exclusive prefix = candidates in higher bins than its own).
   const uint32_t gsum = g4.x + g4.y + g4.z + g4.w;
-  if (gmine != nullptr) hist_zero4<1>(gmine);  // leave the histogram zeroed for the next call
+  if (gmine != nullptr) hist_zero4_n(gmine, a.hist_copies);  // leave the histogram zeroed for the next call
   uint64_t scan_tot = 0;
   const uint64_t scan_ex = block_scan_1b_u64((uint64_t)__popcll(cand) | ((uint64_t)mism << 21) |
                                                  ((uint64_t)gsum << 42), slots64[0], scan_tot);

@@ -232,10 +232,9 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
   uint32_t fw[G];
 #pragma unroll
   for (int i = 0; i < G; ++i) load_group(i, dv[i], fw[i]);
-  // G > 4 groups per thread <=> more than 16384 positions: the counting launch spread the
-  // histogram over kHistCopies copies (hist_copies)
-  constexpr int HC = G > 4 ? kHistCopies : 1;
-  const vec16 g4 = ghist != nullptr ? hist_load4<HC>(ghist + (kTopBins - BPT * (tid + 1))) : vec16{0u, 0u, 0u, 0u};
+  // the histogram's copies, as the counting launch spread it
+  const vec16 g4 =
+      ghist != nullptr ? hist_load4_n(ghist + (kTopBins - BPT * (tid + 1)), a.hist_copies) : vec16{0u, 0u, 0u, 0u};
   ckv_chunk_span sp = {0, 0, 0, 0};
   if (tid < n_chunks) {
     const vec16 v = ld16(chunks + tid);
@@ -547,7 +546,7 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
     counts[CKV_COUNT_TOP_HISTOGRAM] = (use_top ? 1 : 0) | (ranked ? 2 : 0);
   }
   if (ghist != nullptr && s_last) {  // uniform: the last ticket; every workgroup has read the histogram
-    hist_zero4<HC>(ghist + (kTopBins - BPT * (tid + 1)));
+    hist_zero4_n(ghist + (kTopBins - BPT * (tid + 1)), a.hist_copies);
     if (tid == 0) ghist[kHistWords] = 0u;
   }
 
