@@ -110,7 +110,8 @@ typedef struct ckv_chunk_span {
    used). */
 #define CKV_DEVIATION_SELECT_WORKSPACE_BYTES 65792
 
-/* Bytes of the workspace ckv_layer1_repair and ckv_layer1_repair_gather take (the same layout). */
+/* Bytes of the workspace ckv_layer1_repair and ckv_layer1_repair_gather take (the same layout;
+   their counting launch uses the four copies above 2048 positions). */
 #define CKV_LAYER1_REPAIR_WORKSPACE_BYTES 65792
 
 /* ABI version compiled into the library (CKV_ABI_VERSION). */
