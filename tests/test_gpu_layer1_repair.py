@@ -189,6 +189,20 @@ def test_8k_request_shape():
     assert counts[0] == 2976 and req.plan.n_keep == 2976
 
 
+@pytest.mark.parametrize("N_tail", [0, 576])
+def test_uncorrelated_rows_in_histogram_copies(N_tail):
+    """Fresh rows that do not follow the cached ones (noise 30 x the rows' own scale: every
+    deviation within a few percent of the others, most candidates in a few histogram bins) at
+    sizes where the layer-1 pass counts into four histogram copies (above 2048 positions): the
+    call, its merged form and the oracle agree bit for bit."""
+    rng = np.random.default_rng(11 + N_tail)
+    starts, N = _shuffled(rng, 24, 320, N_tail)
+    req = Request(11 + N_tail, [320] * 24, starts, N, noise=30.0, n_layers=4)
+    check(req)
+    _, _, sm, _ = _merged_vs_separate(req)
+    assert int(sm.counts[0].item()) == req.plan.n_keep
+
+
 @pytest.mark.parametrize("ratio", [0.15, 0.3, 0.5])
 def test_config3_shape(ratio):
     """32 chunks x 256 in order (shift 0 keeps the keys bit for bit), T = 4."""
