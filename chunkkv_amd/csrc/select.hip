@@ -20,7 +20,7 @@ template <int KPT, bool SUMS>
 __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(const float* diff, const uint8_t* flags,
                                                                  const int32_t* local, uint32_t* ghist,
                                                                  const ckv_chunk_span* chunks, int n_tokens,
-                                                                 int n_chunks, SelectArgs a) {
+                                                                 int n_chunks, int hist_copies, SelectArgs a) {
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
   a.diff = diff;
   a.flags = flags;
@@ -28,6 +28,7 @@ __global__ __launch_bounds__(kSelThreads) void select_reg_kernel(const float* di
   a.chunks = chunks;
   a.n_tokens = n_tokens;
   a.n_chunks = n_chunks;
+  a.hist_copies = hist_copies;
   if (!SUMS && blockIdx.x > 0) {
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
     for (int c = ((int)blockIdx.x - 1) * kSelWaves + wave; c < a.n_chunks; c += ((int)gridDim.x - 1) * kSelWaves)
@@ -257,7 +258,8 @@ int32_t select_slices_launch(const SelectArgs& args, uint32_t* ghist, const Slic
   SliceRows rw = rows != nullptr ? *rows : SliceRows{};
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(kSlThreads), lds, st, args.diff, args.flags, ghist, args.local, N,
-                       args.n_chunks, args.chunks, S, n_slices, args, rw, err);
+                       args.n_chunks, args.chunks, S | (args.hist_copies > 1 ? kHistCopies : 1) << 16, n_slices, args,
+                       rw, err);
   };
 #define CKV_SL(G)                                                   \
   if (N <= kSlThreads * 4 * G) {                                    \
@@ -287,11 +289,11 @@ int32_t select_launch(const SelectArgs& args, uint32_t* ghist, hipStream_t st) {
   if (kpt <= K) {                                                                                         \
     if (args.has_thr)                                                                                     \
       hipLaunchKernelGGL((select_reg_kernel<K, true>), dim3(1), dim3(kSelThreads), lds, st, args.diff, args.flags, \
-                         args.local, ghist, args.chunks, args.n_tokens, args.n_chunks, args);                   \
+                         args.local, ghist, args.chunks, args.n_tokens, args.n_chunks, args.hist_copies, args);  \
     else                                                                                                  \
       hipLaunchKernelGGL((select_reg_kernel<K, false>), dim3(1 + sum_groups), dim3(kSelThreads), lds, st,  \
                          args.diff, args.flags, args.local, ghist, args.chunks, args.n_tokens, args.n_chunks, \
-                         args);                                                                           \
+                         args.hist_copies, args);                                                         \
     CKV_RETURN_IF_LAUNCH_FAILED();                                                                        \
     return CKV_OK;                                                                                        \
   }

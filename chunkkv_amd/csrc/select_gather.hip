@@ -172,7 +172,8 @@ template <int KPT, int DTYPE, int D>
 __global__ __launch_bounds__(kSelThreads) void select_gather_kernel(const float* diff, const uint8_t* flags,
                                                                     const int32_t* local, uint32_t* ghist,
                                                                     const ckv_chunk_span* chunks, int n_tokens,
-                                                                    int n_chunks, SelectArgs a, const PreGather g) {
+                                                                    int n_chunks, int hist_copies, SelectArgs a,
+                                                                    const PreGather g) {
   extern __shared__ uint32_t masks[];  // esc[W], pool[W]: spans of escalated / pooled chunks
   const int sel_blocks = 1 + g.sum_groups;
   if ((int)blockIdx.x >= sel_blocks) {  // uniform: a gather workgroup
@@ -185,6 +186,7 @@ __global__ __launch_bounds__(kSelThreads) void select_gather_kernel(const float*
   a.chunks = chunks;
   a.n_tokens = n_tokens;
   a.n_chunks = n_chunks;
+  a.hist_copies = hist_copies;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
   if (blockIdx.x > 0) {
     for (int c = ((int)blockIdx.x - 1) * kSelWaves + wave; c < a.n_chunks; c += g.sum_groups * kSelWaves)
@@ -257,7 +259,7 @@ int32_t select_gather_launch(const SelectArgs& args, uint32_t* ghist, PreGather 
 #define CKV_SG(K, DT, HD)                                                                                      \
   if (kpt <= K && dtype == DT && head_dim == HD) {                                                              \
     hipLaunchKernelGGL((select_gather_kernel<K, DT, HD>), grid, dim3(kSelThreads), lds, st, args.diff, args.flags, \
-                       args.local, ghist, args.chunks, args.n_tokens, args.n_chunks, args, g);                   \
+                       args.local, ghist, args.chunks, args.n_tokens, args.n_chunks, args.hist_copies, args, g); \
     CKV_RETURN_IF_LAUNCH_FAILED();                                                                              \
     *n_pre = k;                                                                                                 \
     return CKV_OK;                                                                                              \

@@ -165,7 +165,7 @@ __device__ __forceinline__ uint32_t sl_pass(Each each, uint32_t& prefix, uint32_
 template <int G, bool ROWS, bool C32 = (G <= kSlWideCodes)>
 __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
     const float* diff, const uint8_t* flags, uint32_t* ghist, const int32_t* local, int n_tokens, int n_chunks,
-    const ckv_chunk_span* chunks, int slice_len, int n_slices, SelectArgs a, SliceRows rw, int32_t* err) {
+    const ckv_chunk_span* chunks, int slice_len_copies, int n_slices, SelectArgs a, SliceRows rw, int32_t* err) {
   constexpr int NT = kSlThreads;
   constexpr int BPT = kTopBins / NT;  // histogram bins per thread (4: one 16-byte load)
   static_assert(BPT == 4, "a thread's bins are one 16-byte load");
@@ -200,6 +200,10 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
   const uint32_t* pool_t = poolw + (tid >> 3);  // this thread's words (group i: pool_t[128 i])
   const uint32_t* take_t = takew + (tid >> 3);
   const int nib = (4 * tid) & 31;
+  // slice length in the low 16 bits, the histogram's copies above them: both among the
+  // preloaded arguments, so the first loads wait for no scalar load of the struct arguments
+  const int slice_len = slice_len_copies & 0xffff;
+  const int hcopies = slice_len_copies >> 16;
   const int s0 = (int)blockIdx.x * slice_len;
   const bool aligned = ((uintptr_t)diff % 16 == 0) && ((uintptr_t)flags % 4 == 0);
 
@@ -234,7 +238,7 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
   for (int i = 0; i < G; ++i) load_group(i, dv[i], fw[i]);
   // the histogram's copies, as the counting launch spread it
   const vec16 g4 =
-      ghist != nullptr ? hist_load4_n(ghist + (kTopBins - BPT * (tid + 1)), a.hist_copies) : vec16{0u, 0u, 0u, 0u};
+      ghist != nullptr ? hist_load4_n(ghist + (kTopBins - BPT * (tid + 1)), hcopies) : vec16{0u, 0u, 0u, 0u};
   ckv_chunk_span sp = {0, 0, 0, 0};
   if (tid < n_chunks) {
     const vec16 v = ld16(chunks + tid);
@@ -546,7 +550,7 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
     counts[CKV_COUNT_TOP_HISTOGRAM] = (use_top ? 1 : 0) | (ranked ? 2 : 0);
   }
   if (ghist != nullptr && s_last) {  // uniform: the last ticket; every workgroup has read the histogram
-    hist_zero4_n(ghist + (kTopBins - BPT * (tid + 1)), a.hist_copies);
+    hist_zero4_n(ghist + (kTopBins - BPT * (tid + 1)), hcopies);
     if (tid == 0) ghist[kHistWords] = 0u;
   }
 
