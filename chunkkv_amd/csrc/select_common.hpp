@@ -801,7 +801,45 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   const int n_keep = (int)(all & kField);
   const int sel_cached = (int)((all >> 21) & kField);
   const int uncomputed = (int)((all >> 42) & kField);
-  // four positions at a time: the kept ones' keep_abs / keep_local, then the four keep_rank entries
+  // keep_abs / keep_local go out through LDS, a window of kStage ranks at a time (the radix
+  // histograms' space, no longer read): each thread puts its kept positions at their ranks, then
+  // the workgroup stores the window in rank order, two entries per 16-byte store, instead of
+  // every lane storing 8 bytes at its own rank
+  {
+    int2* stage = reinterpret_cast<int2*>(&hist[0][0][0]);
+    constexpr int kStage = (int)(sizeof(hist) / sizeof(int2));
+    const bool st16_ok = (((uintptr_t)a.keep_abs | (uintptr_t)a.keep_local) % 16) == 0;
+    for (int w0 = 0; w0 < n_keep; w0 += kStage) {  // uniform
+      __syncthreads();  // the histograms' last reads, or the previous window's
+      int r = rank;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        if ((kept >> i) & 1ull) {
+          if (r >= w0 && r < w0 + kStage) stage[r - w0] = make_int2(p0 + i, lv[i] < 0 ? 0 : lv[i]);
+          ++r;
+        }
+      }
+      __syncthreads();
+      const int cnt = min(kStage, n_keep - w0);
+      for (int j = 2 * tid; j < cnt; j += 2 * kSelThreads) {
+        const int2 e0 = stage[j];
+        if (st16_ok && j + 1 < cnt) {
+          const int2 e1 = stage[j + 1];
+          *(longlong2*)(a.keep_abs + w0 + j) = make_longlong2(e0.x, e1.x);
+          *(longlong2*)(a.keep_local + w0 + j) = make_longlong2(e0.y, e1.y);
+        } else {
+          a.keep_abs[w0 + j] = e0.x;
+          a.keep_local[w0 + j] = e0.y;
+          if (j + 1 < cnt) {
+            const int2 e1 = stage[j + 1];
+            a.keep_abs[w0 + j + 1] = e1.x;
+            a.keep_local[w0 + j + 1] = e1.y;
+          }
+        }
+      }
+    }
+  }
+  // four positions at a time: the four keep_rank entries
 #pragma unroll
   for (int i0 = 0; i0 < KPT; i0 += 4) {
     int kr[4];  // keep_rank of positions i0 .. i0 + 3
@@ -810,11 +848,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
       const int i = i0 + j;
       const bool k = i < KPT && ((kept >> i) & 1ull);
       kr[j] = k ? rank : -1;
-      if (k) {
-        a.keep_abs[rank] = p0 + i;
-        a.keep_local[rank] = lv[i] < 0 ? 0 : lv[i];
-        ++rank;
-      }
+      if (k) ++rank;
     }
     if (keep_rank != nullptr) {
       if (vec_ok && p0 + i0 + 4 <= n_tokens) {
