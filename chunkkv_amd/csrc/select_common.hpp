@@ -317,7 +317,7 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
                                            const ckv_chunk_span (&sp0)[kSelPre<KPT>]) {
   static_assert(KPT <= 33, "a run of KPT positions spans at most two mask words and one 64-bit word");
   constexpr int kBatch = 8;  // chunk-sum loads in flight per lane
-  __shared__ uint32_t hist[2][kSelWaves][256];
+  __shared__ __align__(16) uint32_t hist[2][kSelWaves][256];  // also the rank list and the store staging
   __shared__ uint32_t hl[3][256];  // one shared histogram per pass after the top digit (few candidates)
   __shared__ int slots[2][kSelWaves];
   __shared__ uint64_t slots64[2][kSelWaves];
