@@ -53,20 +53,27 @@ __device__ __forceinline__ void deviation_wave(const DevArgs& a, int p_base, flo
   const int n_vecs = a.n_heads * vecs_per_row;
   const int N = a.n_tokens;
 
+  // Lane t < T loads position p_base + t's local index and flag byte. The addresses differ per
+  // lane, so these are vector loads, which complete in issue order: the row loads below go out
+  // right behind them and only the first read of an index waits. (Read as wave-uniform values
+  // they became a scalar load and a byte load plus readfirstlane that every row load waited for:
+  // one whole memory round trip more per wavefront.)
+  const int lp = min(p_base + min(lane, T - 1), N - 1);
+  const int j_lane = a.local[lp];
+  const uint32_t f_lane = a.flags[lp];
   int jraw[T];
   uint32_t fraw[T];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const int pc = min(p_base + t, N - 1);
-    jraw[t] = a.local[pc];
-    fraw[t] = a.flags[pc];
-  }
   float sk[T], sv[T], nk[T], nv[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) sk[t] = sv[t] = nk[t] = nv[t] = 0.0f;
   int jj[T];
   bool cached[T], bad = false;
   auto checks = [&]() {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      jraw[t] = __builtin_amdgcn_readlane(j_lane, t);
+      fraw[t] = (uint32_t)__builtin_amdgcn_readlane((int)f_lane, t);
+    }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const bool valid = p_base + t < N;
@@ -121,6 +128,7 @@ __device__ __forceinline__ void deviation_wave(const DevArgs& a, int p_base, flo
       k16[t] = ld16_stream(a.kf + h * a.kf_hs_b + js[t] * a.kf_ts_b + cb);
       v16[t] = ld16_stream(a.vf + h * a.vf_hs_b + js[t] * a.vf_ts_b + cb);
     }
+    __builtin_amdgcn_sched_barrier(0);  // the row loads stay ahead of the first index read
     checks();
 #pragma unroll
     for (int t = 0; t < T; ++t) {

@@ -348,10 +348,10 @@ __device__ __forceinline__ void select_run(const SelectArgs& a, uint32_t* ghist,
   float dv[KPT];            // the owned positions' deviations (their keys after phase 0)
   uint32_t fl[kFlagWords];  // their flag bytes, four per register
   int lv[KPT];              // their local indices (the compaction's keep_local)
-  // Above 16 positions per thread the local indices are loaded by the compaction, which alone
-  // uses them: held from the start they pushed the 24- and 33-position buckets past the 128
-  // registers a thread of a 1024-thread workgroup has, into scratch memory.
-  constexpr bool kLateLocal = KPT > 16;
+  // From 16 positions per thread the local indices are loaded by the compaction, which alone
+  // uses them: held from the start they pushed the 16-position bucket past the 128 registers a
+  // thread of a 1024-thread workgroup has, 20-28 bytes per thread into scratch memory.
+  constexpr bool kLateLocal = KPT >= 16;
 #pragma unroll
   for (int w = 0; w < kFlagWords; ++w) fl[w] = 0u;
   // A thread's run is contiguous, so lanes are KPT elements apart: with KPT % 4 == 0 and aligned
