@@ -351,9 +351,11 @@ def _deviation_case(rng, N, H, D, bf16, token_major_v=True):
 
 @pytest.mark.parametrize("bf16", [True, False])
 @pytest.mark.parametrize("N", [1, 77, 8192])
-def test_deviation_bit_exact(bf16, N):
-    rng = np.random.default_rng(N + bf16)
-    H, D = 4, 128
+@pytest.mark.parametrize("H,D", [(4, 128), (2, 64), (4, 64)])
+def test_deviation_bit_exact(bf16, N, H, D):
+    """Every row layout of the deviation kernel: one vector of each row per lane (bf16 4 x 128),
+    fewer vectors than lanes (2 x 64, 4 x 64) and several per lane (fp32 4 x 128)."""
+    rng = np.random.default_rng(N + bf16 + 7 * D + H)
     k, v, K, V = _deviation_case(rng, N, H, D, bf16)
     flags = (rng.random(N) < 0.9).astype(np.uint8)
     active = np.sort(rng.choice(N, max(1, int(N * 0.85)), replace=False))
