@@ -231,7 +231,15 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
     }
   };
 
-  // ---- phase 0: every load up front
+  // ---- phase 0: every load up front. The chunk spans go first: phase 1 uses them before anything
+  // else loaded here (vector loads complete in issue order), so it runs while the rest are in
+  // flight. Their index is clamped instead of the load sitting behind tid < n_chunks: entries
+  // past n_chunks are never read (phase 1 tests c < n_chunks first).
+  ckv_chunk_span sp = {0, 0, 0, 0};
+  if (n_chunks > 0) {  // uniform
+    const vec16 v = ld16(chunks + min(tid, n_chunks - 1));
+    sp = ckv_chunk_span{(int32_t)v.x, (int32_t)v.y, (int32_t)v.z, (int32_t)v.w};
+  }
   float dv[G][4];
   uint32_t fw[G];
 #pragma unroll
@@ -239,11 +247,6 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
   // the histogram's copies, as the counting launch spread it
   const vec16 g4 =
       ghist != nullptr ? hist_load4_n(ghist + (kTopBins - BPT * (tid + 1)), hcopies) : vec16{0u, 0u, 0u, 0u};
-  ckv_chunk_span sp = {0, 0, 0, 0};
-  if (tid < n_chunks) {
-    const vec16 v = ld16(chunks + tid);
-    sp = ckv_chunk_span{(int32_t)v.x, (int32_t)v.y, (int32_t)v.z, (int32_t)v.w};
-  }
   // the slice's groups: S/4 consecutive threads at group row ig
   const int sg0 = s0 >> 2;
   const int ig = sg0 / NT, t_first = sg0 % NT;
@@ -328,8 +331,19 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
   uint64_t scan_tot = 0;
   const uint64_t scan_ex =
       sl_scan_u64((uint64_t)n_cand | ((uint64_t)mism << 21) | ((uint64_t)gsum << 42), slots64[0], scan_tot);
-  if (ghist != nullptr && tid == 0)  // every thread's histogram load landed before the scan's barrier
-    s_last = atomicAdd(ghist + kHistWords, 1u) == (uint32_t)(n_slices - 1) ? 1 : 0;
+  // the workgroup's ticket (every thread's histogram load landed before the scan's barrier); its
+  // value is first read in phase 4, so no barrier before then waits for the atomic's round trip.
+  // The address carries threadIdx.y, 0 in this one-dimensional launch but a per-lane value to
+  // the compiler: at a provably uniform address its atomic optimizer broadcasts the returned
+  // value right after the atomic, and phase 3's first barrier then waited for the round trip.
+  // Every load above has landed before it (an explicit wait, free here: the histogram loads, which
+  // the scan needed, were issued after the deviations and flags, and vector loads complete in
+  // order): otherwise a value used after it, such as a code computed late, waits for every memory
+  // operation of the wavefront, the atomic included.
+  const int opaque0 = (int)threadIdx.y;
+  uint32_t ticket = 0u;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt at their maxima (no wait)
+  if (ghist != nullptr && tid == 0) ticket = atomicAdd(ghist + kHistWords + opaque0, 1u);
   const int cand_total = (int)(scan_tot & kField);
   const int budget_req = s_budget_req;
   const int budget = max(0, min(budget_req, cand_total));
@@ -535,6 +549,7 @@ __global__ __launch_bounds__(kSlThreads) void select_slices_kernel(
     n_kept += __popc(k4);
     k4s = i == ig ? k4 : k4s;
   }
+  if (ghist != nullptr && tid == 0) s_last = ticket == (uint32_t)(n_slices - 1) ? 1 : 0;  // the scan's barrier publishes it
   uint64_t red_tot = 0;
   sl_scan_u64((uint64_t)n_before | ((uint64_t)n_kept << 21) | ((uint64_t)n_unc << 42), slots64[1], red_tot);
   const int prefix_keep = (int)(red_tot & kField);
