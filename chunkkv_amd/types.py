@@ -33,18 +33,18 @@ class Placement:
 
     chunk: ChunkKV
     start: int
-    ratio: float | None = None  # per-chunk recompute budget; None = the config default
-    exact: bool = False  # computed after the same prefix: never recomputed, not even at layer 0
+    ratio: float | None = None  # this placement's own recompute fraction; None: BlendConfig.recompute_ratio
+    exact: bool = False  # KV produced under the identical prefix: kept as is at every layer, layer 0 too
 
 
 @dataclass
 class BlendConfig:
     """Blend-prefill knobs (base.py:36-43)."""
 
-    recompute_ratio: float = 0.15  # share of each placement's cached tokens that layers >= 1 recompute
-    n_sink: int = 2  # first tokens of each non-exact chunk, always recomputed
-    full_first_layer: bool = True  # False = naive reuse (no repair)
-    escalate_threshold: float | None = None  # whole-chunk recompute above this layer-1 deviation
+    recompute_ratio: float = 0.15  # per placement, the part of its cached positions re-run in layers 1..L-1
+    n_sink: int = 2  # leading positions of every non-exact placement, re-run unconditionally
+    full_first_layer: bool = True  # layer 0 over every non-exact position; False: plain reuse, no repair
+    escalate_threshold: float | None = None  # a placement whose layer-1 relative deviation exceeds it is re-run whole
 
 
 @dataclass
@@ -56,7 +56,7 @@ class PrefillResult:
     keys: list[Any]
     values: list[Any]
     stats: dict = field(default_factory=dict)
-    copy: Callable[[Any], Any] = lambda a: a  # how a stored chunk copies its slices out of the request's buffers
+    copy: Callable[[Any], Any] = lambda a: a  # detaches a stored chunk's slices from the request's cache buffers
     # Batched extraction hook (spans -> one (2, L, 1, H, len, D) buffer per span); set by HipEngine
     # to its one-launch kernel. None: the per-layer `copy` path of the reference.
     extract: Callable[[list], list] | None = None
