@@ -79,13 +79,13 @@ GATHER_BYTES = N_LAYERS * N_CHUNKS * CHUNK_LEN * ROW_BYTES * 2 * 2
 # HBM bytes per gather launch of this workload from the FETCH_SIZE / WRITE_SIZE counter passes
 # (profiles/traffic_rerope_gather_qwen25_7b_8k.md; FETCH_SIZE calibrated against a kernel of
 # known traffic). Counters cannot be read inside a timed run, so the measured value is recorded.
-GATHER_TRAFFIC_BYTES = 881_167_672
+GATHER_TRAFFIC_BYTES = 881_089_130
 # Same for one gather of the dropped rows of layers 2-27 of the 8k request (FETCH_SIZE median
-# 137,468 KiB / 0.500023 + WRITE_SIZE median 274,565 KiB; 562,298,880 algorithmic bytes).
-DROPPED_TRAFFIC_BYTES = 562_675_830
+# 137,468.3 KiB / 0.500023 + WRITE_SIZE median 274,560 KiB; 562,298,880 algorithmic bytes).
+DROPPED_TRAFFIC_BYTES = 562_671_568
 # rocprofv3 FETCH_SIZE / 0.500023 + WRITE_SIZE of the step's kept rows + dropped rows of layers
-# 4-27 launch (266,094,844 B read, 259,394.9 KiB written)
-MERGED_TRAFFIC_BYTES = 266_094_844 + 265_620_378
+# 4-27 launch (266,093,411 B read, 259,392 KiB written)
+MERGED_TRAFFIC_BYTES = 266_093_411 + 265_617_408
 DEVIATION_BYTES = N_TOKENS * 4 * ROW_BYTES + N_TOKENS * 8
 
 

@@ -116,6 +116,30 @@ __device__ __forceinline__ void st16(void* p, const vec16& v) { *(gvec16*)p = v;
 __device__ __forceinline__ vec16 ld16_stream(const void* p) { return __builtin_nontemporal_load((const gvec16*)p); }
 __device__ __forceinline__ void st16_stream(void* p, const vec16& v) { __builtin_nontemporal_store(v, (gvec16*)p); }
 
+// Stores with device scope (sc1): written through the L2 as they go, so the end-of-launch release
+// has none of their lines left to write back; with nt also non-temporal. No builtin sets sc1 on a
+// 16-byte store, so the instruction is written out, and the compiler does not know it is a store:
+// a store of more than 8 bytes reads its data registers after it issues, and an instruction that
+// overwrites them right after it corrupts the stored data (the compiler pads the stores it emits
+// itself). The s_nop after each store supplies those wait states. The memory clobber keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void st16_agent(void* p, const vec16& v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 4" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st16_agent_stream(void* p, const vec16& v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1 nt\n\ts_nop 4" ::"v"(p), "v"(v) : "memory");
+}
+
+// A 16-byte store by cache policy (a launch shape's property).
+enum StorePolicy { kStRegular = 0, kStStream = 1, kStAgent = 2, kStAgentStream = 3 };
+template <int P>
+__device__ __forceinline__ void st16_policy(void* p, const vec16& v) {
+  if constexpr (P == kStRegular) st16(p, v);
+  else if constexpr (P == kStStream) st16_stream(p, v);
+  else if constexpr (P == kStAgent) st16_agent(p, v);
+  else st16_agent_stream(p, v);
+}
+
 // ---- wavefront reductions -----------------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }

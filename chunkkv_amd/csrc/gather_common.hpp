@@ -29,22 +29,15 @@ namespace ckv {
 #ifndef CKV_GATHER_NT_LOAD
 #define CKV_GATHER_NT_LOAD 1
 #endif
-#ifndef CKV_GATHER_NT_STORE
-#define CKV_GATHER_NT_STORE 1
-#endif
 
 __device__ __forceinline__ vec16 gather_ld(const void* p) {
   if constexpr (CKV_GATHER_NT_LOAD) return ld16_stream(p);
   else return ld16(p);
 }
-__device__ __forceinline__ void gather_st(void* p, const vec16& v) {
-  if constexpr (CKV_GATHER_NT_STORE) st16_stream(p, v);
-  else st16(p, v);
-}
 
-
-// NT_K: the key rows' stores non-temporal (else regular); the value rows' are gather_st's.
-template <int DTYPE, int D, int THREADS, int TILE, int UNROLL, bool SKIP, bool NT_K = true>
+// ST_K / ST_V: the StorePolicy of the key rows' and the value rows' stores.
+template <int DTYPE, int D, int THREADS, int TILE, int UNROLL, bool SKIP, int ST_K = kStStream,
+          int ST_V = kStStream>
 __device__ __forceinline__ void gather_tile(
     char* __restrict__ dst_k, char* __restrict__ dst_v, int64_t dst_layer_stride_b, int64_t dst_head_stride_b,
     const uint64_t* __restrict__ src_tab, int n_chunks, const ckv_segment* __restrict__ segs, int seg_index,
@@ -191,16 +184,11 @@ __device__ __forceinline__ void gather_tile(
         // the compiler, which then drops a non-temporal hint the arms share)
         vec16 y1 = kx1[u], y2 = kx2[u];
         if (rotate) rotate_pairs<DTYPE>(kx1[u], kx2[u], c, sn, y1, y2);
-        if constexpr (NT_K) {
-          gather_st(dk0 + o, y1);
-          gather_st(dk0 + o + HALF_B, y2);
-        } else {
-          st16(dk0 + o, y1);
-          st16(dk0 + o + HALF_B, y2);
-        }
+        st16_policy<ST_K>(dk0 + o, y1);
+        st16_policy<ST_K>(dk0 + o + HALF_B, y2);
         if (with_v) {
-          gather_st(dv0 + o, vx1[u]);
-          gather_st(dv0 + o + HALF_B, vx2[u]);
+          st16_policy<ST_V>(dv0 + o, vx1[u]);
+          st16_policy<ST_V>(dv0 + o + HALF_B, vx2[u]);
         }
       }
     }

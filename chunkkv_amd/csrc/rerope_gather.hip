@@ -29,23 +29,29 @@ namespace ckv {
 //  - Segment-fastest grid (x = segment, y = tile), 256 x 16 x 4, for launches of 64 segments or
 //    more: the replay's 4 concurrent 32k requests (128 segments each) reach 75.0 % of HBM peak
 //    with it, 68.2 % with the tile-fastest shapes above.
-// Stores: rows are loaded non-temporally and value rows stored non-temporally by every shape; the
-// key rows of the skip shape go out as regular stores, those of the others non-temporally
-// (measured, same box: the 8k request's dropped rows of layers 4-27 with layer 1's kept rows
-// 90.3 us against 98.5 us with non-temporal key stores; config 2's dense gather 78.0 against
-// 80.4 us and config 5's rounds 2.908 against 2.984 ms the other way round; both hints regular:
-// 112.0 us / 83.9 us / 3.000 ms).
+// Stores (a StorePolicy per shape; rows are loaded non-temporally by every shape): the skip and
+// dense shapes store the key rows with device scope (sc1: written through the L2, nothing of
+// them left for the end-of-launch writeback) and the value rows with device scope and
+// non-temporally; the wide shape stores both non-temporally. Measured, same box each: the 8k
+// request's dropped rows of layers 4-27 with layer 1's kept rows 88.0 us against 90.1-90.4 us
+// with regular key rows and non-temporal value rows (the request step 219.5-219.8 against 222.7
+// us; earlier: 98.5 us with both non-temporal, 112.0 us both regular); config 2's dense gather
+// 77.3-77.9 against 77.8-78.3 us with both non-temporal; config 5's rounds 2.908-2.919 ms with
+// both non-temporal against 3.015-3.024 ms with either device-scope form.
 struct GatherDense {
   static constexpr int kThreads = 256, kTile = 8, kUnroll = 2;
-  static constexpr bool kSegFastest = false, kNtK = true;
+  static constexpr bool kSegFastest = false;
+  static constexpr int kStK = kStAgent, kStV = kStAgentStream;
 };
 struct GatherSkip {
   static constexpr int kThreads = 512, kTile = 16, kUnroll = 1;
-  static constexpr bool kSegFastest = false, kNtK = false;
+  static constexpr bool kSegFastest = false;
+  static constexpr int kStK = kStAgent, kStV = kStAgentStream;
 };
 struct GatherWide {
   static constexpr int kThreads = 256, kTile = 16, kUnroll = 4;
-  static constexpr bool kSegFastest = true, kNtK = true;
+  static constexpr bool kSegFastest = true;
+  static constexpr int kStK = kStStream, kStV = kStStream;
 };
 constexpr int kGatherWideSegs = 64;  // segment count from which GatherWide is used
 
@@ -75,7 +81,7 @@ __global__ __launch_bounds__(S::kThreads) void rerope_gather_kernel(
     }
     zl -= scat_z;
   }
-  gather_tile<DTYPE, D, S::kThreads, S::kTile, S::kUnroll, true, S::kNtK>(
+  gather_tile<DTYPE, D, S::kThreads, S::kTile, S::kUnroll, true, S::kStK, S::kStV>(
       dst_k, dst_v, dst_layer_stride_b, dst_head_stride_b, src_tab, n_chunks, segs,
       (int)(S::kSegFastest ? blockIdx.x : blockIdx.y), one_seg, one_src_k, one_src_v, one_src_head_stride_b, n_layers,
       layer_begin + zl, (int)(S::kSegFastest ? blockIdx.y : blockIdx.x), n_heads, n_tokens, skip, inv, err);
